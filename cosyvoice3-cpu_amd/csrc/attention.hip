@@ -1,0 +1,257 @@
+// Scaled dot-product attention (cv3cpu/ops.py:244-310) on strided q/k/v.
+//
+//   out[b, h, n, :] = softmax_m((q[b, h, n] * scale) . k[b, h', m]  + mask) . v[b, h', m]
+//   with h' = h / (H / Hk) (grouped-query attention, ops.py:279-283) and masks
+//   none / ("causal", offset) / ("chunk", size, left) (ops.py:244-264).
+//
+// The reference takes one ordinary softmax per query tile; here the softmax is
+// streamed over key tiles (online max/sum rescaling), which changes only
+// rounding.  The head_dim == 64 path runs on the matrix cores with
+// v_mfma_f32_16x16x4_f32.  It computes S^T = K . Q^T so that each lane's
+// accumulator registers already hold P^T in the B-operand layout of the next
+// MFMA, O^T += V^T . P^T: no LDS round trip for the probabilities.
+#include "common.hpp"
+
+using namespace cv3;
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct AttnParams {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_sb, q_sh, q_sn;
+  int64_t k_sb, k_sh, k_sm;
+  int64_t v_sb, v_sh, v_sm;
+  int64_t o_sb, o_sh, o_sn;
+  int h, hk;
+  int64_t n, m;
+  int d;
+  float scale;
+  int mask_kind;  // 0 none, 1 causal(a = offset), 2 chunk(a = size, b = left)
+  int64_t mask_a, mask_b;
+};
+
+__device__ __forceinline__ bool allowed(const AttnParams& p, int64_t qi, int64_t kj) {
+  if (p.mask_kind == 1) return kj <= qi + p.mask_a;
+  if (p.mask_kind == 2) {
+    const int64_t size = p.mask_a;
+    const int64_t end = (qi / size + 1) * size;
+    const int64_t start = p.mask_b < 0 ? 0 : ((qi / size - p.mask_b) * size > 0 ? (qi / size - p.mask_b) * size : 0);
+    return kj < end && kj >= start;
+  }
+  return true;
+}
+
+constexpr int KT = 64;        // keys per LDS tile
+constexpr int KS = 68;        // LDS row stride (floats) for K and V tiles
+constexpr int QW = 16;        // queries per wave
+constexpr int WAVES = 4;      // waves per workgroup
+
+__global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
+  __shared__ float Ks[KT * KS];
+  __shared__ float Vs[KT * KS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.z, hq = blockIdx.y;
+  const int hkv = hq / (p.h / p.hk);
+  const int64_t q0 = (int64_t)blockIdx.x * (QW * WAVES) + wave * QW;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int64_t qi = q0 + c16;
+  const bool qvalid = qi < p.n;
+
+  // Q fragments, pre-scaled like the reference's (q * scale) (ops.py:292)
+  f32x4 qf[4];
+  const float* qrow = p.q + b * p.q_sb + hq * p.q_sh + (qvalid ? qi : 0) * p.q_sn;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    const float4 t = qvalid ? *reinterpret_cast<const float4*>(qrow + s4 * 16 + g * 4) : make_float4(0, 0, 0, 0);
+    qf[s4] = f32x4{t.x * p.scale, t.y * p.scale, t.z * p.scale, t.w * p.scale};
+  }
+
+  f32x4 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
+  const int64_t ntiles = ceil_div(p.m, KT);
+  for (int64_t kt = 0; kt < ntiles; ++kt) {
+    const int64_t k0 = kt * KT;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int idx = tid + 256 * r;
+      const int key = idx >> 4, d4 = (idx & 15) * 4;
+      const int64_t kj = k0 + key;
+      float4 kv = make_float4(0, 0, 0, 0), vv = make_float4(0, 0, 0, 0);
+      if (kj < p.m) {
+        kv = *reinterpret_cast<const float4*>(kbase + kj * p.k_sm + d4);
+        vv = *reinterpret_cast<const float4*>(vbase + kj * p.v_sm + d4);
+      }
+      *reinterpret_cast<float4*>(&Ks[key * KS + d4]) = kv;
+      *reinterpret_cast<float4*>(&Vs[key * KS + d4]) = vv;
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int sub = 0; sub < KT / 16; ++sub) {
+      // S^T tile: rows = 16 keys, cols = 16 queries
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float* krow = &Ks[(sub * 16 + c16) * KS + g * 4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float4 kf = *reinterpret_cast<const float4*>(krow + s4 * 16);
+        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[s4].x, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[s4].y, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[s4].z, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[s4].w, s, 0, 0, 0);
+      }
+      // s[i] = score of key k0 + sub*16 + 4g + i for query qi
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t kj = k0 + sub * 16 + 4 * g + i;
+        if (kj >= p.m || !allowed(p, qi, kj)) s[i] = -INFINITY;
+        mx = fmaxf(mx, s[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Branch-free so the wave-wide MFMAs below see uniform control flow: a
+      // query column with nothing visible yet keeps alpha = 1 and p = 0.
+      const float m_new = fmaxf(m_run, mx);
+      const bool none = m_new == -INFINITY;
+      const float m_use = none ? 0.f : m_new;
+      const float alpha = none ? 1.f : expf(m_run - m_new);
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = expf(s[i] - m_use);
+        psum += s[i];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        oacc[db] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float vf = Vs[(sub * 16 + 4 * g + i) * KS + db * 16 + c16];
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, s[i], oacc[db], 0, 0, 0);
+        }
+      }
+    }
+  }
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (!qvalid) return;
+  float* orow = p.o + b * p.o_sb + hq * p.o_sh + qi * p.o_sn;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) orow[db * 16 + 4 * g + i] = oacc[db][i] / l_tot;
+}
+
+// Generic path for any head dim <= 256: one wave per query row, 64 keys per step.
+__global__ __launch_bounds__(256) void k_attn_generic(AttnParams p) {
+  extern __shared__ float qs_all[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.z, hq = blockIdx.y;
+  const int hkv = hq / (p.h / p.hk);
+  const int64_t qi = (int64_t)blockIdx.x * 4 + wave;
+  float* qs = qs_all + wave * p.d;
+  const bool qvalid = qi < p.n;
+  const float* qrow = p.q + b * p.q_sb + hq * p.q_sh + (qvalid ? qi : 0) * p.q_sn;
+  for (int d = lane; d < p.d; d += 64) qs[d] = qvalid ? qrow[d] * p.scale : 0.f;
+  __syncthreads();
+  if (!qvalid) return;
+  const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  for (int64_t c0 = 0; c0 < p.m; c0 += 64) {
+    const int64_t kj = c0 + lane;
+    float s = -INFINITY;
+    if (kj < p.m && allowed(p, qi, kj)) {
+      const float* kr = kbase + kj * p.k_sm;
+      float t = 0.f;
+      for (int d = 0; d < p.d; ++d) t = fmaf(qs[d], kr[d], t);
+      s = t;
+    }
+    const float mx = wave_max(s);
+    const float m_new = fmaxf(m_run, mx);
+    if (m_new == -INFINITY) continue;
+    const float alpha = expf(m_run - m_new);
+    const float pj = expf(s - m_new);
+    l_run = l_run * alpha + wave_sum(pj);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] *= alpha;
+    const int64_t cnt = p.m - c0 < 64 ? p.m - c0 : 64;
+    for (int jj = 0; jj < cnt; ++jj) {
+      const float pb = __shfl(pj, jj, 64);
+      const float* vr = vbase + (c0 + jj) * p.v_sm;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        if (d < p.d) acc[r] = fmaf(pb, vr[d], acc[r]);
+      }
+    }
+    m_run = m_new;
+  }
+  float* orow = p.o + b * p.o_sb + hq * p.o_sh + qi * p.o_sn;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int d = lane + 64 * r;
+    if (d < p.d) orow[d] = acc[r] / l_run;
+  }
+}
+
+}  // namespace
+
+extern "C" int cv3_attention(const float* q, const float* k, const float* v, float* out, int64_t batch, int h,
+                             int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
+                             const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                             float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+  CV3_REQUIRE(h > 0 && hk > 0, CV3_EINVAL, "head counts must be positive");
+  CV3_REQUIRE(h % hk == 0, CV3_EINVAL, "%d query heads is not a multiple of %d kv heads", h, hk);
+  CV3_REQUIRE(d > 0 && d <= 256, CV3_EUNSUPPORTED, "head dim %d not supported (max 256)", d);
+  CV3_REQUIRE(mask_kind >= 0 && mask_kind <= 2, CV3_EINVAL, "unknown mask spec kind %d", mask_kind);
+  CV3_REQUIRE(mask_kind != 2 || mask_a > 0, CV3_EINVAL, "chunk mask needs a positive chunk size");
+  if (batch <= 0 || n <= 0) return CV3_OK;
+  CV3_REQUIRE(m > 0, CV3_EINVAL, "attention over zero keys");
+  AttnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = out;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_sn = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_sm = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_sm = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_sn = o_strides[2];
+  p.h = h;
+  p.hk = hk;
+  p.n = n;
+  p.m = m;
+  p.d = d;
+  p.scale = scale;
+  p.mask_kind = mask_kind;
+  p.mask_a = mask_a;
+  p.mask_b = mask_b;
+  hipStream_t st = stream_of(s);
+  const bool aligned16 = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
+                         (p.q_sb % 4 == 0) && (p.q_sh % 4 == 0) && (p.q_sn % 4 == 0) && (p.k_sb % 4 == 0) &&
+                         (p.k_sh % 4 == 0) && (p.k_sm % 4 == 0) && (p.v_sb % 4 == 0) && (p.v_sh % 4 == 0) &&
+                         (p.v_sm % 4 == 0);
+  if (d == 64 && aligned16) {
+    const dim3 grid((unsigned)ceil_div(n, QW * WAVES), (unsigned)h, (unsigned)batch);
+    hipLaunchKernelGGL(k_flash64, grid, dim3(256), 0, st, p);
+  } else {
+    const dim3 grid((unsigned)ceil_div(n, 4), (unsigned)h, (unsigned)batch);
+    hipLaunchKernelGGL(k_attn_generic, grid, dim3(256), 4 * d * sizeof(float), st, p);
+  }
+  CV3_LAUNCHED();
+  return CV3_OK;
+}

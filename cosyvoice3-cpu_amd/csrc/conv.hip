@@ -1,0 +1,234 @@
+// 1-D convolution as an implicit GEMM on the matrix cores (cv3cpu/ops.py:165-219).
+//
+//   y[co, t] = epi( sum_{c < Cin/g, j < k} W[co, c, j] * xin[g*Cin/g + c, t*stride + j*dil - pad_l] )
+//
+// where xin is the input after an optional nearest-neighbour upsample by `up`
+// (cv3cpu/ops.py:335-336 followed by a causal conv, cv3cpu/models/hift.py:139-142):
+// xin[c, u] = x[c, u / up] for 0 <= u < T_in * up, zero outside (the zero padding).
+// The upsampled signal is never materialised.  x and y are addressed through
+// (channel, time) strides, so channels-first (C, T) and channels-last (T, C)
+// buffers both work.
+//
+// GEMM view per group: M = Cout/g (rows of W), N = T_out, K = (Cin/g) * k with
+// the weight's natural (c, j) order.  Tiles, MFMA and K permutation are those of
+// the linear GEMM: a 64 x 64 tile per workgroup, 32 x 32 per wave,
+// v_mfma_f32_32x32x2_f32, BK = 16.
+//
+// Epilogue: y = residual + act(acc + bias), or y = snake(acc + bias) with a
+// per-output-channel alpha (the resblock's second Snake, hift.py:124).
+#include "common.hpp"
+#include "epilogue.hpp"
+
+using namespace cv3;
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int BM = 64, BN = 64, BK = 16, LDS_STRIDE = BK + 4;
+
+struct ConvParams {
+  const float* x;
+  int64_t x_cs, x_ts, t_in;
+  const float* w;  // [cout, cin_g, k] contiguous
+  int64_t cout, cin_g, k;
+  const float* bias;
+  int64_t groups, stride, dil, pad_l, up;
+  int64_t t_out;
+  float* y;
+  int64_t y_cs, y_ts;
+  int act;
+  float act_param;
+  const float* snake_alpha;
+  float snake_eps;
+  const float* res;
+  int64_t r_cs, r_ts;
+};
+
+__device__ __forceinline__ float xin(const ConvParams& p, int64_t c, int64_t u) {
+  if (u < 0 || u >= p.t_in * p.up) return 0.f;
+  return p.x[c * p.x_cs + (u / p.up) * p.x_ts];
+}
+
+__global__ __launch_bounds__(256) void k_conv_mfma(ConvParams p) {
+  __shared__ float As[2][BM * LDS_STRIDE];
+  __shared__ float Bs[2][BN * LDS_STRIDE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t g = blockIdx.z;
+  const int64_t cout_g = p.cout / p.groups;
+  const int64_t m0 = (int64_t)blockIdx.y * BM;  // output channel within group
+  const int64_t n0 = (int64_t)blockIdx.x * BN;  // output time
+  const int64_t K = p.cin_g * p.k;
+  const float* wg = p.w + g * cout_g * K;
+  const int64_t cbase = g * p.cin_g;
+
+  // A (weights): thread -> row tid/4, 4 consecutive k at (tid%4)*4
+  const int arow = tid >> 2, ak = (tid & 3) * 4;
+  // B (im2col): thread -> k index tid/16, 4 consecutive times at (tid%16)*4
+  const int bk = tid >> 4, bt = (tid & 15) * 4;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int r32 = lane & 31, h = lane >> 5;
+
+  auto load_a = [&](int64_t kk, float* out4) {
+    const int64_t row = m0 + arow;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out4[i] = (row < cout_g && kk + i < K) ? wg[row * K + kk + i] : 0.f;
+  };
+  auto load_b = [&](int64_t kk, float* out4) {
+    const int64_t kidx = kk + bk;
+    if (kidx >= K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out4[i] = 0.f;
+      return;
+    }
+    const int64_t c = kidx / p.k, j = kidx % p.k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t t = n0 + bt + i;
+      out4[i] = t < p.t_out ? xin(p, cbase + c, t * p.stride + j * p.dil - p.pad_l) : 0.f;
+    }
+  };
+
+  float ra[4], rb[4];
+  load_a(ak, ra);
+  load_b(0, rb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    As[0][arow * LDS_STRIDE + ak + i] = ra[i];
+    Bs[0][(bt + i) * LDS_STRIDE + bk] = rb[i];
+  }
+  __syncthreads();
+
+  f32x16 acc = {0.f};
+  const int64_t ksteps = ceil_div(K, BK);
+  for (int64_t s = 0; s < ksteps; ++s) {
+    const int buf = s & 1;
+    const bool more = s + 1 < ksteps;
+    if (more) {
+      load_a((s + 1) * BK + ak, ra);
+      load_b((s + 1) * BK, rb);
+    }
+    const float* as = &As[buf][(wm + r32) * LDS_STRIDE + h * 4];
+    const float* bs = &Bs[buf][(wn + r32) * LDS_STRIDE + h * 4];
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      const float4 av = *reinterpret_cast<const float4*>(as + gq * 8);
+      const float4 bv = *reinterpret_cast<const float4*>(bs + gq * 8);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        As[buf ^ 1][arow * LDS_STRIDE + ak + i] = ra[i];
+        Bs[buf ^ 1][(bt + i) * LDS_STRIDE + bk] = rb[i];
+      }
+    }
+    __syncthreads();
+  }
+
+  // acc reg i -> (row = output channel, col = time): row (i/4)*8 + h*4 + i%4, col lane%32
+  const int64_t t = n0 + wn + r32;
+  if (t >= p.t_out) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t co_g = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (co_g < cout_g) {
+      const int64_t co = g * cout_g + co_g;
+      float v = acc[i] + (p.bias ? p.bias[co] : 0.f);
+      if (p.snake_alpha) {
+        const float a = p.snake_alpha[co];
+        const float sn = sinf(a * v);
+        v = v + (1.0f / (a + p.snake_eps)) * (sn * sn);
+      } else {
+        v = apply_act(p.act, v, p.act_param);
+      }
+      if (p.res) v = p.res[co * p.r_cs + t * p.r_ts] + v;
+      p.y[co * p.y_cs + t * p.y_ts] = v;
+    }
+  }
+}
+
+// groups == C convolution as k shifted multiply-accumulates (ops.py:222-237)
+__global__ void k_depthwise(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+                            float* __restrict__ y, int64_t c, int64_t t_in, int64_t k, int64_t dil, int64_t pad_l,
+                            int64_t t_out) {
+  const int64_t n = c * t_out;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t ch = i / t_out, t = i % t_out;
+    float acc = 0.f;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t u = t + j * dil - pad_l;
+      const float xv = (u >= 0 && u < t_in) ? x[ch * t_in + u] : 0.f;
+      acc = acc + w[ch * k + j] * xv;
+    }
+    if (bias) acc += bias[ch];
+    y[i] = acc;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t x_ts, const float* w, int64_t cout,
+               int64_t k, const float* bias, int64_t stride, int64_t dilation, int64_t groups, int64_t pad_l,
+               int64_t pad_r, int64_t up, float* y, int64_t y_cs, int64_t y_ts, int64_t* t_out_ptr, int act,
+               float act_param, const float* snake_alpha, float snake_eps, const float* residual, int64_t r_cs,
+               int64_t r_ts, cv3_stream_t s) {
+  CV3_REQUIRE(groups >= 1 && cin % groups == 0 && cout % groups == 0, CV3_EASSERT,
+              "channels %lld/%lld not divisible by groups %lld", (long long)cin, (long long)cout, (long long)groups);
+  CV3_REQUIRE(stride >= 1 && dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0, CV3_EINVAL,
+              "bad conv geometry");
+  const int64_t tp = t_in * up + pad_l + pad_r;
+  const int64_t span = dilation * (k - 1) + 1;
+  const int64_t t_out = tp >= span ? (tp - span) / stride + 1 : 0;
+  if (t_out_ptr) *t_out_ptr = t_out;
+  if (t_out <= 0 || !y) return CV3_OK;
+  ConvParams p{};
+  p.x = x;
+  p.x_cs = x_cs;
+  p.x_ts = x_ts;
+  p.t_in = t_in;
+  p.w = w;
+  p.cout = cout;
+  p.cin_g = cin / groups;
+  p.k = k;
+  p.bias = bias;
+  p.groups = groups;
+  p.stride = stride;
+  p.dil = dilation;
+  p.pad_l = pad_l;
+  p.up = up;
+  p.t_out = t_out;
+  p.y = y;
+  p.y_cs = y_cs;
+  p.y_ts = y_ts;
+  p.act = act;
+  p.act_param = act_param;
+  p.snake_alpha = snake_alpha;
+  p.snake_eps = snake_eps;
+  p.res = residual;
+  p.r_cs = r_cs;
+  p.r_ts = r_ts;
+  const dim3 grid((unsigned)ceil_div(t_out, BN), (unsigned)ceil_div(cout / groups, BM), (unsigned)groups);
+  hipLaunchKernelGGL(k_conv_mfma, grid, dim3(256), 0, stream_of(s), p);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,
+                         int64_t dilation, int64_t pad_l, int64_t pad_r, float* y, int64_t* t_out_ptr,
+                         cv3_stream_t s) {
+  const int64_t t_out = t_in + pad_l + pad_r - dilation * (k - 1);
+  if (t_out_ptr) *t_out_ptr = t_out;
+  if (t_out <= 0 || !y) return CV3_OK;
+  const int64_t n = c * t_out;
+  hipLaunchKernelGGL(k_depthwise, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 65536)), dim3(256), 0,
+                     stream_of(s), x, w, bias, y, c, t_in, k, dilation, pad_l, t_out);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,367 @@
+// Elementwise, row-reduction and table kernels around the GEMMs:
+// activations (cv3cpu/ops.py:30-81), Snake (ops.py:77-81), row softmax /
+// log_softmax (ops.py:84-93), RMSNorm (ops.py:101-104), LayerNorm with optional
+// affine or AdaLN modulation (ops.py:107-118, cv3cpu/models/dit.py:168-178),
+// rotary tables and rotation (dit.py:21-54, cv3cpu/models/qwen2.py:35-71), the
+// CFG combine + Euler update (cv3cpu/models/flow.py:86-87), resampling
+// (ops.py:318-336), Hann window (ops.py:339-343) and 2-D transposes.
+//
+// All of these are HBM-bound: one read and one write per element, fused where a
+// caller would otherwise make several passes.
+#include "common.hpp"
+#include "epilogue.hpp"
+
+using namespace cv3;
+
+namespace {
+
+inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 65536) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, per_block), cap));
+}
+
+__global__ void k_act(int act, float param, const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = apply_act(act, x[i], param);
+}
+
+__global__ void k_binary(int op, const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y,
+                         int64_t n, float alpha, float beta) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float u = a[i], v = b[i];
+    float r;
+    switch (op) {
+      case 0: r = u + v; break;                    // add
+      case 1: r = u * v; break;                    // mul
+      case 2: r = act_silu(u) * v; break;          // silu(a) * b  (qwen2.py:177)
+      default: r = alpha * u + beta * v; break;    // axpby
+    }
+    y[i] = r;
+  }
+}
+
+// Snake over (C, T): x + (1 / (alpha + eps)) * sin(alpha x)^2   (ops.py:77-81)
+__global__ void k_snake(const float* __restrict__ x, const float* __restrict__ alpha, float* __restrict__ y,
+                        int64_t c, int64_t t, float eps) {
+  const int64_t n = c * t;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float a = alpha[i / t];
+    const float v = x[i];
+    const float s = sinf(a * v);
+    y[i] = v + (1.0f / (a + eps)) * (s * s);
+  }
+}
+
+// One workgroup per row.  softmax: e = exp(x - max), e / sum;  log: z - log(sum exp z).
+__global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ x, float* __restrict__ y, int64_t cols,
+                                                      int logmode) {
+  __shared__ float red[4];
+  const float* xr = x + (int64_t)blockIdx.x * cols;
+  float* yr = y + (int64_t)blockIdx.x * cols;
+  float m = -INFINITY;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) m = fmaxf(m, xr[c]);
+  m = block_max(m, red);
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s += expf(xr[c] - m);
+  s = block_sum(s, red);
+  if (logmode) {
+    const float ls = logf(s);
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) yr[c] = (xr[c] - m) - ls;
+  } else {
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) yr[c] = expf(xr[c] - m) / s;
+  }
+}
+
+// RMSNorm: (x * (1/sqrt(mean(x^2) + eps))) * w   (ops.py:101-104)
+__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, const float* __restrict__ w,
+                                                  float* __restrict__ y, int64_t cols, float eps) {
+  __shared__ float red[4];
+  const float* xr = x + (int64_t)blockIdx.x * cols;
+  float* yr = y + (int64_t)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) ss = fmaf(xr[c], xr[c], ss);
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) yr[c] = (xr[c] * inv) * w[c];
+}
+
+// LayerNorm, two-pass centred variance (ops.py:107-118), then either an affine
+// (w, b) or the AdaLN modulation norm * (1 + scale[g]) + shift[g] with
+// g = row / rows_per_group (cv3cpu/models/dit.py:168-169,178).
+__global__ __launch_bounds__(256) void k_layer_norm(const float* __restrict__ x, float* __restrict__ y, int64_t cols,
+                                                    float eps, const float* __restrict__ w,
+                                                    const float* __restrict__ b, const float* __restrict__ shift,
+                                                    const float* __restrict__ scale, int64_t mod_stride,
+                                                    int64_t rows_per_group) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float* yr = y + row * cols;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s += xr[c];
+  const float mu = block_sum(s, red) / (float)cols;
+  float v = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const float d = xr[c] - mu;
+    v = fmaf(d, d, v);
+  }
+  const float var = block_sum(v, red) / (float)cols;
+  const float den = sqrtf(var + eps);
+  const int64_t g = rows_per_group > 0 ? row / rows_per_group : 0;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    float o = (xr[c] - mu) / den;
+    if (w) o = o * w[c];
+    if (b) o = o + b[c];
+    if (scale) o = o * (1.0f + scale[g * mod_stride + c]);
+    if (shift) o = o + shift[g * mod_stride + c];
+    yr[c] = o;
+  }
+}
+
+// Rotary tables.  kind 0 (DiT, dit.py:21-29,51-52): angle_f32 = f32(t * inv_f64),
+// interleaved duplicate, cos/sin in fp32.  kind 1 (Qwen2, qwen2.py:46-56):
+// angle in fp64, half-split duplicate, cos/sin in fp64 then rounded to fp32.
+__global__ void k_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* __restrict__ cosv,
+                             float* __restrict__ sinv) {
+  const int64_t total = n * dim;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / dim + pos0;
+    const int c = (int)(i % dim);
+    const int fi = kind == 0 ? c / 2 : c % (dim / 2);
+    const double inv = 1.0 / pow(theta, (double)(2 * fi) / (double)dim);
+    const double ang = (double)t * inv;
+    if (kind == 0) {
+      const float a = (float)ang;
+      cosv[i] = cosf(a);
+      sinv[i] = sinf(a);
+    } else {
+      cosv[i] = (float)cos(ang);
+      sinv[i] = (float)sin(ang);
+    }
+  }
+}
+
+// DiT partial rotary on the first `rot` channels of rows of width `ld`
+// (before the head split, dit.py:40-54): pairs (2i, 2i+1) -> (x0 c0 - x1 s0, x1 c1 + x0 s1).
+// Row r is time step r % rows_per_batch.  Works in place.
+__global__ void k_rope_pairs(float* __restrict__ x, int64_t ld, int64_t rows, int64_t rows_per_batch, int rot,
+                             const float* __restrict__ cosv, const float* __restrict__ sinv) {
+  const int half = rot / 2;
+  const int64_t total = rows * half;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / half;
+    const int p = (int)(i % half);
+    const int64_t t = r % rows_per_batch;
+    float* xr = x + r * ld;
+    const float x0 = xr[2 * p], x1 = xr[2 * p + 1];
+    const float* c = cosv + t * rot;
+    const float* s = sinv + t * rot;
+    xr[2 * p] = x0 * c[2 * p] + (-x1) * s[2 * p];
+    xr[2 * p + 1] = x1 * c[2 * p + 1] + x0 * s[2 * p + 1];
+  }
+}
+
+// Qwen2 half-split rotary over vectors of length d: x cos + rotate_half(x) sin
+// (qwen2.py:64-71).  Vector v lives at x + (v / per_pos) * ld_pos + (v % per_pos) * d
+// and uses table row pos0 + v / per_pos.  Works in place.
+__global__ void k_rope_half(float* __restrict__ x, int64_t nvec, int64_t per_pos, int64_t ld_pos, int d,
+                            const float* __restrict__ cosv, const float* __restrict__ sinv, int64_t pos0) {
+  const int half = d / 2;
+  const int64_t total = nvec * half;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = i / half;
+    const int j = (int)(i % half);
+    const int64_t t = v / per_pos;
+    float* xv = x + t * ld_pos + (v % per_pos) * d;
+    const float a = xv[j], b = xv[j + half];
+    const float* c = cosv + (pos0 + t) * d;
+    const float* s = sinv + (pos0 + t) * d;
+    xv[j] = a * c[j] + (-b) * s[j];
+    xv[j + half] = b * c[j + half] + a * s[j + half];
+  }
+}
+
+// CFG combine + Euler step: x += dt * ((1 + w) d_cond - w d_uncond)   (flow.py:86-87)
+__global__ void k_cfg_euler(float* __restrict__ x, const float* __restrict__ dc, const float* __restrict__ du,
+                            int64_t n, float dt, float w) {
+  const float a = 1.0f + w;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float dphi = a * dc[i] - w * du[i];
+    x[i] = x[i] + dt * dphi;
+  }
+}
+
+__global__ void k_interp_nearest(const float* __restrict__ x, float* __restrict__ y, int64_t c, int64_t t, int r) {
+  const int64_t n = c * t * r;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / (t * r), j = i % (t * r);
+    y[i] = x[row * t + j / r];
+  }
+}
+
+// F.interpolate(mode='linear') over the last axis (ops.py:318-332); positions in fp64.
+__global__ void k_interp_linear(const float* __restrict__ x, float* __restrict__ y, int64_t c, int64_t t,
+                                int64_t size, int align) {
+  const int64_t n = c * size;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / size, j = i % size;
+    double pos;
+    if (align) {
+      pos = size > 1 ? (double)j * ((double)(t - 1) / (double)(size - 1)) : 0.0;
+    } else {
+      pos = ((double)j + 0.5) * ((double)t / (double)size) - 0.5;
+      pos = fmin(fmax(pos, 0.0), (double)(t - 1));
+    }
+    const int64_t i0 = (int64_t)floor(pos);
+    const int64_t i1 = i0 + 1 < t ? i0 + 1 : t - 1;
+    const float f = (float)(pos - (double)i0);
+    y[i] = x[row * t + i0] * (1.0f - f) + x[row * t + i1] * f;
+  }
+}
+
+__global__ void k_hann(int n, int periodic, float* __restrict__ w) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const double den = periodic ? (double)n : (double)(n - 1);
+    w[i] = (float)(0.5 - 0.5 * cos(2.0 * M_PI * (double)i / den));
+  }
+}
+
+// batch of (rows, cols) -> (cols, rows) transposes through a padded LDS tile
+__global__ void k_transpose(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int64_t cols) {
+  __shared__ float tile[32][33];
+  const int64_t b = blockIdx.z;
+  const float* xb = x + b * rows * cols;
+  float* yb = y + b * rows * cols;
+  const int64_t c0 = (int64_t)blockIdx.x * 32, r0 = (int64_t)blockIdx.y * 32;
+  for (int j = threadIdx.y; j < 32; j += blockDim.y) {
+    const int64_t r = r0 + j, c = c0 + threadIdx.x;
+    if (r < rows && c < cols) tile[j][threadIdx.x] = xb[r * cols + c];
+  }
+  __syncthreads();
+  for (int j = threadIdx.y; j < 32; j += blockDim.y) {
+    const int64_t c = c0 + j, r = r0 + threadIdx.x;
+    if (r < rows && c < cols) yb[c * rows + r] = tile[threadIdx.x][j];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_stream_t s) {
+  if (n <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_act, dim3(grid_for(n)), dim3(256), 0, stream_of(s), act, param, x, y, n);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, float alpha, float beta, cv3_stream_t s) {
+  if (n <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_binary, dim3(grid_for(n)), dim3(256), 0, stream_of(s), op, a, b, y, n, alpha, beta);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s) {
+  if (c * t <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_snake, dim3(grid_for(c * t)), dim3(256), 0, stream_of(s), x, alpha, y, c, t, eps);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, int log_softmax, cv3_stream_t s) {
+  if (rows <= 0 || cols <= 0) return CV3_OK;
+  CV3_REQUIRE(rows < (1ll << 31), CV3_EINVAL, "too many rows");
+  hipLaunchKernelGGL(k_softmax_rows, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, y, cols, log_softmax);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t cols, float eps, cv3_stream_t s) {
+  if (rows <= 0 || cols <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, w, y, cols, eps);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
+                   const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
+                   cv3_stream_t s) {
+  if (rows <= 0 || cols <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_layer_norm, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, y, cols, eps, w, b, shift,
+                     scale, mod_stride, rows_per_group);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* cos_out, float* sin_out,
+                   cv3_stream_t s) {
+  CV3_REQUIRE(kind == 0 || kind == 1, CV3_EINVAL, "rope table kind must be 0 (dit) or 1 (qwen)");
+  CV3_REQUIRE(dim > 0 && dim % 2 == 0, CV3_EINVAL, "rope dim must be even");
+  if (n <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_rope_table, dim3(grid_for(n * dim)), dim3(256), 0, stream_of(s), kind, theta, dim, n, pos0,
+                     cos_out, sin_out);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_rope_pairs(float* x, int64_t ld, int64_t rows, int64_t rows_per_batch, int rot, const float* cos_tab,
+                   const float* sin_tab, cv3_stream_t s) {
+  CV3_REQUIRE(rot % 2 == 0 && rot <= ld, CV3_EINVAL, "rotary width must be even and <= row width");
+  if (rows <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_rope_pairs, dim3(grid_for(rows * rot / 2)), dim3(256), 0, stream_of(s), x, ld, rows,
+                     rows_per_batch, rot, cos_tab, sin_tab);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_rope_half(float* x, int64_t nvec, int64_t per_pos, int64_t ld_pos, int d, const float* cos_tab,
+                  const float* sin_tab, int64_t pos0, cv3_stream_t s) {
+  CV3_REQUIRE(d % 2 == 0, CV3_EINVAL, "head dim must be even");
+  if (nvec <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_rope_half, dim3(grid_for(nvec * d / 2)), dim3(256), 0, stream_of(s), x, nvec, per_pos, ld_pos,
+                     d, cos_tab, sin_tab, pos0);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_cfg_euler(float* x, const float* d_cond, const float* d_uncond, int64_t n, float dt, float w,
+                  cv3_stream_t s) {
+  if (n <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_cfg_euler, dim3(grid_for(n)), dim3(256), 0, stream_of(s), x, d_cond, d_uncond, n, dt, w);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_interp_nearest(const float* x, float* y, int64_t c, int64_t t, int r, cv3_stream_t s) {
+  if (c * t * r <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_interp_nearest, dim3(grid_for(c * t * r)), dim3(256), 0, stream_of(s), x, y, c, t, r);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_interp_linear(const float* x, float* y, int64_t c, int64_t t, int64_t size, int align_corners,
+                      cv3_stream_t s) {
+  if (c * size <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_interp_linear, dim3(grid_for(c * size)), dim3(256), 0, stream_of(s), x, y, c, t, size,
+                     align_corners);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_hann_window(int n, int periodic, float* out, cv3_stream_t s) {
+  if (n <= 0) return CV3_OK;
+  hipLaunchKernelGGL(k_hann, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream_of(s), n, periodic, out);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t cols, cv3_stream_t s) {
+  if (batch * rows * cols <= 0) return CV3_OK;
+  const dim3 grid((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32), (unsigned)batch);
+  hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, stream_of(s), x, y, rows, cols);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+// ops.linear / quant.qmatmul entry points (cv3cpu/ops.py:121-123,
+// cv3cpu/quant.py:156-204): GEMV for up to four activation rows, the MFMA GEMM
+// above that.
+#include "common.hpp"
+
+namespace cv3 {
+int gemv(int wk, bool sf16, bool swiglu, const float* x, int64_t m, int64_t k, int64_t ldx, const void* w,
+         int64_t ldw_bytes, const void* scales, int64_t nb, int64_t block, int64_t n, const float* bias, float* y,
+         int64_t ldy, const cv3_epilogue* epi, const float* rms_w, float rms_eps, hipStream_t st);
+int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb, const void* scales,
+         bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
+         const cv3_epilogue* epi, hipStream_t st);
+}  // namespace cv3
+
+using namespace cv3;
+
+static constexpr int64_t kGemvRows = 4;  // quant.py:43 THREAD_ROW_LIMIT: the decode regime
+
+extern "C" {
+
+int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t ldw, int64_t n,
+                   const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_REQUIRE(m >= 0 && k > 0 && n >= 0 && ldw >= k && ldx >= k && ldy >= n, CV3_EINVAL,
+              "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
+  if (!m || !n) return CV3_OK;
+  hipStream_t st = stream_of(s);
+  if (m <= kGemvRows)
+    return gemv(0, false, false, x, m, k, ldx, w, ldw * 4, nullptr, 1, k, n, bias, y, ldy, epi, nullptr, 0.f, st);
+  return gemm(false, x, m, k, ldx, w, ldw, nullptr, false, 1, k, n, bias, y, ldy, epi, st);
+}
+
+int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
+                 int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
+                 const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_REQUIRE(kind == CV3_KIND_Q8 || kind == CV3_KIND_Q4, CV3_EINVAL, "unknown quant kind %d", kind);
+  CV3_REQUIRE(m >= 0 && k > 0 && kp >= k && block > 0 && kp % block == 0 && ldx >= k && ldy >= n, CV3_EINVAL,
+              "bad quantised linear shape m=%lld k=%lld kp=%lld block=%lld", (long long)m, (long long)k,
+              (long long)kp, (long long)block);
+  if (!m || !n) return CV3_OK;
+  hipStream_t st = stream_of(s);
+  const bool sf16 = scale_dtype == CV3_F16;
+  const int64_t nb = kp / block;
+  if (kind == CV3_KIND_Q8) {
+    if (m <= kGemvRows)
+      return gemv(1, sf16, false, x, m, k, ldx, q, kp, scales, nb, block, n, bias, y, ldy, epi, nullptr, 0.f, st);
+    return gemm(true, x, m, k, ldx, q, kp, scales, sf16, nb, block, n, bias, y, ldy, epi, st);
+  }
+  // q4: GEMV directly; many rows go through the GEMV four rows at a time
+  for (int64_t r = 0; r < m; r += kGemvRows) {
+    const int64_t mm = std::min<int64_t>(kGemvRows, m - r);
+    cv3_epilogue e = epi ? *epi : cv3_epilogue{};
+    if (e.residual) e.residual += r * e.ld_res;
+    if (e.gate && e.rows_per_gate > 0) {
+      // gate rows are indexed by absolute row; shift by whole gate groups only
+      CV3_REQUIRE(r % e.rows_per_gate == 0 || e.rows_per_gate >= m, CV3_EINVAL, "q4 gate grouping");
+      e.gate += (r / e.rows_per_gate) * e.gate_stride;
+    }
+    int rc = gemv(2, true, false, x + r * ldx, mm, k, ldx, q, kp / 2, scales, nb, block, n, bias, y + r * ldy, ldy,
+                  &e, nullptr, 0.f, st);
+    if (rc) return rc;
+  }
+  return CV3_OK;
+}
+
+}  // extern "C"

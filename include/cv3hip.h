@@ -1,0 +1,193 @@
+/*
+ * cv3hip — C ABI of the MI355X (gfx950) tensor-kernel backend for the
+ * CosyVoice 3 NumPy runtime.
+ *
+ * Every entry point takes plain device pointers, int64 sizes and an optional
+ * stream (NULL = the calling thread's own stream), and returns an int status
+ * (CV3_OK = 0).  On failure cv3_last_error() returns a thread-local message.
+ * Status codes map onto the exceptions the reference raises:
+ *   CV3_EINVAL  -> ValueError      CV3_EINDEX -> IndexError
+ *   CV3_EASSERT -> AssertionError  CV3_EHIP   -> RuntimeError (HIP failure)
+ *
+ * The reference (cv3cpu) has no FFI of its own: its kernels are the module
+ * functions of cv3cpu/ops.py and cv3cpu/quant.py, which the models resolve at
+ * call time.  Each entry point below names the reference function whose work it
+ * replaces; the Python host package binds them with ctypes behind those same
+ * function names and signatures.
+ */
+#ifndef CV3HIP_H
+#define CV3HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cv3_stream_opaque* cv3_stream_t;
+
+enum { CV3_OK = 0, CV3_EINVAL = 1, CV3_EINDEX = 2, CV3_EASSERT = 3, CV3_EHIP = 4, CV3_EUNSUPPORTED = 5 };
+
+/* element / weight kinds */
+enum { CV3_F32 = 0, CV3_F16 = 1 };
+enum { CV3_KIND_F32 = 0, CV3_KIND_F16 = 1, CV3_KIND_Q8 = 2, CV3_KIND_Q4 = 3 };
+
+/* activations (cv3cpu/ops.py:30-81) */
+enum {
+  CV3_ACT_NONE = 0,
+  CV3_ACT_SILU = 1,       /* ops.silu        ops.py:30  */
+  CV3_ACT_SIGMOID = 2,    /* ops.sigmoid     ops.py:34  */
+  CV3_ACT_GELU_TANH = 3,  /* ops.gelu_tanh   ops.py:41  */
+  CV3_ACT_GELU = 4,       /* ops.gelu        ops.py:46  */
+  CV3_ACT_MISH = 5,       /* ops.mish        ops.py:63  */
+  CV3_ACT_ELU = 6,        /* ops.elu         ops.py:69  (param = alpha) */
+  CV3_ACT_LEAKY = 7,      /* ops.leaky_relu  ops.py:73  (param = slope) */
+  CV3_ACT_TANH = 8
+};
+
+/*
+ * Linear epilogue: y = residual + gate * act(acc + bias)
+ *   residual: [m, ld_res] or NULL (0);  gate: gate[(row / rows_per_gate) * gate_stride + col] or NULL (1).
+ * `y` may alias `residual` (each element is read and written by one thread).
+ */
+typedef struct {
+  int act;
+  float act_param;
+  const float* residual;
+  int64_t ld_res;
+  const float* gate;
+  int64_t gate_stride;
+  int64_t rows_per_gate;
+} cv3_epilogue;
+
+/* ---------------- runtime ---------------- */
+const char* cv3_last_error(void);
+int cv3_init(int device);
+int cv3_device_info(int* cu_count, int64_t* hbm_bytes, char* arch_name, int name_len);
+int cv3_malloc(void** ptr, size_t bytes); /* stream-aware caching allocator */
+int cv3_free(void* ptr);
+int cv3_empty_cache(void);
+int cv3_mem_stats(size_t* in_use, size_t* cached);
+int cv3_copy_h2d(void* dst, const void* src, size_t bytes, cv3_stream_t s); /* returns when done */
+int cv3_copy_d2h(void* dst, const void* src, size_t bytes, cv3_stream_t s); /* returns when done */
+int cv3_copy_d2d(void* dst, const void* src, size_t bytes, cv3_stream_t s); /* stream-ordered */
+int cv3_fill_zero(void* dst, size_t bytes, cv3_stream_t s);                 /* kernel (graph-safe) */
+int cv3_stream_create(cv3_stream_t* s);
+int cv3_stream_destroy(cv3_stream_t s);
+int cv3_stream_sync(cv3_stream_t s);
+int cv3_device_sync(void);
+int cv3_event_create(void** ev);
+int cv3_event_destroy(void* ev);
+int cv3_event_record(void* ev, cv3_stream_t s);
+int cv3_event_elapsed_ms(void* ev0, void* ev1, float* ms);
+int cv3_graph_begin(cv3_stream_t s);
+int cv3_graph_end(cv3_stream_t s, void** exec);
+int cv3_graph_launch(void* exec, cv3_stream_t s);
+int cv3_graph_destroy(void* exec);
+
+/* ---------------- host RNG (cv3cpu/torch_rng.py; host memory, host code) ---------------- */
+int cv3_mt_create(uint64_t seed, void** gen);                   /* TorchMT19937.__init__  torch_rng.py:30 */
+int cv3_mt_destroy(void* gen);
+int cv3_mt_uniform_f32(void* gen, int64_t n, float* out_host);  /* random_float32 / rand  torch_rng.py:88,145 */
+int cv3_mt_normal_f32(void* gen, int64_t n, float* out_host);   /* randn                  torch_rng.py:117 */
+
+/* ---------------- quantisation (cv3cpu/quant.py) ---------------- */
+/* quantize_q8 (quant.py:56-67): q [n, kp] int8, scales [n, kp/block] f16 (reference) or f32
+ * (per-output-channel layout: block = k).  kp = ceil(k / block) * block.  Bit-exact. */
+int cv3_quantize_q8(const float* w, int64_t n, int64_t k, int64_t block, int scale_dtype, int8_t* q,
+                    void* scales, cv3_stream_t s);
+/* quantize_q4 (quant.py:70-86): q [n, kp/2] packed nibbles, scales [n, kp/block] f16. */
+int cv3_quantize_q4(const float* w, int64_t n, int64_t k, int64_t block, uint8_t* q, void* scales_f16,
+                    cv3_stream_t s);
+/* QTensor.dequant_rows (quant.py:110-133): out[r - r0, :k] (row stride ld_out). */
+int cv3_dequant_rows(int kind, const void* q, const void* scales, int scale_dtype, int64_t kp, int64_t block,
+                     int64_t k, int64_t r0, int64_t r1, float* out, int64_t ld_out, cv3_stream_t s);
+/* ops.embedding (ops.py:126-144): out[i] = table[ids[i]] (f32/f16 rows or dequantised q8/q4 rows).
+ * ids are device int64; out-of-range ids return CV3_EINDEX. */
+int cv3_embedding(int kind, const void* table, const void* scales, int scale_dtype, int64_t rows, int64_t cols,
+                  int64_t kp, int64_t block, const int64_t* ids, int64_t n, float* out, cv3_stream_t s);
+
+/* ---------------- linear (ops.linear ops.py:121 / quant.qmatmul quant.py:156-204) ---------------- */
+/* y[m, n] = epi(x[m, :k] . w[n, :k]).  fp32 weights [n, ldw].  Small m runs a GEMV, large m the MFMA GEMM. */
+int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t ldw, int64_t n,
+                   const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
+/* Quantised weights (q8: q [n, kp] int8; q4: q [n, kp/2]); scales [n, kp/block] (f16 or f32). */
+int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
+                 int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
+                 const cv3_epilogue* epi, cv3_stream_t s);
+
+
+/* ---------------- elementwise / reductions ---------------- */
+/* ops.silu/sigmoid/gelu_tanh/gelu/mish/elu/leaky_relu (ops.py:30-74): y = act(x), param = alpha/slope */
+int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_stream_t s);
+/* op 0: a+b, 1: a*b, 2: silu(a)*b (qwen2.py:177), 3: alpha*a + beta*b */
+int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, float alpha, float beta, cv3_stream_t s);
+/* ops.snake (ops.py:77-81) over (C, T) with per-channel alpha */
+int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s);
+/* ops.softmax / ops.log_softmax over the last axis (ops.py:84-93) */
+int cv3_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, int log_softmax, cv3_stream_t s);
+/* ops.rms_norm (ops.py:101-104) */
+int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t cols, float eps, cv3_stream_t s);
+/* ops.layer_norm (ops.py:107-118) with optional affine (w, b) and/or the DiT AdaLN modulation
+ * y = LN(x) * (1 + scale[g]) + shift[g], g = row / rows_per_group (dit.py:168-169,178). */
+int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
+                   const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
+                   cv3_stream_t s);
+/* rotary tables: kind 0 = DiT rope_freqs + fp32 cos/sin (dit.py:21-29,51-52); kind 1 = Qwen2 RopeCache (qwen2.py:46-56).
+ * cos/sin [n, dim] for positions pos0 .. pos0+n-1. */
+int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* cos_out, float* sin_out,
+                   cv3_stream_t s);
+/* dit.apply_partial_rope (dit.py:40-54), in place on the first `rot` channels of each row */
+int cv3_rope_pairs(float* x, int64_t ld, int64_t rows, int64_t rows_per_batch, int rot, const float* cos_tab,
+                   const float* sin_tab, cv3_stream_t s);
+/* qwen2.apply_rope (qwen2.py:64-71), in place; vector v at x + (v/per_pos)*ld_pos + (v%per_pos)*d, position pos0 + v/per_pos */
+int cv3_rope_half(float* x, int64_t nvec, int64_t per_pos, int64_t ld_pos, int d, const float* cos_tab,
+                  const float* sin_tab, int64_t pos0, cv3_stream_t s);
+/* Flow.solve_euler CFG combine + Euler update (flow.py:86-87): x += dt * ((1 + w) d_cond - w d_uncond) */
+int cv3_cfg_euler(float* x, const float* d_cond, const float* d_uncond, int64_t n, float dt, float w, cv3_stream_t s);
+/* ops.interpolate_nearest (ops.py:335-336) and ops.interpolate_linear (ops.py:318-332) over (C, T) */
+int cv3_interp_nearest(const float* x, float* y, int64_t c, int64_t t, int r, cv3_stream_t s);
+int cv3_interp_linear(const float* x, float* y, int64_t c, int64_t t, int64_t size, int align_corners, cv3_stream_t s);
+/* ops.hann_window (ops.py:339-343) */
+int cv3_hann_window(int n, int periodic, float* out, cv3_stream_t s);
+/* batched (rows, cols) -> (cols, rows) transpose (the reference's swapaxes/ascontiguousarray copies) */
+int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t cols, cv3_stream_t s);
+
+/* ---------------- attention (ops.sdpa ops.py:267-300) ---------------- */
+/* q (b, h, n, d), k/v (b, hk, m, d), out (b, h, n, d), each addressed by {batch, head, row} strides in floats
+ * with d contiguous.  mask_kind 0 none, 1 ("causal", a), 2 ("chunk", a, b) (ops.py:244-264). */
+int cv3_attention(const float* q, const float* k, const float* v, float* out, int64_t batch, int h, int hk,
+                  int64_t n, int64_t m, int d, const int64_t* q_strides, const int64_t* k_strides,
+                  const int64_t* v_strides, const int64_t* o_strides, float scale, int mask_kind, int64_t mask_a,
+                  int64_t mask_b, cv3_stream_t s);
+
+/* ---------------- convolution (ops.conv1d ops.py:165-219, ops.depthwise_conv1d ops.py:222-237) ---------------- */
+/* x (cin, t_in) with strides (x_cs, x_ts), optionally nearest-upsampled by `up` before padding;
+ * w (cout, cin/groups, k) contiguous; y (cout, t_out) with strides (y_cs, y_ts).
+ * Epilogue: snake(acc + bias) if snake_alpha, else act(acc + bias); then + residual (strides r_cs, r_ts).
+ * *t_out_ptr receives t_out; pass y = NULL to query it. */
+int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t x_ts, const float* w, int64_t cout,
+               int64_t k, const float* bias, int64_t stride, int64_t dilation, int64_t groups, int64_t pad_l,
+               int64_t pad_r, int64_t up, float* y, int64_t y_cs, int64_t y_ts, int64_t* t_out_ptr, int act,
+               float act_param, const float* snake_alpha, float snake_eps, const float* residual, int64_t r_cs,
+               int64_t r_ts, cv3_stream_t s);
+int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,
+                         int64_t dilation, int64_t pad_l, int64_t pad_r, float* y, int64_t* t_out_ptr,
+                         cv3_stream_t s);
+
+/* ---------------- STFT (ops.stft ops.py:346-355, ops.istft ops.py:358-377, hift.decode hift.py:204-210) ---------------- */
+/* re/im planes (n_fft/2+1, frames); *frames_ptr receives the frame count (re = NULL to query). */
+int cv3_stft(const float* x, int64_t n, int n_fft, int hop, const float* win, int center, float* re, float* im,
+             int64_t* frames_ptr, cv3_stream_t s);
+/* mode 0: spectrum (re, im) planes; mode 1: HiFT head from conv_post's (log-magnitude, phase) planes with a
+ * +-limit clip.  frame_buf: frames * n_fft floats of caller scratch. */
+int cv3_istft(int mode, const float* a, const float* b, int64_t frames, int n_fft, int hop, const float* win,
+              int center, int64_t length, float limit, float* frame_buf, float* y, int64_t* out_len_ptr,
+              cv3_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CV3HIP_H */

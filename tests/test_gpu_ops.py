@@ -1,0 +1,260 @@
+"""GPU parity of every drop-in op (cv3amd.ops / cv3amd.quant) against the oracle.
+
+Tolerances: int8 codes and scales bit-exact; fp32 outputs within 1e-5 of the
+oracle in the reference's max-norm relative error (rel_err).
+"""
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+import oracle.ops as ref
+import oracle.quant as refq
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev(gpu):
+    import cv3amd.ops as ops
+    import cv3amd.quant as quant
+    return ops, quant
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(0)
+
+
+@pytest.mark.parametrize("name,args", [("silu", ()), ("sigmoid", ()), ("gelu_tanh", ()), ("gelu", ()),
+                                       ("mish", ()), ("elu", (1.0,)), ("leaky_relu", (0.1,))])
+def test_activations(dev, rng, name, args):
+    ops, _ = dev
+    x = (rng.normal(size=(7, 333)) * 4).astype(np.float32)
+    x[0, :6] = [0.0, -0.0, 30.0, -30.0, 1e-20, -1e-20]
+    assert rel_err(getattr(ops, name)(x, *args), getattr(ref, name)(x, *args)) < TOL
+
+
+def test_mish_large_inputs(dev):
+    ops, _ = dev
+    x = np.array([-50.0, 0.0, 20.0, 100.0, 1e4], dtype=np.float32)
+    got = ops.mish(x)
+    assert np.isfinite(got).all() and rel_err(got, ref.mish(x)) < TOL
+
+
+def test_snake(dev, rng):
+    ops, _ = dev
+    a = (np.abs(rng.normal(size=64)) + 0.5).astype(np.float32)
+    x = (rng.normal(size=(64, 1001)) * 3).astype(np.float32)
+    assert rel_err(ops.snake(x, a), ref.snake(x, a)) < TOL
+
+
+@pytest.mark.parametrize("shape", [(4, 9), (1, 6761), (3, 5, 17)])
+def test_softmax(dev, rng, shape):
+    ops, _ = dev
+    x = (rng.normal(size=shape) * 20).astype(np.float32)
+    assert rel_err(ops.softmax(x), ref.softmax(x)) < TOL
+    assert rel_err(ops.log_softmax(x), ref.log_softmax(x)) < TOL
+    assert rel_err(ops.softmax(x, axis=0), ref.softmax(x, axis=0)) < TOL
+
+
+def test_norms(dev, rng):
+    ops, _ = dev
+    x = rng.normal(size=(6, 1024)).astype(np.float32) * 3 + 1
+    w = rng.normal(size=1024).astype(np.float32)
+    b = rng.normal(size=1024).astype(np.float32)
+    assert rel_err(ops.rms_norm(x[:, :896], w[:896]), ref.rms_norm(x[:, :896], w[:896])) < TOL
+    assert rel_err(ops.layer_norm(x, None, None, 1e-6), ref.layer_norm(x, None, None, 1e-6)) < TOL
+    assert rel_err(ops.layer_norm(x, w, b), ref.layer_norm(x, w, b)) < TOL
+
+
+@pytest.mark.parametrize("n,k,block", [(896, 896, 64), (128, 896, 64), (4864, 896, 64), (896, 4864, 64),
+                                       (37, 200, 64), (9, 100, 64), (6144, 1024, 64)])
+def test_quantize_q8_bit_exact(dev, n, k, block):
+    _, quant = dev
+    w = (np.random.default_rng(n + k).normal(size=(n, k)) * 0.02).astype(np.float32)
+    w[0, :3] = [1e-40, -3e-39, 0.0]       # fp32 denormals in a block
+    w[1 % n, :] = 0.0                      # an all-zero row
+    q, s, kp = quant.quantize_q8(w, block)
+    rq, rs, rkp = refq.quantize_q8(w, block)
+    assert kp == rkp
+    assert np.array_equal(q, rq)
+    assert s.dtype == np.float16 and np.array_equal(s.view(np.uint16), rs.view(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(896, 896), (4864, 896), (896, 4864), (1024, 2048)])
+def test_quantize_q8_per_channel_bit_exact(dev, n, k):
+    _, quant = dev
+    w = (np.random.default_rng(k).normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, _ = quant.quantize_q8(w, k, np.float32)
+    rq, rs, _ = refq.quantize_q8(w, k, np.float32)
+    assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+def test_quantize_q8_tiny_scales_are_fp16_subnormals(dev):
+    """amax below 127 * 2^-14 gives fp16-subnormal scales; they must round like numpy."""
+    _, quant = dev
+    w = (np.random.default_rng(5).normal(size=(16, 128)) * 1e-4).astype(np.float32)
+    q, s, _ = quant.quantize_q8(w)
+    rq, rs, _ = refq.quantize_q8(w)
+    assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint16), rs.view(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(896, 896), (33, 100), (4864, 896)])
+def test_quantize_q4_bit_exact(dev, n, k):
+    _, quant = dev
+    w = (np.random.default_rng(n).normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, _ = quant.quantize_q4(w)
+    rq, rs, _ = refq.quantize_q4(w)
+    assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint16), rs.view(np.uint16))
+
+
+def test_dequant_rows(dev):
+    _, quant = dev
+    w = (np.random.default_rng(2).normal(size=(70, 150)) * 0.02).astype(np.float32)
+    for kind, fn, blk in (("q8", refq.quantize_q8, 64), ("q4", refq.quantize_q4, 32)):
+        q, s, _ = fn(w)
+        mine = quant.QTensor(kind, q, s, (70, 150), blk)
+        theirs = refq.QTensor(kind, q, s, (70, 150), blk)
+        assert np.array_equal(mine.dequant_rows(5, 40), theirs.dequant_rows(5, 40))
+        assert np.array_equal(mine.dequant(), theirs.dequant())
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 64, 1000])
+@pytest.mark.parametrize("k,n", [(896, 1152), (1024, 6144), (257, 130), (320, 1024), (9, 1), (2048, 80)])
+def test_linear_f32(dev, rng, m, k, n):
+    ops, _ = dev
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    assert rel_err(ops.linear(x, w, b), ref.linear(x, w, b)) < TOL
+    assert rel_err(ops.linear(x, w), ref.linear(x, w)) < TOL
+
+
+@pytest.mark.parametrize("m", [1, 3, 4, 7, 300])
+@pytest.mark.parametrize("k,n,block,sdt", [(896, 896, 64, np.float16), (896, 4864, 64, np.float16),
+                                           (4864, 896, 64, np.float16), (896, 896, 896, np.float32),
+                                           (4864, 896, 4864, np.float32), (100, 9, 64, np.float16)])
+def test_linear_q8(dev, rng, m, k, n, block, sdt):
+    ops, quant = dev
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, _ = refq.quantize_q8(w, block, sdt)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    mine = quant.QTensor("q8", q, s, (n, k), block)
+    theirs = refq.QTensor("q8", q, s, (n, k), block)
+    assert rel_err(ops.linear(x, mine, b), ref.linear(x, theirs, b)) < TOL
+
+
+@pytest.mark.parametrize("m", [1, 4, 9])
+def test_linear_q4(dev, rng, m):
+    ops, quant = dev
+    w = (rng.normal(size=(300, 896)) * 0.02).astype(np.float32)
+    q, s, _ = refq.quantize_q4(w)
+    x = rng.normal(size=(m, 896)).astype(np.float32)
+    assert rel_err(ops.linear(x, quant.QTensor("q4", q, s, (300, 896), 32)),
+                   ref.linear(x, refq.QTensor("q4", q, s, (300, 896), 32))) < TOL
+
+
+def test_embedding(dev, rng):
+    ops, quant = dev
+    table = rng.normal(size=(50, 80)).astype(np.float32)
+    ids = np.array([[3, 7, 3], [49, 0, 12]])
+    assert np.array_equal(ops.embedding(table, ids), ref.embedding(table, ids))
+    t16 = table.astype(np.float16)
+    assert np.array_equal(ops.embedding(t16, ids), ref.embedding(t16, ids))
+    q, s, _ = refq.quantize_q8(table)
+    assert np.array_equal(ops.embedding(quant.QTensor("q8", q, s, (50, 80), 64), ids),
+                          ref.embedding(refq.QTensor("q8", q, s, (50, 80), 64), ids))
+    with pytest.raises(IndexError, match="outside"):
+        ops.embedding(table, np.array([50]))
+
+
+CONV_CASES = [
+    (4, 6, 3, 1, 1, 1, 12, (1, 1)),
+    (4, 6, 5, 1, 2, 1, 16, (4, 0)),
+    (8, 8, 3, 1, 1, 4, 13, (2, 2)),
+    (3, 6, 4, 2, 1, 1, 17, (0, 0)),
+    (18, 8, 30, 15, 1, 1, 61, (14, 0)),
+    (16, 16, 7, 1, 1, 4, 20, (6, 0)),
+    (256, 256, 11, 1, 5, 1, 700, (50, 0)),     # HiFT resblock, dilation 5
+    (1024, 1024, 31, 1, 1, 16, 130, (30, 0)),  # DiT conv_pos
+    (80, 512, 5, 1, 1, 1, 77, (0, 4)),         # HiFT conv_pre (lookahead)
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,stride,dil,groups,T,pad", CONV_CASES)
+def test_conv1d(dev, rng, cin, cout, k, stride, dil, groups, T, pad):
+    ops, _ = dev
+    w = (rng.normal(size=(cout, cin // groups, k)) * 0.1).astype(np.float32)
+    b = rng.normal(size=cout).astype(np.float32)
+    x = rng.normal(size=(cin, T)).astype(np.float32)
+    got = ops.conv1d(x, w, b, stride=stride, dilation=dil, groups=groups, pad=pad)
+    want = ref.conv1d(x, w, b, stride=stride, dilation=dil, groups=groups, pad=pad)
+    assert got.shape == want.shape and rel_err(got, want) < TOL
+
+
+def test_conv1d_quantised_weight(dev, rng):
+    ops, quant = dev
+    w = (rng.normal(size=(6, 4, 3)) * 0.1).astype(np.float32)
+    x = rng.normal(size=(4, 15)).astype(np.float32)
+    q, s, _ = refq.quantize_q8(w.reshape(6, -1))
+    got = ops.conv1d(x, quant.QTensor("q8", q, s, (6, 12), 64, orig_shape=(6, 4, 3)), None, pad=(2, 0))
+    want = ref.conv1d(x, refq.QTensor("q8", q, s, (6, 12), 64, orig_shape=(6, 4, 3)), None, pad=(2, 0))
+    assert rel_err(got, want) < TOL
+    with pytest.raises(ValueError):
+        ops.conv1d(x, quant.QTensor("q8", q, s, (6, 12), 64), None)
+
+
+def test_depthwise(dev, rng):
+    ops, _ = dev
+    w = rng.normal(size=(12, 1, 7)).astype(np.float32)
+    b = rng.normal(size=12).astype(np.float32)
+    x = rng.normal(size=(12, 20)).astype(np.float32)
+    assert rel_err(ops.depthwise_conv1d(x, w, b, pad=(3, 3)), ref.depthwise_conv1d(x, w, b, pad=(3, 3))) < TOL
+
+
+@pytest.mark.parametrize("h,hk,n,m,d", [(4, 4, 23, 23, 16), (4, 2, 19, 19, 16), (16, 16, 500, 500, 64),
+                                        (14, 2, 1, 513, 64), (2, 1, 37, 37, 64), (3, 3, 70, 130, 32)])
+@pytest.mark.parametrize("mask", [None, ("causal",), ("chunk", 8, 1), ("chunk", 50, -1), ("chunk", 5, 0)])
+def test_sdpa(dev, rng, h, hk, n, m, d, mask):
+    ops, _ = dev
+    if mask is not None and mask[0] == "causal" and n != m:
+        mask = ("causal", m - n)
+    q = rng.normal(size=(h, n, d)).astype(np.float32)
+    k = rng.normal(size=(hk, m, d)).astype(np.float32)
+    v = rng.normal(size=(hk, m, d)).astype(np.float32)
+    assert rel_err(ops.sdpa(q, k, v, mask), ref.sdpa(q, k, v, mask)) < TOL
+
+
+def test_sdpa_errors(dev, rng):
+    ops, _ = dev
+    q = rng.normal(size=(4, 3, 16)).astype(np.float32)
+    k = rng.normal(size=(3, 3, 16)).astype(np.float32)
+    with pytest.raises(ValueError):
+        ops.sdpa(q, k, k)
+    with pytest.raises(ValueError):
+        ops.sdpa(q, q, q, ("sliding", 3))
+
+
+def test_stft_istft(dev, rng):
+    ops, _ = dev
+    win = ref.hann_window(16)
+    assert np.abs(ops.hann_window(16) - win).max() < 1e-7
+    sig = rng.normal(size=4001).astype(np.float32)
+    got, want = ops.stft(sig, 16, 4, win), ref.stft(sig, 16, 4, win)
+    assert got.shape == want.shape
+    assert rel_err(np.stack([got.real, got.imag]), np.stack([want.real, want.imag])) < TOL
+    spec = (rng.normal(size=(9, 301)) + 1j * rng.normal(size=(9, 301))).astype(np.complex64)
+    assert rel_err(ops.istft(spec, 16, 4, win), ref.istft(spec, 16, 4, win)) < TOL
+    assert rel_err(ops.istft(spec, 16, 4, win, length=1500), ref.istft(spec, 16, 4, win, length=1500)) < TOL
+
+
+def test_interpolation(dev, rng):
+    ops, _ = dev
+    x = rng.normal(size=(5, 37)).astype(np.float32)
+    for size, ac in ((100, False), (20, False), (100, True)):
+        assert rel_err(ops.interpolate_linear(x, size, ac), ref.interpolate_linear(x, size, ac)) < TOL
+    assert np.array_equal(ops.interpolate_nearest(x, 3), ref.interpolate_nearest(x, 3))
