@@ -35,15 +35,20 @@ struct AttnParams {
   int64_t mask_a, mask_b;
 };
 
-__device__ __forceinline__ bool allowed(const AttnParams& p, int64_t qi, int64_t kj) {
-  if (p.mask_kind == 1) return kj <= qi + p.mask_a;
-  if (p.mask_kind == 2) {
-    const int64_t size = p.mask_a;
-    const int64_t end = (qi / size + 1) * size;
-    const int64_t start = p.mask_b < 0 ? 0 : ((qi / size - p.mask_b) * size > 0 ? (qi / size - p.mask_b) * size : 0);
-    return kj < end && kj >= start;
+// Every mask spec leaves query qi an interval of visible keys [lo, hi):
+//   none  -> [0, m);   ("causal", a) -> [0, qi + a + 1);
+//   ("chunk", size, left) -> [max((qi/size - left) * size, 0), (qi/size + 1) * size), left < 0: from 0.
+// (ops.py:244-264.)  Computed once per query, applied with selects.
+__device__ __forceinline__ void visible_keys(const AttnParams& p, int64_t qi, int64_t& lo, int64_t& hi) {
+  lo = 0;
+  hi = p.m;
+  if (p.mask_kind == 1) {
+    hi = min(hi, qi + p.mask_a + 1);
+  } else if (p.mask_kind == 2) {
+    const int64_t c = qi / p.mask_a;
+    hi = min(hi, (c + 1) * p.mask_a);
+    if (p.mask_b >= 0) lo = max((int64_t)0, (c - p.mask_b) * p.mask_a);
   }
-  return true;
 }
 
 constexpr int KT = 64;        // keys per LDS tile
@@ -61,6 +66,8 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
   const int c16 = lane & 15, g = lane >> 4;
   const int64_t qi = q0 + c16;
   const bool qvalid = qi < p.n;
+  int64_t klo, khi;
+  visible_keys(p, qi, klo, khi);
 
   // Q fragments, pre-scaled like the reference's (q * scale) (ops.py:292)
   f32x4 qf[4];
@@ -110,13 +117,16 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
         s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[s4].z, s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[s4].w, s, 0, 0, 0);
       }
-      // s[i] = score of key k0 + sub*16 + 4g + i for query qi
+      // s[i] = score of key k0 + sub*16 + 4g + i for query qi; copy out of the
+      // accumulator and mask with selects (no divergent writes into it)
+      float sc[4];
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t kj = k0 + sub * 16 + 4 * g + i;
-        if (kj >= p.m || !allowed(p, qi, kj)) s[i] = -INFINITY;
-        mx = fmaxf(mx, s[i]);
+        const bool ok = kj >= klo && kj < khi;
+        sc[i] = ok ? s[i] : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -129,8 +139,8 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = expf(s[i] - m_use);
-        psum += s[i];
+        sc[i] = expf(sc[i] - m_use);
+        psum += sc[i];
       }
       l_run = l_run * alpha + psum;
       m_run = m_new;
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float vf = Vs[(sub * 16 + 4 * g + i) * KS + db * 16 + c16];
-          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, s[i], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, sc[i], oacc[db], 0, 0, 0);
         }
       }
     }
@@ -172,10 +182,12 @@ __global__ __launch_bounds__(256) void k_attn_generic(AttnParams p) {
   const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
+  int64_t klo, khi;
+  visible_keys(p, qi, klo, khi);
   for (int64_t c0 = 0; c0 < p.m; c0 += 64) {
     const int64_t kj = c0 + lane;
     float s = -INFINITY;
-    if (kj < p.m && allowed(p, qi, kj)) {
+    if (kj >= klo && kj < khi) {
       const float* kr = kbase + kj * p.k_sm;
       float t = 0.f;
       for (int d = 0; d < p.d; ++d) t = fmaf(qs[d], kr[d], t);

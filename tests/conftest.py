@@ -64,5 +64,10 @@ def toy_oracle_store():
 def gpu():
     """Initialise the device; fails loudly if the library or the GPU is missing."""
     from cv3amd import _lib
+    print("\n[gpu] loading libcv3hip.so", flush=True)
+    _lib.lib()
+    print("[gpu] initialising device 0", flush=True)
     _lib.init(0)
-    return _lib.device_info()
+    info = _lib.device_info()
+    print(f"[gpu] {info}", flush=True)
+    return info
