@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tensor-kernel backend on its two headline workloads.
+
+  * Qwen2-0.5B int8 greedy decode, batch 1 (the reported ``value``): 24 layers,
+    hidden 896, 14/2 heads x 64, SwiGLU 4864, per-output-channel int8 weights with
+    float32 scales, KV cache pre-filled to 512 positions of N(0, 1), K tokens
+    decoded from speech_embedding[sos] (one "step" = one token).
+  * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
+    fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
+    of torch.randn((1, 80, 15000), seed 0).
+
+Weights are synthetic (seeded N(0, 0.02), norms 1; cv3amd/synth.py); inputs are
+resident in HBM before the timed regions start.  Each workload reports its
+dominant kernel against the MI355X roofline (HBM 8 TB/s for the int8 GEMV, fp32
+matrix 157.3 TFLOP/s for the DiT GEMM), timed live with HIP events, and the
+oracle's NumPy restatement timed on the host cores on a bounded sample.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "cosyvoice3-cpu_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "DiT flow RTF (10 s, CFG) + int8 LM decode tok/s, each as % of roofline"
+HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
+PREFILL = 512
+AUDIO_SECONDS = 10.0       # 500 mel frames at 50 Hz
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------
+
+def build_lm(layers: int, profile: str):
+    import cv3amd.quant as quant
+    from cv3amd import synth
+    from cv3amd.weights import WeightStore
+    t = synth.qwen2_tensors(layers=layers)
+    t = synth.quantize_store(t, profile, quant.quantize_q8)   # device quantiser
+    return t, synth.qwen2_meta(layers=layers)
+
+
+def bench_decode(args, tensors, meta):
+    import cv3amd.quant as quant
+    from cv3amd import _lib
+    from cv3amd.device import Graph, Timer, synchronize
+    from cv3amd.qwen2 import DeviceQwen2
+    from cv3amd.weights import WeightStore
+
+    store = WeightStore(tensors, meta, quant.QTensor)
+    layers = meta["qwen2"]["num_hidden_layers"]
+    lm = DeviceQwen2(store, cap=1024)
+    rng = np.random.default_rng(0)
+    shape = (layers, lm.kv_heads, PREFILL, lm.head_dim)
+    k = rng.standard_normal(shape, dtype=np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    lm.fill_cache(k, v)
+    sos = int(meta["speech_token_size"])
+    log(f"decode: warmup {args.warmup} tokens (captures the step graph)")
+    lm.begin(sos, PREFILL)
+    for _ in range(args.warmup):
+        lm.step(graph=True)
+    synchronize()
+    lm.fill_cache(k, v)
+    lm.begin(sos, PREFILL)
+    synchronize()
+    log(f"decode: timing {args.steps} tokens")
+    tm = Timer()
+    tm.start()
+    for _ in range(args.steps):
+        lm.step(graph=True)
+    ms = tm.stop()
+    synchronize()
+    tokens = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + args.steps]]
+    tok_s = args.steps / (ms / 1e3)
+    avg_len = PREFILL + (args.steps - 1) / 2.0
+    b = lm.bytes_per_token(int(round(avg_len)))
+    per_token = b["body"] + b["kv"] + b["norms_biases"] + b["head"]
+    log(f"decode: {ms:.2f} ms for {args.steps} tokens = {tok_s:.1f} tok/s; "
+        f"{per_token / 1e6:.1f} MB/token -> {per_token * tok_s / 1e9:.0f} GB/s")
+
+    # Dominant kernel: the gate/up GEMV (RMSNorm prologue + SwiGLU), one layer's
+    # [gate; up] = 2 x 4864 x 896 int8 + scales per launch.  Timed back-to-back
+    # over the 24 layers (so the weights stream from HBM, as in the decode),
+    # replayed from a captured graph.
+    gu = lm.gate_up.struct()
+    gu_bytes = lm.gate_up.nbytes // layers + lm.hidden * 4 * 2 + lm.inter * 4
+    out = lm.workspace
+    def gate_up_sweep():
+        for layer in range(layers):
+            _lib.call("gemv_q8", ctypes.byref(gu), layer, lm.x.ptr, lm.ln2.ptr + layer * lm.hidden * 4, lm.eps,
+                      None, out.ptr, 2, None)
+    g = Graph()
+    with g:
+        gate_up_sweep()
+    g.launch()
+    synchronize()
+    reps = 20
+    tm.start()
+    for _ in range(reps):
+        g.launch()
+    kms = tm.stop() / (reps * layers)
+    achieved = gu_bytes / (kms / 1e3)
+    log(f"decode: gate/up GEMV {kms * 1e3:.2f} us/launch, {achieved / 1e9:.0f} GB/s")
+    return {
+        "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
+        "kernel": {"name": "k_dec_gemv<8,8,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
+                   "bytes_per_launch": gu_bytes, "us_per_launch": kms * 1e3, "achieved_Bps": achieved},
+    }
+
+
+def cpu_decode(tensors, meta, n_tokens: int):
+    """The oracle's NumPy restatement of the same decode on the host cores."""
+    import oracle.quant
+    from oracle.llm import CosyVoice3LM
+    from cv3amd.weights import WeightStore
+    store = WeightStore(tensors, meta, oracle.quant.QTensor)
+    lm = CosyVoice3LM(store, "llm.")
+    layers = lm.cfg.num_hidden_layers
+    rng = np.random.default_rng(0)
+    shape = (layers, lm.cfg.num_key_value_heads, PREFILL, lm.cfg.head_dim)
+    k = rng.standard_normal(shape, dtype=np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    cache = lm.body.new_cache()
+    cache._reserve(PREFILL + n_tokens + 2)
+    for i in range(layers):
+        cache.k[i][:, :PREFILL] = k[i]
+        cache.v[i][:, :PREFILL] = v[i]
+    cache.length = PREFILL
+    x = lm.speech_emb([lm.sos])
+    logits = lm.head(lm.body.forward(x, cache)[-1:])[0]   # warm-up token
+    x = lm.speech_emb([int(np.argmax(logits))])
+    t0 = time.perf_counter()
+    toks = []
+    for _ in range(n_tokens):
+        logits = lm.head(lm.body.forward(x, cache)[-1:])[0]
+        top = int(np.argmax(logits))
+        toks.append(top)
+        x = lm.speech_emb([top])
+    dt = time.perf_counter() - t0
+    return n_tokens / dt, dt
+
+
+# ---------------------------------------------------------------------------
+# flow
+# ---------------------------------------------------------------------------
+
+def flow_inputs(T: int):
+    from cv3amd.torch_rng import randn
+    rng = np.random.default_rng(0)
+    mu = rng.standard_normal((1, 80, T), dtype=np.float32)
+    cond = rng.standard_normal((1, 80, T), dtype=np.float32)
+    spks = rng.standard_normal((1, 80), dtype=np.float32)
+    x0 = randn((1, 80, 15000), 0)[:, :, :T]            # flow.py:16-17,36-43
+    return mu, cond, spks, np.ascontiguousarray(x0)
+
+
+def bench_flow(args, tensors, meta):
+    import cv3amd.quant as quant
+    from cv3amd import _lib
+    from cv3amd.device import Graph, Timer, synchronize
+    from cv3amd.dit import DeviceDiT
+    from cv3amd.weights import WeightStore
+    T = 500
+    store = WeightStore(tensors, meta, quant.QTensor)
+    d = DeviceDiT(store)
+    mu, cond, spks, x0 = flow_inputs(T)
+    d.prepare(mu, spks, cond)
+    log("flow: warmup solve (captures the solve graph)")
+    d.solve(x0, graph=True)
+    synchronize()
+    tm = Timer()
+    n = args.flow_solves
+    log(f"flow: timing {n} solves")
+    tm.start()
+    for _ in range(n):
+        d.solve(x0, graph=True)
+    ms = tm.stop() / n
+    flops = d.flops_per_solve()
+    log(f"flow: {ms:.2f} ms/solve, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
+
+    # Dominant kernel: the fused QKV projection GEMM, [1000, 1024] x [3072, 1024]^T, timed
+    # over the 22 blocks' weights back-to-back from a captured graph.
+    M, K, N = 2 * T, d.dim, 3 * d.dim
+    def qkv_sweep():
+        for i in range(d.depth):
+            d.qkv[i](d.n.ptr, M, K, d.qkvb.ptr, N)
+    g = Graph()
+    with g:
+        qkv_sweep()
+    g.launch()
+    synchronize()
+    reps = 10
+    tm.start()
+    for _ in range(reps):
+        g.launch()
+    kms = tm.stop() / (reps * d.depth)
+    kflops = 2.0 * M * N * K
+    log(f"flow: QKV GEMM {kms * 1e3:.1f} us/launch, {kflops / (kms / 1e3) / 1e12:.1f} TFLOP/s")
+    return {"ms": ms, "flops": flops, "T": T, "depth": d.depth,
+            "kernel": {"name": "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)", "flops_per_launch": kflops,
+                       "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
+
+
+def cpu_flow(tensors, meta):
+    """One estimator evaluation (22 blocks, the 10-step solve's unit) of the oracle."""
+    import oracle.quant
+    from oracle.dit import DiT
+    from cv3amd.weights import WeightStore
+    store = WeightStore(tensors, meta, oracle.quant.QTensor)
+    mu, cond, spks, x0 = flow_inputs(500)
+    T = 500
+    mu_in = np.zeros((2, 80, T), np.float32)
+    mu_in[0] = mu[0]
+    cond_in = np.zeros((2, 80, T), np.float32)
+    cond_in[0] = cond[0]
+    spk_in = np.zeros((2, 80), np.float32)
+    spk_in[0] = spks[0]
+    dit = DiT(store, "flow.decoder.estimator.")
+    t0 = time.perf_counter()
+    dit.forward(np.broadcast_to(x0, (2, 80, T)), mu_in, np.array([0.0, 0.0], np.float32), spk_in, cond_in)
+    return time.perf_counter() - t0
+
+
+# ---------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="decode tokens timed")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens first")
+    ap.add_argument("--flow-solves", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--profile", default="per_channel", choices=["per_channel", "balanced"],
+                    help="int8 scale layout of the LM weights")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host-core baseline")
+    ap.add_argument("--no-flow", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is "
+              "described in DESIGN.md and is not measured", file=sys.stderr)
+        sys.exit(2)
+    if PREFILL + args.warmup + args.steps + 1 >= 1024 or PREFILL + args.steps + 1 >= 1024:
+        sys.exit("decode length does not fit the 1024-position cache")
+
+    from cv3amd import _lib
+    _lib.lib()
+    _lib.init(0)
+    info = _lib.device_info()
+    log(f"device {info['arch']} with {info['cu_count']} CUs")
+
+    t0 = time.time()
+    lm_t, lm_meta = build_lm(args.layers, args.profile)
+    log(f"LM weights ready ({time.time() - t0:.1f} s)")
+    dec = bench_decode(args, lm_t, lm_meta)
+
+    flow = None
+    dit_t = dit_meta = None
+    if not args.no_flow:
+        from cv3amd import synth
+        dit_t = synth.dit_tensors(depth=22)
+        dit_meta = synth.dit_meta(depth=22)
+        flow = bench_flow(args, dit_t, dit_meta)
+
+    cores = cpu_cores()
+    cpu = None
+    cpu_flow_s = None
+    if not args.no_cpu:
+        log(f"cpu baseline: oracle decode of {args.cpu_tokens} tokens on {cores} host cores")
+        cpu_tok_s, cpu_dt = cpu_decode(lm_t, lm_meta, args.cpu_tokens)
+        log(f"cpu baseline: {cpu_tok_s:.2f} tok/s ({cpu_dt:.1f} s)")
+        cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+               "sample": f"{args.cpu_tokens} greedy tokens of the same 24-layer per-channel int8 decode "
+                         f"(KV 513..{PREFILL + args.cpu_tokens}) by the oracle's NumPy restatement, "
+                         f"OpenBLAS threads = {cores}, host '{cpu_model()}'"}
+        if flow is not None:
+            log("cpu baseline: one 22-block estimator evaluation of the oracle")
+            cpu_flow_s = cpu_flow(dit_t, dit_meta)
+            log(f"cpu baseline: {cpu_flow_s:.2f} s per evaluation")
+
+    kern = dec["kernel"]
+    line = {
+        "metric": METRIC,
+        "value": round(dec["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"] / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (int8 weights, per-channel f32 scales)" if args.profile == "per_channel"
+        else "f32 (int8 weights, block-64 f16 scales)",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) KV prefill)",
+        "config": {"workload": f"Qwen2-0.5B greedy decode, batch 1, {args.layers} layers, hidden 896, 14/2 heads x 64, "
+                               f"SwiGLU 4864, int8 {args.profile}, KV {PREFILL}->{PREFILL + args.steps}",
+                   "decode_tokens": args.steps, "kv_prefill": PREFILL},
+        "hbm_roofline_frac": round(dec["bytes_per_token"] * dec["tok_s"] / HBM_PEAK, 4),
+        "bytes_per_token": dec["bytes_per_token"],
+        "roofline": {"bound": "hbm", "achieved": round(kern["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(kern["achieved_Bps"] / HBM_PEAK, 4), "traffic": None,
+                     "kernel": kern["name"], "bytes_per_launch": kern["bytes_per_launch"],
+                     "us_per_launch": round(kern["us_per_launch"], 3)},
+        "cpu_baseline": cpu,
+        "tokens_head": dec["tokens"][:8],
+    }
+    if flow is not None:
+        fk = flow["kernel"]
+        rtf = flow["ms"] / 1e3 / AUDIO_SECONDS
+        line["flow"] = {
+            "workload": "DiT flow decoder, 10 s audio (500 frames), 22 blocks, 10 Euler steps, CFG, fp32",
+            "ms_per_solve": round(flow["ms"], 3), "rtf": round(rtf, 6),
+            "tflops": round(flow["flops"] / (flow["ms"] / 1e3) / 1e12, 2),
+            "mfma_roofline_frac": round(flow["flops"] / (flow["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
+            "flops_per_solve": flow["flops"],
+            "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
+                         "peak": FP32_MFMA_PEAK / 1e12, "unit": "TFLOP/s",
+                         "frac": round(fk["achieved_flops"] / FP32_MFMA_PEAK, 4), "traffic": None,
+                         "kernel": fk["name"], "us_per_launch": round(fk["us_per_launch"], 2)},
+            "cpu_baseline": None if cpu_flow_s is None else {
+                "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
+                "sample": "one 22-block estimator evaluation (of the solve's 10) by the oracle, x10 extrapolated"},
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

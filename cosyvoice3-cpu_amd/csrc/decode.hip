@@ -1,0 +1,526 @@
+// Qwen2 single-token decode step, resident on the device (cv3cpu/models/qwen2.py:139-179,
+// cv3cpu/models/llm.py:68-77,112-123 with greedy selection).
+//
+// One token costs 5 kernels per layer plus 2 at the end, all enqueued by
+// cv3_qwen2_decode_step so the whole step can be captured into one HIP graph and
+// replayed: the position and the last token live in device memory, so every
+// token's launch sequence is identical.
+//
+//   per layer
+//     qkv   : RMSNorm prologue -> int8 GEMV of [q; k; v] + bias -> half-split
+//             rotary on q and k -> k, v appended to the cache at `pos`
+//     attn  : GQA decode attention over keys [0, pos], split over key chunks;
+//             the last workgroup of each kv head merges the chunks
+//     o     : int8 GEMV, x += W_o . attn
+//     mlp   : RMSNorm prologue -> int8 GEMV of [gate; up] -> silu(gate) * up
+//     down  : int8 GEMV, x += W_down . h
+//   end
+//     head  : final RMSNorm prologue -> int8 GEMV + bias -> logits
+//     next  : argmax (ties to the lowest index, np.argsort(-p, stable)[0]),
+//             history[pos + 1] = id, x = speech_embedding[id], pos += 1
+//
+// The int8 GEMV (the HBM-bound part, cv3cpu/quant.py:172-204 at m = 1): a row
+// group of LPR lanes owns one weight row; each lane streams CPL 16-byte chunks
+// of it (128 contiguous bytes per 8 lanes), issued before the activation vector
+// is staged into LDS so the two memory latencies overlap.  Codes are widened in
+// registers; per-row float32 scales are applied once after the dot product,
+// block float16 scales once per 16-code chunk (a chunk never straddles a block
+// because block % 16 == 0).
+#include "common.hpp"
+#include "epilogue.hpp"
+
+using namespace cv3;
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct QW {            // one stacked int8 weight: layer l, row r at q + (l * rows + r) * kp
+  const int8_t* q;
+  const void* scales;  // [layers * rows, kp / block]
+  int64_t rows, k, kp, block;
+  int sf16;
+};
+
+__device__ __forceinline__ float sc_at(const QW& w, int64_t row, int64_t kk) {
+  const int64_t nb = w.kp / w.block;
+  const int64_t i = row * nb + kk / w.block;
+  return w.sf16 ? __half2float(reinterpret_cast<const __half*>(w.scales)[i])
+                : reinterpret_cast<const float*>(w.scales)[i];
+}
+
+__device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ xs) {
+  const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+  float a = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float4 xv = *reinterpret_cast<const float4*>(xs + 4 * d);
+    const uint32_t u = ws[d];
+    a = fmaf((float)((int32_t)(u << 24) >> 24), xv.x, a);
+    a = fmaf((float)((int32_t)(u << 16) >> 24), xv.y, a);
+    a = fmaf((float)((int32_t)(u << 8) >> 24), xv.z, a);
+    a = fmaf((float)((int32_t)u >> 24), xv.w, a);
+  }
+  return a;
+}
+
+// Stage x[0:k) into LDS (zero padded to kx), optionally RMS-normalised with weight
+// rms_w: x * (1 / sqrt(mean(x^2) + eps)) * w (cv3cpu/ops.py:101-104).
+__device__ void stage_vec(const float* __restrict__ x, int64_t k, int64_t kx, const float* __restrict__ rms_w,
+                          float eps, float* xs, float* red) {
+  float inv = 1.f;
+  if (rms_w) {
+    float ss = 0.f;
+    for (int64_t c = threadIdx.x; c < k; c += blockDim.x) ss = fmaf(x[c], x[c], ss);
+    ss = block_sum(ss, red);
+    inv = 1.0f / sqrtf(ss / (float)k + eps);
+  }
+  for (int64_t c = threadIdx.x; c < kx; c += blockDim.x) {
+    float v = 0.f;
+    if (c < k) v = rms_w ? (x[c] * inv) * rms_w[c] : x[c];
+    xs[c] = v;
+  }
+  __syncthreads();
+}
+
+// Dot products of one row group: lanes [g*LPR, g*LPR + LPR) cover row `row`.
+// Loads are issued first (wv), then the caller stages x, then finish_dot().
+template <int LPR, int CPL>
+struct RowDot {
+  u32x4 wv[CPL];
+  __device__ __forceinline__ void load(const QW& w, int64_t row, int sub, bool live) {
+    const u32x4* base = reinterpret_cast<const u32x4*>(w.q + row * w.kp);
+    const int64_t nch = w.kp / 16;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int64_t c = sub + (int64_t)i * LPR;
+      wv[i] = (live && c < nch) ? __builtin_nontemporal_load(base + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // sum over this lane's chunks; per-row scales are applied by the caller
+  __device__ __forceinline__ float dot(const QW& w, int64_t row, int sub, const float* xs, bool per_row) {
+    float acc = 0.f;
+    const int64_t nch = w.kp / 16;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int64_t c = sub + (int64_t)i * LPR;
+      if (c < nch) {
+        const float d = dot16(wv[i], xs + c * 16);
+        acc = per_row ? acc + d : fmaf(d, sc_at(w, row, c * 16), acc);
+      }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    return per_row ? acc * sc_at(w, row, 0) : acc;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Generic GEMV y = epi(W . vec): 256 threads, RPW = 64 / LPR rows per wave.
+//   mode 0: y[r] = acc + bias[r]             (head)
+//   mode 1: y[r] = y[r] + acc                (o / down: residual add, in place)
+//   mode 2: y[r] = silu(acc_gate) * acc_up   (gate rows r, up rows r + n)
+// ---------------------------------------------------------------------------
+struct GemvArgs {
+  QW w;
+  int64_t layer_row0;   // first weight row of this layer (layer * rows)
+  int64_t n;            // outputs
+  const float* x;
+  const float* rms_w;
+  float eps;
+  const float* bias;
+  float* y;
+  int mode;
+};
+
+template <int LPR, int CPL, int MODE>
+__global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[4];
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = lane / LPR, sub = lane % LPR;
+  constexpr bool swiglu = MODE == 2;
+  // output column handled by this row group
+  const int64_t outs_per_wave = swiglu ? RPW / 2 : RPW;
+  const int64_t col = ((int64_t)blockIdx.x * 4 + wave) * outs_per_wave + (swiglu ? grp / 2 : grp);
+  const bool live = col < a.n;
+  const int64_t wrow = a.layer_row0 + (swiglu ? ((grp & 1) ? col + a.n : col) : col);
+  RowDot<LPR, CPL> rd;
+  rd.load(a.w, live ? wrow : a.layer_row0, sub, live);
+  const int64_t kx = a.w.kp;
+  stage_vec(a.x, a.w.k, kx, a.rms_w, a.eps, xs, red);
+  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
+  const float acc = rd.dot(a.w, live ? wrow : a.layer_row0, sub, xs, per_row);
+  if (swiglu) {
+    const float up = __shfl_xor(acc, LPR, 64);  // partner row group (gate <-> up)
+    if (live && sub == 0 && (grp & 1) == 0) a.y[col] = (acc / (1.0f + expf(-acc))) * up;
+  } else if (live && sub == 0) {
+    if constexpr (MODE == 1)
+      a.y[col] = a.y[col] + acc;
+    else
+      a.y[col] = acc + (a.bias ? a.bias[col] : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// QKV: RMSNorm prologue, GEMV of the stacked [q; k; v] rows (+ bias), half-split
+// rotary on q and k (qwen2.py:64-71), k and v written to the cache at `pos`.
+// A wave owns 4 rotary pairs (rows h*64 + j and h*64 + 32 + j), LPR = 8.
+// ---------------------------------------------------------------------------
+struct QkvArgs {
+  QW w;
+  int64_t layer_row0;
+  const float* x;
+  const float* rms_w;
+  float eps;
+  const float* bias;       // layer's [q; k; v] bias
+  int heads, kv_heads, dh;
+  const float* cos_t;      // [cap, dh]
+  const float* sin_t;
+  const int64_t* pos;
+  float* q_out;            // [heads * dh]
+  float* k_cache;          // layer's [kv_heads, cap, dh]
+  float* v_cache;
+  int64_t cap;
+};
+
+template <int CPL>
+__global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[4];
+  constexpr int LPR = 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = lane / LPR, sub = lane % LPR;
+  const int half = a.dh / 2;
+  const int64_t nrows = (int64_t)(a.heads + 2 * a.kv_heads) * a.dh;
+  // pair index p covers rows (head, j) and (head, j + half); 4 pairs per wave
+  const int64_t pair = ((int64_t)blockIdx.x * 4 + wave) * 4 + grp / 2;
+  const int64_t head = pair / half, j = pair % half;
+  const bool live = head * a.dh < nrows;
+  const int64_t r = head * a.dh + j + ((grp & 1) ? half : 0);
+  const int64_t wrow = a.layer_row0 + (live ? r : 0);
+  RowDot<LPR, CPL> rd;
+  rd.load(a.w, wrow, sub, live);
+  stage_vec(a.x, a.w.k, a.w.kp, a.rms_w, a.eps, xs, red);
+  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
+  float v = rd.dot(a.w, wrow, sub, xs, per_row);
+  if (live) v += a.bias[r];
+  const float other = __shfl_xor(v, LPR, 64);  // the pair partner
+  if (!live || sub != 0) return;
+  const int64_t p = *a.pos;
+  const bool upper = grp & 1;
+  const int jj = (int)j + (upper ? half : 0);
+  const int64_t nq = a.heads, nk = a.kv_heads;
+  float out = v;
+  if (head < nq + nk) {
+    // x cos + rotate_half(x) sin, rotate_half = concat(-x2, x1)
+    const float c = a.cos_t[p * a.dh + jj], s = a.sin_t[p * a.dh + jj];
+    out = upper ? v * c + other * s : v * c + (-other) * s;
+  }
+  if (head < nq) {
+    a.q_out[head * a.dh + jj] = out;
+  } else if (head < nq + nk) {
+    a.k_cache[((head - nq) * a.cap + p) * a.dh + jj] = out;
+  } else {
+    a.v_cache[((head - nq - nk) * a.cap + p) * a.dh + jj] = out;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention (cv3cpu/ops.py:267-300 with one query and no mask,
+// qwen2.py:148,169): the G = heads / kv_heads query heads of one kv head
+// against keys [0, pos].  Workgroup (split, g) covers keys [split*64, split*64+64),
+// writes (max, sum, unnormalised out) per head, and the last workgroup to finish
+// for kv head g merges the splits: out = sum_s e^{m_s - M} o_s / sum_s e^{m_s - M} l_s.
+// ---------------------------------------------------------------------------
+constexpr int KCH = 64;
+struct AttnArgs {
+  const float* q;          // [heads * dh]
+  const float* k_cache;    // layer's [kv_heads, cap, dh]
+  const float* v_cache;
+  int heads, kv_heads, dh;
+  int64_t cap;
+  const int64_t* pos;
+  float scale;
+  float* part;             // [heads, nsplit, dh + 2]
+  int nsplit;
+  unsigned* counters;      // [kv_heads], zero between uses
+  float* out;              // [heads * dh]
+};
+
+__global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
+  __shared__ float Ks[KCH * 65];
+  __shared__ float Vs[KCH * 64];
+  __shared__ float qs[8 * 64];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int split = blockIdx.x, g = blockIdx.y;
+  const int G = a.heads / a.kv_heads;
+  const int64_t L = *a.pos + 1;
+  const int active = (int)((L + KCH - 1) / KCH);
+  if (split >= active) return;
+  const int64_t k0 = (int64_t)split * KCH;
+  const float* kb = a.k_cache + (int64_t)g * a.cap * a.dh;
+  const float* vb = a.v_cache + (int64_t)g * a.cap * a.dh;
+  for (int i = threadIdx.x; i < KCH * 64; i += 256) {
+    const int key = i / 64, d = i % 64;
+    const bool ok = k0 + key < L && d < a.dh;
+    Ks[key * 65 + d] = ok ? kb[(k0 + key) * a.dh + d] : 0.f;
+    Vs[key * 64 + d] = ok ? vb[(k0 + key) * a.dh + d] : 0.f;
+  }
+  for (int i = threadIdx.x; i < G * 64; i += 256) {
+    const int h = i / 64, d = i % 64;
+    qs[i] = d < a.dh ? a.q[(g * G + h) * a.dh + d] * a.scale : 0.f;  // (q * scale) first (ops.py:292)
+  }
+  __syncthreads();
+  for (int h = wave; h < G; h += 4) {
+    const int key = lane;
+    float s = 0.f;
+    for (int d = 0; d < a.dh; ++d) s = fmaf(qs[h * 64 + d], Ks[key * 65 + d], s);
+    if (k0 + key >= L) s = -INFINITY;
+    const float m = wave_max(s);
+    const float p = expf(s - m);
+    const float l = wave_sum(p);
+    float o = 0.f;
+    for (int kk = 0; kk < KCH; ++kk) o = fmaf(__shfl(p, kk, 64), Vs[kk * 64 + lane], o);
+    const int hq = g * G + h;
+    float* pr = a.part + ((int64_t)hq * a.nsplit + split) * (a.dh + 2);
+    if (lane < a.dh) pr[lane] = o;
+    if (lane == 0) {
+      pr[a.dh] = m;
+      pr[a.dh + 1] = l;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const unsigned prev = atomicAdd(&a.counters[g], 1u);
+    last = prev == (unsigned)(active - 1);
+    if (last) {
+      __threadfence();
+      a.counters[g] = 0u;  // ready for the next layer / token
+    }
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int h = wave; h < G; h += 4) {
+    const int hq = g * G + h;
+    const float* pr = a.part + (int64_t)hq * a.nsplit * (a.dh + 2);
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < active; ++s2) M = fmaxf(M, __builtin_nontemporal_load(pr + s2 * (a.dh + 2) + a.dh));
+    float den = 0.f, num = 0.f;
+    for (int s2 = 0; s2 < active; ++s2) {
+      const float* ps = pr + s2 * (a.dh + 2);
+      const float w = expf(__builtin_nontemporal_load(ps + a.dh) - M);
+      den = fmaf(__builtin_nontemporal_load(ps + a.dh + 1), w, den);
+      if (lane < a.dh) num = fmaf(__builtin_nontemporal_load(ps + lane), w, num);
+    }
+    if (lane < a.dh) a.out[hq * a.dh + lane] = num / den;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy selection and the next input row.
+// ---------------------------------------------------------------------------
+struct NextArgs {
+  const float* logits;
+  int64_t vocab;
+  QW emb;                  // speech_embedding [vocab, hidden] (q8)
+  float* x;                // next input, [hidden]
+  int64_t* pos;
+  int64_t* history;        // [cap]
+  int64_t* token;
+};
+
+__global__ __launch_bounds__(1024) void k_dec_next(NextArgs a) {
+  __shared__ float bv[16];
+  __shared__ int64_t bi[16];
+  __shared__ int64_t pick;
+  float best = -INFINITY;
+  int64_t bidx = 0x7fffffffffffffffll;
+  for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
+    const float v = a.logits[i];
+    if (v > best || (v == best && i < bidx)) {
+      best = v;
+      bidx = i;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int64_t oi = __shfl_xor(bidx, o, 64);
+    if (ov > best || (ov == best && oi < bidx)) {
+      best = ov;
+      bidx = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = bidx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = bv[0];
+    int64_t id = bi[0];
+    for (int w = 1; w < (int)(blockDim.x / 64); ++w)
+      if (bv[w] > b || (bv[w] == b && bi[w] < id)) {
+        b = bv[w];
+        id = bi[w];
+      }
+    if (id >= a.vocab) id = 0;  // all-NaN logits: keep a valid row
+    pick = id;
+  }
+  __syncthreads();
+  const int64_t id = pick;
+  // x = dequant(speech_embedding[id])  (cv3cpu/ops.py:126-144, llm.py:121)
+  for (int64_t c = threadIdx.x; c < a.emb.k; c += blockDim.x)
+    a.x[c] = (float)a.emb.q[id * a.emb.kp + c] * sc_at(a.emb, id, c);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int64_t p = *a.pos;
+    a.history[p + 1] = id;
+    *a.token = id;
+    *a.pos = p + 1;
+  }
+}
+
+__global__ void k_dec_embed(QW emb, const int64_t* token, float* x) {
+  const int64_t id = *token;
+  for (int64_t c = threadIdx.x; c < emb.k; c += blockDim.x) x[c] = (float)emb.q[id * emb.kp + c] * sc_at(emb, id, c);
+}
+
+QW make_qw(const cv3_qweight& w) {
+  QW q;
+  q.q = reinterpret_cast<const int8_t*>(w.q);
+  q.scales = w.scales;
+  q.rows = w.rows;
+  q.k = w.k;
+  q.kp = w.kp;
+  q.block = w.block;
+  q.sf16 = w.scale_dtype == CV3_F16;
+  return q;
+}
+
+int check_qw(const cv3_qweight& w, const char* what, int64_t k) {
+  CV3_REQUIRE(w.q && w.scales, CV3_EINVAL, "%s: missing weight", what);
+  CV3_REQUIRE(w.k == k, CV3_EINVAL, "%s: K is %lld, expected %lld", what, (long long)w.k, (long long)k);
+  CV3_REQUIRE(w.block > 0 && w.block % 16 == 0 && w.kp % w.block == 0 && w.kp >= w.k && w.kp % 16 == 0,
+              CV3_EINVAL, "%s: block %lld / padded K %lld must be multiples of 16", what, (long long)w.block,
+              (long long)w.kp);
+  CV3_REQUIRE((uintptr_t)w.q % 16 == 0, CV3_EINVAL, "%s: codes must be 16-byte aligned", what);
+  CV3_REQUIRE(w.scale_dtype == CV3_F16 || w.scale_dtype == CV3_F32, CV3_EINVAL, "%s: scale dtype", what);
+  return CV3_OK;
+}
+
+template <int LPR, int CPL>
+void launch_gemv(const GemvArgs& a, hipStream_t st) {
+  const int64_t rows_per_block = 4 * (64 / LPR) / (a.mode == 2 ? 2 : 1);
+  const dim3 grid((unsigned)ceil_div(a.n, rows_per_block));
+  const size_t lds = a.w.kp * sizeof(float);
+  if (a.mode == 2)
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 2>), grid, dim3(256), lds, st, a);
+  else if (a.mode == 1)
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 1>), grid, dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 0>), grid, dim3(256), lds, st, a);
+}
+
+// chunks per lane for a padded K, at LPR lanes per row
+int gemv(const GemvArgs& a, hipStream_t st) {
+  const int64_t nch = a.w.kp / 16;
+  if (nch <= 8 * 8) {
+    launch_gemv<8, 8>(a, st);
+  } else if (nch <= 16 * 20) {
+    launch_gemv<16, 20>(a, st);
+  } else if (nch <= 64 * 16) {
+    launch_gemv<64, 16>(a, st);
+  } else {
+    return fail(CV3_EUNSUPPORTED, "decode GEMV K=%lld too large", (long long)a.w.kp);
+  }
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
+  const int64_t H = m->heads, Hk = m->kv_heads, dh = m->head_dim, D = m->hidden, I = m->inter;
+  CV3_REQUIRE(H > 0 && Hk > 0 && H % Hk == 0 && H / Hk <= 8, CV3_EINVAL, "heads %lld / kv heads %lld",
+              (long long)H, (long long)Hk);
+  CV3_REQUIRE(dh > 0 && dh <= 64 && dh % 2 == 0 && H * dh == D, CV3_EINVAL, "head dim %lld", (long long)dh);
+  CV3_REQUIRE(m->layers > 0 && s->cap > 0 && s->cap % KCH == 0, CV3_EINVAL, "cache capacity must be a multiple of 64");
+  int rc;
+  if ((rc = check_qw(m->qkv, "qkv", D))) return rc;
+  if ((rc = check_qw(m->o, "o_proj", H * dh))) return rc;
+  if ((rc = check_qw(m->gate_up, "gate_up", D))) return rc;
+  if ((rc = check_qw(m->down, "down", I))) return rc;
+  if ((rc = check_qw(m->head, "llm_decoder", D))) return rc;
+  if ((rc = check_qw(m->embedding, "speech_embedding", D))) return rc;
+  CV3_REQUIRE(m->qkv.rows == (H + 2 * Hk) * dh && m->o.rows == D && m->gate_up.rows == 2 * I && m->down.rows == D,
+              CV3_EINVAL, "stacked weight rows do not match the geometry");
+  CV3_REQUIRE(m->qkv.kp / 16 <= 8 * 8, CV3_EUNSUPPORTED, "qkv K too large for the fused rotary GEMV");
+  CV3_REQUIRE(s->workspace_floats >= H * dh + H * (s->cap / KCH) * (dh + 2) + I, CV3_EINVAL,
+              "workspace too small");
+  hipStream_t st = stream_of(stream);
+  const QW qkv = make_qw(m->qkv), o = make_qw(m->o), gu = make_qw(m->gate_up), dn = make_qw(m->down);
+  const QW head = make_qw(m->head), emb = make_qw(m->embedding);
+  float* qbuf = s->workspace;
+  float* part = qbuf + H * dh;
+  float* hbuf = part + H * (s->cap / KCH) * (dh + 2);
+  const int nsplit = (int)(s->cap / KCH);
+  const float scale = 1.0f / sqrtf((float)dh);
+  for (int64_t l = 0; l < m->layers; ++l) {
+    float* kc = s->k_cache + l * Hk * s->cap * dh;
+    float* vc = s->v_cache + l * Hk * s->cap * dh;
+    QkvArgs qa{qkv, l * qkv.rows, s->x, m->ln1 + l * D, m->eps, m->qkv_bias + l * qkv.rows, (int)H, (int)Hk,
+               (int)dh, m->rope_cos, m->rope_sin, s->pos, qbuf, kc, vc, s->cap};
+    const int64_t pairs = (H + 2 * Hk) * dh / 2;
+    hipLaunchKernelGGL(k_dec_qkv<8>, dim3((unsigned)ceil_div(pairs, 16)), dim3(256), qkv.kp * sizeof(float), st,
+                       qa);
+    CV3_LAUNCHED();
+    AttnArgs aa{qbuf, kc, vc, (int)H, (int)Hk, (int)dh, s->cap, s->pos, scale, part, nsplit,
+                s->counters + 0, s->attn};
+    hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)nsplit, (unsigned)Hk), dim3(256), 0, st, aa);
+    CV3_LAUNCHED();
+    GemvArgs ga{o, l * o.rows, D, s->attn, nullptr, 0.f, nullptr, s->x, 1};
+    if ((rc = gemv(ga, st))) return rc;
+    GemvArgs gb{gu, l * gu.rows, I, s->x, m->ln2 + l * D, m->eps, nullptr, hbuf, 2};
+    if ((rc = gemv(gb, st))) return rc;
+    GemvArgs gc{dn, l * dn.rows, D, hbuf, nullptr, 0.f, nullptr, s->x, 1};
+    if ((rc = gemv(gc, st))) return rc;
+  }
+  GemvArgs gh{head, 0, head.rows, s->x, m->norm, m->eps, m->head_bias, s->logits, 0};
+  if ((rc = gemv(gh, st))) return rc;
+  NextArgs na{s->logits, head.rows, emb, s->x, s->pos, s->history, s->token};
+  hipLaunchKernelGGL(k_dec_next, dim3(1), dim3(1024), 0, st, na);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
+                float* y, int mode, cv3_stream_t stream) {
+  CV3_REQUIRE(w && x && y, CV3_EINVAL, "null argument");
+  CV3_REQUIRE(mode >= 0 && mode <= 2, CV3_EINVAL, "gemv mode %d", mode);
+  CV3_REQUIRE(layer >= 0, CV3_EINVAL, "negative layer");
+  CV3_REQUIRE(mode != 2 || w->rows % 2 == 0, CV3_EINVAL, "SwiGLU needs [gate; up] rows");
+  int rc;
+  if ((rc = check_qw(*w, "gemv", w->k))) return rc;
+  GemvArgs a{make_qw(*w), layer * w->rows, mode == 2 ? w->rows / 2 : w->rows, x, rms_w, eps, bias, y, mode};
+  return gemv(a, stream_of(stream));
+}
+
+int cv3_qwen2_embed_token(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
+  int rc;
+  if ((rc = check_qw(m->embedding, "speech_embedding", m->hidden))) return rc;
+  hipLaunchKernelGGL(k_dec_embed, dim3(1), dim3(256), 0, stream_of(stream), make_qw(m->embedding), s->token, s->x);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+}  // extern "C"

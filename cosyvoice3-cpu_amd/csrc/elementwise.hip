@@ -244,6 +244,18 @@ __global__ void k_transpose(const float* __restrict__ x, float* __restrict__ y, 
   }
 }
 
+// Strided 3-D copy y[i, j, l] = x[i, j, l], each side addressed by its own
+// element strides: the batch transposes and channel packs around the DiT
+// (cv3cpu/models/dit.py:151-153,96, cv3cpu/models/flow.py:83) without host copies.
+__global__ void k_copy3(const float* __restrict__ x, float* __restrict__ y, int64_t d0, int64_t d1, int64_t d2,
+                        int64_t xs0, int64_t xs1, int64_t xs2, int64_t ys0, int64_t ys1, int64_t ys2) {
+  const int64_t n = d0 * d1 * d2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t l = i % d2, r = i / d2, j = r % d1, b = r / d1;
+    y[b * ys0 + j * ys1 + l * ys2] = x[b * xs0 + j * xs1 + l * xs2];
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -360,6 +372,16 @@ int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t
   if (batch * rows * cols <= 0) return CV3_OK;
   const dim3 grid((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32), (unsigned)batch);
   hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, stream_of(s), x, y, rows, cols);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_copy_strided(const float* x, float* y, int64_t d0, int64_t d1, int64_t d2, const int64_t* x_strides,
+                     const int64_t* y_strides, cv3_stream_t s) {
+  CV3_REQUIRE(d0 >= 0 && d1 >= 0 && d2 >= 0, CV3_EINVAL, "negative copy extent");
+  if (d0 * d1 * d2 == 0) return CV3_OK;
+  hipLaunchKernelGGL(k_copy3, dim3(grid_for(d0 * d1 * d2)), dim3(256), 0, stream_of(s), x, y, d0, d1, d2,
+                     x_strides[0], x_strides[1], x_strides[2], y_strides[0], y_strides[1], y_strides[2]);
   CV3_LAUNCHED();
   return CV3_OK;
 }

@@ -15,7 +15,7 @@ import numpy as np
 
 from . import _lib
 
-_DTYPES = {np.dtype(t) for t in (np.float32, np.float16, np.int8, np.uint8, np.int64, np.int32,
+_DTYPES = {np.dtype(t) for t in (np.float32, np.float16, np.int8, np.uint8, np.int64, np.int32, np.uint32,
                                  np.float64, np.uint16)}
 
 

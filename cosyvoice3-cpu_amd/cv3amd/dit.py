@@ -1,0 +1,332 @@
+"""Device-resident DiT estimator and the Euler / classifier-free-guidance flow solve.
+
+Restates the call sequences of cv3cpu/models/dit.py:86-180 (``DiT.forward``)
+and cv3cpu/models/flow.py:58-93 (``Flow.solve_euler``) with every activation
+resident in HBM and every step a kernel of ``libcv3hip.so``.  Only the
+t-schedule and the sinusoidal time features (a few hundred floats, computed with
+the reference's own float32 expressions) are prepared on the host.
+
+Layout in HBM (B = 2 for the CFG pair, T mel frames, D = 1024):
+  * ``h``   [B*T, D]     the residual stream, updated in place by the GEMM epilogues
+  * ``qkv`` [B*T, 3D]    fused q|k|v projection (weights concatenated row-wise in
+                         [q; k; v] order, biases likewise)
+  * ``att`` [B*T, D]     attention output, heads interleaved as [T, H*dh]
+  * ``ff``  [B*T, 2D]    GELU-tanh hidden
+  * ``mod`` [S, L]       every AdaLN modulation row of the solve, one per Euler step:
+                         the time embedding depends only on t, so the S = 10 rows of
+                         ``Linear(silu(temb))`` for all 22 blocks and ``norm_out`` are
+                         one GEMM over the concatenated weights (L = 22*6D + 2D).  Both
+                         CFG rows share t (cv3cpu/models/flow.py:82-84), so one row
+                         serves the pair.
+
+Work per Euler step, in order (reference lines in brackets):
+  pack x into the [x | cond | mu | spk] input  (dit.py:92-97, flow.py:72-84)
+  input projection GEMM                        (dit.py:98)
+  two grouped causal convs + Mish, residual    (dit.py:99-112)
+  22 x [ LayerNorm+AdaLN -> QKV GEMM -> partial rotary on q,k -> attention ->
+         out GEMM with gate*y + h epilogue -> LayerNorm+AdaLN -> FF1 GEMM with
+         GELU-tanh -> FF2 GEMM with gate*y + h ]  (dit.py:114-173)
+  LayerNorm + (scale, shift) -> proj_out GEMM  (dit.py:175-180)
+  CFG combine + Euler update                   (flow.py:86-90)
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, Graph, to_device
+from .quant import QTensor
+
+ACT = _lib.ACT
+
+
+def _is_q(w) -> bool:
+    return hasattr(w, "kind") and hasattr(w, "scales")
+
+
+def _host(a) -> np.ndarray:
+    return a.numpy() if isinstance(a, DeviceArray) else np.asarray(a)
+
+
+class DeviceLinear:
+    """One resident linear weight: float32 ``[N, K]`` or q8 codes + scales."""
+
+    def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]]):
+        ws = list(weights)
+        if all(_is_q(w) for w in ws):
+            kinds = {w.kind for w in ws}
+            blocks = {int(w.block) for w in ws}
+            sdt = {np.dtype(_host(w.scales).dtype) for w in ws}
+            if kinds != {"q8"} or len(blocks) != 1 or len(sdt) != 1:
+                raise ValueError("only q8 weights of one block size and scale dtype can be concatenated")
+            self.q8 = True
+            q = np.concatenate([_host(w.q) for w in ws], axis=0)
+            s = np.concatenate([_host(w.scales) for w in ws], axis=0)
+            self.k = int(ws[0].shape[1])
+            if any(int(w.shape[1]) != self.k for w in ws):
+                raise ValueError("concatenated weights disagree on K")
+            self.n = int(q.shape[0])
+            self.block = blocks.pop()
+            self.kp = int(s.shape[1]) * self.block
+            self.sf16 = sdt.pop() == np.dtype(np.float16)
+            self.q = to_device(np.ascontiguousarray(q))
+            self.scales = to_device(np.ascontiguousarray(s))
+        elif not any(_is_q(w) for w in ws):
+            self.q8 = False
+            w = np.concatenate([np.asarray(_host(w), dtype=np.float32).reshape(np.shape(w)[0], -1) for w in ws],
+                               axis=0)
+            self.n, self.k = w.shape
+            self.w = to_device(np.ascontiguousarray(w))
+        else:
+            raise ValueError("cannot concatenate quantised and float weights")
+        if any(b is not None for b in biases):
+            parts = []
+            for w, b in zip(ws, biases):
+                rows = int(w.shape[0])
+                parts.append(np.zeros(rows, np.float32) if b is None else np.asarray(_host(b), np.float32))
+            self.bias = to_device(np.concatenate(parts))
+        else:
+            self.bias = None
+
+    @property
+    def nbytes(self) -> int:
+        if self.q8:
+            return self.q.nbytes + self.scales.nbytes
+        return self.w.nbytes
+
+    def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None):
+        """y[m, n] = epi(x[m, :k] . W^T + bias) on the calling thread's stream."""
+        b = self.bias.ptr if self.bias is not None else None
+        e = ctypes.byref(epi) if epi is not None else None
+        if self.q8:
+            _lib.call("linear_q", _lib.KIND_Q8, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
+                      _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, None)
+        else:
+            _lib.call("linear_f32", x, m, self.k, ldx, self.w.ptr, self.k, self.n, b, y, ldy, e, None)
+
+
+def sinus_features(t: np.ndarray, dim: int = 256, scale: float = 1000.0) -> np.ndarray:
+    """[sin(scale t f), cos(scale t f)], f = exp(-i log(1e4)/(dim/2 - 1)), float32 (dit.py:13-18)."""
+    half = dim // 2
+    f = np.exp(np.arange(half, dtype=np.float32) * -(math.log(10000.0) / (half - 1)))
+    arg = scale * np.asarray(t).reshape(-1, 1).astype(np.float32) * f[None, :]
+    return np.concatenate([np.sin(arg), np.cos(arg)], axis=-1).astype(np.float32)
+
+
+def cosine_t_span(steps: int) -> np.ndarray:
+    """1 - cos(linspace(0, 1, steps+1) pi/2) in float64, stored float32 (flow.py:68-69)."""
+    return (1.0 - np.cos(np.linspace(0.0, 1.0, steps + 1, dtype=np.float64) * 0.5 * np.pi)).astype(np.float32)
+
+
+def euler_schedule(steps: int):
+    """(t, dt) of each Euler step with the reference's float32 recurrence: t += dt, then
+    dt = t_span[s+1] - t (flow.py:78-90), so t drifts from t_span by rounding exactly as there."""
+    t_span = cosine_t_span(steps)
+    t = t_span[0]
+    dt = t_span[1] - t_span[0]
+    ts, dts = [], []
+    for s in range(1, len(t_span)):
+        ts.append(t)
+        dts.append(dt)
+        t = t + dt
+        if s < len(t_span) - 1:
+            dt = t_span[s + 1] - t
+    return np.array(ts, np.float32), np.array(dts, np.float32)
+
+
+def dit_rope_tables(n: int, dim_head: int, theta: float = 10000.0):
+    """cos/sin of the interleaved DiT rotary angles: fp64 angles stored float32, then
+    float32 cos/sin (dit.py:21-29,51-52)."""
+    inv = 1.0 / (theta ** (np.arange(0, dim_head, 2, dtype=np.float64) / dim_head))
+    ang = np.repeat(np.arange(n, dtype=np.float64)[:, None] * inv[None, :], 2, axis=-1).astype(np.float32)
+    return np.cos(ang), np.sin(ang)
+
+
+class DeviceDiT:
+    """The DiT estimator's weights resident in HBM, plus the solve driver.
+
+    ``weights`` has the reference WeightFile read API (``get(name)`` returning a
+    float array or a q8 QTensor, ``meta``).
+    """
+
+    def __init__(self, weights, prefix: str = "flow.decoder.estimator.", cfg_rate: float = 0.7,
+                 steps: int = 10):
+        _lib.init()
+        m = weights.meta.get("dit", {})
+        self.dim = int(m.get("dim", 1024))
+        self.depth = int(m.get("depth", 22))
+        self.heads = int(m.get("heads", 16))
+        self.dim_head = int(m.get("dim_head", 64))
+        self.conv_k = int(m.get("conv_pos_kernel", 31))
+        self.conv_groups = int(m.get("conv_pos_groups", 16))
+        self.cfg_rate = float(cfg_rate)
+        self.steps = int(steps)
+        g = lambda n: weights.get(prefix + n)  # noqa: E731
+        D = self.dim
+        self.time0 = DeviceLinear([g("time_embed.time_mlp.0.weight")], [g("time_embed.time_mlp.0.bias")])
+        self.time2 = DeviceLinear([g("time_embed.time_mlp.2.weight")], [g("time_embed.time_mlp.2.bias")])
+        self.proj_in = DeviceLinear([g("input_embed.proj.weight")], [g("input_embed.proj.bias")])
+        self.mel = self.proj_in.k // 4
+        self.conv_w, self.conv_b = [], []
+        for c in ("conv1", "conv2"):
+            w = g(f"input_embed.conv_pos_embed.{c}.0.weight")
+            if _is_q(w):
+                raise ValueError("conv_pos weights are float on this path")
+            self.conv_w.append(to_device(np.asarray(w, np.float32)))
+            self.conv_b.append(to_device(np.asarray(g(f"input_embed.conv_pos_embed.{c}.0.bias"), np.float32)))
+        mods = [g(f"transformer_blocks.{i}.attn_norm.linear.weight") for i in range(self.depth)]
+        mods.append(g("norm_out.linear.weight"))
+        mbias = [g(f"transformer_blocks.{i}.attn_norm.linear.bias") for i in range(self.depth)]
+        mbias.append(g("norm_out.linear.bias"))
+        self.mod = DeviceLinear(mods, mbias)
+        self.ld_mod = self.mod.n
+        self.qkv, self.out, self.ff1, self.ff2 = [], [], [], []
+        for i in range(self.depth):
+            b = f"transformer_blocks.{i}."
+            self.qkv.append(DeviceLinear([g(b + f"attn.to_{p}.weight") for p in "qkv"],
+                                         [g(b + f"attn.to_{p}.bias") for p in "qkv"]))
+            self.out.append(DeviceLinear([g(b + "attn.to_out.0.weight")], [g(b + "attn.to_out.0.bias")]))
+            self.ff1.append(DeviceLinear([g(b + "ff.ff.0.0.weight")], [g(b + "ff.ff.0.0.bias")]))
+            self.ff2.append(DeviceLinear([g(b + "ff.ff.2.weight")], [g(b + "ff.ff.2.bias")]))
+        self.ff_dim = self.ff1[0].n if self.depth else 2 * D
+        self.proj_out = DeviceLinear([g("proj_out.weight")], [g("proj_out.bias")])
+        self._T = None
+        self._graph = None
+
+    # -- workspace ------------------------------------------------------------
+    def prepare(self, mu: np.ndarray, spks: np.ndarray, cond: np.ndarray):
+        """Upload the conditioning of one utterance and size the workspace.
+
+        mu/cond (1, 80, T), spks (1, 80).  The CFG batch holds them in slot 0 and
+        zeros in slot 1 (flow.py:72-77).
+        """
+        T = int(mu.shape[2])
+        D, B, mel = self.dim, 2, self.mel
+        inp = np.zeros((B, T, 4 * mel), np.float32)
+        inp[0, :, mel:2 * mel] = np.asarray(cond[0], np.float32).T
+        inp[0, :, 2 * mel:3 * mel] = np.asarray(mu[0], np.float32).T
+        inp[0, :, 3 * mel:] = np.asarray(spks[0], np.float32)[None, :]
+        self.inp = to_device(inp)
+        if self._T != T:
+            self._T = T
+            self.h = DeviceArray((B * T, D))
+            self.n = DeviceArray((B * T, D))
+            self.qkvb = DeviceArray((B * T, 3 * D))
+            self.att = DeviceArray((B * T, D))
+            self.ffb = DeviceArray((B * T, self.ff_dim))
+            self.z1 = DeviceArray((D, T))
+            self.outb = DeviceArray((B * T, mel))
+            self.outT = DeviceArray((B, mel, T))
+            self.x = DeviceArray((mel, T))
+            c, s = dit_rope_tables(T, self.dim_head)
+            self.cos, self.sin = to_device(c), to_device(s)
+        self.ts, self.dts = euler_schedule(self.steps)
+        S = self.steps
+        self.sin_feat = to_device(sinus_features(self.ts))
+        self.temb = DeviceArray((S, D))
+        self.temb_h = DeviceArray((S, D))
+        self.stemb = DeviceArray((S, D))
+        self.mods = DeviceArray((S, self.ld_mod))
+        self._graph = None
+
+    # -- one estimator evaluation + Euler update ---------------------------
+    def _time_and_mod(self):
+        """temb = time_mlp(sinus(t_s)) for every step, then every AdaLN row (dit.py:86-90,164-167,175-177)."""
+        S, D = self.steps, self.dim
+        self.time0(self.sin_feat.ptr, S, 256, self.temb_h.ptr, D, _lib.epilogue("silu"))
+        self.time2(self.temb_h.ptr, S, D, self.temb.ptr, D)
+        _lib.call("act", ACT["silu"], 0.0, self.temb.ptr, self.stemb.ptr, S * D, None)
+        self.mod(self.stemb.ptr, S, D, self.mods.ptr, self.ld_mod)
+
+    def _step(self, s: int, dt: float, update: bool = True):
+        T, D, B, mel, H, dh = self._T, self.dim, 2, self.mel, self.heads, self.dim_head
+        BT = B * T
+        f4 = 4
+        S3 = ctypes.c_int64 * 3
+        # x (80, T) -> columns 0..79 of both batch rows of the packed input (dit.py:151-153,96)
+        _lib.call("copy_strided", self.x.ptr, self.inp.ptr, B, T, mel, S3(0, 1, T), S3(T * 4 * mel, 4 * mel, 1),
+                  None)
+        self.proj_in(self.inp.ptr, BT, 4 * mel, self.h.ptr, D)
+        # conv_pos: two grouped causal convs with Mish, read/written channels-last (dit.py:99-112)
+        k = self.conv_k
+        for b in range(B):
+            hb = self.h.ptr + b * T * D * f4
+            _lib.call("conv1d", hb, D, T, 1, D, self.conv_w[0].ptr, D, k, self.conv_b[0].ptr, 1, 1,
+                      self.conv_groups, k - 1, 0, 1, self.z1.ptr, T, 1, None, ACT["mish"], 0.0, None, 0.0,
+                      None, 0, 0, None)
+            _lib.call("conv1d", self.z1.ptr, D, T, T, 1, self.conv_w[1].ptr, D, k, self.conv_b[1].ptr, 1, 1,
+                      self.conv_groups, k - 1, 0, 1, hb, 1, D, None, ACT["mish"], 0.0, None, 0.0,
+                      hb, 1, D, None)
+        mrow = self.mods.ptr + s * self.ld_mod * f4
+        qs = S3(T * 3 * D, dh, 3 * D)
+        os_ = S3(T * D, dh, D)
+        scale = float(np.float32(1.0 / math.sqrt(dh)))
+        for i in range(self.depth):
+            base = mrow + i * 6 * D * f4
+            sh_a, sc_a, g_a, sh_m, sc_m, g_m = (base + j * D * f4 for j in range(6))
+            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_a, sc_a, 0, 0, None)
+            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D)
+            for off in (0, D):   # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120)
+                _lib.call("rope_pairs", self.qkvb.ptr + off * f4, 3 * D, BT, T, dh, self.cos.ptr, self.sin.ptr,
+                          None)
+            _lib.call("attention", self.qkvb.ptr, self.qkvb.ptr + D * f4, self.qkvb.ptr + 2 * D * f4,
+                      self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None)
+            self.out[i](self.att.ptr, BT, D, self.h.ptr, D,
+                        _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_a, gate_stride=0, rows_per_gate=1))
+            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_m, sc_m, 0, 0, None)
+            self.ff1[i](self.n.ptr, BT, D, self.ffb.ptr, self.ff_dim, _lib.epilogue("gelu_tanh"))
+            self.ff2[i](self.ffb.ptr, BT, self.ff_dim, self.h.ptr, D,
+                        _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_m, gate_stride=0, rows_per_gate=1))
+        base = mrow + self.depth * 6 * D * f4      # norm_out: (scale, shift) (dit.py:175-178)
+        _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, base + D * f4, base, 0, 0, None)
+        self.proj_out(self.n.ptr, BT, D, self.outb.ptr, mel)
+        # (B, T, 80) -> (B, 80, T), then x += dt ((1 + w) d0 - w d1)  (dit.py:180, flow.py:86-87)
+        _lib.call("copy_strided", self.outb.ptr, self.outT.ptr, B, T, mel, S3(T * mel, mel, 1),
+                  S3(mel * T, 1, T), None)
+        if not update:
+            return
+        _lib.call("cfg_euler", self.x.ptr, self.outT.ptr, self.outT.ptr + mel * T * f4, mel * T,
+                  float(dt), float(self.cfg_rate), None)
+
+    def _enqueue_solve(self):
+        self._time_and_mod()
+        for s in range(self.steps):
+            self._step(s, float(self.dts[s]))
+
+    def solve(self, x0: np.ndarray, graph: bool = False) -> DeviceArray:
+        """Euler solve from x0 (1, 80, T) (already scaled by the temperature); returns the
+        resident (80, T) result.  ``graph=True`` replays one captured HIP graph."""
+        self.x.copy_from(np.asarray(x0, np.float32).reshape(self.mel, self._T))
+        if not graph:
+            self._enqueue_solve()
+            return self.x
+        if self._graph is None:
+            g = Graph()
+            with g:
+                self._enqueue_solve()
+            self._graph = g
+        self._graph.launch()
+        return self.x
+
+    def estimate(self, x0: np.ndarray, s: int) -> np.ndarray:
+        """One estimator evaluation at the s-th Euler time on the CFG pair built from x0 (1, 80, T);
+        returns the (2, 80, T) velocity, i.e. ``DiT.forward`` (dit.py:144-180) without the update."""
+        self.x.copy_from(np.asarray(x0, np.float32).reshape(self.mel, self._T))
+        self._time_and_mod()
+        self._step(s, 0.0, update=False)
+        return self.outT.numpy()
+
+    def flops_per_solve(self) -> float:
+        """Algorithmic flops of one solve (every contraction, 2 flops per MAC)."""
+        T, D, B = self._T, self.dim, 2
+        M = B * T
+        per_block = 2 * M * D * (3 * D + D + 2 * self.ff_dim) + 4 * B * self.heads * T * T * self.dim_head
+        conv = 2 * 2 * M * D * (D // self.conv_groups) * self.conv_k
+        edges = 2 * M * (4 * self.mel) * D + 2 * M * D * self.mel
+        mod = 2 * self.ld_mod * D * B
+        return float(self.steps * (self.depth * per_block + conv + edges + mod))

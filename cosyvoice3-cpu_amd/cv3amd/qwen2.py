@@ -1,0 +1,215 @@
+"""Device-resident Qwen2 decode (the CosyVoice3 LM's token loop) on ``cv3_qwen2_decode_step``.
+
+Restates the single-token path of cv3cpu/models/qwen2.py:139-179 and the head /
+speech-embedding of cv3cpu/models/llm.py:68-77,121.  The reference samples
+(llm.py:112-149); this path is greedy: argmax of the head logits with ties to
+the lowest id, which is the first entry of the reference's stable
+``np.argsort(-p)`` (llm.py:138).
+
+Layout in HBM (L layers, D = hidden, dh = head_dim, I = intermediate):
+  * per projection, one stacked int8 array for all layers: ``qkv`` [L*(H+2Hk)*dh, Kp]
+    ([q; k; v] rows per layer), ``o`` [L*D, Kp], ``gate_up`` [L*2I, Kp]
+    ([gate; up] rows per layer), ``down`` [L*D, Kp], each with its scales;
+  * ``k_cache`` / ``v_cache`` [L, Hk, cap, dh] float32 (qwen2.py:74-121);
+  * rotary tables cos / sin [cap, dh] built once on the host with the reference's
+    float64 expressions (qwen2.py:46-56);
+  * ``pos``, ``token``, ``history`` in device memory so that a captured graph of
+    one step replays for every token.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, Graph, to_device
+
+c_i64, c_vp = ctypes.c_int64, ctypes.c_void_p
+
+
+class QWeight(ctypes.Structure):
+    _fields_ = [("q", c_vp), ("scales", c_vp), ("rows", c_i64), ("k", c_i64), ("kp", c_i64), ("block", c_i64),
+                ("scale_dtype", ctypes.c_int)]
+
+
+class Model(ctypes.Structure):
+    _fields_ = [("layers", c_i64), ("hidden", c_i64), ("heads", c_i64), ("kv_heads", c_i64), ("head_dim", c_i64),
+                ("inter", c_i64), ("eps", ctypes.c_float),
+                ("qkv", QWeight), ("o", QWeight), ("gate_up", QWeight), ("down", QWeight), ("head", QWeight),
+                ("embedding", QWeight),
+                ("qkv_bias", c_vp), ("ln1", c_vp), ("ln2", c_vp), ("norm", c_vp), ("head_bias", c_vp),
+                ("rope_cos", c_vp), ("rope_sin", c_vp)]
+
+
+class State(ctypes.Structure):
+    _fields_ = [("k_cache", c_vp), ("v_cache", c_vp), ("cap", c_i64), ("pos", c_vp), ("token", c_vp),
+                ("history", c_vp), ("x", c_vp), ("attn", c_vp), ("logits", c_vp), ("workspace", c_vp),
+                ("workspace_floats", c_i64), ("counters", c_vp)]
+
+
+def rope_tables(dim: int, theta: float, n: int):
+    """HF half-split cos/sin: float64 angles and cos/sin, stored float32 (qwen2.py:46-56)."""
+    inv = 1.0 / (theta ** (np.arange(0, dim, 2, dtype=np.float64) / dim))
+    ang = np.arange(n, dtype=np.float64)[:, None] * inv[None, :]
+    ang = np.concatenate([ang, ang], axis=-1)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def _is_q8(w) -> bool:
+    return getattr(w, "kind", None) == "q8"
+
+
+def _host(a):
+    return a.numpy() if isinstance(a, DeviceArray) else np.asarray(a)
+
+
+class _Stacked:
+    """Rows of several q8 QTensors (per layer, in order) stacked into one device array."""
+
+    def __init__(self, per_layer: List[List[object]]):
+        qs, ss = [], []
+        first = per_layer[0][0]
+        self.k = int(first.shape[1])
+        self.block = int(first.block)
+        sdt = np.dtype(_host(first.scales).dtype)
+        for parts in per_layer:
+            for w in parts:
+                if not _is_q8(w):
+                    raise ValueError("the device decode takes q8 weights (per-channel or block scales)")
+                if int(w.shape[1]) != self.k or int(w.block) != self.block or _host(w.scales).dtype != sdt:
+                    raise ValueError("stacked weights must share K, block and scale dtype")
+                qs.append(_host(w.q))
+                ss.append(_host(w.scales))
+        self.rows = sum(int(w.shape[0]) for w in per_layer[0])
+        q = np.concatenate(qs, axis=0)
+        s = np.concatenate(ss, axis=0)
+        self.kp = int(q.shape[1])
+        if self.kp % 16 or self.block % 16:
+            raise ValueError("padded K and block must be multiples of 16")
+        self.sf16 = sdt == np.dtype(np.float16)
+        self.q = to_device(np.ascontiguousarray(q))
+        self.scales = to_device(np.ascontiguousarray(s))
+
+    def struct(self) -> QWeight:
+        return QWeight(self.q.ptr, self.scales.ptr, self.rows, self.k, self.kp, self.block,
+                       _lib.F16 if self.sf16 else _lib.F32)
+
+    @property
+    def nbytes(self):
+        return self.q.nbytes + self.scales.nbytes
+
+
+class DeviceQwen2:
+    """Qwen2 body + CosyVoice3 LM head resident on the device, decoding greedily."""
+
+    def __init__(self, weights, prefix: str = "llm.", cap: int = 1024):
+        _lib.init()
+        m = weights.meta["qwen2"]
+        self.layers = int(m["num_hidden_layers"])
+        self.hidden = int(m["hidden_size"])
+        self.heads = int(m["num_attention_heads"])
+        self.kv_heads = int(m["num_key_value_heads"])
+        self.inter = int(m["intermediate_size"])
+        self.eps = float(m.get("rms_norm_eps", 1e-6))
+        self.theta = float(m.get("rope_theta", 1e6))
+        self.head_dim = self.hidden // self.heads
+        if cap % 64:
+            raise ValueError("cache capacity must be a multiple of 64")
+        self.cap = int(cap)
+        body = prefix + "model."
+        g = weights.get
+        L = range(self.layers)
+        lp = [f"{body}layers.{i}." for i in L]
+        self.qkv = _Stacked([[g(p + f"self_attn.{x}_proj.weight") for x in "qkv"] for p in lp])
+        self.o = _Stacked([[g(p + "self_attn.o_proj.weight")] for p in lp])
+        self.gate_up = _Stacked([[g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")] for p in lp])
+        self.down = _Stacked([[g(p + "mlp.down_proj.weight")] for p in lp])
+        self.head = _Stacked([[g(prefix + "llm_decoder.weight")]])
+        self.emb = _Stacked([[g(prefix + "speech_embedding")]])
+        f32 = lambda a: np.asarray(_host(a), np.float32)  # noqa: E731
+        self.qkv_bias = to_device(np.concatenate([f32(g(p + f"self_attn.{x}_proj.bias")) for p in lp for x in "qkv"]))
+        self.ln1 = to_device(np.concatenate([f32(g(p + "input_layernorm")) for p in lp]))
+        self.ln2 = to_device(np.concatenate([f32(g(p + "post_attention_layernorm")) for p in lp]))
+        self.norm = to_device(f32(g(body + "norm")))
+        hb = prefix + "llm_decoder.bias"
+        self.head_bias = to_device(f32(g(hb))) if hb in weights else None
+        c, s = rope_tables(self.head_dim, self.theta, self.cap)
+        self.rope_cos, self.rope_sin = to_device(c), to_device(s)
+        self.vocab = self.head.rows
+        self.model = Model(self.layers, self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter,
+                           self.eps, self.qkv.struct(), self.o.struct(), self.gate_up.struct(), self.down.struct(),
+                           self.head.struct(), self.emb.struct(), self.qkv_bias.ptr, self.ln1.ptr, self.ln2.ptr,
+                           self.norm.ptr, self.head_bias.ptr if self.head_bias is not None else None,
+                           self.rope_cos.ptr, self.rope_sin.ptr)
+        # state
+        cache_shape = (self.layers, self.kv_heads, self.cap, self.head_dim)
+        self.k_cache = DeviceArray(cache_shape).zero_()
+        self.v_cache = DeviceArray(cache_shape).zero_()
+        self.ints = DeviceArray((2 + self.cap,), np.int64).zero_()   # pos, token, history[cap]
+        self.x = DeviceArray((self.hidden,))
+        self.attn = DeviceArray((self.heads * self.head_dim,))
+        self.logits = DeviceArray((self.vocab,))
+        nws = self.heads * self.head_dim + self.heads * (self.cap // 64) * (self.head_dim + 2) + self.inter
+        self.workspace = DeviceArray((nws,))
+        self.counters = DeviceArray((max(self.kv_heads, 1),), np.uint32).zero_()
+        p0 = self.ints.ptr
+        self.state = State(self.k_cache.ptr, self.v_cache.ptr, self.cap, p0, p0 + 8, p0 + 16, self.x.ptr,
+                           self.attn.ptr, self.logits.ptr, self.workspace.ptr, nws, self.counters.ptr)
+        self._graph: Optional[Graph] = None
+        self._pos_host = 0
+
+    # -- weights streamed per token (the HBM roofline numerator) -----------
+    def bytes_per_token(self, length: int) -> dict:
+        """Algorithmic HBM bytes of one token at KV length ``length`` (keys read = length + 1)."""
+        body = self.qkv.nbytes + self.o.nbytes + self.gate_up.nbytes + self.down.nbytes
+        kv = 2 * self.layers * self.kv_heads * (length + 1) * self.head_dim * 4
+        small = 4 * (self.qkv_bias.size + self.ln1.size + self.ln2.size + self.norm.size)
+        return {"body": body, "kv": kv, "norms_biases": small, "head": self.head.nbytes}
+
+    # -- state ------------------------------------------------------------
+    def fill_cache(self, k: np.ndarray, v: np.ndarray):
+        """Pre-fill positions [0, n) of every layer's cache from host (L, Hk, n, dh) arrays."""
+        n = k.shape[2]
+        if n >= self.cap:
+            raise ValueError("prefill does not fit the cache")
+        kc = np.zeros((self.layers, self.kv_heads, self.cap, self.head_dim), np.float32)
+        vc = np.zeros_like(kc)
+        kc[:, :, :n] = k
+        vc[:, :, :n] = v
+        self.k_cache.copy_from(kc)
+        self.v_cache.copy_from(vc)
+
+    def begin(self, token: int, pos: int):
+        """Start decoding with input ``speech_embedding[token]`` at position ``pos``."""
+        if not 0 <= pos < self.cap - 1:
+            raise ValueError("position outside the cache")
+        ints = np.zeros(2 + self.cap, np.int64)
+        ints[0], ints[1] = pos, token
+        self.ints.copy_from(ints)
+        self._pos_host = pos
+        _lib.call("qwen2_embed_token", ctypes.byref(self.model), ctypes.byref(self.state), None)
+
+    def step(self, graph: bool = False):
+        """Enqueue one greedy token (no host synchronisation)."""
+        if self._pos_host + 1 >= self.cap:
+            raise ValueError("the KV cache is full")
+        if graph:
+            if self._graph is None:
+                g = Graph()
+                with g:
+                    _lib.call("qwen2_decode_step", ctypes.byref(self.model), ctypes.byref(self.state), None)
+                self._graph = g
+            self._graph.launch()
+        else:
+            _lib.call("qwen2_decode_step", ctypes.byref(self.model), ctypes.byref(self.state), None)
+        self._pos_host += 1
+
+    def generate(self, first_token: int, pos: int, steps: int, graph: bool = True) -> List[int]:
+        self.begin(first_token, pos)
+        for _ in range(steps):
+            self.step(graph)
+        ints = self.ints.numpy()
+        return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + steps]]

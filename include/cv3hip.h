@@ -153,6 +153,10 @@ int cv3_interp_linear(const float* x, float* y, int64_t c, int64_t t, int64_t si
 int cv3_hann_window(int n, int periodic, float* out, cv3_stream_t s);
 /* batched (rows, cols) -> (cols, rows) transpose (the reference's swapaxes/ascontiguousarray copies) */
 int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t cols, cv3_stream_t s);
+/* y[i, j, l] = x[i, j, l] over a (d0, d1, d2) box, each side with its own element strides {s0, s1, s2}
+ * (the DiT's [B, 80, T] <-> [B, T, 80] swaps and channel concat, dit.py:96,151-153,180) */
+int cv3_copy_strided(const float* x, float* y, int64_t d0, int64_t d1, int64_t d2, const int64_t* x_strides,
+                     const int64_t* y_strides, cv3_stream_t s);
 
 /* ---------------- attention (ops.sdpa ops.py:267-300) ---------------- */
 /* q (b, h, n, d), k/v (b, hk, m, d), out (b, h, n, d), each addressed by {batch, head, row} strides in floats
@@ -185,6 +189,69 @@ int cv3_stft(const float* x, int64_t n, int n_fft, int hop, const float* win, in
 int cv3_istft(int mode, const float* a, const float* b, int64_t frames, int n_fft, int hop, const float* win,
               int center, int64_t length, float limit, float* frame_buf, float* y, int64_t* out_len_ptr,
               cv3_stream_t s);
+
+/* ---------------- Qwen2 decode step (cv3cpu/models/qwen2.py:139-179, cv3cpu/models/llm.py:68-77,112-123) --------- */
+/* One stacked int8 weight: `rows` rows per layer, layer l row r at q + (l * rows + r) * kp, its scales at
+ * scales + (l * rows + r) * (kp / block).  Per-output-channel: block = kp, float32 scales; the reference's
+ * q8 (quant.py:56-67): block = 64, float16 scales.  kp and block are multiples of 16. */
+typedef struct {
+  const void* q;
+  const void* scales;
+  int64_t rows, k, kp, block;
+  int scale_dtype; /* CV3_F32 or CV3_F16 */
+} cv3_qweight;
+
+/* Device pointers of a resident Qwen2 body + CosyVoice3 LM head.  qkv stacks [q; k; v] rows per layer
+ * (heads*dh + 2*kv_heads*dh), gate_up stacks [gate; up] (2*inter); qkv_bias [layers, qkv rows];
+ * ln1 / ln2 [layers, hidden]; norm [hidden]; head = llm_decoder [vocab, hidden] with head_bias (may be
+ * NULL); embedding = speech_embedding [vocab, hidden]; rope_cos / rope_sin [cap, head_dim] from
+ * RopeCache (qwen2.py:35-61). */
+typedef struct {
+  int64_t layers, hidden, heads, kv_heads, head_dim, inter;
+  float eps;
+  cv3_qweight qkv, o, gate_up, down, head, embedding;
+  const float* qkv_bias;
+  const float* ln1;
+  const float* ln2;
+  const float* norm;
+  const float* head_bias;
+  const float* rope_cos;
+  const float* rope_sin;
+} cv3_qwen2_model;
+
+/* Device state of one decode stream.  k_cache / v_cache [layers, kv_heads, cap, head_dim] (the KVCache of
+ * qwen2.py:74-121); pos = position of the current input token; token = last selected id; history [cap]
+ * receives each selected id at its input position; x [hidden] is the residual stream and holds the
+ * current input embedding between steps; attn [heads*head_dim]; logits [vocab]; workspace of at least
+ * heads*dh + heads*(cap/64)*(dh+2) + inter floats; counters [kv_heads] zeroed once before the first step. */
+typedef struct {
+  float* k_cache;
+  float* v_cache;
+  int64_t cap;
+  int64_t* pos;
+  int64_t* token;
+  int64_t* history;
+  float* x;
+  float* attn;
+  float* logits;
+  float* workspace;
+  int64_t workspace_floats;
+  unsigned* counters;
+} cv3_qwen2_state;
+
+/* One greedy token: Qwen2Model.forward on x at position pos (qwen2.py:139-179), llm_decoder head
+ * (llm.py:74-77), argmax with ties to the lowest id (the stable argsort of llm.py:138), then
+ * x = speech_embedding[id] (llm.py:121), history[pos + 1] = id, pos += 1.  Reads pos from device
+ * memory, so one captured graph of this call serves every step.  The caller keeps pos + 1 < cap. */
+int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
+/* The decode step's int8 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
+ * y = W . v with v = x, or v = rms_norm(x, rms_w, eps) when rms_w is given (ops.py:101-104).
+ * mode 0: y = W v + bias (bias may be NULL); 1: y += W v; 2: rows are [gate; up] (rows/2 each) and
+ * y = silu(gate . v) * (up . v) (qwen2.py:175-177).  K <= 16384. */
+int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
+                float* y, int mode, cv3_stream_t stream);
+/* x = speech_embedding[*token] (ops.py:126-144): the first input of a decode. */
+int cv3_qwen2_embed_token(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
 
 #ifdef __cplusplus
 }
