@@ -63,6 +63,18 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def replayer(graph: bool, enqueue):
+    """A callable that enqueues ``enqueue``'s launches: replayed from one captured HIP
+    graph, or issued directly (the mode used under the kernel-trace profiler)."""
+    if not graph:
+        return enqueue
+    from cv3amd.device import Graph
+    g = Graph()
+    with g:
+        enqueue()
+    return g.launch
+
+
 # ---------------------------------------------------------------------------
 # decode
 # ---------------------------------------------------------------------------
@@ -95,7 +107,7 @@ def bench_decode(args, tensors, meta):
     log(f"decode: warmup {args.warmup} tokens (captures the step graph)")
     lm.begin(sos, PREFILL)
     for _ in range(args.warmup):
-        lm.step(graph=True)
+        lm.step(graph=args.graph)
     synchronize()
     lm.fill_cache(k, v)
     lm.begin(sos, PREFILL)
@@ -104,7 +116,7 @@ def bench_decode(args, tensors, meta):
     tm = Timer()
     tm.start()
     for _ in range(args.steps):
-        lm.step(graph=True)
+        lm.step(graph=args.graph)
     ms = tm.stop()
     synchronize()
     tokens = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + args.steps]]
@@ -126,15 +138,13 @@ def bench_decode(args, tensors, meta):
         for layer in range(layers):
             _lib.call("gemv_q8", ctypes.byref(gu), layer, lm.x.ptr, lm.ln2.ptr + layer * lm.hidden * 4, lm.eps,
                       None, out.ptr, 2, None)
-    g = Graph()
-    with g:
-        gate_up_sweep()
-    g.launch()
+    run = replayer(args.graph, gate_up_sweep)
+    run()
     synchronize()
     reps = 20
     tm.start()
     for _ in range(reps):
-        g.launch()
+        run()
     kms = tm.stop() / (reps * layers)
     achieved = gu_bytes / (kms / 1e3)
     log(f"decode: gate/up GEMV {kms * 1e3:.2f} us/launch, {achieved / 1e9:.0f} GB/s")
@@ -203,14 +213,14 @@ def bench_flow(args, tensors, meta):
     mu, cond, spks, x0 = flow_inputs(T)
     d.prepare(mu, spks, cond)
     log("flow: warmup solve (captures the solve graph)")
-    d.solve(x0, graph=True)
+    d.solve(x0, graph=args.graph)
     synchronize()
     tm = Timer()
     n = args.flow_solves
     log(f"flow: timing {n} solves")
     tm.start()
     for _ in range(n):
-        d.solve(x0, graph=True)
+        d.solve(x0, graph=args.graph)
     ms = tm.stop() / n
     flops = d.flops_per_solve()
     log(f"flow: {ms:.2f} ms/solve, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
@@ -221,15 +231,13 @@ def bench_flow(args, tensors, meta):
     def qkv_sweep():
         for i in range(d.depth):
             d.qkv[i](d.n.ptr, M, K, d.qkvb.ptr, N)
-    g = Graph()
-    with g:
-        qkv_sweep()
-    g.launch()
+    run = replayer(args.graph, qkv_sweep)
+    run()
     synchronize()
     reps = 10
     tm.start()
     for _ in range(reps):
-        g.launch()
+        run()
     kms = tm.stop() / (reps * d.depth)
     kflops = 2.0 * M * N * K
     log(f"flow: QKV GEMM {kms * 1e3:.1f} us/launch, {kflops / (kms / 1e3) / 1e12:.1f} TFLOP/s")
@@ -271,7 +279,9 @@ def main():
                     help="int8 scale layout of the LM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-core baseline")
     ap.add_argument("--no-flow", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=128)
+    ap.add_argument("--no-graph", dest="graph", action="store_false",
+                    help="issue every launch directly instead of replaying captured HIP graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is "
@@ -318,6 +328,7 @@ def main():
     kern = dec["kernel"]
     line = {
         "metric": METRIC,
+        "launch_mode": "hip-graph replay" if args.graph else "direct launches",
         "value": round(dec["tok_s"], 2),
         "unit": "tok/s",
         "n_gpus": 1,

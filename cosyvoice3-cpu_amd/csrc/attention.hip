@@ -86,23 +86,40 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
   const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
   const int64_t ntiles = ceil_div(p.m, KT);
+  // The next tile's K/V rows are loaded into registers while the current tile is
+  // computed.  Rows past m are clamped to m - 1 (always in bounds); their scores
+  // are masked to -inf below, so the loads carry no predicates.
+  // thread -> keys tid/16 + 16r (r < 4), dims (tid%16)*4 .. +3
+  const int lkey = tid >> 4, ld4 = (tid & 15) * 4;
+  float4 k0r, k1r, k2r, k3r, v0r, v1r, v2r, v3r;
+#define CV3_KV_LOAD(KOFF)                                                                        \
+  {                                                                                              \
+    const int64_t j0 = min((KOFF) + lkey, p.m - 1), j1 = min((KOFF) + lkey + 16, p.m - 1);      \
+    const int64_t j2 = min((KOFF) + lkey + 32, p.m - 1), j3 = min((KOFF) + lkey + 48, p.m - 1); \
+    k0r = *reinterpret_cast<const float4*>(kbase + j0 * p.k_sm + ld4);                           \
+    k1r = *reinterpret_cast<const float4*>(kbase + j1 * p.k_sm + ld4);                           \
+    k2r = *reinterpret_cast<const float4*>(kbase + j2 * p.k_sm + ld4);                           \
+    k3r = *reinterpret_cast<const float4*>(kbase + j3 * p.k_sm + ld4);                           \
+    v0r = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + ld4);                           \
+    v1r = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + ld4);                           \
+    v2r = *reinterpret_cast<const float4*>(vbase + j2 * p.v_sm + ld4);                           \
+    v3r = *reinterpret_cast<const float4*>(vbase + j3 * p.v_sm + ld4);                           \
+  }
+  CV3_KV_LOAD((int64_t)0)
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t k0 = kt * KT;
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int idx = tid + 256 * r;
-      const int key = idx >> 4, d4 = (idx & 15) * 4;
-      const int64_t kj = k0 + key;
-      float4 kv = make_float4(0, 0, 0, 0), vv = make_float4(0, 0, 0, 0);
-      if (kj < p.m) {
-        kv = *reinterpret_cast<const float4*>(kbase + kj * p.k_sm + d4);
-        vv = *reinterpret_cast<const float4*>(vbase + kj * p.v_sm + d4);
-      }
-      *reinterpret_cast<float4*>(&Ks[key * KS + d4]) = kv;
-      *reinterpret_cast<float4*>(&Vs[key * KS + d4]) = vv;
-    }
+    *reinterpret_cast<float4*>(&Ks[lkey * KS + ld4]) = k0r;
+    *reinterpret_cast<float4*>(&Ks[(lkey + 16) * KS + ld4]) = k1r;
+    *reinterpret_cast<float4*>(&Ks[(lkey + 32) * KS + ld4]) = k2r;
+    *reinterpret_cast<float4*>(&Ks[(lkey + 48) * KS + ld4]) = k3r;
+    *reinterpret_cast<float4*>(&Vs[lkey * KS + ld4]) = v0r;
+    *reinterpret_cast<float4*>(&Vs[(lkey + 16) * KS + ld4]) = v1r;
+    *reinterpret_cast<float4*>(&Vs[(lkey + 32) * KS + ld4]) = v2r;
+    *reinterpret_cast<float4*>(&Vs[(lkey + 48) * KS + ld4]) = v3r;
     __syncthreads();
+    if (kt + 1 < ntiles) CV3_KV_LOAD(k0 + KT)
+    __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this tile's math
 
 #pragma unroll
     for (int sub = 0; sub < KT / 16; ++sub) {
@@ -155,6 +172,7 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
       }
     }
   }
+#undef CV3_KV_LOAD
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (!qvalid) return;

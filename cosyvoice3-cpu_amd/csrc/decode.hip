@@ -49,6 +49,13 @@ __device__ __forceinline__ float sc_at(const QW& w, int64_t row, int64_t kk) {
                 : reinterpret_cast<const float*>(w.scales)[i];
 }
 
+// Scale of 16-code chunk c of a row whose scales start at `srow`: 32-bit index math
+// (cpb = block / 16 chunks per scale).
+__device__ __forceinline__ float sc_chunk(const QW& w, const void* srow, unsigned c, unsigned cpb) {
+  const unsigned i = c / cpb;
+  return w.sf16 ? __half2float(reinterpret_cast<const __half*>(srow)[i]) : reinterpret_cast<const float*>(srow)[i];
+}
+
 __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ xs) {
   const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
   float a = 0.f;
@@ -65,20 +72,49 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ 
 }
 
 // Stage x[0:k) into LDS (zero padded to kx), optionally RMS-normalised with weight
-// rms_w: x * (1 / sqrt(mean(x^2) + eps)) * w (cv3cpu/ops.py:101-104).
+// rms_w: x * (1 / sqrt(mean(x^2) + eps)) * w (cv3cpu/ops.py:101-104).  Every
+// thread issues all of its float4 loads before using any of them (NV per thread,
+// unrolled), so the vector costs one memory latency, not one per loop trip.
+// Needs k % 4 == 0 and 16-byte aligned x / rms_w.
+template <int NV>
 __device__ void stage_vec(const float* __restrict__ x, int64_t k, int64_t kx, const float* __restrict__ rms_w,
                           float eps, float* xs, float* red) {
+  const int64_t k4 = k / 4, n4 = kx / 4;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* w4 = reinterpret_cast<const float4*>(rms_w);
+  float4 v[NV], w[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+    v[i] = idx < k4 ? x4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    w[i] = (rms_w && idx < k4) ? w4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   float inv = 1.f;
   if (rms_w) {
     float ss = 0.f;
-    for (int64_t c = threadIdx.x; c < k; c += blockDim.x) ss = fmaf(x[c], x[c], ss);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      ss = fmaf(v[i].x, v[i].x, ss);
+      ss = fmaf(v[i].y, v[i].y, ss);
+      ss = fmaf(v[i].z, v[i].z, ss);
+      ss = fmaf(v[i].w, v[i].w, ss);
+    }
     ss = block_sum(ss, red);
     inv = 1.0f / sqrtf(ss / (float)k + eps);
   }
-  for (int64_t c = threadIdx.x; c < kx; c += blockDim.x) {
-    float v = 0.f;
-    if (c < k) v = rms_w ? (x[c] * inv) * rms_w[c] : x[c];
-    xs[c] = v;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+    if (idx < n4) {
+      float4 o = v[i];
+      if (rms_w) {
+        o.x = (o.x * inv) * w[i].x;
+        o.y = (o.y * inv) * w[i].y;
+        o.z = (o.z * inv) * w[i].z;
+        o.w = (o.w * inv) * w[i].w;
+      }
+      reinterpret_cast<float4*>(xs)[idx] = o;
+    }
   }
   __syncthreads();
 }
@@ -100,13 +136,16 @@ struct RowDot {
   // sum over this lane's chunks; per-row scales are applied by the caller
   __device__ __forceinline__ float dot(const QW& w, int64_t row, int sub, const float* xs, bool per_row) {
     float acc = 0.f;
-    const int64_t nch = w.kp / 16;
+    const unsigned nch = (unsigned)(w.kp / 16), cpb = (unsigned)(w.block / 16);
+    const int64_t nb = w.kp / w.block;
+    const void* srow = w.sf16 ? (const void*)(reinterpret_cast<const __half*>(w.scales) + row * nb)
+                              : (const void*)(reinterpret_cast<const float*>(w.scales) + row * nb);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int64_t c = sub + (int64_t)i * LPR;
+      const unsigned c = (unsigned)sub + (unsigned)i * LPR;
       if (c < nch) {
         const float d = dot16(wv[i], xs + c * 16);
-        acc = per_row ? acc + d : fmaf(d, sc_at(w, row, c * 16), acc);
+        acc = per_row ? acc + d : fmaf(d, sc_chunk(w, srow, c, cpb), acc);
       }
     }
 #pragma unroll
@@ -149,7 +188,7 @@ __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   RowDot<LPR, CPL> rd;
   rd.load(a.w, live ? wrow : a.layer_row0, sub, live);
   const int64_t kx = a.w.kp;
-  stage_vec(a.x, a.w.k, kx, a.rms_w, a.eps, xs, red);
+  stage_vec<(LPR * CPL + 63) / 64>(a.x, a.w.k, kx, a.rms_w, a.eps, xs, red);
   const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
   const float acc = rd.dot(a.w, live ? wrow : a.layer_row0, sub, xs, per_row);
   if (swiglu) {
@@ -202,7 +241,7 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   const int64_t wrow = a.layer_row0 + (live ? r : 0);
   RowDot<LPR, CPL> rd;
   rd.load(a.w, wrow, sub, live);
-  stage_vec(a.x, a.w.k, a.w.kp, a.rms_w, a.eps, xs, red);
+  stage_vec<(LPR * CPL + 63) / 64>(a.x, a.w.k, a.w.kp, a.rms_w, a.eps, xs, red);
   const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
   float v = rd.dot(a.w, wrow, sub, xs, per_row);
   if (live) v += a.bias[r];
@@ -230,11 +269,15 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
 // ---------------------------------------------------------------------------
 // Decode attention (cv3cpu/ops.py:267-300 with one query and no mask,
 // qwen2.py:148,169): the G = heads / kv_heads query heads of one kv head
-// against keys [0, pos].  Workgroup (split, g) covers keys [split*64, split*64+64),
-// writes (max, sum, unnormalised out) per head, and the last workgroup to finish
-// for kv head g merges the splits: out = sum_s e^{m_s - M} o_s / sum_s e^{m_s - M} l_s.
+// against keys [0, pos].  Workgroup (split, g) covers keys [split*64, split*64+64)
+// and writes, per query head, the chunk's max score m_s, sum l_s = sum e^{s - m_s}
+// and unnormalised output o_s = sum e^{s - m_s} v.  The o_proj kernel merges the
+// chunks when it stages its input (out = sum_s e^{m_s - M} o_s / sum_s e^{m_s - M} l_s),
+// so no workgroup ever waits on another inside a kernel.
 // ---------------------------------------------------------------------------
-constexpr int KCH = 64;
+constexpr int KCH = 64;      // keys per chunk
+constexpr int64_t kWsQ = 1024;  // q slot of the workspace
+constexpr int NSMAX = 16;    // chunks per head: cache capacity <= 1024
 struct AttnArgs {
   const float* q;          // [heads * dh]
   const float* k_cache;    // layer's [kv_heads, cap, dh]
@@ -243,17 +286,14 @@ struct AttnArgs {
   int64_t cap;
   const int64_t* pos;
   float scale;
-  float* part;             // [heads, nsplit, dh + 2]
-  int nsplit;
-  unsigned* counters;      // [kv_heads], zero between uses
-  float* out;              // [heads * dh]
+  float* part_o;           // [heads, NSMAX, 64]
+  float* part_ml;          // [heads, NSMAX, 2]
 };
 
 __global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
-  __shared__ float Ks[KCH * 65];
-  __shared__ float Vs[KCH * 64];
+  __shared__ float Kt[64 * (KCH + 1)];   // K^T: [d][key], padded
+  __shared__ float Vs[KCH * 64];         // V: [key][d]
   __shared__ float qs[8 * 64];
-  __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int split = blockIdx.x, g = blockIdx.y;
   const int G = a.heads / a.kv_heads;
@@ -263,21 +303,40 @@ __global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
   const int64_t k0 = (int64_t)split * KCH;
   const float* kb = a.k_cache + (int64_t)g * a.cap * a.dh;
   const float* vb = a.v_cache + (int64_t)g * a.cap * a.dh;
-  for (int i = threadIdx.x; i < KCH * 64; i += 256) {
-    const int key = i / 64, d = i % 64;
-    const bool ok = k0 + key < L && d < a.dh;
-    Ks[key * 65 + d] = ok ? kb[(k0 + key) * a.dh + d] : 0.f;
-    Vs[key * 64 + d] = ok ? vb[(k0 + key) * a.dh + d] : 0.f;
+  // all loads first (4 float4 of K and 4 of V per thread), then the LDS writes
+  const int d4n = a.dh / 4;  // float4 per key row
+  float4 kr[4], vr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int idx = threadIdx.x + 256 * r;  // (key, d4) over 64 x 16
+    const int key = idx >> 4, d4 = idx & 15;
+    const bool ok = k0 + key < L && d4 < d4n;
+    kr[r] = ok ? reinterpret_cast<const float4*>(kb + (k0 + key) * a.dh)[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[r] = ok ? reinterpret_cast<const float4*>(vb + (k0 + key) * a.dh)[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (int i = threadIdx.x; i < G * 64; i += 256) {
-    const int h = i / 64, d = i % 64;
-    qs[i] = d < a.dh ? a.q[(g * G + h) * a.dh + d] * a.scale : 0.f;  // (q * scale) first (ops.py:292)
+  // q of the G <= 8 heads: (head, d4) over 8 x 16 float4, one per thread of the first 128
+  const int qh = threadIdx.x >> 4, qd4 = threadIdx.x & 15;
+  const float4 qv = (threadIdx.x < 128 && qh < G && qd4 < d4n)
+                        ? reinterpret_cast<const float4*>(a.q + (g * G + qh) * a.dh)[qd4]
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int idx = threadIdx.x + 256 * r;
+    const int key = idx >> 4, d = (idx & 15) * 4;
+    Kt[(d + 0) * (KCH + 1) + key] = kr[r].x;
+    Kt[(d + 1) * (KCH + 1) + key] = kr[r].y;
+    Kt[(d + 2) * (KCH + 1) + key] = kr[r].z;
+    Kt[(d + 3) * (KCH + 1) + key] = kr[r].w;
+    reinterpret_cast<float4*>(Vs)[idx] = vr[r];
   }
+  if (threadIdx.x < 128)  // (q * scale) first (ops.py:292)
+    reinterpret_cast<float4*>(qs)[threadIdx.x] = make_float4(qv.x * a.scale, qv.y * a.scale, qv.z * a.scale,
+                                                             qv.w * a.scale);
   __syncthreads();
   for (int h = wave; h < G; h += 4) {
     const int key = lane;
     float s = 0.f;
-    for (int d = 0; d < a.dh; ++d) s = fmaf(qs[h * 64 + d], Ks[key * 65 + d], s);
+    for (int d = 0; d < a.dh; ++d) s = fmaf(qs[h * 64 + d], Kt[d * (KCH + 1) + key], s);
     if (k0 + key >= L) s = -INFINITY;
     const float m = wave_max(s);
     const float p = expf(s - m);
@@ -285,40 +344,83 @@ __global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
     float o = 0.f;
     for (int kk = 0; kk < KCH; ++kk) o = fmaf(__shfl(p, kk, 64), Vs[kk * 64 + lane], o);
     const int hq = g * G + h;
-    float* pr = a.part + ((int64_t)hq * a.nsplit + split) * (a.dh + 2);
-    if (lane < a.dh) pr[lane] = o;
+    a.part_o[((int64_t)hq * NSMAX + split) * 64 + lane] = o;
     if (lane == 0) {
-      pr[a.dh] = m;
-      pr[a.dh + 1] = l;
+      a.part_ml[((int64_t)hq * NSMAX + split) * 2] = m;
+      a.part_ml[((int64_t)hq * NSMAX + split) * 2 + 1] = l;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// o_proj with the attention merge as its prologue: stage
+// attn[h*dh + d] = sum_s e^{m_s - M_h} o_s[d] / sum_s e^{m_s - M_h} l_s  (H*dh <= 1024),
+// then x += W_o . attn (mode-1 GEMV, LPR = 8).
+// ---------------------------------------------------------------------------
+struct OprojArgs {
+  QW w;
+  int64_t layer_row0;
+  int64_t n;
+  const float* part_o;
+  const float* part_ml;
+  int heads, dh;
+  const int64_t* pos;
+  float* x;                // residual stream, updated in place
+};
+
+template <int CPL>
+__global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float ml[16 * NSMAX * 2];
+  constexpr int LPR = 8, RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = lane / LPR, sub = lane % LPR;
+  const int64_t col = ((int64_t)blockIdx.x * 4 + wave) * RPW + grp;
+  const bool live = col < a.n;
+  const int64_t wrow = a.layer_row0 + (live ? col : 0);
+  RowDot<LPR, CPL> rd;
+  rd.load(a.w, wrow, sub, live);
+  const int active = (int)((*a.pos + 1 + KCH - 1) / KCH);
+  // (m, l) of every (head, chunk) into LDS; this thread's output float4s (head, d4)
+  // gather their chunks' o in registers meanwhile
+  const int t = threadIdx.x;
+  float2 mlv = make_float2(-INFINITY, 0.f);
+  if (t < a.heads * NSMAX && (t % NSMAX) < active) mlv = reinterpret_cast<const float2*>(a.part_ml)[t];
+  const int d4n = a.dh / 4;
+  const int oh = t / 16, od4 = t % 16;
+  const bool owns = oh < a.heads && od4 < d4n;
+  float4 ov[NSMAX];
+#pragma unroll
+  for (int s2 = 0; s2 < NSMAX; ++s2)
+    ov[s2] = (owns && s2 < active)
+                 ? reinterpret_cast<const float4*>(a.part_o + ((int64_t)oh * NSMAX + s2) * 64)[od4]
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t < 16 * NSMAX) reinterpret_cast<float2*>(ml)[t] = mlv;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned prev = atomicAdd(&a.counters[g], 1u);
-    last = prev == (unsigned)(active - 1);
-    if (last) {
-      __threadfence();
-      a.counters[g] = 0u;  // ready for the next layer / token
-    }
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int h = wave; h < G; h += 4) {
-    const int hq = g * G + h;
-    const float* pr = a.part + (int64_t)hq * a.nsplit * (a.dh + 2);
+  if (owns) {
     float M = -INFINITY;
-    for (int s2 = 0; s2 < active; ++s2) M = fmaxf(M, __builtin_nontemporal_load(pr + s2 * (a.dh + 2) + a.dh));
-    float den = 0.f, num = 0.f;
-    for (int s2 = 0; s2 < active; ++s2) {
-      const float* ps = pr + s2 * (a.dh + 2);
-      const float w = expf(__builtin_nontemporal_load(ps + a.dh) - M);
-      den = fmaf(__builtin_nontemporal_load(ps + a.dh + 1), w, den);
-      if (lane < a.dh) num = fmaf(__builtin_nontemporal_load(ps + lane), w, num);
+    for (int s2 = 0; s2 < active; ++s2) M = fmaxf(M, ml[(oh * NSMAX + s2) * 2]);
+    float den = 0.f;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s2 = 0; s2 < NSMAX; ++s2) {
+      if (s2 < active) {
+        const float wgt = expf(ml[(oh * NSMAX + s2) * 2] - M);
+        den = fmaf(ml[(oh * NSMAX + s2) * 2 + 1], wgt, den);
+        num.x = fmaf(ov[s2].x, wgt, num.x);
+        num.y = fmaf(ov[s2].y, wgt, num.y);
+        num.z = fmaf(ov[s2].z, wgt, num.z);
+        num.w = fmaf(ov[s2].w, wgt, num.w);
+      }
     }
-    if (lane < a.dh) a.out[hq * a.dh + lane] = num / den;
+    reinterpret_cast<float4*>(xs + oh * a.dh)[od4] = make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
   }
+  // zero padding up to the weight's padded K
+  for (int64_t c = (int64_t)a.heads * a.dh + t; c < a.w.kp; c += 256) xs[c] = 0.f;
+  __syncthreads();
+  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
+  const float acc = rd.dot(a.w, wrow, sub, xs, per_row);
+  if (live && sub == 0) a.x[col] = a.x[col] + acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -464,15 +566,19 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
   CV3_REQUIRE(m->qkv.rows == (H + 2 * Hk) * dh && m->o.rows == D && m->gate_up.rows == 2 * I && m->down.rows == D,
               CV3_EINVAL, "stacked weight rows do not match the geometry");
   CV3_REQUIRE(m->qkv.kp / 16 <= 8 * 8, CV3_EUNSUPPORTED, "qkv K too large for the fused rotary GEMV");
-  CV3_REQUIRE(s->workspace_floats >= H * dh + H * (s->cap / KCH) * (dh + 2) + I, CV3_EINVAL,
+  CV3_REQUIRE(s->cap / KCH <= NSMAX, CV3_EUNSUPPORTED, "cache capacity above %d positions", NSMAX * KCH);
+  CV3_REQUIRE(H <= 16 && dh % 4 == 0 && D % 4 == 0 && I % 4 == 0, CV3_EUNSUPPORTED, "decode geometry");
+  CV3_REQUIRE(m->o.kp / 16 <= 8 * 8, CV3_EUNSUPPORTED, "o_proj K too large");
+  CV3_REQUIRE(s->workspace_floats >= kWsQ + H * NSMAX * 64 + H * NSMAX * 2 + I + 64, CV3_EINVAL,
               "workspace too small");
   hipStream_t st = stream_of(stream);
   const QW qkv = make_qw(m->qkv), o = make_qw(m->o), gu = make_qw(m->gate_up), dn = make_qw(m->down);
   const QW head = make_qw(m->head), emb = make_qw(m->embedding);
+  // workspace: q [1024] | part_o [H, NSMAX, 64] | part_ml [H, NSMAX, 2] | h [I] (16-byte aligned pieces)
   float* qbuf = s->workspace;
-  float* part = qbuf + H * dh;
-  float* hbuf = part + H * (s->cap / KCH) * (dh + 2);
-  const int nsplit = (int)(s->cap / KCH);
+  float* part_o = qbuf + kWsQ;
+  float* part_ml = part_o + H * NSMAX * 64;
+  float* hbuf = part_ml + ((H * NSMAX * 2 + 3) / 4) * 4;
   const float scale = 1.0f / sqrtf((float)dh);
   for (int64_t l = 0; l < m->layers; ++l) {
     float* kc = s->k_cache + l * Hk * s->cap * dh;
@@ -483,12 +589,12 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
     hipLaunchKernelGGL(k_dec_qkv<8>, dim3((unsigned)ceil_div(pairs, 16)), dim3(256), qkv.kp * sizeof(float), st,
                        qa);
     CV3_LAUNCHED();
-    AttnArgs aa{qbuf, kc, vc, (int)H, (int)Hk, (int)dh, s->cap, s->pos, scale, part, nsplit,
-                s->counters + 0, s->attn};
-    hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)nsplit, (unsigned)Hk), dim3(256), 0, st, aa);
+    AttnArgs aa{qbuf, kc, vc, (int)H, (int)Hk, (int)dh, s->cap, s->pos, scale, part_o, part_ml};
+    hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)(s->cap / KCH), (unsigned)Hk), dim3(256), 0, st, aa);
     CV3_LAUNCHED();
-    GemvArgs ga{o, l * o.rows, D, s->attn, nullptr, 0.f, nullptr, s->x, 1};
-    if ((rc = gemv(ga, st))) return rc;
+    OprojArgs oa{o, l * o.rows, D, part_o, part_ml, (int)H, (int)dh, s->pos, s->x};
+    hipLaunchKernelGGL(k_dec_oproj<8>, dim3((unsigned)ceil_div(D, 32)), dim3(256), o.kp * sizeof(float), st, oa);
+    CV3_LAUNCHED();
     GemvArgs gb{gu, l * gu.rows, I, s->x, m->ln2 + l * D, m->eps, nullptr, hbuf, 2};
     if ((rc = gemv(gb, st))) return rc;
     GemvArgs gc{dn, l * dn.rows, D, hbuf, nullptr, 0.f, nullptr, s->x, 1};

@@ -6,13 +6,20 @@
 //
 // Tiling: a 256-thread workgroup owns a BM x BN = 64 x 64 output tile; each of
 // its four waves owns a 32 x 32 quadrant computed with v_mfma_f32_32x32x2_f32
-// (fp32 in, fp32 accumulate).  K advances in steps of BK = 16, staged through
-// LDS with the next step's global loads held in registers meanwhile.
+// (fp32 in, fp32 accumulate).  K advances in stages of BK = 32 through a
+// double-buffered LDS tile, and the global loads run two stages ahead in
+// registers (ping-pong sets r0 / r1), so each load has two stages of MFMA work
+// (32 MFMAs per wave) to hide behind.
 //
-// K permutation: an MFMA step j consumes two k values per lane half (h = lane/32).
-// Mapping step j, half h -> k = (j/4)*8 + h*4 + j%4 lets every lane read four
-// consecutive k with one 16-byte LDS load for four consecutive MFMAs.  The
-// same map is used for A and B, so the products pair correctly.
+// K permutation: within a stage, group g (8 k values) and lane half h = lane/32
+// give MFMA j the k value g*8 + h*4 + j, so every lane reads four consecutive k
+// with one 16-byte LDS load for four consecutive MFMAs.  A and B use the same
+// map, so the products pair correctly.
+//
+// Workgroup -> tile mapping is XCD-aware: workgroups are dispatched round-robin
+// over the 8 XCDs, so linear id L runs on XCD L % 8; tile t = (L % 8) * (T / 8) +
+// L / 8 with M-tiles fastest gives each XCD whole columns of N-tiles, and each
+// weight tile is fetched into one XCD's L2 only.
 #include "common.hpp"
 #include "epilogue.hpp"
 
@@ -22,7 +29,11 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 64, BN = 64, BK = 16, LDS_STRIDE = BK + 4;
+constexpr int BM = 64, BN = 64, BK = 32, LDS_STRIDE = BK + 4;
+
+struct Stage {
+  float4 a0, a1, b0, b1;
+};
 
 enum { B_F32 = 0, B_Q8 = 1 };
 
@@ -39,7 +50,30 @@ struct GemmParams {
   float* c;
   int64_t ldc;
   cv3_epilogue epi;
+  // channels-last grouped temporal conv as an implicit GEMM (A_CONV): rows are
+  // (batch, time) with conv_t rows per batch, K = (tap, channel-in-group)
+  int conv_t, conv_cg, conv_pad;
 };
+
+enum { A_ROWS = 0, A_CONV = 1 };
+
+// A operand of the FAST kernel.  A_ROWS: base = a + row * lda + lk.
+// A_CONV: base = x + batch * conv_t * lda + group channel base + lk, t_row = the
+// row's time index; k = tap * conv_cg + channel, so x[t_row + tap - pad, channel]
+// with zeros outside [0, conv_t) (loaded from the row itself and replaced by a select).
+template <int AMODE>
+__device__ __forceinline__ float4 load_a_fast(const GemmParams& p, const float* base, int t_row, int64_t koff) {
+  if constexpr (AMODE == A_ROWS) {
+    return *reinterpret_cast<const float4*>(base + koff);
+  } else {
+    const int kk = (int)koff;
+    const int tap = kk / p.conv_cg, c = kk - tap * p.conv_cg;
+    const int tt = t_row + tap - p.conv_pad;
+    const bool ok = (unsigned)tt < (unsigned)p.conv_t;
+    const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)(ok ? tt : t_row) * p.lda + c);
+    return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
 
 template <int BK_KIND>
 __device__ __forceinline__ float4 load_b(const GemmParams& p, int64_t row, int64_t kk, bool fast) {
@@ -58,7 +92,7 @@ __device__ __forceinline__ float4 load_b(const GemmParams& p, int64_t row, int64
     if (fast) {
       // four codes in one word share a scale because block % 4 == 0 on this path
       const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
-      const int64_t si = row * p.nb + kk / p.block;
+      const int64_t si = row * p.nb + (int64_t)((uint32_t)kk / (uint32_t)p.block);
       const float s = p.sf16 ? __half2float(reinterpret_cast<const __half*>(p.scales)[si])
                              : reinterpret_cast<const float*>(p.scales)[si];
 #pragma unroll
@@ -89,52 +123,150 @@ __device__ __forceinline__ float4 load_a(const GemmParams& p, int64_t row, int64
   return make_float4(t[0], t[1], t[2], t[3]);
 }
 
+// Branch-free loads for the FAST kernel: K % BK == 0, 16-byte aligned rows; rows past
+// M / N are clamped to the last row (their results are never stored), so the
+// loads carry no predicates and the compiler can count them (vmcnt) across the
+// two-stage pipeline.
 template <int BK_KIND>
-__global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast_b) {
+__device__ __forceinline__ float4 load_b_fast(const GemmParams& p, int64_t row, int64_t kk) {
+  if constexpr (BK_KIND == B_F32) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.b) + row * p.ldb + kk);
+  } else {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(p.b) + row * p.ldb + kk);
+    const int64_t si = row * p.nb + (int64_t)((uint32_t)kk / (uint32_t)p.block);
+    const float s = p.sf16 ? __half2float(reinterpret_cast<const __half*>(p.scales)[si])
+                           : reinterpret_cast<const float*>(p.scales)[si];
+    return make_float4((float)((int32_t)(w << 24) >> 24) * s, (float)((int32_t)(w << 16) >> 24) * s,
+                       (float)((int32_t)(w << 8) >> 24) * s, (float)((int32_t)w >> 24) * s);
+  }
+}
+
+// thread -> rows lrow and lrow + 32 of the A and B tiles, 4 consecutive k at lk
+template <int BK_KIND, bool FAST>
+__device__ __forceinline__ void load_stage(const GemmParams& p, int64_t m0, int64_t n0, int64_t k0, int lrow, int lk,
+                                           bool fa, bool fb, Stage& st) {
+  const int64_t kk = k0 + lk;
+  if constexpr (FAST) {
+    const int64_t ra0 = min(m0 + lrow, p.m - 1), ra1 = min(m0 + lrow + 32, p.m - 1);
+    const int64_t rb0 = min(n0 + lrow, p.n - 1), rb1 = min(n0 + lrow + 32, p.n - 1);
+    st.a0 = *reinterpret_cast<const float4*>(p.a + ra0 * p.lda + kk);
+    st.a1 = *reinterpret_cast<const float4*>(p.a + ra1 * p.lda + kk);
+    st.b0 = load_b_fast<BK_KIND>(p, rb0, kk);
+    st.b1 = load_b_fast<BK_KIND>(p, rb1, kk);
+  } else {
+    const bool kfull = kk + 4 <= p.k;
+    st.a0 = load_a(p, m0 + lrow, kk, fa && kfull);
+    st.a1 = load_a(p, m0 + lrow + 32, kk, fa && kfull);
+    st.b0 = load_b<BK_KIND>(p, n0 + lrow, kk, fb && kfull);
+    st.b1 = load_b<BK_KIND>(p, n0 + lrow + 32, kk, fb && kfull);
+  }
+}
+
+__device__ __forceinline__ void store_stage(float* As, float* Bs, int lrow, int lk, const Stage& st) {
+  *reinterpret_cast<float4*>(&As[lrow * LDS_STRIDE + lk]) = st.a0;
+  *reinterpret_cast<float4*>(&As[(lrow + 32) * LDS_STRIDE + lk]) = st.a1;
+  *reinterpret_cast<float4*>(&Bs[lrow * LDS_STRIDE + lk]) = st.b0;
+  *reinterpret_cast<float4*>(&Bs[(lrow + 32) * LDS_STRIDE + lk]) = st.b1;
+}
+
+__device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int wm, int wn, int r32, int h, f32x16& acc) {
+  const float* as = &As[(wm + r32) * LDS_STRIDE + h * 4];
+  const float* bs = &Bs[(wn + r32) * LDS_STRIDE + h * 4];
+#pragma unroll
+  for (int g = 0; g < BK / 8; ++g) {
+    const float4 av = *reinterpret_cast<const float4*>(as + g * 8);
+    const float4 bv = *reinterpret_cast<const float4*>(bs + g * 8);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+  }
+}
+
+template <int BK_KIND, bool FAST, int AMODE = A_ROWS>
+__global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast_b, int tiles_m) {
   __shared__ float As[2][BM * LDS_STRIDE];
   __shared__ float Bs[2][BN * LDS_STRIDE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  // global -> LDS assignment: each thread moves one float4 of A and of B per K step
-  const int lrow = tid >> 2, lk = (tid & 3) * 4;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  const int lrow = tid >> 3, lk = (tid & 7) * 4;
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const int r32 = lane & 31, h = lane >> 5;
-
-  const int64_t ksteps = ceil_div(p.k, BK);
   const bool fa = fast_a, fb = fast_b;
 
-  float4 ra = load_a(p, m0 + lrow, lk, fa && lk + 4 <= p.k);
-  float4 rb = load_b<BK_KIND>(p, n0 + lrow, lk, fb && lk + 4 <= p.k);
-  *reinterpret_cast<float4*>(&As[0][lrow * LDS_STRIDE + lk]) = ra;
-  *reinterpret_cast<float4*>(&Bs[0][lrow * LDS_STRIDE + lk]) = rb;
-  __syncthreads();
-
+  const int64_t S = ceil_div(p.k, BK);
   f32x16 acc = {0.f};
-  for (int64_t s = 0; s < ksteps; ++s) {
-    const int buf = s & 1;
-    const bool more = s + 1 < ksteps;
-    if (more) {
-      const int64_t kk = (s + 1) * BK + lk;
-      ra = load_a(p, m0 + lrow, kk, fa && kk + 4 <= p.k);
-      rb = load_b<BK_KIND>(p, n0 + lrow, kk, fb && kk + 4 <= p.k);
+  if constexpr (FAST) {
+    // S even and >= 2 (K % 64 == 0): straight-line ping-pong between two register
+    // sets (x0 / x1: A rows lrow, lrow + 32 and B rows lrow, lrow + 32), no predicates
+    const int64_t ra0 = min(m0 + lrow, p.m - 1), ra1 = min(m0 + lrow + 32, p.m - 1);
+    const int64_t rb0 = min(n0 + lrow, p.n - 1), rb1 = min(n0 + lrow + 32, p.n - 1);
+    const float* pa0;
+    const float* pa1;
+    int t0 = 0, t1 = 0;
+    if constexpr (AMODE == A_ROWS) {
+      pa0 = p.a + ra0 * p.lda + lk;
+      pa1 = p.a + ra1 * p.lda + lk;
+    } else {
+      // output channels of this N-tile form one group: channel base = group * conv_cg
+      const int64_t cbase = (n0 / BN) * p.conv_cg;
+      const int b0 = (int)ra0 / p.conv_t, b1 = (int)ra1 / p.conv_t;
+      t0 = (int)ra0 - b0 * p.conv_t;
+      t1 = (int)ra1 - b1 * p.conv_t;
+      pa0 = p.a + (int64_t)b0 * p.conv_t * p.lda + cbase + lk;
+      pa1 = p.a + (int64_t)b1 * p.conv_t * p.lda + cbase + lk;
     }
-    const float* as = &As[buf][(wm + r32) * LDS_STRIDE + h * 4];
-    const float* bs = &Bs[buf][(wn + r32) * LDS_STRIDE + h * 4];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float4 av = *reinterpret_cast<const float4*>(as + g * 8);
-      const float4 bv = *reinterpret_cast<const float4*>(bs + g * 8);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
-    }
-    if (more) {
-      *reinterpret_cast<float4*>(&As[buf ^ 1][lrow * LDS_STRIDE + lk]) = ra;
-      *reinterpret_cast<float4*>(&Bs[buf ^ 1][lrow * LDS_STRIDE + lk]) = rb;
-    }
+    float4 xa0, xa1, xb0, xb1, ya0, ya1, yb0, yb1;
+#define CV3_LOAD(A0, A1, B0, B1, KOFF)                                   \
+  A0 = load_a_fast<AMODE>(p, pa0, t0, (KOFF));                           \
+  A1 = load_a_fast<AMODE>(p, pa1, t1, (KOFF));                           \
+  B0 = load_b_fast<BK_KIND>(p, rb0, (KOFF) + lk);                        \
+  B1 = load_b_fast<BK_KIND>(p, rb1, (KOFF) + lk);
+#define CV3_STORE(BUF, A0, A1, B0, B1)                                               \
+  *reinterpret_cast<float4*>(&As[BUF][lrow * LDS_STRIDE + lk]) = A0;                 \
+  *reinterpret_cast<float4*>(&As[BUF][(lrow + 32) * LDS_STRIDE + lk]) = A1;          \
+  *reinterpret_cast<float4*>(&Bs[BUF][lrow * LDS_STRIDE + lk]) = B0;                 \
+  *reinterpret_cast<float4*>(&Bs[BUF][(lrow + 32) * LDS_STRIDE + lk]) = B1;
+    CV3_LOAD(xa0, xa1, xb0, xb1, 0)
+    CV3_LOAD(ya0, ya1, yb0, yb1, BK)
+    CV3_STORE(0, xa0, xa1, xb0, xb1)
     __syncthreads();
+    for (int64_t s = 0; s + 2 < S; s += 2) {
+      // LDS[0] = stage s, y = stage s + 1 in flight
+      CV3_LOAD(xa0, xa1, xb0, xb1, (s + 2) * BK)
+      __builtin_amdgcn_sched_barrier(0);  // issue the loads before anything below
+      mma_stage(As[0], Bs[0], wm, wn, r32, h, acc);
+      CV3_STORE(1, ya0, ya1, yb0, yb1)
+      __syncthreads();
+      // LDS[1] = stage s + 1, x = stage s + 2 in flight
+      CV3_LOAD(ya0, ya1, yb0, yb1, (s + 3) * BK)
+      __builtin_amdgcn_sched_barrier(0);
+      mma_stage(As[1], Bs[1], wm, wn, r32, h, acc);
+      CV3_STORE(0, xa0, xa1, xb0, xb1)
+      __syncthreads();
+    }
+    mma_stage(As[0], Bs[0], wm, wn, r32, h, acc);
+    CV3_STORE(1, ya0, ya1, yb0, yb1)
+    __syncthreads();
+    mma_stage(As[1], Bs[1], wm, wn, r32, h, acc);
+#undef CV3_LOAD
+#undef CV3_STORE
+  } else {
+    // ragged K / unaligned rows: one stage of register prefetch, guarded loads
+    Stage r0;
+    load_stage<BK_KIND, FAST>(p, m0, n0, 0, lrow, lk, fa, fb, r0);
+    store_stage(As[0], Bs[0], lrow, lk, r0);
+    __syncthreads();
+    for (int64_t s = 0; s < S; ++s) {
+      const int buf = s & 1;
+      if (s + 1 < S) load_stage<BK_KIND, FAST>(p, m0, n0, (s + 1) * BK, lrow, lk, fa, fb, r0);
+      mma_stage(As[buf], Bs[buf], wm, wn, r32, h, acc);
+      if (s + 1 < S) store_stage(As[buf ^ 1], Bs[buf ^ 1], lrow, lk, r0);
+      __syncthreads();
+    }
   }
 
   // accumulator layout (32x32x2 f32): reg i -> row (i/4)*8 + h*4 + i%4, col = lane%32
@@ -178,11 +310,57 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   const int fast_a = ((uintptr_t)a % 16 == 0) && (lda % 4 == 0);
   const int fast_b = q8 ? (((uintptr_t)b % 4 == 0) && (ldb % 4 == 0) && (block % 4 == 0))
                         : (((uintptr_t)b % 16 == 0) && (ldb % 4 == 0));
-  const dim3 grid((unsigned)ceil_div(n, BN), (unsigned)ceil_div(m, BM));
-  if (q8)
-    hipLaunchKernelGGL(k_gemm<B_Q8>, grid, dim3(256), 0, st, p, fast_a, fast_b);
-  else
-    hipLaunchKernelGGL(k_gemm<B_F32>, grid, dim3(256), 0, st, p, fast_a, fast_b);
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  p.conv_t = p.conv_cg = p.conv_pad = 0;
+  // the branch-free kernel: whole K stages and aligned rows for both operands
+  const bool fast = fast_a && fast_b && k % (2 * BK) == 0;
+  if (q8) {
+    if (fast)
+      hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+    else
+      hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+  } else {
+    if (fast)
+      hipLaunchKernelGGL((k_gemm<B_F32, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+    else
+      hipLaunchKernelGGL((k_gemm<B_F32, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+  }
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// y[b, t, co] = epi(bias[co] + sum_{tap, c} w[co, tap, c] * x[b, t + tap - pad_l, g * cin_g + c]),
+// g = co / 64: the DiT's grouped conv_pos (cv3cpu/models/dit.py:99-112) on
+// channels-last activations, as an implicit GEMM on the FAST kernel.  w is the
+// reference's (cout, cin_g, k) weight repacked as (cout, k, cin_g).
+int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* w, int64_t cout, int64_t k,
+            int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
+            hipStream_t st) {
+  CV3_REQUIRE(cin_g % BK == 0 && (k * cin_g) % (2 * BK) == 0 && cout % BN == 0, CV3_EUNSUPPORTED,
+              "channels-last conv needs cin/groups %% 32 == 0, k*cin/groups %% 64 == 0, 64 outputs per group");
+  CV3_REQUIRE(((uintptr_t)x % 16 == 0) && ldx % 4 == 0 && ((uintptr_t)w % 16 == 0), CV3_EINVAL,
+              "channels-last conv operands must be 16-byte aligned");
+  CV3_REQUIRE(batch * t < (1ll << 31) && pad_l >= 0 && pad_l < k, CV3_EINVAL, "bad conv geometry");
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.b = w;
+  p.ldb = k * cin_g;
+  p.m = batch * t;
+  p.n = cout;
+  p.k = k * cin_g;
+  p.bias = bias;
+  p.c = y;
+  p.ldc = ldy;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  p.conv_t = (int)t;
+  p.conv_cg = (int)cin_g;
+  p.conv_pad = (int)pad_l;
+  const int64_t tiles_m = ceil_div(p.m, BM), tiles_n = cout / BN;
+  hipLaunchKernelGGL((k_gemm<B_F32, true, A_CONV>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, 1, 1,
+                     (int)tiles_m);
   CV3_LAUNCHED();
   return CV3_OK;
 }

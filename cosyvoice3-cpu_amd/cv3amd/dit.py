@@ -12,6 +12,7 @@ Layout in HBM (B = 2 for the CFG pair, T mel frames, D = 1024):
                          [q; k; v] order, biases likewise)
   * ``att`` [B*T, D]     attention output, heads interleaved as [T, H*dh]
   * ``ff``  [B*T, 2D]    GELU-tanh hidden
+  * ``z1``  [B*T, D]     first conv_pos output (channels-last like everything else)
   * ``mod`` [S, L]       every AdaLN modulation row of the solve, one per Euler step:
                          the time embedding depends only on t, so the S = 10 rows of
                          ``Linear(silu(temb))`` for all 22 blocks and ``norm_out`` are
@@ -177,7 +178,8 @@ class DeviceDiT:
             w = g(f"input_embed.conv_pos_embed.{c}.0.weight")
             if _is_q(w):
                 raise ValueError("conv_pos weights are float on this path")
-            self.conv_w.append(to_device(np.asarray(w, np.float32)))
+            # (cout, cin/groups, k) -> (cout, k, cin/groups): K-contiguous rows for the implicit GEMM
+            self.conv_w.append(to_device(np.ascontiguousarray(np.asarray(w, np.float32).transpose(0, 2, 1))))
             self.conv_b.append(to_device(np.asarray(g(f"input_embed.conv_pos_embed.{c}.0.bias"), np.float32)))
         mods = [g(f"transformer_blocks.{i}.attn_norm.linear.weight") for i in range(self.depth)]
         mods.append(g("norm_out.linear.weight"))
@@ -219,7 +221,7 @@ class DeviceDiT:
             self.qkvb = DeviceArray((B * T, 3 * D))
             self.att = DeviceArray((B * T, D))
             self.ffb = DeviceArray((B * T, self.ff_dim))
-            self.z1 = DeviceArray((D, T))
+            self.z1 = DeviceArray((B * T, D))
             self.outb = DeviceArray((B * T, mel))
             self.outT = DeviceArray((B, mel, T))
             self.x = DeviceArray((mel, T))
@@ -252,16 +254,14 @@ class DeviceDiT:
         _lib.call("copy_strided", self.x.ptr, self.inp.ptr, B, T, mel, S3(0, 1, T), S3(T * 4 * mel, 4 * mel, 1),
                   None)
         self.proj_in(self.inp.ptr, BT, 4 * mel, self.h.ptr, D)
-        # conv_pos: two grouped causal convs with Mish, read/written channels-last (dit.py:99-112)
+        # conv_pos: two grouped causal convs with Mish on channels-last [B*T, D] activations,
+        # the second adding the projection back in place (dit.py:99-112)
         k = self.conv_k
-        for b in range(B):
-            hb = self.h.ptr + b * T * D * f4
-            _lib.call("conv1d", hb, D, T, 1, D, self.conv_w[0].ptr, D, k, self.conv_b[0].ptr, 1, 1,
-                      self.conv_groups, k - 1, 0, 1, self.z1.ptr, T, 1, None, ACT["mish"], 0.0, None, 0.0,
-                      None, 0, 0, None)
-            _lib.call("conv1d", self.z1.ptr, D, T, T, 1, self.conv_w[1].ptr, D, k, self.conv_b[1].ptr, 1, 1,
-                      self.conv_groups, k - 1, 0, 1, hb, 1, D, None, ACT["mish"], 0.0, None, 0.0,
-                      hb, 1, D, None)
+        _lib.call("conv1d_cl", self.h.ptr, B, T, D, D, self.conv_w[0].ptr, D, k, self.conv_groups, k - 1,
+                  self.conv_b[0].ptr, self.z1.ptr, D, ctypes.byref(_lib.epilogue("mish")), None)
+        _lib.call("conv1d_cl", self.z1.ptr, B, T, D, D, self.conv_w[1].ptr, D, k, self.conv_groups, k - 1,
+                  self.conv_b[1].ptr, self.h.ptr, D,
+                  ctypes.byref(_lib.epilogue("mish", residual=self.h.ptr, ld_res=D)), None)
         mrow = self.mods.ptr + s * self.ld_mod * f4
         qs = S3(T * 3 * D, dh, 3 * D)
         os_ = S3(T * D, dh, D)

@@ -46,8 +46,8 @@ class Model(ctypes.Structure):
 
 class State(ctypes.Structure):
     _fields_ = [("k_cache", c_vp), ("v_cache", c_vp), ("cap", c_i64), ("pos", c_vp), ("token", c_vp),
-                ("history", c_vp), ("x", c_vp), ("attn", c_vp), ("logits", c_vp), ("workspace", c_vp),
-                ("workspace_floats", c_i64), ("counters", c_vp)]
+                ("history", c_vp), ("x", c_vp), ("logits", c_vp), ("workspace", c_vp),
+                ("workspace_floats", c_i64)]
 
 
 def rope_tables(dim: int, theta: float, n: int):
@@ -116,8 +116,8 @@ class DeviceQwen2:
         self.eps = float(m.get("rms_norm_eps", 1e-6))
         self.theta = float(m.get("rope_theta", 1e6))
         self.head_dim = self.hidden // self.heads
-        if cap % 64:
-            raise ValueError("cache capacity must be a multiple of 64")
+        if cap % 64 or cap > 1024:
+            raise ValueError("cache capacity must be a multiple of 64, at most 1024")
         self.cap = int(cap)
         body = prefix + "model."
         g = weights.get
@@ -150,14 +150,12 @@ class DeviceQwen2:
         self.v_cache = DeviceArray(cache_shape).zero_()
         self.ints = DeviceArray((2 + self.cap,), np.int64).zero_()   # pos, token, history[cap]
         self.x = DeviceArray((self.hidden,))
-        self.attn = DeviceArray((self.heads * self.head_dim,))
         self.logits = DeviceArray((self.vocab,))
-        nws = self.heads * self.head_dim + self.heads * (self.cap // 64) * (self.head_dim + 2) + self.inter
+        nws = 1024 + self.heads * 16 * 64 + self.heads * 16 * 2 + self.inter + 64
         self.workspace = DeviceArray((nws,))
-        self.counters = DeviceArray((max(self.kv_heads, 1),), np.uint32).zero_()
         p0 = self.ints.ptr
         self.state = State(self.k_cache.ptr, self.v_cache.ptr, self.cap, p0, p0 + 8, p0 + 16, self.x.ptr,
-                           self.attn.ptr, self.logits.ptr, self.workspace.ptr, nws, self.counters.ptr)
+                           self.logits.ptr, self.workspace.ptr, nws)
         self._graph: Optional[Graph] = None
         self._pos_host = 0
 

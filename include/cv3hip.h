@@ -176,6 +176,15 @@ int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t 
                int64_t pad_r, int64_t up, float* y, int64_t y_cs, int64_t y_ts, int64_t* t_out_ptr, int act,
                float act_param, const float* snake_alpha, float snake_eps, const float* residual, int64_t r_cs,
                int64_t r_ts, cv3_stream_t s);
+/* The DiT's grouped causal conv_pos (dit.py:99-112, ops.conv1d with groups) on channels-last activations:
+ * x [batch, t, ldx] (cin channels), y [batch, t, ldy] (cout channels),
+ * y[b, s, co] = epi(bias[co] + sum_{j<k, c<cin/groups} W[co, c, j] x[b, s + j - pad_l, g*cin/groups + c]),
+ * g = co / (cout/groups), zero outside [0, t); output length t (pad_r = k - 1 - pad_l).  w_packed is W
+ * (cout, cin/groups, k) repacked as (cout, k, cin/groups).  Needs 64 output channels per group,
+ * cin/groups % 32 == 0 and k*cin/groups % 64 == 0 (else CV3_EUNSUPPORTED); epilogue as for linears. */
+int cv3_conv1d_cl(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t ldx, const float* w_packed,
+                  int64_t cout, int64_t k, int64_t groups, int64_t pad_l, const float* bias, float* y, int64_t ldy,
+                  const cv3_epilogue* epi, cv3_stream_t s);
 int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,
                          int64_t dilation, int64_t pad_l, int64_t pad_r, float* y, int64_t* t_out_ptr,
                          cv3_stream_t s);
@@ -222,8 +231,9 @@ typedef struct {
 /* Device state of one decode stream.  k_cache / v_cache [layers, kv_heads, cap, head_dim] (the KVCache of
  * qwen2.py:74-121); pos = position of the current input token; token = last selected id; history [cap]
  * receives each selected id at its input position; x [hidden] is the residual stream and holds the
- * current input embedding between steps; attn [heads*head_dim]; logits [vocab]; workspace of at least
- * heads*dh + heads*(cap/64)*(dh+2) + inter floats; counters [kv_heads] zeroed once before the first step. */
+ * current input embedding between steps; logits [vocab]; workspace of at least
+ * 1024 + heads*16*64 + heads*16*2 + inter + 64 floats.
+ * cap <= 1024, heads <= 16, head_dim <= 64. */
 typedef struct {
   float* k_cache;
   float* v_cache;
@@ -232,11 +242,9 @@ typedef struct {
   int64_t* token;
   int64_t* history;
   float* x;
-  float* attn;
   float* logits;
   float* workspace;
   int64_t workspace_floats;
-  unsigned* counters;
 } cv3_qwen2_state;
 
 /* One greedy token: Qwen2Model.forward on x at position pos (qwen2.py:139-179), llm_decoder head

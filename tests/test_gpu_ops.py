@@ -123,7 +123,8 @@ def test_dequant_rows(dev):
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 64, 1000])
-@pytest.mark.parametrize("k,n", [(896, 1152), (1024, 6144), (257, 130), (320, 1024), (9, 1), (2048, 80)])
+@pytest.mark.parametrize("k,n", [(896, 1152), (1024, 6144), (257, 130), (320, 1024), (9, 1), (2048, 80),
+                                 (64, 96), (128, 200)])
 def test_linear_f32(dev, rng, m, k, n):
     ops, _ = dev
     x = rng.normal(size=(m, k)).astype(np.float32)
@@ -258,3 +259,27 @@ def test_interpolation(dev, rng):
     for size, ac in ((100, False), (20, False), (100, True)):
         assert rel_err(ops.interpolate_linear(x, size, ac), ref.interpolate_linear(x, size, ac)) < TOL
     assert np.array_equal(ops.interpolate_nearest(x, 3), ref.interpolate_nearest(x, 3))
+
+
+@pytest.mark.parametrize("T,k,cin,groups", [(500, 31, 1024, 16), (37, 31, 1024, 16), (70, 5, 256, 4)])
+def test_conv1d_channels_last(dev, rng, T, k, cin, groups):
+    """The DiT conv_pos path: grouped causal conv on [batch, time, channel] activations
+    against the oracle's (channel, time) conv1d, per batch row, with the Mish + residual epilogue."""
+    import ctypes
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray, to_device
+    B, cout = 2, cin
+    x = rng.normal(size=(B, T, cin)).astype(np.float32)
+    w = (rng.normal(size=(cout, cin // groups, k)) * 0.02).astype(np.float32)
+    b = (rng.normal(size=cout) * 0.02).astype(np.float32)
+    res = rng.normal(size=(B, T, cout)).astype(np.float32)
+    want = np.stack([ref.mish(ref.conv1d(np.ascontiguousarray(x[i].T), w, b, groups=groups, pad=(k - 1, 0))).T
+                     + res[i] for i in range(B)])
+    xd = to_device(x)
+    wd = to_device(np.ascontiguousarray(w.transpose(0, 2, 1)))
+    bd = to_device(b)
+    yd = to_device(res)
+    epi = _lib.epilogue("mish", residual=yd.ptr, ld_res=cout)
+    _lib.call("conv1d_cl", xd.ptr, B, T, cin, cin, wd.ptr, cout, k, groups, k - 1, bd.ptr, yd.ptr, cout,
+              ctypes.byref(epi), None)
+    assert rel_err(yd.numpy(), want) < TOL
