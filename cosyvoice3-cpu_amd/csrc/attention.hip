@@ -54,15 +54,22 @@ __device__ __forceinline__ void visible_keys(const AttnParams& p, int64_t qi, in
 constexpr int KT = 64;        // keys per LDS tile
 constexpr int KS = 68;        // LDS row stride (floats) for K and V tiles
 constexpr int QW = 16;        // queries per wave
-constexpr int WAVES = 4;      // waves per workgroup
+constexpr int QT = 64;        // queries per workgroup
 
-__global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
-  __shared__ float Ks[KT * KS];
-  __shared__ float Vs[KT * KS];
+// 8 waves: wave w takes queries (w % 4) * 16 .. +15 of the workgroup's 64 and key
+// group kg = w / 4.  Each stage stages 2 tiles of 64 keys; key group kg works on
+// tile 2 * stage + kg, so every SIMD runs two waves (one per key group) and the
+// key range is split between them.  Each wave keeps its own online softmax
+// (max, sum, output) and the two groups merge in LDS at the end:
+//   M = max(m0, m1), l = l0 e^{m0-M} + l1 e^{m1-M}, o = o0 e^{m0-M} + o1 e^{m1-M}.
+__global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
+  __shared__ float Ks[2][KT * KS];
+  __shared__ float Vs[2][KT * KS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qw = wave & 3, kg = wave >> 2;
   const int b = blockIdx.z, hq = blockIdx.y;
   const int hkv = hq / (p.h / p.hk);
-  const int64_t q0 = (int64_t)blockIdx.x * (QW * WAVES) + wave * QW;
+  const int64_t q0 = (int64_t)blockIdx.x * QT + qw * QW;
   const int c16 = lane & 15, g = lane >> 4;
   const int64_t qi = q0 + c16;
   const bool qvalid = qi < p.n;
@@ -85,17 +92,18 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
 
   const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  const int64_t ntiles = ceil_div(p.m, KT);
-  // The next tile's K/V rows are loaded into registers while the current tile is
-  // computed.  Rows past m are clamped to m - 1 (always in bounds); their scores
+  const int64_t nstages = ceil_div(p.m, 2 * KT);
+  // The next stage's 128 K/V rows are loaded into registers while the current stage
+  // is computed.  Rows past m are clamped to m - 1 (always in bounds); their scores
   // are masked to -inf below, so the loads carry no predicates.
-  // thread -> keys tid/16 + 16r (r < 4), dims (tid%16)*4 .. +3
-  const int lkey = tid >> 4, ld4 = (tid & 15) * 4;
+  // thread -> tile tid/256, keys (tid%256)/16 + 16r (r < 4), dims (tid%16)*4 .. +3
+  const int ltile = tid >> 8, lkey = (tid & 255) >> 4, ld4 = (tid & 15) * 4;
   float4 k0r, k1r, k2r, k3r, v0r, v1r, v2r, v3r;
 #define CV3_KV_LOAD(KOFF)                                                                        \
   {                                                                                              \
-    const int64_t j0 = min((KOFF) + lkey, p.m - 1), j1 = min((KOFF) + lkey + 16, p.m - 1);      \
-    const int64_t j2 = min((KOFF) + lkey + 32, p.m - 1), j3 = min((KOFF) + lkey + 48, p.m - 1); \
+    const int64_t kb0 = (KOFF) + ltile * KT + lkey;                                              \
+    const int64_t j0 = min(kb0, p.m - 1), j1 = min(kb0 + 16, p.m - 1);                           \
+    const int64_t j2 = min(kb0 + 32, p.m - 1), j3 = min(kb0 + 48, p.m - 1);                      \
     k0r = *reinterpret_cast<const float4*>(kbase + j0 * p.k_sm + ld4);                           \
     k1r = *reinterpret_cast<const float4*>(kbase + j1 * p.k_sm + ld4);                           \
     k2r = *reinterpret_cast<const float4*>(kbase + j2 * p.k_sm + ld4);                           \
@@ -106,26 +114,30 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
     v3r = *reinterpret_cast<const float4*>(vbase + j3 * p.v_sm + ld4);                           \
   }
   CV3_KV_LOAD((int64_t)0)
-  for (int64_t kt = 0; kt < ntiles; ++kt) {
-    const int64_t k0 = kt * KT;
+  for (int64_t st = 0; st < nstages; ++st) {
+    const int64_t k0 = st * 2 * KT + kg * KT;  // first key of this wave's tile
     __syncthreads();
-    *reinterpret_cast<float4*>(&Ks[lkey * KS + ld4]) = k0r;
-    *reinterpret_cast<float4*>(&Ks[(lkey + 16) * KS + ld4]) = k1r;
-    *reinterpret_cast<float4*>(&Ks[(lkey + 32) * KS + ld4]) = k2r;
-    *reinterpret_cast<float4*>(&Ks[(lkey + 48) * KS + ld4]) = k3r;
-    *reinterpret_cast<float4*>(&Vs[lkey * KS + ld4]) = v0r;
-    *reinterpret_cast<float4*>(&Vs[(lkey + 16) * KS + ld4]) = v1r;
-    *reinterpret_cast<float4*>(&Vs[(lkey + 32) * KS + ld4]) = v2r;
-    *reinterpret_cast<float4*>(&Vs[(lkey + 48) * KS + ld4]) = v3r;
+    float* kt_ = Ks[ltile];
+    float* vt_ = Vs[ltile];
+    *reinterpret_cast<float4*>(&kt_[lkey * KS + ld4]) = k0r;
+    *reinterpret_cast<float4*>(&kt_[(lkey + 16) * KS + ld4]) = k1r;
+    *reinterpret_cast<float4*>(&kt_[(lkey + 32) * KS + ld4]) = k2r;
+    *reinterpret_cast<float4*>(&kt_[(lkey + 48) * KS + ld4]) = k3r;
+    *reinterpret_cast<float4*>(&vt_[lkey * KS + ld4]) = v0r;
+    *reinterpret_cast<float4*>(&vt_[(lkey + 16) * KS + ld4]) = v1r;
+    *reinterpret_cast<float4*>(&vt_[(lkey + 32) * KS + ld4]) = v2r;
+    *reinterpret_cast<float4*>(&vt_[(lkey + 48) * KS + ld4]) = v3r;
     __syncthreads();
-    if (kt + 1 < ntiles) CV3_KV_LOAD(k0 + KT)
-    __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this tile's math
+    if (st + 1 < nstages) CV3_KV_LOAD((st + 1) * 2 * KT)
+    __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this stage's math
+    const float* Kt = Ks[kg];
+    const float* Vt = Vs[kg];
 
 #pragma unroll
     for (int sub = 0; sub < KT / 16; ++sub) {
       // S^T tile: rows = 16 keys, cols = 16 queries
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float* krow = &Ks[(sub * 16 + c16) * KS + g * 4];
+      const float* krow = &Kt[(sub * 16 + c16) * KS + g * 4];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const float4 kf = *reinterpret_cast<const float4*>(krow + s4 * 16);
@@ -166,13 +178,36 @@ __global__ __launch_bounds__(256) void k_flash64(AttnParams p) {
         oacc[db] *= alpha;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float vf = Vs[(sub * 16 + 4 * g + i) * KS + db * 16 + c16];
+          const float vf = Vt[(sub * 16 + 4 * g + i) * KS + db * 16 + c16];
           oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, sc[i], oacc[db], 0, 0, 0);
         }
       }
     }
   }
 #undef CV3_KV_LOAD
+  // merge the two key groups through LDS (each lane's state is per query column)
+  __syncthreads();
+  float* mb = &Ks[0][0];  // 4 waves x 64 lanes x 18 floats = 4608 <= 2 * 64 * 68
+  float* slot = mb + (qw * 64 + lane) * 18;
+  if (kg == 1) {
+    slot[0] = m_run;
+    slot[1] = l_run;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) slot[2 + db * 4 + i] = oacc[db][i];
+  }
+  __syncthreads();
+  if (kg == 1) return;
+  const float m1 = slot[0], l1 = slot[1];
+  const float M = fmaxf(m_run, m1);
+  const float a0 = M == -INFINITY ? 1.f : expf(m_run - M);
+  const float a1 = M == -INFINITY ? 0.f : expf(m1 - M);
+  l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) oacc[db][i] = oacc[db][i] * a0 + slot[2 + db * 4 + i] * a1;
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (!qvalid) return;
@@ -276,8 +311,8 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
                          (p.k_sh % 4 == 0) && (p.k_sm % 4 == 0) && (p.v_sb % 4 == 0) && (p.v_sh % 4 == 0) &&
                          (p.v_sm % 4 == 0);
   if (d == 64 && aligned16) {
-    const dim3 grid((unsigned)ceil_div(n, QW * WAVES), (unsigned)h, (unsigned)batch);
-    hipLaunchKernelGGL(k_flash64, grid, dim3(256), 0, st, p);
+    const dim3 grid((unsigned)ceil_div(n, QT), (unsigned)h, (unsigned)batch);
+    hipLaunchKernelGGL(k_flash64, grid, dim3(512), 0, st, p);
   } else {
     const dim3 grid((unsigned)ceil_div(n, 4), (unsigned)h, (unsigned)batch);
     hipLaunchKernelGGL(k_attn_generic, grid, dim3(256), 4 * d * sizeof(float), st, p);

@@ -183,6 +183,22 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int 
   }
 }
 
+// DiT partial rotary applied in the epilogue (dit.py:40-54): columns c < rope_limit with
+// c % rope_period < rope_width are interleaved pairs (2i, 2i+1) -> (a cos - b sin, b cos + a sin),
+// table row = row % rope_rows.  The pair partner of column c is held by lane ^ 1.
+__device__ __forceinline__ float rope_epilogue(const cv3_epilogue& e, float v, int64_t row, int64_t col) {
+  const float other = __shfl_xor(v, 1, 64);
+  const int64_t cc = col % e.rope_period;
+  if (col < e.rope_limit && cc < e.rope_width) {
+    const int64_t ti = (row % e.rope_rows) * e.rope_width + cc;
+    const float c = e.rope_cos[ti], sn = e.rope_sin[ti];
+    v = (col & 1) ? v * c + other * sn : v * c + (-other) * sn;
+  }
+  return v;
+}
+
+// The GEMM kernel: 4 waves, 64 x 64 tile.  FAST (K % 64 == 0, aligned rows):
+// branch-free loads two stages ahead; otherwise one stage of guarded prefetch.
 template <int BK_KIND, bool FAST, int AMODE = A_ROWS>
 __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast_b, int tiles_m) {
   __shared__ float As[2][BM * LDS_STRIDE];
@@ -271,18 +287,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
 
   // accumulator layout (32x32x2 f32): reg i -> row (i/4)*8 + h*4 + i%4, col = lane%32
   const int64_t col = n0 + wn + r32;
-  if (col >= p.n) return;
-  const float bv = p.bias ? p.bias[col] : 0.f;
+  const float bv = (p.bias && col < p.n) ? p.bias[col] : 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t row = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
-    if (row < p.m) {
-      float v = acc[i] + bv;
+    float v = acc[i] + bv;
+    if (p.epi.rope_cos) v = rope_epilogue(p.epi, v, row, col);  // uniform branch, shuffles inside
+    if (row < p.m && col < p.n) {
       v = apply_epilogue(p.epi, v, row, col, false);
       p.c[row * p.ldc + col] = v;
     }
   }
 }
+
 
 }  // namespace
 
@@ -316,6 +333,7 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   p.conv_t = p.conv_cg = p.conv_pad = 0;
   // the branch-free kernel: whole K stages and aligned rows for both operands
   const bool fast = fast_a && fast_b && k % (2 * BK) == 0;
+  CV3_REQUIRE(fast || !p.epi.rope_cos, CV3_EUNSUPPORTED, "rotary epilogue needs aligned rows and K %% 64 == 0");
   if (q8) {
     if (fast)
       hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);

@@ -24,7 +24,8 @@ int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const floa
               "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
   if (!m || !n) return CV3_OK;
   hipStream_t st = stream_of(s);
-  if (m <= kGemvRows)
+  const bool rope = epi && epi->rope_cos;  // the rotary epilogue lives in the GEMM only
+  if (m <= kGemvRows && !rope)
     return gemv(0, false, false, x, m, k, ldx, w, ldw * 4, nullptr, 1, k, n, bias, y, ldy, epi, nullptr, 0.f, st);
   return gemm(false, x, m, k, ldx, w, ldw, nullptr, false, 1, k, n, bias, y, ldy, epi, st);
 }
@@ -40,8 +41,10 @@ int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, co
   hipStream_t st = stream_of(s);
   const bool sf16 = scale_dtype == CV3_F16;
   const int64_t nb = kp / block;
+  const bool rope = epi && epi->rope_cos;
+  CV3_REQUIRE(!rope || kind == CV3_KIND_Q8, CV3_EUNSUPPORTED, "rotary epilogue on q4 weights");
   if (kind == CV3_KIND_Q8) {
-    if (m <= kGemvRows)
+    if (m <= kGemvRows && !rope)
       return gemv(1, sf16, false, x, m, k, ldx, q, kp, scales, nb, block, n, bias, y, ldy, epi, nullptr, 0.f, st);
     return gemm(true, x, m, k, ldx, q, kp, scales, sf16, nb, block, n, bias, y, ldy, epi, st);
   }

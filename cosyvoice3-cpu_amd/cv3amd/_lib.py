@@ -34,7 +34,9 @@ class Epilogue(ctypes.Structure):
     _fields_ = [("act", ctypes.c_int), ("act_param", ctypes.c_float),
                 ("residual", ctypes.c_void_p), ("ld_res", ctypes.c_int64),
                 ("gate", ctypes.c_void_p), ("gate_stride", ctypes.c_int64),
-                ("rows_per_gate", ctypes.c_int64)]
+                ("rows_per_gate", ctypes.c_int64),
+                ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_rows", ctypes.c_int64),
+                ("rope_period", ctypes.c_int64), ("rope_width", ctypes.c_int64), ("rope_limit", ctypes.c_int64)]
 
 
 _SCALARS = {
@@ -134,9 +136,11 @@ def device_info():
 
 
 def epilogue(act: str = "none", act_param: float = 0.0, residual=None, ld_res: int = 0,
-             gate=None, gate_stride: int = 0, rows_per_gate: int = 0):
-    """Build a ``cv3_epilogue`` (pointers are ints or None)."""
-    return Epilogue(ACT[act], act_param, residual, ld_res, gate, gate_stride, rows_per_gate)
+             gate=None, gate_stride: int = 0, rows_per_gate: int = 0, rope=None):
+    """Build a ``cv3_epilogue`` (pointers are ints or None).  ``rope`` is
+    ``(cos_ptr, sin_ptr, rows, period, width, limit)`` for the fused DiT rotary."""
+    r = rope or (None, None, 0, 1, 0, 0)
+    return Epilogue(ACT[act], act_param, residual, ld_res, gate, gate_stride, rows_per_gate, *r)
 
 
 def ptr(obj) -> int:

@@ -9,7 +9,8 @@ the reference's own float32 expressions) are prepared on the host.
 Layout in HBM (B = 2 for the CFG pair, T mel frames, D = 1024):
   * ``h``   [B*T, D]     the residual stream, updated in place by the GEMM epilogues
   * ``qkv`` [B*T, 3D]    fused q|k|v projection (weights concatenated row-wise in
-                         [q; k; v] order, biases likewise)
+                         [q; k; v] order, biases likewise), the partial rotary of q
+                         and k applied in the GEMM's epilogue
   * ``att`` [B*T, D]     attention output, heads interleaved as [T, H*dh]
   * ``ff``  [B*T, 2D]    GELU-tanh hidden
   * ``z1``  [B*T, D]     first conv_pos output (channels-last like everything else)
@@ -24,7 +25,7 @@ Work per Euler step, in order (reference lines in brackets):
   pack x into the [x | cond | mu | spk] input  (dit.py:92-97, flow.py:72-84)
   input projection GEMM                        (dit.py:98)
   two grouped causal convs + Mish, residual    (dit.py:99-112)
-  22 x [ LayerNorm+AdaLN -> QKV GEMM -> partial rotary on q,k -> attention ->
+  22 x [ LayerNorm+AdaLN -> QKV GEMM with partial rotary on q,k -> attention ->
          out GEMM with gate*y + h epilogue -> LayerNorm+AdaLN -> FF1 GEMM with
          GELU-tanh -> FF2 GEMM with gate*y + h ]  (dit.py:114-173)
   LayerNorm + (scale, shift) -> proj_out GEMM  (dit.py:175-180)
@@ -264,16 +265,15 @@ class DeviceDiT:
                   ctypes.byref(_lib.epilogue("mish", residual=self.h.ptr, ld_res=D)), None)
         mrow = self.mods.ptr + s * self.ld_mod * f4
         qs = S3(T * 3 * D, dh, 3 * D)
+        rope_epi = _lib.epilogue(rope=(self.cos.ptr, self.sin.ptr, T, D, dh, 2 * D))
         os_ = S3(T * D, dh, D)
         scale = float(np.float32(1.0 / math.sqrt(dh)))
         for i in range(self.depth):
             base = mrow + i * 6 * D * f4
             sh_a, sc_a, g_a, sh_m, sc_m, g_m = (base + j * D * f4 for j in range(6))
             _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_a, sc_a, 0, 0, None)
-            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D)
-            for off in (0, D):   # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120)
-                _lib.call("rope_pairs", self.qkvb.ptr + off * f4, 3 * D, BT, T, dh, self.cos.ptr, self.sin.ptr,
-                          None)
+            # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120), in the GEMM epilogue
+            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D, rope_epi)
             _lib.call("attention", self.qkvb.ptr, self.qkvb.ptr + D * f4, self.qkvb.ptr + 2 * D * f4,
                       self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None)
             self.out[i](self.att.ptr, BT, D, self.h.ptr, D,

@@ -47,8 +47,11 @@ enum {
 };
 
 /*
- * Linear epilogue: y = residual + gate * act(acc + bias)
+ * Linear epilogue: y = residual + gate * act(rope(acc + bias))
  *   residual: [m, ld_res] or NULL (0);  gate: gate[(row / rows_per_gate) * gate_stride + col] or NULL (1).
+ *   rope (multi-row GEMMs only, rope_cos non-NULL): the DiT's interleaved partial rotary (dit.py:40-54) on
+ *   columns c < rope_limit with c % rope_period < rope_width, using table row (row % rope_rows) of
+ *   rope_cos / rope_sin [rope_rows, rope_width].
  * `y` may alias `residual` (each element is read and written by one thread).
  */
 typedef struct {
@@ -59,6 +62,9 @@ typedef struct {
   const float* gate;
   int64_t gate_stride;
   int64_t rows_per_gate;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_rows, rope_period, rope_width, rope_limit;
 } cv3_epilogue;
 
 /* ---------------- runtime ---------------- */
