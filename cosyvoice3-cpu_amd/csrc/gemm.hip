@@ -127,39 +127,53 @@ __device__ __forceinline__ float4 load_a(const GemmParams& p, int64_t row, int64
 // M / N are clamped to the last row (their results are never stored), so the
 // loads carry no predicates and the compiler can count them (vmcnt) across the
 // two-stage pipeline.
+// B row pointer of the FAST kernels: thread's row `row`, k offset lk folded in.
+struct BRow {
+  const void* codes;   // float* or int8_t* at (row, lk)
+  const void* scales;  // q8: the row's scales
+  int lk;
+};
+
 template <int BK_KIND>
-__device__ __forceinline__ float4 load_b_fast(const GemmParams& p, int64_t row, int64_t kk) {
+__device__ __forceinline__ BRow b_row(const GemmParams& p, int64_t row, int lk) {
+  BRow r;
   if constexpr (BK_KIND == B_F32) {
-    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.b) + row * p.ldb + kk);
+    r.codes = reinterpret_cast<const float*>(p.b) + row * p.ldb + lk;
+    r.scales = nullptr;
   } else {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(p.b) + row * p.ldb + kk);
-    const int64_t si = row * p.nb + (int64_t)((uint32_t)kk / (uint32_t)p.block);
-    const float s = p.sf16 ? __half2float(reinterpret_cast<const __half*>(p.scales)[si])
-                           : reinterpret_cast<const float*>(p.scales)[si];
+    r.codes = reinterpret_cast<const int8_t*>(p.b) + row * p.ldb + lk;
+    r.scales = p.sf16 ? (const void*)(reinterpret_cast<const __half*>(p.scales) + row * p.nb)
+                      : (const void*)(reinterpret_cast<const float*>(p.scales) + row * p.nb);
+  }
+  r.lk = lk;
+  return r;
+}
+
+template <int BK_KIND>
+__device__ __forceinline__ float4 load_b_fast(const GemmParams& p, const BRow& r, int64_t koff) {
+  if constexpr (BK_KIND == B_F32) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(r.codes) + koff);
+  } else {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(r.codes) + koff);
+    const uint32_t si = ((uint32_t)koff + (uint32_t)r.lk) / (uint32_t)p.block;
+    const float s = p.sf16 ? __half2float(reinterpret_cast<const __half*>(r.scales)[si])
+                           : reinterpret_cast<const float*>(r.scales)[si];
     return make_float4((float)((int32_t)(w << 24) >> 24) * s, (float)((int32_t)(w << 16) >> 24) * s,
                        (float)((int32_t)(w << 8) >> 24) * s, (float)((int32_t)w >> 24) * s);
   }
 }
 
-// thread -> rows lrow and lrow + 32 of the A and B tiles, 4 consecutive k at lk
-template <int BK_KIND, bool FAST>
+// General-kernel loads: thread -> rows lrow and lrow + 32 of the A and B tiles,
+// 4 consecutive k at lk, every element guarded.
+template <int BK_KIND>
 __device__ __forceinline__ void load_stage(const GemmParams& p, int64_t m0, int64_t n0, int64_t k0, int lrow, int lk,
                                            bool fa, bool fb, Stage& st) {
   const int64_t kk = k0 + lk;
-  if constexpr (FAST) {
-    const int64_t ra0 = min(m0 + lrow, p.m - 1), ra1 = min(m0 + lrow + 32, p.m - 1);
-    const int64_t rb0 = min(n0 + lrow, p.n - 1), rb1 = min(n0 + lrow + 32, p.n - 1);
-    st.a0 = *reinterpret_cast<const float4*>(p.a + ra0 * p.lda + kk);
-    st.a1 = *reinterpret_cast<const float4*>(p.a + ra1 * p.lda + kk);
-    st.b0 = load_b_fast<BK_KIND>(p, rb0, kk);
-    st.b1 = load_b_fast<BK_KIND>(p, rb1, kk);
-  } else {
-    const bool kfull = kk + 4 <= p.k;
-    st.a0 = load_a(p, m0 + lrow, kk, fa && kfull);
-    st.a1 = load_a(p, m0 + lrow + 32, kk, fa && kfull);
-    st.b0 = load_b<BK_KIND>(p, n0 + lrow, kk, fb && kfull);
-    st.b1 = load_b<BK_KIND>(p, n0 + lrow + 32, kk, fb && kfull);
-  }
+  const bool kfull = kk + 4 <= p.k;
+  st.a0 = load_a(p, m0 + lrow, kk, fa && kfull);
+  st.a1 = load_a(p, m0 + lrow + 32, kk, fa && kfull);
+  st.b0 = load_b<BK_KIND>(p, n0 + lrow, kk, fb && kfull);
+  st.b1 = load_b<BK_KIND>(p, n0 + lrow + 32, kk, fb && kfull);
 }
 
 __device__ __forceinline__ void store_stage(float* As, float* Bs, int lrow, int lk, const Stage& st) {
@@ -219,7 +233,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
     // S even and >= 2 (K % 64 == 0): straight-line ping-pong between two register
     // sets (x0 / x1: A rows lrow, lrow + 32 and B rows lrow, lrow + 32), no predicates
     const int64_t ra0 = min(m0 + lrow, p.m - 1), ra1 = min(m0 + lrow + 32, p.m - 1);
-    const int64_t rb0 = min(n0 + lrow, p.n - 1), rb1 = min(n0 + lrow + 32, p.n - 1);
+    const BRow rb0 = b_row<BK_KIND>(p, min(n0 + lrow, p.n - 1), lk);
+    const BRow rb1 = b_row<BK_KIND>(p, min(n0 + lrow + 32, p.n - 1), lk);
     const float* pa0;
     const float* pa1;
     int t0 = 0, t1 = 0;
@@ -239,8 +254,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
 #define CV3_LOAD(A0, A1, B0, B1, KOFF)                                   \
   A0 = load_a_fast<AMODE>(p, pa0, t0, (KOFF));                           \
   A1 = load_a_fast<AMODE>(p, pa1, t1, (KOFF));                           \
-  B0 = load_b_fast<BK_KIND>(p, rb0, (KOFF) + lk);                        \
-  B1 = load_b_fast<BK_KIND>(p, rb1, (KOFF) + lk);
+  B0 = load_b_fast<BK_KIND>(p, rb0, (KOFF));                             \
+  B1 = load_b_fast<BK_KIND>(p, rb1, (KOFF));
 #define CV3_STORE(BUF, A0, A1, B0, B1)                                               \
   *reinterpret_cast<float4*>(&As[BUF][lrow * LDS_STRIDE + lk]) = A0;                 \
   *reinterpret_cast<float4*>(&As[BUF][(lrow + 32) * LDS_STRIDE + lk]) = A1;          \
@@ -273,12 +288,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
   } else {
     // ragged K / unaligned rows: one stage of register prefetch, guarded loads
     Stage r0;
-    load_stage<BK_KIND, FAST>(p, m0, n0, 0, lrow, lk, fa, fb, r0);
+    load_stage<BK_KIND>(p, m0, n0, 0, lrow, lk, fa, fb, r0);
     store_stage(As[0], Bs[0], lrow, lk, r0);
     __syncthreads();
     for (int64_t s = 0; s < S; ++s) {
       const int buf = s & 1;
-      if (s + 1 < S) load_stage<BK_KIND, FAST>(p, m0, n0, (s + 1) * BK, lrow, lk, fa, fb, r0);
+      if (s + 1 < S) load_stage<BK_KIND>(p, m0, n0, (s + 1) * BK, lrow, lk, fa, fb, r0);
       mma_stage(As[buf], Bs[buf], wm, wn, r32, h, acc);
       if (s + 1 < S) store_stage(As[buf ^ 1], Bs[buf ^ 1], lrow, lk, r0);
       __syncthreads();
@@ -300,6 +315,108 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
   }
 }
 
+
+
+// Half of a stage's MFMAs: k groups 2*kh and 2*kh + 1 of the 4 in a BK = 32 stage.
+__device__ __forceinline__ void mma_half(const float* As, const float* Bs, int wm, int wn, int r32, int h, int kh,
+                                         f32x16& acc) {
+  const float* as = &As[(wm + r32) * LDS_STRIDE + h * 4 + kh * 16];
+  const float* bs = &Bs[(wn + r32) * LDS_STRIDE + h * 4 + kh * 16];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const float4 av = *reinterpret_cast<const float4*>(as + g * 8);
+    const float4 bv = *reinterpret_cast<const float4*>(bs + g * 8);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+  }
+}
+
+// The FAST kernel with 8 waves, for grids of at most one workgroup per CU (e.g.
+// [1000, 1024] outputs): waves q and q + 4 share output quadrant q and split each
+// stage's K between them (k groups 0-1 / 2-3), so two waves per SIMD keep the
+// matrix core busy while the other waits on LDS or the barrier.  The halves meet
+// in LDS at the end.  One A and one B float4 per thread per stage.
+template <int BK_KIND, int AMODE>
+__global__ __launch_bounds__(512) void k_gemm8(GemmParams p, int tiles_m) {
+  __shared__ float As[2][BM * LDS_STRIDE];
+  __shared__ float Bs[2][BN * LDS_STRIDE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  const int lrow = tid >> 3, lk = (tid & 7) * 4;
+  const int quad = wave & 3, kh = wave >> 2;
+  const int wm = (quad >> 1) * 32, wn = (quad & 1) * 32;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int64_t S = p.k / BK;  // even, >= 2
+  const int64_t ra = min(m0 + lrow, p.m - 1);
+  const BRow rb = b_row<BK_KIND>(p, min(n0 + lrow, p.n - 1), lk);
+  const float* pa;
+  int t0 = 0;
+  if constexpr (AMODE == A_ROWS) {
+    pa = p.a + ra * p.lda + lk;
+  } else {
+    const int64_t cbase = (n0 / BN) * p.conv_cg;
+    const int b0 = (int)ra / p.conv_t;
+    t0 = (int)ra - b0 * p.conv_t;
+    pa = p.a + (int64_t)b0 * p.conv_t * p.lda + cbase + lk;
+  }
+  f32x16 acc = {0.f};
+  float4 xa, xb, ya, yb;
+#define CV3_LOAD8(A, B, KOFF)                  \
+  A = load_a_fast<AMODE>(p, pa, t0, (KOFF));   \
+  B = load_b_fast<BK_KIND>(p, rb, (KOFF));
+#define CV3_STORE8(BUF, A, B)                                          \
+  *reinterpret_cast<float4*>(&As[BUF][lrow * LDS_STRIDE + lk]) = A;    \
+  *reinterpret_cast<float4*>(&Bs[BUF][lrow * LDS_STRIDE + lk]) = B;
+  CV3_LOAD8(xa, xb, 0)
+  CV3_LOAD8(ya, yb, BK)
+  CV3_STORE8(0, xa, xb)
+  __syncthreads();
+  for (int64_t s = 0; s + 2 < S; s += 2) {
+    CV3_LOAD8(xa, xb, (s + 2) * BK)
+    __builtin_amdgcn_sched_barrier(0);
+    mma_half(As[0], Bs[0], wm, wn, r32, h, kh, acc);
+    CV3_STORE8(1, ya, yb)
+    __syncthreads();
+    CV3_LOAD8(ya, yb, (s + 3) * BK)
+    __builtin_amdgcn_sched_barrier(0);
+    mma_half(As[1], Bs[1], wm, wn, r32, h, kh, acc);
+    CV3_STORE8(0, xa, xb)
+    __syncthreads();
+  }
+  mma_half(As[0], Bs[0], wm, wn, r32, h, kh, acc);
+  CV3_STORE8(1, ya, yb)
+  __syncthreads();
+  mma_half(As[1], Bs[1], wm, wn, r32, h, kh, acc);
+#undef CV3_LOAD8
+#undef CV3_STORE8
+  // the K halves meet: waves 4..7 park their quadrant in LDS, waves 0..3 add it
+  __syncthreads();
+  float* red = &As[0][0];  // 4 quadrants x 16 regs x 64 lanes = 4096 floats
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(quad * 16 + i) * 64 + lane] = acc[i];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] += red[(quad * 16 + i) * 64 + lane];
+  const int64_t col = n0 + wn + r32;
+  const float bv = (p.bias && col < p.n) ? p.bias[col] : 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+    float v = acc[i] + bv;
+    if (p.epi.rope_cos) v = rope_epilogue(p.epi, v, row, col);  // uniform branch, shuffles inside
+    if (row < p.m && col < p.n) {
+      v = apply_epilogue(p.epi, v, row, col, false);
+      p.c[row * p.ldc + col] = v;
+    }
+  }
+}
 
 }  // namespace
 
@@ -334,13 +451,19 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   // the branch-free kernel: whole K stages and aligned rows for both operands
   const bool fast = fast_a && fast_b && k % (2 * BK) == 0;
   CV3_REQUIRE(fast || !p.epi.rope_cos, CV3_EUNSUPPORTED, "rotary epilogue needs aligned rows and K %% 64 == 0");
+  // at most one 64 x 64 tile per CU: the 8-wave kernel keeps two waves per SIMD
+  const bool small = tiles_m * tiles_n <= 256;
   if (q8) {
-    if (fast)
+    if (fast && small)
+      hipLaunchKernelGGL((k_gemm8<B_Q8, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
+    else if (fast)
       hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
     else
       hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
   } else {
-    if (fast)
+    if (fast && small)
+      hipLaunchKernelGGL((k_gemm8<B_F32, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
+    else if (fast)
       hipLaunchKernelGGL((k_gemm<B_F32, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
     else
       hipLaunchKernelGGL((k_gemm<B_F32, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
@@ -377,8 +500,12 @@ int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* 
   p.conv_cg = (int)cin_g;
   p.conv_pad = (int)pad_l;
   const int64_t tiles_m = ceil_div(p.m, BM), tiles_n = cout / BN;
-  hipLaunchKernelGGL((k_gemm<B_F32, true, A_CONV>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, 1, 1,
-                     (int)tiles_m);
+  if (tiles_m * tiles_n <= 256)
+    hipLaunchKernelGGL((k_gemm8<B_F32, A_CONV>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st, p,
+                       (int)tiles_m);
+  else
+    hipLaunchKernelGGL((k_gemm<B_F32, true, A_CONV>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, 1,
+                       1, (int)tiles_m);
   CV3_LAUNCHED();
   return CV3_OK;
 }
