@@ -63,6 +63,24 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def copy_bandwidth(nbytes: int = 256 << 20, reps: int = 10) -> float:
+    """Device-to-device copy rate (bytes/s) of one nbytes buffer: the achievable-HBM
+    reference next to the 8 TB/s peak, and the known-size kernel that scales the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray, Timer, synchronize
+    a = DeviceArray((nbytes // 4,)).zero_()
+    b = DeviceArray((nbytes // 4,))
+    _lib.call("copy_d2d", b.ptr, a.ptr, nbytes, None)
+    synchronize()
+    tm = Timer()
+    tm.start()
+    for _ in range(reps):
+        _lib.call("copy_d2d", b.ptr, a.ptr, nbytes, None)
+    ms = tm.stop() / reps
+    return 2.0 * nbytes / (ms / 1e3)
+
+
 def replayer(graph: bool, enqueue):
     """A callable that enqueues ``enqueue``'s launches: replayed from one captured HIP
     graph, or issued directly (the mode used under the kernel-trace profiler)."""
@@ -296,6 +314,8 @@ def main():
     info = _lib.device_info()
     log(f"device {info['arch']} with {info['cu_count']} CUs")
 
+    copy_bps = copy_bandwidth()
+    log(f"device copy: {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")
     t0 = time.time()
     lm_t, lm_meta = build_lm(args.layers, args.profile)
     log(f"LM weights ready ({time.time() - t0:.1f} s)")
@@ -351,6 +371,7 @@ def main():
                      "kernel": kern["name"], "bytes_per_launch": kern["bytes_per_launch"],
                      "us_per_launch": round(kern["us_per_launch"], 3)},
         "cpu_baseline": cpu,
+        "copy_GBps": round(copy_bps / 1e9, 1),
         "tokens_head": dec["tokens"][:8],
     }
     if flow is not None:
