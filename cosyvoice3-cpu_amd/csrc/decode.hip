@@ -72,85 +72,101 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ 
 }
 
 // Stage x[0:k) into LDS (zero padded to kx), optionally RMS-normalised with weight
-// rms_w: x * (1 / sqrt(mean(x^2) + eps)) * w (cv3cpu/ops.py:101-104).  Every
-// thread issues all of its float4 loads before using any of them (NV per thread,
-// unrolled), so the vector costs one memory latency, not one per loop trip.
+// rms_w: x * (1 / sqrt(mean(x^2) + eps)) * w (cv3cpu/ops.py:101-104).
+// load() issues every float4 load of this thread at once (NV per thread, clamped
+// indices, no predicates); kernels call it BEFORE issuing their weight stream,
+// because loads complete in issue order: a vector loaded after the weights would
+// wait for all of them.  finish() reduces, scales, writes LDS and synchronises.
 // Needs k % 4 == 0 and 16-byte aligned x / rms_w.
 template <int NV>
-__device__ void stage_vec(const float* __restrict__ x, int64_t k, int64_t kx, const float* __restrict__ rms_w,
-                          float eps, float* xs, float* red) {
-  const int64_t k4 = k / 4, n4 = kx / 4;
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  const float4* w4 = reinterpret_cast<const float4*>(rms_w);
+struct VecStage {
   float4 v[NV], w[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
-    v[i] = idx < k4 ? x4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-    w[i] = (rms_w && idx < k4) ? w4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  float inv = 1.f;
-  if (rms_w) {
-    float ss = 0.f;
+  __device__ __forceinline__ void load(const float* __restrict__ x, int64_t k, const float* __restrict__ rms_w) {
+    const int64_t k4 = k / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(rms_w ? rms_w : x);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      ss = fmaf(v[i].x, v[i].x, ss);
-      ss = fmaf(v[i].y, v[i].y, ss);
-      ss = fmaf(v[i].z, v[i].z, ss);
-      ss = fmaf(v[i].w, v[i].w, ss);
+      const int64_t idx = min((int64_t)threadIdx.x + (int64_t)i * blockDim.x, k4 - 1);
+      v[i] = x4[idx];
+      w[i] = w4[idx];
     }
-    ss = block_sum(ss, red);
-    inv = 1.0f / sqrtf(ss / (float)k + eps);
   }
+  __device__ __forceinline__ void finish(int64_t k, int64_t kx, bool rms, float eps, float* xs, float* red) {
+    const int64_t k4 = k / 4, n4 = kx / 4;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
-    if (idx < n4) {
-      float4 o = v[i];
-      if (rms_w) {
-        o.x = (o.x * inv) * w[i].x;
-        o.y = (o.y * inv) * w[i].y;
-        o.z = (o.z * inv) * w[i].z;
-        o.w = (o.w * inv) * w[i].w;
-      }
-      reinterpret_cast<float4*>(xs)[idx] = o;
+    for (int i = 0; i < NV; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+      if (idx >= k4) v[i] = z;
     }
+    float inv = 1.f;
+    if (rms) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        ss = fmaf(v[i].x, v[i].x, ss);
+        ss = fmaf(v[i].y, v[i].y, ss);
+        ss = fmaf(v[i].z, v[i].z, ss);
+        ss = fmaf(v[i].w, v[i].w, ss);
+      }
+      ss = block_sum(ss, red);
+      inv = 1.0f / sqrtf(ss / (float)k + eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+      if (idx < n4) {
+        float4 o = v[i];
+        if (rms) {
+          o.x = (o.x * inv) * w[i].x;
+          o.y = (o.y * inv) * w[i].y;
+          o.z = (o.z * inv) * w[i].z;
+          o.w = (o.w * inv) * w[i].w;
+        }
+        reinterpret_cast<float4*>(xs)[idx] = o;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-}
+};
 
 // Dot products of one row group: lanes [g*LPR, g*LPR + LPR) cover row `row`.
-// Loads are issued first (wv), then the caller stages x, then finish_dot().
-template <int LPR, int CPL>
+// load() issues the lane's CPL 16-byte chunks and their scales (one per chunk: the
+// per-row layout repeats the row's scale) with no predicates; dot() consumes them.
+template <int LPR, int CPL, bool SF16>
 struct RowDot {
   u32x4 wv[CPL];
+  float sc[CPL];
+  // `row` must be a valid row even when !live; chunks past the row are clamped to its
+  // last chunk and zeroed after the load
   __device__ __forceinline__ void load(const QW& w, int64_t row, int sub, bool live) {
     const u32x4* base = reinterpret_cast<const u32x4*>(w.q + row * w.kp);
-    const int64_t nch = w.kp / 16;
+    const int nch = (int)(w.kp / 16);
+    const unsigned cpb = (unsigned)(w.block / 16);
+    const int64_t srow = row * (w.kp / w.block);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int64_t c = sub + (int64_t)i * LPR;
-      wv[i] = (live && c < nch) ? __builtin_nontemporal_load(base + c) : u32x4{0u, 0u, 0u, 0u};
+      const int c = min(sub + i * LPR, nch - 1);
+      wv[i] = base[c];
+      const int64_t si = srow + (int64_t)((unsigned)c / cpb);
+      if constexpr (SF16)
+        sc[i] = __half2float(reinterpret_cast<const __half*>(w.scales)[si]);
+      else
+        sc[i] = reinterpret_cast<const float*>(w.scales)[si];
     }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      if (!(live && sub + i * LPR < nch)) wv[i] = u32x4{0u, 0u, 0u, 0u};
   }
-  // sum over this lane's chunks; per-row scales are applied by the caller
-  __device__ __forceinline__ float dot(const QW& w, int64_t row, int sub, const float* xs, bool per_row) {
+  // full row dot product, reduced over the row group (every lane of the group gets it)
+  __device__ __forceinline__ float dot(const float* xs, int sub) {
     float acc = 0.f;
-    const unsigned nch = (unsigned)(w.kp / 16), cpb = (unsigned)(w.block / 16);
-    const int64_t nb = w.kp / w.block;
-    const void* srow = w.sf16 ? (const void*)(reinterpret_cast<const __half*>(w.scales) + row * nb)
-                              : (const void*)(reinterpret_cast<const float*>(w.scales) + row * nb);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const unsigned c = (unsigned)sub + (unsigned)i * LPR;
-      if (c < nch) {
-        const float d = dot16(wv[i], xs + c * 16);
-        acc = per_row ? acc + d : fmaf(d, sc_chunk(w, srow, c, cpb), acc);
-      }
-    }
+    for (int i = 0; i < CPL; ++i) acc = fmaf(dot16(wv[i], xs + (sub + i * LPR) * 16), sc[i], acc);
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    return per_row ? acc * sc_at(w, row, 0) : acc;
+    return acc;
   }
 };
 
@@ -172,7 +188,7 @@ struct GemvArgs {
   int mode;
 };
 
-template <int LPR, int CPL, int MODE>
+template <int LPR, int CPL, int MODE, bool SF16>
 __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   extern __shared__ float xs[];
   __shared__ float red[4];
@@ -185,18 +201,21 @@ __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   const int64_t col = ((int64_t)blockIdx.x * 4 + wave) * outs_per_wave + (swiglu ? grp / 2 : grp);
   const bool live = col < a.n;
   const int64_t wrow = a.layer_row0 + (swiglu ? ((grp & 1) ? col + a.n : col) : col);
-  RowDot<LPR, CPL> rd;
+  VecStage<(LPR * CPL + 63) / 64> vs;
+  vs.load(a.x, a.w.k, a.rms_w);
+  const float yres = MODE == 1 ? a.y[live ? col : 0] : 0.f;
+  __builtin_amdgcn_sched_barrier(0);  // the vector's loads go out before the weight stream
+  RowDot<LPR, CPL, SF16> rd;
   rd.load(a.w, live ? wrow : a.layer_row0, sub, live);
-  const int64_t kx = a.w.kp;
-  stage_vec<(LPR * CPL + 63) / 64>(a.x, a.w.k, kx, a.rms_w, a.eps, xs, red);
-  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
-  const float acc = rd.dot(a.w, live ? wrow : a.layer_row0, sub, xs, per_row);
+  __builtin_amdgcn_sched_barrier(0);
+  vs.finish(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  const float acc = rd.dot(xs, sub);
   if (swiglu) {
     const float up = __shfl_xor(acc, LPR, 64);  // partner row group (gate <-> up)
     if (live && sub == 0 && (grp & 1) == 0) a.y[col] = (acc / (1.0f + expf(-acc))) * up;
   } else if (live && sub == 0) {
     if constexpr (MODE == 1)
-      a.y[col] = a.y[col] + acc;
+      a.y[col] = yres + acc;
     else
       a.y[col] = acc + (a.bias ? a.bias[col] : 0.f);
   }
@@ -224,7 +243,7 @@ struct QkvArgs {
   int64_t cap;
 };
 
-template <int CPL>
+template <int CPL, bool SF16>
 __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   extern __shared__ float xs[];
   __shared__ float red[4];
@@ -239,15 +258,19 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   const bool live = head * a.dh < nrows;
   const int64_t r = head * a.dh + j + ((grp & 1) ? half : 0);
   const int64_t wrow = a.layer_row0 + (live ? r : 0);
-  RowDot<LPR, CPL> rd;
+  const int64_t p = *a.pos;  // issued first: the rotary tables depend on it
+  VecStage<(LPR * CPL + 63) / 64> vs;
+  vs.load(a.x, a.w.k, a.rms_w);
+  __builtin_amdgcn_sched_barrier(0);
+  RowDot<LPR, CPL, SF16> rd;
   rd.load(a.w, wrow, sub, live);
-  stage_vec<(LPR * CPL + 63) / 64>(a.x, a.w.k, a.w.kp, a.rms_w, a.eps, xs, red);
-  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
-  float v = rd.dot(a.w, wrow, sub, xs, per_row);
-  if (live) v += a.bias[r];
+  const float bias = a.bias[live ? r : 0];
+  __builtin_amdgcn_sched_barrier(0);
+  vs.finish(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  float v = rd.dot(xs, sub);
+  if (live) v += bias;
   const float other = __shfl_xor(v, LPR, 64);  // the pair partner
   if (!live || sub != 0) return;
-  const int64_t p = *a.pos;
   const bool upper = grp & 1;
   const int jj = (int)j + (upper ? half : 0);
   const int64_t nq = a.heads, nk = a.kv_heads;
@@ -290,39 +313,47 @@ struct AttnArgs {
   float* part_ml;          // [heads, NSMAX, 2]
 };
 
-__global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
+__global__ __launch_bounds__(512) void k_dec_attn(AttnArgs a) {
   __shared__ float Kt[64 * (KCH + 1)];   // K^T: [d][key], padded
   __shared__ float Vs[KCH * 64];         // V: [key][d]
   __shared__ float qs[8 * 64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float ps[8 * KCH];          // probabilities, one row per head
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;  // wave = query head within the group
   const int split = blockIdx.x, g = blockIdx.y;
   const int G = a.heads / a.kv_heads;
-  const int64_t L = *a.pos + 1;
-  const int active = (int)((L + KCH - 1) / KCH);
-  if (split >= active) return;
+  // Every load is issued before the position is known: keys are clamped to the
+  // cache (rows < cap), masked once L is in.
+  const int64_t pos = *a.pos;
   const int64_t k0 = (int64_t)split * KCH;
   const float* kb = a.k_cache + (int64_t)g * a.cap * a.dh;
   const float* vb = a.v_cache + (int64_t)g * a.cap * a.dh;
-  // all loads first (4 float4 of K and 4 of V per thread), then the LDS writes
   const int d4n = a.dh / 4;  // float4 per key row
-  float4 kr[4], vr[4];
+  float4 kr[2], vr[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int idx = threadIdx.x + 256 * r;  // (key, d4) over 64 x 16
-    const int key = idx >> 4, d4 = idx & 15;
-    const bool ok = k0 + key < L && d4 < d4n;
-    kr[r] = ok ? reinterpret_cast<const float4*>(kb + (k0 + key) * a.dh)[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    vr[r] = ok ? reinterpret_cast<const float4*>(vb + (k0 + key) * a.dh)[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < 2; ++r) {
+    const int idx = threadIdx.x + 512 * r;  // (key, d4) over 64 x 16
+    const int key = idx >> 4, d4 = min(idx & 15, d4n - 1);
+    const int64_t row = min(k0 + key, a.cap - 1);
+    kr[r] = reinterpret_cast<const float4*>(kb + row * a.dh)[d4];
+    vr[r] = reinterpret_cast<const float4*>(vb + row * a.dh)[d4];
   }
   // q of the G <= 8 heads: (head, d4) over 8 x 16 float4, one per thread of the first 128
   const int qh = threadIdx.x >> 4, qd4 = threadIdx.x & 15;
-  const float4 qv = (threadIdx.x < 128 && qh < G && qd4 < d4n)
-                        ? reinterpret_cast<const float4*>(a.q + (g * G + qh) * a.dh)[qd4]
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 qraw =
+      reinterpret_cast<const float4*>(a.q + (g * G + min(qh, G - 1)) * a.dh)[min(qd4, d4n - 1)];
+  const float4 qv = (threadIdx.x < 128 && qh < G && qd4 < d4n) ? qraw : make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t L = pos + 1;
+  const int active = (int)((L + KCH - 1) / KCH);
+  if (split >= active) return;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int idx = threadIdx.x + 256 * r;
-    const int key = idx >> 4, d = (idx & 15) * 4;
+  for (int r = 0; r < 2; ++r) {
+    const int idx = threadIdx.x + 512 * r;
+    const int key = idx >> 4, d4 = idx & 15;
+    if (k0 + key >= L || d4 >= d4n) {
+      kr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int d = d4 * 4;
     Kt[(d + 0) * (KCH + 1) + key] = kr[r].x;
     Kt[(d + 1) * (KCH + 1) + key] = kr[r].y;
     Kt[(d + 2) * (KCH + 1) + key] = kr[r].z;
@@ -333,22 +364,40 @@ __global__ __launch_bounds__(256) void k_dec_attn(AttnArgs a) {
     reinterpret_cast<float4*>(qs)[threadIdx.x] = make_float4(qv.x * a.scale, qv.y * a.scale, qv.z * a.scale,
                                                              qv.w * a.scale);
   __syncthreads();
-  for (int h = wave; h < G; h += 4) {
-    const int key = lane;
-    float s = 0.f;
-    for (int d = 0; d < a.dh; ++d) s = fmaf(qs[h * 64 + d], Kt[d * (KCH + 1) + key], s);
-    if (k0 + key >= L) s = -INFINITY;
-    const float m = wave_max(s);
-    const float p = expf(s - m);
-    const float l = wave_sum(p);
-    float o = 0.f;
-    for (int kk = 0; kk < KCH; ++kk) o = fmaf(__shfl(p, kk, 64), Vs[kk * 64 + lane], o);
-    const int hq = g * G + h;
-    a.part_o[((int64_t)hq * NSMAX + split) * 64 + lane] = o;
-    if (lane == 0) {
-      a.part_ml[((int64_t)hq * NSMAX + split) * 2] = m;
-      a.part_ml[((int64_t)hq * NSMAX + split) * 2 + 1] = l;
-    }
+  const int h = wave;
+  if (h >= G) return;
+  // score of key `lane` for head h; q read as broadcast float4s
+  float s = 0.f;
+  const float4* q4 = reinterpret_cast<const float4*>(qs + h * 64);
+#pragma unroll
+  for (int d4 = 0; d4 < 16; ++d4) {
+    const float4 qq = q4[d4];
+    s = fmaf(qq.x, Kt[(4 * d4 + 0) * (KCH + 1) + lane], s);
+    s = fmaf(qq.y, Kt[(4 * d4 + 1) * (KCH + 1) + lane], s);
+    s = fmaf(qq.z, Kt[(4 * d4 + 2) * (KCH + 1) + lane], s);
+    s = fmaf(qq.w, Kt[(4 * d4 + 3) * (KCH + 1) + lane], s);
+  }
+  if (k0 + lane >= L) s = -INFINITY;
+  const float m = wave_max(s);
+  const float p = expf(s - m);
+  const float l = wave_sum(p);
+  ps[h * KCH + lane] = p;  // read back by the same wave only
+  // o[d = lane] = sum_key p[key] v[key][d]; p read as broadcast float4s
+  float o = 0.f;
+  const float4* p4 = reinterpret_cast<const float4*>(ps + h * KCH);
+#pragma unroll
+  for (int k4 = 0; k4 < KCH / 4; ++k4) {
+    const float4 pp = p4[k4];
+    o = fmaf(pp.x, Vs[(4 * k4 + 0) * 64 + lane], o);
+    o = fmaf(pp.y, Vs[(4 * k4 + 1) * 64 + lane], o);
+    o = fmaf(pp.z, Vs[(4 * k4 + 2) * 64 + lane], o);
+    o = fmaf(pp.w, Vs[(4 * k4 + 3) * 64 + lane], o);
+  }
+  const int hq = g * G + h;
+  a.part_o[((int64_t)hq * NSMAX + split) * 64 + lane] = o;
+  if (lane == 0) {
+    a.part_ml[((int64_t)hq * NSMAX + split) * 2] = m;
+    a.part_ml[((int64_t)hq * NSMAX + split) * 2 + 1] = l;
   }
 }
 
@@ -368,7 +417,7 @@ struct OprojArgs {
   float* x;                // residual stream, updated in place
 };
 
-template <int CPL>
+template <int CPL, bool SF16>
 __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   extern __shared__ float xs[];
   __shared__ float ml[16 * NSMAX * 2];
@@ -378,23 +427,27 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   const int64_t col = ((int64_t)blockIdx.x * 4 + wave) * RPW + grp;
   const bool live = col < a.n;
   const int64_t wrow = a.layer_row0 + (live ? col : 0);
-  RowDot<LPR, CPL> rd;
-  rd.load(a.w, wrow, sub, live);
-  const int active = (int)((*a.pos + 1 + KCH - 1) / KCH);
-  // (m, l) of every (head, chunk) into LDS; this thread's output float4s (head, d4)
-  // gather their chunks' o in registers meanwhile
+  // the attention partials (every chunk, unconditionally), then the weight stream;
+  // the chunk count is applied after the loads are out
   const int t = threadIdx.x;
-  float2 mlv = make_float2(-INFINITY, 0.f);
-  if (t < a.heads * NSMAX && (t % NSMAX) < active) mlv = reinterpret_cast<const float2*>(a.part_ml)[t];
+  const int64_t pos = *a.pos;
+  const float xres = a.x[live ? col : 0];
+  const float2 mlraw = reinterpret_cast<const float2*>(a.part_ml)[min(t, a.heads * NSMAX - 1)];
   const int d4n = a.dh / 4;
   const int oh = t / 16, od4 = t % 16;
   const bool owns = oh < a.heads && od4 < d4n;
   float4 ov[NSMAX];
 #pragma unroll
   for (int s2 = 0; s2 < NSMAX; ++s2)
-    ov[s2] = (owns && s2 < active)
-                 ? reinterpret_cast<const float4*>(a.part_o + ((int64_t)oh * NSMAX + s2) * 64)[od4]
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    ov[s2] = reinterpret_cast<const float4*>(a.part_o + ((int64_t)min(oh, a.heads - 1) * NSMAX + s2) * 64)
+        [min(od4, d4n - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  RowDot<LPR, CPL, SF16> rd;
+  rd.load(a.w, wrow, sub, live);
+  __builtin_amdgcn_sched_barrier(0);
+  const int active = (int)((pos + 1 + KCH - 1) / KCH);
+  float2 mlv = make_float2(-INFINITY, 0.f);
+  if (t < a.heads * NSMAX && (t % NSMAX) < active) mlv = mlraw;
   if (t < 16 * NSMAX) reinterpret_cast<float2*>(ml)[t] = mlv;
   __syncthreads();
   if (owns) {
@@ -415,12 +468,11 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
     }
     reinterpret_cast<float4*>(xs + oh * a.dh)[od4] = make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
   }
-  // zero padding up to the weight's padded K
-  for (int64_t c = (int64_t)a.heads * a.dh + t; c < a.w.kp; c += 256) xs[c] = 0.f;
+  // zero padding up to the staged width (chunks past the row read zeros)
+  for (int64_t c = (int64_t)a.heads * a.dh + t; c < LPR * CPL * 16; c += 256) xs[c] = 0.f;
   __syncthreads();
-  const bool per_row = a.w.block == a.w.kp && !a.w.sf16;
-  const float acc = rd.dot(a.w, wrow, sub, xs, per_row);
-  if (live && sub == 0) a.x[col] = a.x[col] + acc;
+  const float acc = rd.dot(xs, sub);
+  if (live && sub == 0) a.x[col] = xres + acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -442,7 +494,19 @@ __global__ __launch_bounds__(1024) void k_dec_next(NextArgs a) {
   __shared__ int64_t pick;
   float best = -INFINITY;
   int64_t bidx = 0x7fffffffffffffffll;
-  for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
+  // the first 8 * 1024 logits in one batch of loads, any rest in a loop
+  float lv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lv[j] = a.logits[min((int64_t)threadIdx.x + 1024 * j, a.vocab - 1)];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t i = threadIdx.x + 1024 * j;
+    if (i < a.vocab && (lv[j] > best || (lv[j] == best && i < bidx))) {
+      best = lv[j];
+      bidx = i;
+    }
+  }
+  for (int64_t i = threadIdx.x + 8 * 1024; i < a.vocab; i += blockDim.x) {
     const float v = a.logits[i];
     if (v > best || (v == best && i < bidx)) {
       best = v;
@@ -520,13 +584,20 @@ template <int LPR, int CPL>
 void launch_gemv(const GemvArgs& a, hipStream_t st) {
   const int64_t rows_per_block = 4 * (64 / LPR) / (a.mode == 2 ? 2 : 1);
   const dim3 grid((unsigned)ceil_div(a.n, rows_per_block));
-  const size_t lds = a.w.kp * sizeof(float);
-  if (a.mode == 2)
-    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 2>), grid, dim3(256), lds, st, a);
-  else if (a.mode == 1)
-    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 1>), grid, dim3(256), lds, st, a);
-  else
-    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, 0>), grid, dim3(256), lds, st, a);
+  const size_t lds = (size_t)LPR * CPL * 16 * sizeof(float);
+#define CV3_GEMV_LAUNCH(MODE)                                                                 \
+  if (a.w.sf16)                                                                              \
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, true>), grid, dim3(256), lds, st, a);     \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, false>), grid, dim3(256), lds, st, a);
+  if (a.mode == 2) {
+    CV3_GEMV_LAUNCH(2)
+  } else if (a.mode == 1) {
+    CV3_GEMV_LAUNCH(1)
+  } else {
+    CV3_GEMV_LAUNCH(0)
+  }
+#undef CV3_GEMV_LAUNCH
 }
 
 // chunks per lane for a padded K, at LPR lanes per row
@@ -534,9 +605,11 @@ int gemv(const GemvArgs& a, hipStream_t st) {
   const int64_t nch = a.w.kp / 16;
   if (nch <= 8 * 8) {
     launch_gemv<8, 8>(a, st);
-  } else if (nch <= 16 * 20) {
-    launch_gemv<16, 20>(a, st);
-  } else if (nch <= 64 * 16) {
+  } else if (a.mode == 2 && nch <= 16 * 20) {
+    launch_gemv<16, 20>(a, st);  // SwiGLU pairs two row groups of one wave
+  } else if (a.mode != 2 && nch <= 64 * 5) {
+    launch_gemv<64, 5>(a, st);   // e.g. K = 4864: one row per wave, 4 rows per workgroup
+  } else if (a.mode != 2 && nch <= 64 * 16) {
     launch_gemv<64, 16>(a, st);
   } else {
     return fail(CV3_EUNSUPPORTED, "decode GEMV K=%lld too large", (long long)a.w.kp);
@@ -586,14 +659,23 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
     QkvArgs qa{qkv, l * qkv.rows, s->x, m->ln1 + l * D, m->eps, m->qkv_bias + l * qkv.rows, (int)H, (int)Hk,
                (int)dh, m->rope_cos, m->rope_sin, s->pos, qbuf, kc, vc, s->cap};
     const int64_t pairs = (H + 2 * Hk) * dh / 2;
-    hipLaunchKernelGGL(k_dec_qkv<8>, dim3((unsigned)ceil_div(pairs, 16)), dim3(256), qkv.kp * sizeof(float), st,
-                       qa);
+    if (qkv.sf16)
+      hipLaunchKernelGGL((k_dec_qkv<8, true>), dim3((unsigned)ceil_div(pairs, 16)), dim3(256), 64 * 16 * sizeof(float),
+                         st, qa);
+    else
+      hipLaunchKernelGGL((k_dec_qkv<8, false>), dim3((unsigned)ceil_div(pairs, 16)), dim3(256),
+                         64 * 16 * sizeof(float), st, qa);
     CV3_LAUNCHED();
     AttnArgs aa{qbuf, kc, vc, (int)H, (int)Hk, (int)dh, s->cap, s->pos, scale, part_o, part_ml};
-    hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)(s->cap / KCH), (unsigned)Hk), dim3(256), 0, st, aa);
+    hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)(s->cap / KCH), (unsigned)Hk), dim3(512), 0, st, aa);
     CV3_LAUNCHED();
     OprojArgs oa{o, l * o.rows, D, part_o, part_ml, (int)H, (int)dh, s->pos, s->x};
-    hipLaunchKernelGGL(k_dec_oproj<8>, dim3((unsigned)ceil_div(D, 32)), dim3(256), o.kp * sizeof(float), st, oa);
+    if (o.sf16)
+      hipLaunchKernelGGL((k_dec_oproj<8, true>), dim3((unsigned)ceil_div(D, 32)), dim3(256), 64 * 16 * sizeof(float),
+                         st, oa);
+    else
+      hipLaunchKernelGGL((k_dec_oproj<8, false>), dim3((unsigned)ceil_div(D, 32)), dim3(256),
+                         64 * 16 * sizeof(float), st, oa);
     CV3_LAUNCHED();
     GemvArgs gb{gu, l * gu.rows, I, s->x, m->ln2 + l * D, m->eps, nullptr, hbuf, 2};
     if ((rc = gemv(gb, st))) return rc;

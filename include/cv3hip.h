@@ -261,7 +261,7 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
 /* The decode step's int8 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
  * y = W . v with v = x, or v = rms_norm(x, rms_w, eps) when rms_w is given (ops.py:101-104).
  * mode 0: y = W v + bias (bias may be NULL); 1: y += W v; 2: rows are [gate; up] (rows/2 each) and
- * y = silu(gate . v) * (up . v) (qwen2.py:175-177).  K <= 16384. */
+ * y = silu(gate . v) * (up . v) (qwen2.py:175-177).  K <= 16384 (mode 2: K <= 5120). */
 int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
                 float* y, int mode, cv3_stream_t stream);
 /* x = speech_embedding[*token] (ops.py:126-144): the first input of a decode. */
