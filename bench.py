@@ -285,6 +285,53 @@ def cpu_flow(tensors, meta):
 
 
 # ---------------------------------------------------------------------------
+# vocoder
+# ---------------------------------------------------------------------------
+
+def hift_inputs(T: int):
+    rng = np.random.default_rng(0)
+    mel = (rng.standard_normal((80, T), dtype=np.float32) * np.float32(2.0) - np.float32(5.0)).astype(np.float32)
+    # the NSF excitation's range: tanh of a small harmonic + noise mix (hift.py:90-111)
+    source = np.tanh(rng.standard_normal(480 * T, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    return mel, source
+
+
+def bench_hift(args, tensors, meta):
+    from cv3amd.device import Timer, synchronize, to_device
+    from cv3amd.hift import DeviceHiFT
+    from cv3amd.weights import WeightStore
+    T = 500
+    d = DeviceHiFT(WeightStore(tensors, meta))
+    mel, source = hift_inputs(T)
+    mel_d, src_d = to_device(mel), to_device(source)
+    out = {}
+    for label, chunk in (("whole", None), ("chunked_1s", 50)):
+        d.decode(mel_d, src_d, chunk=chunk)
+        synchronize()
+        tm = Timer()
+        tm.start()
+        for _ in range(args.hift_runs):
+            d.decode(mel_d, src_d, chunk=chunk)
+        ms = tm.stop() / args.hift_runs
+        out[label] = ms
+        log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
+    out["flops_whole"] = d.flops(T)
+    return out
+
+
+def cpu_hift(tensors, meta):
+    """The oracle's whole-utterance decode of the same input on the host cores."""
+    import oracle.quant
+    from oracle.hift import HiFTGenerator
+    from cv3amd.weights import WeightStore
+    h = HiFTGenerator(WeightStore(tensors, meta, oracle.quant.QTensor), "hift.")
+    mel, source = hift_inputs(500)
+    t0 = time.perf_counter()
+    h.decode(mel, source)
+    return time.perf_counter() - t0
+
+
+# ---------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
@@ -297,6 +344,8 @@ def main():
                     help="int8 scale layout of the LM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-core baseline")
     ap.add_argument("--no-flow", action="store_true")
+    ap.add_argument("--no-hift", action="store_true")
+    ap.add_argument("--hift-runs", type=int, default=3)
     ap.add_argument("--cpu-tokens", type=int, default=128)
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
@@ -329,9 +378,18 @@ def main():
         dit_meta = synth.dit_meta(depth=22)
         flow = bench_flow(args, dit_t, dit_meta)
 
+    voc = None
+    hift_t = hift_meta = None
+    if not args.no_hift:
+        from cv3amd import synth
+        hift_t = synth.hift_tensors(base=512)
+        hift_meta = synth.hift_meta()
+        voc = bench_hift(args, hift_t, hift_meta)
+
     cores = cpu_cores()
     cpu = None
     cpu_flow_s = None
+    cpu_hift_s = None
     if not args.no_cpu:
         log(f"cpu baseline: oracle decode of {args.cpu_tokens} tokens on {cores} host cores")
         cpu_tok_s, cpu_dt = cpu_decode(lm_t, lm_meta, args.cpu_tokens)
@@ -344,6 +402,10 @@ def main():
             log("cpu baseline: one 22-block estimator evaluation of the oracle")
             cpu_flow_s = cpu_flow(dit_t, dit_meta)
             log(f"cpu baseline: {cpu_flow_s:.2f} s per evaluation")
+        if voc is not None:
+            log("cpu baseline: one whole-utterance vocoder decode of the oracle")
+            cpu_hift_s = cpu_hift(hift_t, hift_meta)
+            log(f"cpu baseline: {cpu_hift_s:.2f} s per 10 s of audio")
 
     kern = dec["kernel"]
     line = {
@@ -390,6 +452,18 @@ def main():
             "cpu_baseline": None if cpu_flow_s is None else {
                 "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
                 "sample": "one 22-block estimator evaluation (of the solve's 10) by the oracle, x10 extrapolated"},
+        }
+    if voc is not None:
+        line["vocoder"] = {
+            "workload": "causal HiFTNet decode, mel [1, 80, 500] (10 s), base 512, ups x8/x5/x3, iSTFT 16/4, fp32",
+            "ms_whole": round(voc["whole"], 3), "rtf_whole": round(voc["whole"] / 1e3 / AUDIO_SECONDS, 6),
+            "ms_chunked_1s": round(voc["chunked_1s"], 3),
+            "rtf_chunked_1s": round(voc["chunked_1s"] / 1e3 / AUDIO_SECONDS, 6),
+            "conv_tflops_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / 1e12, 2),
+            "mfma_roofline_frac_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / FP32_MFMA_PEAK, 4),
+            "cpu_baseline": None if cpu_hift_s is None else {
+                "value": round(cpu_hift_s / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
+                "sample": "one whole-utterance decode of the same input by the oracle"},
         }
     print(json.dumps(line), flush=True)
 

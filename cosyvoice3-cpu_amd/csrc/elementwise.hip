@@ -33,6 +33,7 @@ __global__ void k_binary(int op, const float* __restrict__ a, const float* __res
       case 0: r = u + v; break;                    // add
       case 1: r = u * v; break;                    // mul
       case 2: r = act_silu(u) * v; break;          // silu(a) * b  (qwen2.py:177)
+      case 4: r = (u + v) / alpha; break;          // (a + b) / alpha: the resblock mean (hift.py:165)
       default: r = alpha * u + beta * v; break;    // axpby
     }
     y[i] = r;

@@ -1,0 +1,248 @@
+"""Device-resident causal HiFTNet decode: source STFT -> conv stack -> iSTFT head.
+
+Restates cv3cpu/models/hift.py:114-210 (``_resblock``, ``_spectral``,
+``_spectral_chunked``, ``decode``) with every activation resident in HBM, in the
+reference's (channels, time) layout.  The F0 predictor and the NSF excitation
+(hift.py:56-111, float64 host code in the reference) produce the ``source``
+signal this class takes as input.
+
+Per upsampling stage i (reference lines in brackets):
+  leaky(x, 0.1), nearest x r_i fused into the causal ``ups`` conv      (hift.py:137-142)
+  last stage: reflect pad (1, 0) as a one-column copy                  (hift.py:143-144)
+  source_downs conv on the source STFT (stride u_i) + source resblock  (hift.py:145-156)
+  x + s, then the mean of three resblocks                              (hift.py:157-165)
+A resblock's step is  snake(x, a1) -> dilated causal conv with snake(., a2) in its
+epilogue -> causal conv with the residual x added in its epilogue  (hift.py:114-129).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, to_device
+
+ACT = _lib.ACT
+F4 = 4
+
+
+def causal_pad(kernel_size: int, dilation: int = 1) -> int:
+    """int((k d - d) / 2) * 2 + (k + 1) % 2 (hift.py:14-16)."""
+    return int((kernel_size * dilation - dilation) / 2) * 2 + (kernel_size + 1) % 2
+
+
+def hann_window(n: int) -> np.ndarray:
+    """Periodic Hann window, float64 -> float32 (ops.py:339-343)."""
+    i = np.arange(n, dtype=np.float64)
+    return (0.5 - 0.5 * np.cos(2.0 * np.pi * i / n)).astype(np.float32)
+
+
+class DeviceHiFT:
+    """HiFTNet weights resident in HBM; ``weights`` has ``get(name)`` and ``meta``."""
+
+    def __init__(self, weights, prefix: str = "hift."):
+        _lib.init()
+        m = weights.meta.get("hift", {})
+        self.rates = list(m.get("upsample_rates", [8, 5, 3]))
+        self.rb_k = list(m.get("resblock_kernel_sizes", [3, 7, 11]))
+        self.rb_d = [list(d) for d in m.get("resblock_dilation_sizes", [[1, 3, 5]] * 3)]
+        self.src_k = list(m.get("source_resblock_kernel_sizes", [7, 7, 11]))
+        self.src_d = [list(d) for d in m.get("source_resblock_dilation_sizes", [[1, 3, 5]] * 3)]
+        self.n_fft = int(m.get("istft_n_fft", 16))
+        self.hop = int(m.get("istft_hop_len", 4))
+        self.slope = float(m.get("lrelu_slope", 0.1))
+        self.limit = float(m.get("audio_limit", 0.99))
+        self.nk = len(self.rb_k)
+        self.up_total = int(np.prod(self.rates))
+        self.w = {}
+        self.shape = {}
+        for name in weights.keys():
+            if not name.startswith(prefix) or "f0_predictor" in name or "m_source" in name:
+                continue
+            arr = np.asarray(weights.get(name), np.float32)
+            key = name[len(prefix):]
+            self.w[key] = to_device(np.ascontiguousarray(arr))
+            self.shape[key] = arr.shape
+        self.window = to_device(hann_window(self.n_fft))
+
+    # -- building blocks ------------------------------------------------------
+    def _conv(self, x: DeviceArray, key: str, stride: int = 1, dilation: int = 1, pad=(0, 0), up: int = 1,
+              act: str = "none", act_param: float = 0.0, snake: Optional[str] = None,
+              residual: Optional[DeviceArray] = None, out: Optional[DeviceArray] = None,
+              out_col0: int = 0, out_ld: Optional[int] = None) -> DeviceArray:
+        """conv1d over (C_in, T) -> (C_out, T_out) (ops.py:165-219), with the fused
+        nearest upsample, activation / Snake and residual epilogues."""
+        cout, cin_g, k = self.shape[key + ".weight"]
+        cin, t_in = x.shape
+        t_out = ctypes.c_int64()
+        _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k, None, stride,
+                  dilation, 1, pad[0], pad[1], up, None, 0, 0, _lib.ptr(t_out), 0, 0.0, None, 0.0, None, 0, 0, None)
+        n = t_out.value
+        if out is None:
+            out = DeviceArray((cout, n))
+        ld = out_ld if out_ld is not None else out.shape[1]
+        alpha = self.w[snake].ptr if snake else None
+        res = residual.ptr if residual is not None else None
+        rld = residual.shape[1] if residual is not None else 0
+        _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k,
+                  self.w[key + ".bias"].ptr, stride, dilation, 1, pad[0], pad[1], up, out.ptr + out_col0 * F4,
+                  ld, 1, None, ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
+        return out
+
+    def _snake(self, x: DeviceArray, key: str) -> DeviceArray:
+        y = DeviceArray(x.shape)
+        _lib.call("snake", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, None)
+        return y
+
+    def _act(self, x: DeviceArray, name: str, param: float) -> DeviceArray:
+        y = DeviceArray(x.shape)
+        _lib.call("act", ACT[name], float(param), x.ptr, y.ptr, x.size, None)
+        return y
+
+    def _resblock(self, group: str, idx: int, x: DeviceArray, kernel: int, dilations) -> DeviceArray:
+        """3 x [snake, dilated causal conv, snake, causal conv] + residual (hift.py:114-129).
+        ``x`` is left untouched; the result is a new buffer."""
+        base = f"{group}.{idx}."
+        cur = x
+        for j, d in enumerate(dilations):
+            y = self._snake(cur, base + f"activations1.{j}.alpha")
+            y = self._conv(y, base + f"convs1.{j}", dilation=d, pad=(causal_pad(kernel, d), 0),
+                           snake=base + f"activations2.{j}.alpha")
+            out = DeviceArray(x.shape) if cur is x else cur   # in place after the first step
+            cur = self._conv(y, base + f"convs2.{j}", pad=(causal_pad(kernel, 1), 0), residual=cur, out=out)
+        return cur
+
+    # -- the spectral stack -------------------------------------------------
+    def spectral(self, mel: DeviceArray, s_stft: DeviceArray) -> DeviceArray:
+        """conv_pre .. conv_post: (80, T) -> (n_fft + 2, 120 T + 1) (hift.py:131-168)."""
+        kpre = self.shape["conv_pre.weight"][2]
+        x = self._conv(mel, "conv_pre", pad=(0, causal_pad(kpre)))
+        downs = [1] + self.rates[::-1][:-1]
+        down_cum = list(np.cumprod(downs))[::-1]
+        for i, r in enumerate(self.rates):
+            xl = self._act(x, "leaky", self.slope)
+            k = self.shape[f"ups.{i}.weight"][2]
+            cout = self.shape[f"ups.{i}.weight"][0]
+            t_up = x.shape[1] * r
+            if i == len(self.rates) - 1:
+                # reflect pad (1, 0): columns 1.. hold the conv, column 0 copies column 2 (hift.py:144)
+                xu = DeviceArray((cout, t_up + 1))
+                self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0), out=xu, out_col0=1, out_ld=t_up + 1)
+                S3 = ctypes.c_int64 * 3
+                _lib.call("copy_strided", xu.ptr + 2 * F4, xu.ptr, 1, cout, 1, S3(0, t_up + 1, 1),
+                          S3(0, t_up + 1, 1), None)
+            else:
+                xu = self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0))
+            u = int(down_cum[i])
+            ks = self.shape[f"source_downs.{i}.weight"][2]
+            if u == 1:
+                si = self._conv(s_stft, f"source_downs.{i}", pad=(causal_pad(ks), 0))
+            else:
+                si = self._conv(s_stft, f"source_downs.{i}", stride=u, pad=(u - 1, 0))
+            si = self._resblock("source_resblocks", i, si, self.src_k[i], self.src_d[i])
+            if si.shape != xu.shape:
+                raise ValueError(f"stage {i}: source branch {si.shape} vs upsampled {xu.shape}")
+            xs = DeviceArray(xu.shape)
+            _lib.call("binary", 0, xu.ptr, si.ptr, xs.ptr, xs.size, 0.0, 0.0, None)
+            rs = [self._resblock("resblocks", i * self.nk + j, xs, self.rb_k[j], self.rb_d[j])
+                  for j in range(self.nk)]
+            acc = rs[0]
+            for j in range(1, self.nk):
+                nxt = DeviceArray(xs.shape)
+                if j == self.nk - 1:   # ((r0 + r1) + r2) / 3 (hift.py:161-165)
+                    _lib.call("binary", 4, acc.ptr, rs[j].ptr, nxt.ptr, nxt.size, float(self.nk), 0.0, None)
+                else:
+                    _lib.call("binary", 0, acc.ptr, rs[j].ptr, nxt.ptr, nxt.size, 0.0, 0.0, None)
+                acc = nxt
+            x = acc
+        x = self._act(x, "leaky", 0.01)
+        kpost = self.shape["conv_post.weight"][2]
+        return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0))
+
+    def spectral_chunked(self, mel: DeviceArray, s_stft: DeviceArray, chunk: int, context: int) -> DeviceArray:
+        """Windows of ``chunk`` frames with ``context`` frames of history and conv_pre's
+        lookahead, cut back to the window's own samples (hift.py:170-194)."""
+        up = self.up_total
+        t = mel.shape[1]
+        look = causal_pad(self.shape["conv_pre.weight"][2])
+        nout = self.n_fft + 2
+        out = DeviceArray((nout, t * up + 1))
+        S3 = ctypes.c_int64 * 3
+        for m0 in range(0, t, chunk):
+            m1 = min(t, m0 + chunk)
+            c0 = max(0, m0 - context)
+            c1 = min(t, m1 + look)
+            sub_mel = DeviceArray((mel.shape[0], c1 - c0))
+            _lib.call("copy_strided", mel.ptr + c0 * F4, sub_mel.ptr, 1, mel.shape[0], c1 - c0,
+                      S3(0, t, 1), S3(0, c1 - c0, 1), None)
+            fs = s_stft.shape[1]
+            f0, f1 = c0 * up, min(fs, c1 * up + 1)
+            sub_s = DeviceArray((s_stft.shape[0], f1 - f0))
+            _lib.call("copy_strided", s_stft.ptr + f0 * F4, sub_s.ptr, 1, s_stft.shape[0], f1 - f0,
+                      S3(0, fs, 1), S3(0, f1 - f0, 1), None)
+            sub = self.spectral(sub_mel, sub_s)
+            lead = (m0 - c0) * up
+            take = (m1 - m0) * up
+            src0, dst0, n = (0, 0, 1 + take) if m0 == 0 else (1 + lead, 1 + m0 * up, take)
+            _lib.call("copy_strided", sub.ptr + src0 * F4, out.ptr + dst0 * F4, 1, nout, n,
+                      S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), None)
+        return out
+
+    def source_stft(self, source: DeviceArray) -> DeviceArray:
+        """(n_fft + 2, frames) real / imaginary stack of the source STFT (hift.py:198-199)."""
+        frames = ctypes.c_int64()
+        _lib.call("stft", source.ptr, source.size, self.n_fft, self.hop, self.window.ptr, 1, None, None,
+                  _lib.ptr(frames), None)
+        half = self.n_fft // 2 + 1
+        s = DeviceArray((2 * half, frames.value))
+        _lib.call("stft", source.ptr, source.size, self.n_fft, self.hop, self.window.ptr, 1, s.ptr,
+                  s.ptr + half * frames.value * F4, None, None)
+        return s
+
+    def istft_head(self, x: DeviceArray) -> DeviceArray:
+        """clip(exp(min(x,80)),100) magnitude, sin(x) phase, iSTFT, clip +-limit (hift.py:204-210)."""
+        half = self.n_fft // 2 + 1
+        frames = x.shape[1]
+        buf = DeviceArray((frames, self.n_fft))
+        n = ctypes.c_int64()
+        _lib.call("istft", 1, x.ptr, x.ptr + half * frames * F4, frames, self.n_fft, self.hop, self.window.ptr, 1,
+                  -1, self.limit, buf.ptr, None, _lib.ptr(n), None)
+        y = DeviceArray((n.value,))
+        _lib.call("istft", 1, x.ptr, x.ptr + half * frames * F4, frames, self.n_fft, self.hop, self.window.ptr, 1,
+                  -1, self.limit, buf.ptr, y.ptr, None, None)
+        return y
+
+    def decode(self, mel, source, chunk: Optional[int] = None, context: int = 64) -> DeviceArray:
+        """(80, T) mel + (480 T,) source -> (480 T,) waveform (hift.py:196-210).  Host or
+        device inputs; the result stays resident."""
+        mel_d = mel if isinstance(mel, DeviceArray) else to_device(np.ascontiguousarray(mel, np.float32))
+        src_d = source if isinstance(source, DeviceArray) else to_device(np.ascontiguousarray(source, np.float32))
+        s_stft = self.source_stft(src_d)
+        if chunk is None or mel_d.shape[1] <= chunk:
+            x = self.spectral(mel_d, s_stft)
+        else:
+            x = self.spectral_chunked(mel_d, s_stft, chunk, context)
+        return self.istft_head(x)
+
+    def flops(self, t: int) -> float:
+        """Algorithmic conv flops of a whole-utterance decode of t mel frames."""
+        total = 0.0
+        cur_t = t
+        kpre = self.shape["conv_pre.weight"]
+        total += 2.0 * kpre[0] * kpre[1] * kpre[2] * cur_t
+        for i, r in enumerate(self.rates):
+            cur_t *= r
+            co, ci, k = self.shape[f"ups.{i}.weight"]
+            total += 2.0 * co * ci * k * cur_t
+            co, ci, k = self.shape[f"source_downs.{i}.weight"]
+            total += 2.0 * co * ci * k * cur_t
+            for g, idx, kk in [("source_resblocks", i, self.src_k[i])] + \
+                    [("resblocks", i * self.nk + j, self.rb_k[j]) for j in range(self.nk)]:
+                c = self.shape[f"{g}.{idx}.convs1.0.weight"][0]
+                total += 2 * 3 * 2.0 * c * c * kk * cur_t
+        co, ci, k = self.shape["conv_post.weight"]
+        total += 2.0 * co * ci * k * cur_t
+        return total

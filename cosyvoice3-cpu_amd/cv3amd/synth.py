@@ -80,6 +80,53 @@ def dit_meta(depth: int = 22, dim: int = 1024, heads: int = 16, dim_head: int = 
             "flow": dict(FLOW_META)}
 
 
+HIFT_META = dict(upsample_rates=[8, 5, 3], upsample_kernel_sizes=[16, 11, 7], resblock_kernel_sizes=[3, 7, 11],
+                 resblock_dilation_sizes=[[1, 3, 5]] * 3, source_resblock_kernel_sizes=[7, 7, 11],
+                 source_resblock_dilation_sizes=[[1, 3, 5]] * 3, istft_n_fft=16, istft_hop_len=4,
+                 lrelu_slope=0.1, audio_limit=0.99, sampling_rate=24000, nb_harmonics=8, nsf_alpha=0.1,
+                 nsf_sigma=0.003, nsf_voiced_threshold=10.0, conv_pre_look_right=4)
+
+
+def hift_tensors(base: int = 512, f0_ch: int = 512, mel: int = 80, seed: int = 0,
+                 prefix: str = "hift.") -> Dict[str, np.ndarray]:
+    """float32 HiFTNet weights, weight-norm already folded (cv3cpu/convert.py:52-76),
+    Snake alphas ones (cv3cpu/models/hift.py:19-218, tools/make_dummy_model.py:88-90)."""
+    m = HIFT_META
+    n_fft = m["istft_n_fft"]
+    shapes = {"conv_pre.weight": (base, mel, 5), "conv_pre.bias": (base,),
+              "conv_post.weight": (n_fft + 2, base // 8, 7), "conv_post.bias": (n_fft + 2,),
+              "m_source.l_linear.weight": (1, m["nb_harmonics"] + 1), "m_source.l_linear.bias": (1,),
+              "f0_predictor.classifier.weight": (1, f0_ch), "f0_predictor.classifier.bias": (1,)}
+    for i in range(5):
+        shapes[f"f0_predictor.condnet.{i}.weight"] = (f0_ch, mel if i == 0 else f0_ch, 4 if i == 0 else 3)
+        shapes[f"f0_predictor.condnet.{i}.bias"] = (f0_ch,)
+    downs = [1] + m["upsample_rates"][::-1][:-1]
+    down_cum = list(np.cumprod(downs))[::-1]
+    ones = []
+    for i, (r, k) in enumerate(zip(m["upsample_rates"], m["upsample_kernel_sizes"])):
+        cin, cout = base // (2 ** i), base // (2 ** (i + 1))
+        shapes[f"ups.{i}.weight"] = (cout, cin, k)
+        shapes[f"ups.{i}.bias"] = (cout,)
+        u = int(down_cum[i])
+        shapes[f"source_downs.{i}.weight"] = (cout, n_fft + 2, 2 * u if u > 1 else 1)
+        shapes[f"source_downs.{i}.bias"] = (cout,)
+        groups = [("source_resblocks", i, m["source_resblock_kernel_sizes"][i])]
+        groups += [("resblocks", i * 3 + j, kj) for j, kj in enumerate(m["resblock_kernel_sizes"])]
+        for g, idx, kk in groups:
+            for j in range(3):
+                for c in ("convs1", "convs2"):
+                    shapes[f"{g}.{idx}.{c}.{j}.weight"] = (cout, cout, kk)
+                    shapes[f"{g}.{idx}.{c}.{j}.bias"] = (cout,)
+                for a in ("activations1", "activations2"):
+                    shapes[f"{g}.{idx}.{a}.{j}.alpha"] = (cout,)
+                    ones.append(f"{g}.{idx}.{a}.{j}.alpha")
+    return {prefix + k: tensor(prefix + k, sh, seed, ones=k in ones) for k, sh in shapes.items()}
+
+
+def hift_meta() -> dict:
+    return {"hift": dict(HIFT_META)}
+
+
 def qwen2_tensors(layers: int = 24, hidden: int = 896, heads: int = 14, kv_heads: int = 2,
                   inter: int = 4864, head_rows: int = LM_HEAD_ROWS, seed: int = 0,
                   prefix: str = "llm.") -> Dict[str, np.ndarray]:

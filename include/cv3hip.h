@@ -127,7 +127,7 @@ int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, co
 /* ---------------- elementwise / reductions ---------------- */
 /* ops.silu/sigmoid/gelu_tanh/gelu/mish/elu/leaky_relu (ops.py:30-74): y = act(x), param = alpha/slope */
 int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_stream_t s);
-/* op 0: a+b, 1: a*b, 2: silu(a)*b (qwen2.py:177), 3: alpha*a + beta*b */
+/* op 0: a+b, 1: a*b, 2: silu(a)*b (qwen2.py:177), 3: alpha*a + beta*b, 4: (a+b)/alpha (hift.py:165) */
 int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, float alpha, float beta, cv3_stream_t s);
 /* ops.snake (ops.py:77-81) over (C, T) with per-channel alpha */
 int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s);
