@@ -197,18 +197,56 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int 
   }
 }
 
-// DiT partial rotary applied in the epilogue (dit.py:40-54): columns c < rope_limit with
-// c % rope_period < rope_width are interleaved pairs (2i, 2i+1) -> (a cos - b sin, b cos + a sin),
-// table row = row % rope_rows.  The pair partner of column c is held by lane ^ 1.
-__device__ __forceinline__ float rope_epilogue(const cv3_epilogue& e, float v, int64_t row, int64_t col) {
-  const float other = __shfl_xor(v, 1, 64);
-  const int64_t cc = col % e.rope_period;
-  if (col < e.rope_limit && cc < e.rope_width) {
-    const int64_t ti = (row % e.rope_rows) * e.rope_width + cc;
-    const float c = e.rope_cos[ti], sn = e.rope_sin[ti];
-    v = (col & 1) ? v * c + other * sn : v * c + (-other) * sn;
+// Epilogue of one wave's 32 x 32 accumulator tile (32x32x2 f32 layout: reg i -> row
+// r0 + (i/4)*8 + h*4 + i%4, column col = lane's column).  Every operand the epilogue
+// reads (rotary table, gate, residual) is loaded for all 16 registers before the first
+// store: C may be the residual itself (in-place residual adds), so a load issued after
+// a store to C would have to wait for it, one memory round trip per register.  Each
+// element is read and written by the same lane, so the early loads are exact.
+//
+// DiT partial rotary (dit.py:40-54): columns c < rope_limit with c % rope_period <
+// rope_width are interleaved pairs (2i, 2i+1) -> (a cos - b sin, b cos + a sin), table
+// row = row % rope_rows; the pair partner of column c is held by lane ^ 1.
+__device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16& acc, int64_t r0, int h, int64_t col) {
+  const cv3_epilogue& e = p.epi;
+  const bool cin = col < p.n;
+  const int64_t cc = cin ? col : p.n - 1;
+  const float bv = p.bias ? p.bias[cc] : 0.f;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = acc[i] + bv;
+  if (e.rope_cos) {  // uniform branch, shuffles inside
+    const int64_t cp = col % e.rope_period;
+    const bool rot = col < e.rope_limit && cp < e.rope_width;
+    float cs[16], sn[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t row = min(r0 + (i >> 2) * 8 + h * 4 + (i & 3), p.m - 1);
+      const int64_t ti = (row % e.rope_rows) * e.rope_width + (rot ? cp : 0);
+      cs[i] = e.rope_cos[ti];
+      sn[i] = e.rope_sin[ti];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float other = __shfl_xor(v[i], 1, 64);
+      if (rot) v[i] = (col & 1) ? v[i] * cs[i] + other * sn[i] : v[i] * cs[i] + (-other) * sn[i];
+    }
   }
-  return v;
+  float g[16], res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = min(r0 + (i >> 2) * 8 + h * 4 + (i & 3), p.m - 1);
+    g[i] = e.gate ? e.gate[(e.rows_per_gate > 1 ? row / e.rows_per_gate : row) * e.gate_stride + cc] : 1.f;
+    res[i] = e.residual ? e.residual[row * e.ld_res + cc] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = r0 + (i >> 2) * 8 + h * 4 + (i & 3);
+    float y = apply_act(e.act, v[i], e.act_param);
+    if (e.gate) y = g[i] * y;
+    if (e.residual) y = res[i] + y;
+    if (row < p.m && cin) p.c[row * p.ldc + col] = y;
+  }
 }
 
 // The GEMM kernel: 4 waves, 64 x 64 tile.  FAST (K % 64 == 0, aligned rows):
@@ -300,19 +338,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast
     }
   }
 
-  // accumulator layout (32x32x2 f32): reg i -> row (i/4)*8 + h*4 + i%4, col = lane%32
-  const int64_t col = n0 + wn + r32;
-  const float bv = (p.bias && col < p.n) ? p.bias[col] : 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t row = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
-    float v = acc[i] + bv;
-    if (p.epi.rope_cos) v = rope_epilogue(p.epi, v, row, col);  // uniform branch, shuffles inside
-    if (row < p.m && col < p.n) {
-      v = apply_epilogue(p.epi, v, row, col, false);
-      p.c[row * p.ldc + col] = v;
-    }
-  }
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
 }
 
 
@@ -404,18 +430,102 @@ __global__ __launch_bounds__(512) void k_gemm8(GemmParams p, int tiles_m) {
   if (kh == 1) return;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] += red[(quad * 16 + i) * 64 + lane];
-  const int64_t col = n0 + wn + r32;
-  const float bv = (p.bias && col < p.n) ? p.bias[col] : 0.f;
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
+}
+
+// fp32 GEMM fed by global -> LDS DMA (global_load_lds_dwordx4): no register
+// staging, so the ring holds NST stages of BK = 32 and NST - 1 of them are in
+// flight while the waves run MFMAs on the oldest.  Each stage is its own LDS
+// array, so the compiler can tell a DMA into one stage from the MFMA reads of
+// another and leaves the waiting to the explicit vmcnt below.
+//
+// A DMA writes 64 lanes x 16 B contiguously; lane l of a wave's load covers tile
+// row r = base + l / 8 and slot l % 8, and fetches the row's 16-byte chunk
+// (l % 8) ^ (r % 8).  Chunk c of row r therefore sits at r * 32 + ((c ^ (r % 8)) * 4)
+// floats, which spreads the eight rows an MFMA read touches over all banks.
+//
+// Per step: wait until this wave's DMA of the current stage has landed (vmcnt:
+// loads complete in order), barrier (every wave's DMA has landed and every wave
+// is done with the previous stage), issue the stage NST - 1 ahead into the
+// buffer the previous stage used, run the MFMAs.  sched_barrier pins that
+// order against the scheduler; the barrier carries no fence, which would wait
+// for every outstanding DMA.
+constexpr int DMA_NST = 3;
+#define CV3_VMCNT(n) (((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+struct DmaSrc {
+  const float* a0;
+  const float* a1;
+  const float* b0;
+  const float* b1;
+};
+
+__device__ __forceinline__ void dma_stage(const DmaSrc& s, int64_t koff, float* as, float* bs, int w) {
+  __builtin_amdgcn_global_load_lds(s.a0 + koff, as + (w * 16) * BK, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(s.a1 + koff, as + (w * 16 + 8) * BK, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(s.b0 + koff, bs + (w * 16) * BK, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(s.b1 + koff, bs + (w * 16 + 8) * BK, 16, 0, 0);
+}
+
+__device__ __forceinline__ void mma_swz(const float* as, const float* bs, int arow, int brow, int sw, int h,
+                                        f32x16& acc) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t row = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
-    float v = acc[i] + bv;
-    if (p.epi.rope_cos) v = rope_epilogue(p.epi, v, row, col);  // uniform branch, shuffles inside
-    if (row < p.m && col < p.n) {
-      v = apply_epilogue(p.epi, v, row, col, false);
-      p.c[row * p.ldc + col] = v;
-    }
+  for (int g = 0; g < BK / 8; ++g) {
+    const int c = ((2 * g + h) ^ sw) * 4;
+    const float4 av = *reinterpret_cast<const float4*>(as + arow + c);
+    const float4 bv = *reinterpret_cast<const float4*>(bs + brow + c);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
   }
+}
+
+// fp32 A rows and fp32 B rows, 16-byte aligned, K % 32 == 0.
+__global__ __launch_bounds__(256) void k_gemm_dma(GemmParams p, int tiles_m) {
+  static_assert(DMA_NST == 3, "the step sequence below is written for a ring of three stages");
+  __shared__ float A0[BM * BK], A1[BM * BK], A2[BM * BK];
+  __shared__ float B0[BN * BK], B1[BN * BK], B2[BN * BK];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  const int lr = lane >> 3, lc = ((lane & 7) ^ lr) * 4;
+  const float* b = reinterpret_cast<const float*>(p.b);
+  DmaSrc src;
+  src.a0 = p.a + min(m0 + w * 16 + lr, p.m - 1) * p.lda + lc;
+  src.a1 = p.a + min(m0 + w * 16 + 8 + lr, p.m - 1) * p.lda + lc;
+  src.b0 = b + min(n0 + w * 16 + lr, p.n - 1) * p.ldb + lc;
+  src.b1 = b + min(n0 + w * 16 + 8 + lr, p.n - 1) * p.ldb + lc;
+  const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
+  const int r32 = lane & 31, h = lane >> 5, sw = r32 & 7;
+  const int arow = (wm + r32) * BK, brow = (wn + r32) * BK;
+  const int64_t S = p.k / BK;
+  f32x16 acc = {0.f};
+  dma_stage(src, 0, A0, B0, w);
+  dma_stage(src, min((int64_t)1, S - 1) * BK, A1, B1, w);
+#define CV3_DMA_STEP(AN, BN_, AC, BC, ST)                           \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  __builtin_amdgcn_s_waitcnt(CV3_VMCNT(4 * (DMA_NST - 2)));         \
+  __builtin_amdgcn_s_barrier();                                     \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  dma_stage(src, min((ST) + DMA_NST - 1, S - 1) * BK, AN, BN_, w);  \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  mma_swz(AC, BC, arow, brow, sw, h, acc);
+  int64_t st = 0;
+  for (; st + 3 <= S; st += 3) {
+    CV3_DMA_STEP(A2, B2, A0, B0, st)
+    CV3_DMA_STEP(A0, B0, A1, B1, st + 1)
+    CV3_DMA_STEP(A1, B1, A2, B2, st + 2)
+  }
+  if (st < S) {
+    CV3_DMA_STEP(A2, B2, A0, B0, st)
+    if (st + 1 < S) { CV3_DMA_STEP(A0, B0, A1, B1, st + 1) }
+  }
+#undef CV3_DMA_STEP
+  // no DMA may still be writing this workgroup's LDS when it ends
+  __builtin_amdgcn_s_waitcnt(CV3_VMCNT(0));
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
 }
 
 }  // namespace
@@ -461,8 +571,8 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
     else
       hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
   } else {
-    if (fast && small)
-      hipLaunchKernelGGL((k_gemm8<B_F32, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
+    if (fast && tiles_m * tiles_n <= 512)
+      hipLaunchKernelGGL(k_gemm_dma, grid, dim3(256), 0, st, p, (int)tiles_m);
     else if (fast)
       hipLaunchKernelGGL((k_gemm<B_F32, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
     else
