@@ -128,23 +128,34 @@ __global__ __launch_bounds__(256) void k_conv_mfma(ConvParams p) {
     __syncthreads();
   }
 
-  // acc reg i -> (row = output channel, col = time): row (i/4)*8 + h*4 + i%4, col lane%32
+  // acc reg i -> (row = output channel, col = time): row (i/4)*8 + h*4 + i%4, col lane%32.
+  // The epilogue's operands are loaded for all 16 registers before the first store:
+  // y may alias the residual, and a load after a store to y would wait for it.
   const int64_t t = n0 + wn + r32;
   if (t >= p.t_out) return;
+  float bias[16], alpha[16], res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t co_g = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), cout_g - 1);
+    const int64_t co = g * cout_g + co_g;
+    bias[i] = p.bias ? p.bias[co] : 0.f;
+    alpha[i] = p.snake_alpha ? p.snake_alpha[co] : 0.f;
+    res[i] = p.res ? p.res[co * p.r_cs + t * p.r_ts] : 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t co_g = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
     if (co_g < cout_g) {
       const int64_t co = g * cout_g + co_g;
-      float v = acc[i] + (p.bias ? p.bias[co] : 0.f);
+      float v = acc[i] + bias[i];
       if (p.snake_alpha) {
-        const float a = p.snake_alpha[co];
+        const float a = alpha[i];
         const float sn = sinf(a * v);
         v = v + (1.0f / (a + p.snake_eps)) * (sn * sn);
       } else {
         v = apply_act(p.act, v, p.act_param);
       }
-      if (p.res) v = p.res[co * p.r_cs + t * p.r_ts] + v;
+      if (p.res) v = res[i] + v;
       p.y[co * p.y_cs + t * p.y_ts] = v;
     }
   }

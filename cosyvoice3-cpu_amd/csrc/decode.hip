@@ -134,13 +134,15 @@ struct VecStage {
 // Dot products of one row group: lanes [g*LPR, g*LPR + LPR) cover row `row`.
 // load() issues the lane's CPL 16-byte chunks and their scales (one per chunk: the
 // per-row layout repeats the row's scale) with no predicates; dot() consumes them.
+// Chunks past the row are clamped to its last chunk and meet the zero padding of
+// the staged vector (xs is zero from K up to LPR * CPL * 16), so they add exactly
+// 0; nothing selects on a loaded value, which would wait for the load right there.
+// A dead row group (`row` clamped to a valid row) computes a value nobody stores.
 template <int LPR, int CPL, bool SF16>
 struct RowDot {
   u32x4 wv[CPL];
   float sc[CPL];
-  // `row` must be a valid row even when !live; chunks past the row are clamped to its
-  // last chunk and zeroed after the load
-  __device__ __forceinline__ void load(const QW& w, int64_t row, int sub, bool live) {
+  __device__ __forceinline__ void load(const QW& w, int64_t row, int sub, bool /*live*/) {
     const u32x4* base = reinterpret_cast<const u32x4*>(w.q + row * w.kp);
     const int nch = (int)(w.kp / 16);
     const unsigned cpb = (unsigned)(w.block / 16);
@@ -155,9 +157,6 @@ struct RowDot {
       else
         sc[i] = reinterpret_cast<const float*>(w.scales)[si];
     }
-#pragma unroll
-    for (int i = 0; i < CPL; ++i)
-      if (!(live && sub + i * LPR < nch)) wv[i] = u32x4{0u, 0u, 0u, 0u};
   }
   // full row dot product, reduced over the row group (every lane of the group gets it)
   __device__ __forceinline__ float dot(const float* xs, int sub) {
