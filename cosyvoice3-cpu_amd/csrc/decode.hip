@@ -265,19 +265,21 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   rd.load(a.w, wrow, sub, live);
   const float bias = a.bias[live ? r : 0];
   __builtin_amdgcn_sched_barrier(0);
+  // the row's rotary table entries: they wait for `pos`, so they go out after the
+  // weight stream and arrive while the RMSNorm and the dot product run
+  const bool upper = grp & 1;
+  const int jj = (int)j + (upper ? half : 0);
+  const float rc = a.cos_t[p * a.dh + jj], rs = a.sin_t[p * a.dh + jj];
   vs.finish(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
   float v = rd.dot(xs, sub);
   if (live) v += bias;
   const float other = __shfl_xor(v, LPR, 64);  // the pair partner
   if (!live || sub != 0) return;
-  const bool upper = grp & 1;
-  const int jj = (int)j + (upper ? half : 0);
   const int64_t nq = a.heads, nk = a.kv_heads;
   float out = v;
   if (head < nq + nk) {
     // x cos + rotate_half(x) sin, rotate_half = concat(-x2, x1)
-    const float c = a.cos_t[p * a.dh + jj], s = a.sin_t[p * a.dh + jj];
-    out = upper ? v * c + other * s : v * c + (-other) * s;
+    out = upper ? v * rc + other * rs : v * rc + (-other) * rs;
   }
   if (head < nq) {
     a.q_out[head * a.dh + jj] = out;
