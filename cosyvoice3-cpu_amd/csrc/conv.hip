@@ -161,6 +161,137 @@ __global__ __launch_bounds__(256) void k_conv_mfma(ConvParams p) {
   }
 }
 
+// Fast path for stride 1 and groups 1 (every HiFT conv but the strided source_downs):
+// the weight is repacked (cout, k, cin), so with cin % 64 == 0 a BK = 32 stage is 32
+// channels of one tap and its im2col rows are plain shifted rows of x, with 32-bit
+// index math done once per stage.  A thread owns one time column and 8 channels of
+// the B tile, so its 8 loads per stage are coalesced over the wave along time (x
+// time-contiguous).  Global loads run two stages ahead in ping-pong register sets, as
+// in the linear GEMM; taps and channels of the K loop follow from the stage index.
+struct ConvFast {
+  const float* x;
+  int64_t x_cs;
+  int t_in, up;
+  const float* w;  // [cout, k, cin]
+  int cout, cin, k, dil, pad_l, t_out;
+  const float* bias;
+  float* y;
+  int64_t y_cs, y_ts;
+  int act;
+  float act_param;
+  const float* snake_alpha;
+  float snake_eps;
+  const float* res;
+  int64_t r_cs, r_ts;
+};
+constexpr int FBK = 32, FLS = FBK + 4;
+
+__device__ __forceinline__ void fast_mma(const float* As, const float* Bs, int wm, int wn, int r32, int h,
+                                         f32x16& acc) {
+  const float* as = &As[(wm + r32) * FLS + h * 4];
+  const float* bs = &Bs[(wn + r32) * FLS + h * 4];
+#pragma unroll
+  for (int g = 0; g < FBK / 8; ++g) {
+    const float4 av = *reinterpret_cast<const float4*>(as + g * 8);
+    const float4 bv = *reinterpret_cast<const float4*>(bs + g * 8);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_conv_fast(ConvFast p) {
+  __shared__ float As[2][64 * FLS];  // [co][k]
+  __shared__ float Bs[2][64 * FLS];  // [t][k]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int lrow = tid >> 3, lk = (tid & 7) * 4;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int K = p.k * p.cin;
+  const float* wa0 = p.w + (int64_t)min(m0 + lrow, p.cout - 1) * K + lk;
+  const float* wa1 = p.w + (int64_t)min(m0 + lrow + 32, p.cout - 1) * K + lk;
+  const int tt = tid & 63, cg = tid >> 6;  // B: time column, group of 8 channels
+  const int t = n0 + tt;
+  const int tin_up = p.t_in * p.up;
+  const float* xb = p.x + (int64_t)(cg * 8) * p.x_cs;
+  const int S = K / FBK;        // even: cin % 64 == 0
+  const int cpt = p.cin / FBK;  // stages per tap
+  f32x16 acc = {0.f};
+  float4 xa0, xa1, ya0, ya1;
+  float xv[8], yv[8];
+  // stage s: tap j = s / cpt, channels [c0, c0 + 32), c0 = (s % cpt) * 32; the padded and
+  // out-of-range time positions load a valid element and are replaced by zero after the load
+#define CV3_CLOAD(A0, A1, V, S_)                                                                  \
+  {                                                                                               \
+    const int s_ = (S_);                                                                          \
+    const int j_ = s_ / cpt, c0_ = (s_ - j_ * cpt) * FBK;                                         \
+    A0 = *reinterpret_cast<const float4*>(wa0 + s_ * FBK);                                        \
+    A1 = *reinterpret_cast<const float4*>(wa1 + s_ * FBK);                                        \
+    const int u_ = t + j_ * p.dil - p.pad_l;                                                      \
+    const bool ok_ = u_ >= 0 && u_ < tin_up && t < p.t_out;                                       \
+    const int src_ = ok_ ? (p.up == 1 ? u_ : (int)((unsigned)u_ / (unsigned)p.up)) : 0;           \
+    const float* xp_ = xb + (int64_t)c0_ * p.x_cs + src_;                                         \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) V[i_] = xp_[(int64_t)i_ * p.x_cs];           \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) V[i_] = ok_ ? V[i_] : 0.f;                   \
+  }
+#define CV3_CSTORE(BUF, A0, A1, V)                                                                       \
+  *reinterpret_cast<float4*>(&As[BUF][lrow * FLS + lk]) = A0;                                            \
+  *reinterpret_cast<float4*>(&As[BUF][(lrow + 32) * FLS + lk]) = A1;                                     \
+  *reinterpret_cast<float4*>(&Bs[BUF][tt * FLS + cg * 8]) = make_float4(V[0], V[1], V[2], V[3]);         \
+  *reinterpret_cast<float4*>(&Bs[BUF][tt * FLS + cg * 8 + 4]) = make_float4(V[4], V[5], V[6], V[7]);
+  CV3_CLOAD(xa0, xa1, xv, 0)
+  CV3_CLOAD(ya0, ya1, yv, 1)
+  CV3_CSTORE(0, xa0, xa1, xv)
+  __syncthreads();
+  for (int s = 0; s + 2 < S; s += 2) {
+    // LDS[0] = stage s, y = stage s + 1 in flight
+    CV3_CLOAD(xa0, xa1, xv, s + 2)
+    __builtin_amdgcn_sched_barrier(0);  // issue the loads before the MFMAs
+    fast_mma(As[0], Bs[0], wm, wn, r32, h, acc);
+    CV3_CSTORE(1, ya0, ya1, yv)
+    __syncthreads();
+    CV3_CLOAD(ya0, ya1, yv, s + 3)
+    __builtin_amdgcn_sched_barrier(0);
+    fast_mma(As[1], Bs[1], wm, wn, r32, h, acc);
+    CV3_CSTORE(0, xa0, xa1, xv)
+    __syncthreads();
+  }
+  fast_mma(As[0], Bs[0], wm, wn, r32, h, acc);
+  CV3_CSTORE(1, ya0, ya1, yv)
+  __syncthreads();
+  fast_mma(As[1], Bs[1], wm, wn, r32, h, acc);
+#undef CV3_CLOAD
+#undef CV3_CSTORE
+  // epilogue (same operand-first order as k_conv_mfma)
+  const int tc = n0 + wn + r32;
+  if (tc >= p.t_out) return;
+  float bias[16], alpha[16], res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int co = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), p.cout - 1);
+    bias[i] = p.bias ? p.bias[co] : 0.f;
+    alpha[i] = p.snake_alpha ? p.snake_alpha[co] : 0.f;
+    res[i] = p.res ? p.res[co * p.r_cs + tc * p.r_ts] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int co = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (co < p.cout) {
+      float v = acc[i] + bias[i];
+      if (p.snake_alpha) {
+        const float sn = sinf(alpha[i] * v);
+        v = v + (1.0f / (alpha[i] + p.snake_eps)) * (sn * sn);
+      } else {
+        v = apply_act(p.act, v, p.act_param);
+      }
+      if (p.res) v = res[i] + v;
+      p.y[co * p.y_cs + tc * p.y_ts] = v;
+    }
+  }
+}
+
 // groups == C convolution as k shifted multiply-accumulates (ops.py:222-237)
 __global__ void k_depthwise(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
                             float* __restrict__ y, int64_t c, int64_t t_in, int64_t k, int64_t dil, int64_t pad_l,
@@ -243,6 +374,50 @@ int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t 
   p.r_ts = r_ts;
   const dim3 grid((unsigned)ceil_div(t_out, BN), (unsigned)ceil_div(cout / groups, BM), (unsigned)groups);
   hipLaunchKernelGGL(k_conv_mfma, grid, dim3(256), 0, stream_of(s), p);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, const float* w_packed, int64_t cout,
+                      int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r, int64_t up,
+                      float* y, int64_t y_cs, int64_t y_ts, int act, float act_param, const float* snake_alpha,
+                      float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, cv3_stream_t s) {
+  CV3_REQUIRE(dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0 && cin > 0 && cout > 0, CV3_EINVAL,
+              "bad conv geometry");
+  CV3_REQUIRE(cin % 64 == 0, CV3_EUNSUPPORTED, "packed conv needs cin %% 64 == 0 (cin %lld)", (long long)cin);
+  CV3_REQUIRE(((uintptr_t)w_packed % 16) == 0, CV3_EINVAL, "packed conv weight must be 16-byte aligned");
+  const int64_t tp = t_in * up + pad_l + pad_r;
+  const int64_t span = dilation * (k - 1) + 1;
+  const int64_t t_out = tp >= span ? tp - span + 1 : 0;
+  CV3_REQUIRE(t_in * up < (1ll << 31) && tp < (1ll << 31) && cin * k < (1ll << 31) && cout < (1ll << 31) &&
+                  dilation * k < (1ll << 31),
+              CV3_EINVAL, "packed conv sizes exceed 32-bit indexing");
+  if (t_out <= 0) return CV3_OK;
+  ConvFast p{};
+  p.x = x;
+  p.x_cs = x_cs;
+  p.t_in = (int)t_in;
+  p.up = (int)up;
+  p.w = w_packed;
+  p.cout = (int)cout;
+  p.cin = (int)cin;
+  p.k = (int)k;
+  p.dil = (int)dilation;
+  p.pad_l = (int)pad_l;
+  p.t_out = (int)t_out;
+  p.bias = bias;
+  p.y = y;
+  p.y_cs = y_cs;
+  p.y_ts = y_ts;
+  p.act = act;
+  p.act_param = act_param;
+  p.snake_alpha = snake_alpha;
+  p.snake_eps = snake_eps;
+  p.res = residual;
+  p.r_cs = r_cs;
+  p.r_ts = r_ts;
+  const dim3 grid((unsigned)ceil_div(t_out, 64), (unsigned)ceil_div(cout, 64));
+  hipLaunchKernelGGL(k_conv_fast, grid, dim3(256), 0, stream_of(s), p);
   CV3_LAUNCHED();
   return CV3_OK;
 }

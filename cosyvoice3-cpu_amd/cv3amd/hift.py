@@ -58,6 +58,7 @@ class DeviceHiFT:
         self.nk = len(self.rb_k)
         self.up_total = int(np.prod(self.rates))
         self.w = {}
+        self.wp = {}   # conv weights repacked (out, k, in) for the stride-1 fast path
         self.shape = {}
         for name in weights.keys():
             if not name.startswith(prefix) or "f0_predictor" in name or "m_source" in name:
@@ -66,6 +67,8 @@ class DeviceHiFT:
             key = name[len(prefix):]
             self.w[key] = to_device(np.ascontiguousarray(arr))
             self.shape[key] = arr.shape
+            if arr.ndim == 3 and arr.shape[1] % 64 == 0:
+                self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
         self.window = to_device(hann_window(self.n_fft))
 
     # -- building blocks ------------------------------------------------------
@@ -77,19 +80,25 @@ class DeviceHiFT:
         nearest upsample, activation / Snake and residual epilogues."""
         cout, cin_g, k = self.shape[key + ".weight"]
         cin, t_in = x.shape
-        t_out = ctypes.c_int64()
-        _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k, None, stride,
-                  dilation, 1, pad[0], pad[1], up, None, 0, 0, _lib.ptr(t_out), 0, 0.0, None, 0.0, None, 0, 0, None)
-        n = t_out.value
+        if cin_g != cin:
+            raise ValueError(f"{key}: input has {cin} channels, weight expects {cin_g}")
+        span = dilation * (k - 1) + 1
+        n = max(0, (t_in * up + pad[0] + pad[1] - span) // stride + 1)
         if out is None:
             out = DeviceArray((cout, n))
         ld = out_ld if out_ld is not None else out.shape[1]
         alpha = self.w[snake].ptr if snake else None
         res = residual.ptr if residual is not None else None
         rld = residual.shape[1] if residual is not None else 0
-        _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k,
-                  self.w[key + ".bias"].ptr, stride, dilation, 1, pad[0], pad[1], up, out.ptr + out_col0 * F4,
-                  ld, 1, None, ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
+        wkey = key + ".weight"
+        if stride == 1 and wkey in self.wp:
+            _lib.call("conv1d_packed", x.ptr, cin, t_in, t_in, self.wp[wkey].ptr, cout, k,
+                      self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_col0 * F4, ld, 1,
+                      ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
+        else:
+            _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[wkey].ptr, cout, k,
+                      self.w[key + ".bias"].ptr, stride, dilation, 1, pad[0], pad[1], up, out.ptr + out_col0 * F4,
+                      ld, 1, None, ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
         return out
 
     def _snake(self, x: DeviceArray, key: str) -> DeviceArray:

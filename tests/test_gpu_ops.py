@@ -283,3 +283,57 @@ def test_conv1d_channels_last(dev, rng, T, k, cin, groups):
     _lib.call("conv1d_cl", xd.ptr, B, T, cin, cin, wd.ptr, cout, k, groups, k - 1, bd.ptr, yd.ptr, cout,
               ctypes.byref(epi), None)
     assert rel_err(yd.numpy(), want) < TOL
+
+
+PACKED_CASES = [
+    # cin, cout, k, dil, up, T, pad, epilogue
+    (64, 64, 11, 5, 1, 300, (50, 0), "snake"),       # HiFT stage-2 resblock conv1 + Snake
+    (64, 64, 11, 1, 1, 301, (10, 0), "residual"),    # resblock conv2 + residual
+    (128, 64, 7, 1, 3, 150, (6, 0), "none"),         # last upsampling conv (nearest x3 fused)
+    (512, 256, 16, 1, 8, 40, (15, 0), "none"),       # first upsampling conv (nearest x8 fused)
+    (256, 256, 3, 3, 1, 70, (6, 0), "leaky"),
+    (64, 18, 7, 1, 1, 200, (6, 0), "none"),          # conv_post, 18 outputs
+    (192, 100, 5, 2, 2, 33, (3, 4), "residual"),     # ragged tiles, left and right padding
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi", PACKED_CASES)
+def test_conv1d_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi):
+    """The stride-1 fast path with the weight repacked (out, k, in), against the oracle's
+    upsample + conv1d + epilogue on (channel, time) data."""
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray, to_device
+    x = rng.normal(size=(cin, T)).astype(np.float32)
+    w = (rng.normal(size=(cout, cin, k)) * 0.05).astype(np.float32)
+    b = (rng.normal(size=cout) * 0.05).astype(np.float32)
+    alpha = (np.abs(rng.normal(size=cout)) + 0.5).astype(np.float32)
+    xin = ref.interpolate_nearest(x, up) if up > 1 else x
+    y = ref.conv1d(xin, w, b, dilation=dil, pad=pad)
+    t_out = y.shape[1]
+    res = rng.normal(size=(cout, t_out)).astype(np.float32)
+    if epi == "snake":
+        want = ref.snake(y, alpha)
+    elif epi == "leaky":
+        want = ref.leaky_relu(y, 0.1)
+    elif epi == "residual":
+        want = y + res
+    else:
+        want = y
+    xd = to_device(x)
+    wd = to_device(np.ascontiguousarray(w.transpose(0, 2, 1)))
+    bd = to_device(b)
+    ad = to_device(alpha)
+    yd = to_device(res) if epi == "residual" else DeviceArray((cout, t_out))
+    _lib.call("conv1d_packed", xd.ptr, cin, T, T, wd.ptr, cout, k, bd.ptr, dil, pad[0], pad[1], up, yd.ptr,
+              t_out, 1, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
+              ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, t_out, 1, None)
+    assert rel_err(yd.numpy(), want) < TOL
+
+
+def test_conv1d_packed_rejects_unaligned_channels(dev):
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray
+    x, w, y = DeviceArray((80, 16)), DeviceArray((8, 5, 80)), DeviceArray((8, 16))
+    with pytest.raises(NotImplementedError):
+        _lib.call("conv1d_packed", x.ptr, 80, 16, 16, w.ptr, 8, 5, None, 1, 4, 0, 1, y.ptr, 16, 1, 0, 0.0,
+                  None, 1e-9, None, 0, 0, None)
