@@ -183,6 +183,8 @@ struct ConvFast {
   float snake_eps;
   const float* res;
   int64_t r_cs, r_ts;
+  float* part;  // split-K partials [ksplit, cout, t_out] (ksplit > 1), epilogue in k_conv_reduce
+  int ksplit;
 };
 constexpr int FBK = 32, FLS = FBK + 4;
 
@@ -216,7 +218,9 @@ __global__ __launch_bounds__(256) void k_conv_fast(ConvFast p) {
   const int t = n0 + tt;
   const int tin_up = p.t_in * p.up;
   const float* xb = p.x + (int64_t)(cg * 8) * p.x_cs;
-  const int S = K / FBK;        // even: cin % 64 == 0
+  // this workgroup's stages: all of them, or slice blockIdx.z of ksplit (an even count)
+  const int S = K / FBK / p.ksplit;
+  const int sb = blockIdx.z * S;
   const int cpt = p.cin / FBK;  // stages per tap
   f32x16 acc = {0.f};
   float4 xa0, xa1, ya0, ya1;
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(256) void k_conv_fast(ConvFast p) {
   // out-of-range time positions load a valid element and are replaced by zero after the load
 #define CV3_CLOAD(A0, A1, V, S_)                                                                  \
   {                                                                                               \
-    const int s_ = (S_);                                                                          \
+    const int s_ = sb + (S_);                                                                     \
     const int j_ = s_ / cpt, c0_ = (s_ - j_ * cpt) * FBK;                                         \
     A0 = *reinterpret_cast<const float4*>(wa0 + s_ * FBK);                                        \
     A1 = *reinterpret_cast<const float4*>(wa1 + s_ * FBK);                                        \
@@ -264,9 +268,18 @@ __global__ __launch_bounds__(256) void k_conv_fast(ConvFast p) {
   fast_mma(As[1], Bs[1], wm, wn, r32, h, acc);
 #undef CV3_CLOAD
 #undef CV3_CSTORE
-  // epilogue (same operand-first order as k_conv_mfma)
   const int tc = n0 + wn + r32;
   if (tc >= p.t_out) return;
+  if (p.ksplit > 1) {  // raw partial sums; k_conv_reduce adds the slices in order
+    float* dst = p.part + (int64_t)blockIdx.z * p.cout * p.t_out + tc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+      if (co < p.cout) dst[(int64_t)co * p.t_out] = acc[i];
+    }
+    return;
+  }
+  // epilogue (same operand-first order as k_conv_mfma)
   float bias[16], alpha[16], res[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -289,6 +302,28 @@ __global__ __launch_bounds__(256) void k_conv_fast(ConvFast p) {
       if (p.res) v = res[i] + v;
       p.y[co * p.y_cs + tc * p.y_ts] = v;
     }
+  }
+}
+
+// Split-K epilogue: y[co, t] = epi(sum_z part[z, co, t] + bias[co]), slices added in
+// order z = 0, 1, ... so the result does not depend on scheduling.
+__global__ void k_conv_reduce(ConvFast p) {
+  const int64_t n = (int64_t)p.cout * p.t_out;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int co = (int)(e / p.t_out), t = (int)(e - (int64_t)co * p.t_out);
+    const float r = p.res ? p.res[co * p.r_cs + t * p.r_ts] : 0.f;
+    float acc = p.part[e];
+    for (int z = 1; z < p.ksplit; ++z) acc += p.part[(int64_t)z * n + e];
+    float v = acc + (p.bias ? p.bias[co] : 0.f);
+    if (p.snake_alpha) {
+      const float a = p.snake_alpha[co];
+      const float sn = sinf(a * v);
+      v = v + (1.0f / (a + p.snake_eps)) * (sn * sn);
+    } else {
+      v = apply_act(p.act, v, p.act_param);
+    }
+    if (p.res) v = r + v;
+    p.y[co * p.y_cs + t * p.y_ts] = v;
   }
 }
 
@@ -381,9 +416,13 @@ int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t 
 int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, const float* w_packed, int64_t cout,
                       int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r, int64_t up,
                       float* y, int64_t y_cs, int64_t y_ts, int act, float act_param, const float* snake_alpha,
-                      float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, cv3_stream_t s) {
+                      float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, int64_t ksplit,
+                      float* workspace, int64_t workspace_floats, cv3_stream_t s) {
   CV3_REQUIRE(dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0 && cin > 0 && cout > 0, CV3_EINVAL,
               "bad conv geometry");
+  CV3_REQUIRE(ksplit >= 1 && ksplit <= 16 && (k * cin / FBK) % (2 * ksplit) == 0, CV3_EINVAL,
+              "ksplit %lld must divide the %lld K stages into even slices", (long long)ksplit,
+              (long long)(k * cin / FBK));
   CV3_REQUIRE(cin % 64 == 0, CV3_EUNSUPPORTED, "packed conv needs cin %% 64 == 0 (cin %lld)", (long long)cin);
   CV3_REQUIRE(((uintptr_t)w_packed % 16) == 0, CV3_EINVAL, "packed conv weight must be 16-byte aligned");
   const int64_t tp = t_in * up + pad_l + pad_r;
@@ -393,6 +432,8 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
                   dilation * k < (1ll << 31),
               CV3_EINVAL, "packed conv sizes exceed 32-bit indexing");
   if (t_out <= 0) return CV3_OK;
+  CV3_REQUIRE(ksplit == 1 || (workspace && workspace_floats >= ksplit * cout * t_out), CV3_EINVAL,
+              "split-K conv needs a workspace of ksplit * cout * t_out floats");
   ConvFast p{};
   p.x = x;
   p.x_cs = x_cs;
@@ -416,9 +457,17 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
   p.res = residual;
   p.r_cs = r_cs;
   p.r_ts = r_ts;
-  const dim3 grid((unsigned)ceil_div(t_out, 64), (unsigned)ceil_div(cout, 64));
+  p.part = workspace;
+  p.ksplit = (int)ksplit;
+  const dim3 grid((unsigned)ceil_div(t_out, 64), (unsigned)ceil_div(cout, 64), (unsigned)ksplit);
   hipLaunchKernelGGL(k_conv_fast, grid, dim3(256), 0, stream_of(s), p);
   CV3_LAUNCHED();
+  if (ksplit > 1) {
+    const int64_t n = cout * t_out;
+    hipLaunchKernelGGL(k_conv_reduce, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0,
+                       stream_of(s), p);
+    CV3_LAUNCHED();
+  }
   return CV3_OK;
 }
 

@@ -23,7 +23,7 @@ from typing import Optional
 import numpy as np
 
 from . import _lib
-from .device import DeviceArray, to_device
+from .device import DeviceArray, Graph, to_device
 
 ACT = _lib.ACT
 F4 = 4
@@ -32,6 +32,19 @@ F4 = 4
 def causal_pad(kernel_size: int, dilation: int = 1) -> int:
     """int((k d - d) / 2) * 2 + (k + 1) % 2 (hift.py:14-16)."""
     return int((kernel_size * dilation - dilation) / 2) * 2 + (kernel_size + 1) % 2
+
+
+def split_k(t_out: int, cout: int, stages: int) -> int:
+    """K slices for the packed conv: grids under 160 tiles of 64 x 64 (a 1 s chunk's
+    256-channel stage has 60) are split until they cover about two tiles per CU; each
+    slice keeps an even number of the k*cin/32 stages."""
+    tiles = -(-t_out // 64) * -(-cout // 64)
+    if tiles >= 160:
+        return 1
+    for ks in (8, 4, 2):
+        if tiles * ks <= 512 and stages % (2 * ks) == 0:
+            return ks
+    return 1
 
 
 def hann_window(n: int) -> np.ndarray:
@@ -70,6 +83,26 @@ class DeviceHiFT:
             if arr.ndim == 3 and arr.shape[1] % 64 == 0:
                 self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
         self.window = to_device(hann_window(self.n_fft))
+        # captured spectral stacks, one per input length: (graph, mel in, source STFT in, out, arena)
+        self._graphs = {}
+        self._arena = None       # while recording or capturing: every intermediate of the stack
+        self._arena_i = -1       # >= 0 while capturing: the next arena entry to hand out
+
+    def _new(self, shape) -> DeviceArray:
+        """A fresh intermediate.  While a stack is recorded, every intermediate is kept
+        (the arena); while it is captured, the recorded arrays are handed out again in
+        order, so the capture allocates and frees nothing and the graph owns its memory."""
+        if self._arena is None:
+            return DeviceArray(shape)
+        if self._arena_i >= 0:
+            a = self._arena[self._arena_i]
+            self._arena_i += 1
+            if a.shape != tuple(shape):
+                raise RuntimeError(f"captured stack diverged from its recording: {a.shape} vs {tuple(shape)}")
+            return a
+        a = DeviceArray(shape)
+        self._arena.append(a)
+        return a
 
     # -- building blocks ------------------------------------------------------
     def _conv(self, x: DeviceArray, key: str, stride: int = 1, dilation: int = 1, pad=(0, 0), up: int = 1,
@@ -85,16 +118,19 @@ class DeviceHiFT:
         span = dilation * (k - 1) + 1
         n = max(0, (t_in * up + pad[0] + pad[1] - span) // stride + 1)
         if out is None:
-            out = DeviceArray((cout, n))
+            out = self._new((cout, n))
         ld = out_ld if out_ld is not None else out.shape[1]
         alpha = self.w[snake].ptr if snake else None
         res = residual.ptr if residual is not None else None
         rld = residual.shape[1] if residual is not None else 0
         wkey = key + ".weight"
         if stride == 1 and wkey in self.wp:
+            ks = split_k(n, cout, k * cin // 32)
+            ws = self._new((ks * cout * n,)) if ks > 1 else None
             _lib.call("conv1d_packed", x.ptr, cin, t_in, t_in, self.wp[wkey].ptr, cout, k,
                       self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_col0 * F4, ld, 1,
-                      ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
+                      ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, ks, ws.ptr if ws else None,
+                      ws.size if ws else 0, None)
         else:
             _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[wkey].ptr, cout, k,
                       self.w[key + ".bias"].ptr, stride, dilation, 1, pad[0], pad[1], up, out.ptr + out_col0 * F4,
@@ -102,12 +138,12 @@ class DeviceHiFT:
         return out
 
     def _snake(self, x: DeviceArray, key: str) -> DeviceArray:
-        y = DeviceArray(x.shape)
+        y = self._new(x.shape)
         _lib.call("snake", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, None)
         return y
 
     def _act(self, x: DeviceArray, name: str, param: float) -> DeviceArray:
-        y = DeviceArray(x.shape)
+        y = self._new(x.shape)
         _lib.call("act", ACT[name], float(param), x.ptr, y.ptr, x.size, None)
         return y
 
@@ -120,7 +156,7 @@ class DeviceHiFT:
             y = self._snake(cur, base + f"activations1.{j}.alpha")
             y = self._conv(y, base + f"convs1.{j}", dilation=d, pad=(causal_pad(kernel, d), 0),
                            snake=base + f"activations2.{j}.alpha")
-            out = DeviceArray(x.shape) if cur is x else cur   # in place after the first step
+            out = self._new(x.shape) if cur is x else cur   # in place after the first step
             cur = self._conv(y, base + f"convs2.{j}", pad=(causal_pad(kernel, 1), 0), residual=cur, out=out)
         return cur
 
@@ -138,7 +174,7 @@ class DeviceHiFT:
             t_up = x.shape[1] * r
             if i == len(self.rates) - 1:
                 # reflect pad (1, 0): columns 1.. hold the conv, column 0 copies column 2 (hift.py:144)
-                xu = DeviceArray((cout, t_up + 1))
+                xu = self._new((cout, t_up + 1))
                 self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0), out=xu, out_col0=1, out_ld=t_up + 1)
                 S3 = ctypes.c_int64 * 3
                 _lib.call("copy_strided", xu.ptr + 2 * F4, xu.ptr, 1, cout, 1, S3(0, t_up + 1, 1),
@@ -154,13 +190,13 @@ class DeviceHiFT:
             si = self._resblock("source_resblocks", i, si, self.src_k[i], self.src_d[i])
             if si.shape != xu.shape:
                 raise ValueError(f"stage {i}: source branch {si.shape} vs upsampled {xu.shape}")
-            xs = DeviceArray(xu.shape)
+            xs = self._new(xu.shape)
             _lib.call("binary", 0, xu.ptr, si.ptr, xs.ptr, xs.size, 0.0, 0.0, None)
             rs = [self._resblock("resblocks", i * self.nk + j, xs, self.rb_k[j], self.rb_d[j])
                   for j in range(self.nk)]
             acc = rs[0]
             for j in range(1, self.nk):
-                nxt = DeviceArray(xs.shape)
+                nxt = self._new(xs.shape)
                 if j == self.nk - 1:   # ((r0 + r1) + r2) / 3 (hift.py:161-165)
                     _lib.call("binary", 4, acc.ptr, rs[j].ptr, nxt.ptr, nxt.size, float(self.nk), 0.0, None)
                 else:
@@ -171,7 +207,52 @@ class DeviceHiFT:
         kpost = self.shape["conv_post.weight"][2]
         return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0))
 
-    def spectral_chunked(self, mel: DeviceArray, s_stft: DeviceArray, chunk: int, context: int) -> DeviceArray:
+    def _stack(self, w: int):
+        """The spectral stack for a w-frame input, captured once: its staging inputs, its
+        output and the graph.  Recorded eagerly first (on zeroed inputs), then captured
+        with the recorded intermediates (see ``_new``)."""
+        g = self._graphs.get(w)
+        if g is None:
+            mel_w = DeviceArray((self.shape["conv_pre.weight"][1], w))
+            st_w = DeviceArray((self.n_fft + 2, w * self.up_total + 1))
+            _lib.call("fill_zero", mel_w.ptr, mel_w.nbytes, None)
+            _lib.call("fill_zero", st_w.ptr, st_w.nbytes, None)
+            self._arena, self._arena_i = [], -1
+            try:
+                out = self.spectral(mel_w, st_w)
+                self._arena_i = 0
+                graph = Graph()
+                with graph:
+                    again = self.spectral(mel_w, st_w)
+                if again is not out or self._arena_i != len(self._arena):
+                    raise RuntimeError("captured stack diverged from its recording")
+                g = (graph, mel_w, st_w, out, self._arena)
+            finally:
+                self._arena, self._arena_i = None, -1
+            self._graphs[w] = g
+        return g
+
+    def spectral_graph(self, mel: DeviceArray, s_stft: DeviceArray, c0: int = 0, c1: Optional[int] = None):
+        """spectral() of mel[:, c0:c1] and its source STFT columns by graph replay; returns the
+        stack's own output buffer, valid until the next replay of the same length."""
+        t = mel.shape[1]
+        c1 = t if c1 is None else c1
+        w = c1 - c0
+        graph, mel_w, st_w, out, _ = self._stack(w)
+        S3 = ctypes.c_int64 * 3
+        up = self.up_total
+        _lib.call("copy_strided", mel.ptr + c0 * F4, mel_w.ptr, 1, mel.shape[0], w, S3(0, t, 1), S3(0, w, 1), None)
+        fs = s_stft.shape[1]
+        f0, f1 = c0 * up, min(fs, c1 * up + 1)
+        if f1 - f0 != st_w.shape[1]:
+            raise ValueError(f"source STFT has {fs} frames, expected {t * up + 1}")
+        _lib.call("copy_strided", s_stft.ptr + f0 * F4, st_w.ptr, 1, s_stft.shape[0], f1 - f0, S3(0, fs, 1),
+                  S3(0, f1 - f0, 1), None)
+        graph.launch()
+        return out
+
+    def spectral_chunked(self, mel: DeviceArray, s_stft: DeviceArray, chunk: int, context: int,
+                         graph: bool = True) -> DeviceArray:
         """Windows of ``chunk`` frames with ``context`` frames of history and conv_pre's
         lookahead, cut back to the window's own samples (hift.py:170-194)."""
         up = self.up_total
@@ -184,6 +265,14 @@ class DeviceHiFT:
             m1 = min(t, m0 + chunk)
             c0 = max(0, m0 - context)
             c1 = min(t, m1 + look)
+            lead = (m0 - c0) * up
+            take = (m1 - m0) * up
+            src0, dst0, n = (0, 0, 1 + take) if m0 == 0 else (1 + lead, 1 + m0 * up, take)
+            if graph:
+                sub = self.spectral_graph(mel, s_stft, c0, c1)
+                _lib.call("copy_strided", sub.ptr + src0 * F4, out.ptr + dst0 * F4, 1, nout, n,
+                          S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), None)
+                continue
             sub_mel = DeviceArray((mel.shape[0], c1 - c0))
             _lib.call("copy_strided", mel.ptr + c0 * F4, sub_mel.ptr, 1, mel.shape[0], c1 - c0,
                       S3(0, t, 1), S3(0, c1 - c0, 1), None)
@@ -193,9 +282,6 @@ class DeviceHiFT:
             _lib.call("copy_strided", s_stft.ptr + f0 * F4, sub_s.ptr, 1, s_stft.shape[0], f1 - f0,
                       S3(0, fs, 1), S3(0, f1 - f0, 1), None)
             sub = self.spectral(sub_mel, sub_s)
-            lead = (m0 - c0) * up
-            take = (m1 - m0) * up
-            src0, dst0, n = (0, 0, 1 + take) if m0 == 0 else (1 + lead, 1 + m0 * up, take)
             _lib.call("copy_strided", sub.ptr + src0 * F4, out.ptr + dst0 * F4, 1, nout, n,
                       S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), None)
         return out
@@ -224,16 +310,17 @@ class DeviceHiFT:
                   -1, self.limit, buf.ptr, y.ptr, None, None)
         return y
 
-    def decode(self, mel, source, chunk: Optional[int] = None, context: int = 64) -> DeviceArray:
+    def decode(self, mel, source, chunk: Optional[int] = None, context: int = 64, graph: bool = True) -> DeviceArray:
         """(80, T) mel + (480 T,) source -> (480 T,) waveform (hift.py:196-210).  Host or
-        device inputs; the result stays resident."""
+        device inputs; the result stays resident.  With ``graph`` the spectral stack of each
+        input length is captured on first use and replayed (one launch per window)."""
         mel_d = mel if isinstance(mel, DeviceArray) else to_device(np.ascontiguousarray(mel, np.float32))
         src_d = source if isinstance(source, DeviceArray) else to_device(np.ascontiguousarray(source, np.float32))
         s_stft = self.source_stft(src_d)
         if chunk is None or mel_d.shape[1] <= chunk:
-            x = self.spectral(mel_d, s_stft)
+            x = self.spectral_graph(mel_d, s_stft) if graph else self.spectral(mel_d, s_stft)
         else:
-            x = self.spectral_chunked(mel_d, s_stft, chunk, context)
+            x = self.spectral_chunked(mel_d, s_stft, chunk, context, graph=graph)
         return self.istft_head(x)
 
     def flops(self, t: int) -> float:

@@ -184,11 +184,14 @@ int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t 
                int64_t r_ts, cv3_stream_t s);
 /* ops.conv1d (ops.py:165-219) for stride 1 and groups 1, the HiFT convs (hift.py:112-163): as cv3_conv1d, with
  * W (cout, cin, k) repacked as w_packed (cout, k, cin) and x time-contiguous (x_ts == 1); output length
- * t_in*up + pad_l + pad_r - dilation*(k-1).  Needs cin % 64 == 0 (else CV3_EUNSUPPORTED). */
+ * t_in*up + pad_l + pad_r - dilation*(k-1).  Needs cin % 64 == 0 (else CV3_EUNSUPPORTED).  ksplit > 1 splits
+ * the k*cin/32 reduction stages into ksplit even slices for small grids: partial sums go to `workspace`
+ * (>= ksplit*cout*t_out floats) and are added in slice order before the epilogue (deterministic). */
 int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, const float* w_packed, int64_t cout,
                       int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r, int64_t up,
                       float* y, int64_t y_cs, int64_t y_ts, int act, float act_param, const float* snake_alpha,
-                      float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, cv3_stream_t s);
+                      float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, int64_t ksplit,
+                      float* workspace, int64_t workspace_floats, cv3_stream_t s);
 /* The DiT's grouped causal conv_pos (dit.py:99-112, ops.conv1d with groups) on channels-last activations:
  * x [batch, t, ldx] (cin channels), y [batch, t, ldy] (cout channels),
  * y[b, s, co] = epi(bias[co] + sum_{j<k, c<cin/groups} W[co, c, j] x[b, s + j - pad_l, g*cin/groups + c]),

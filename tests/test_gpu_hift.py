@@ -5,7 +5,8 @@ reference) comes from the oracle; the device decodes it.  Bars:
 * the reference's toy checkpoint: the frozen upstream waveform within the
   reference's 2e-3, the oracle within 1e-4, chunked == full within 1e-5;
 * the 512-channel geometry of config 4 on 1 s of mel: the oracle within 1e-4, whole
-  and in chunks (the reference's 1 s windows with 64 frames of context).
+  and in chunks (the reference's 1 s windows with 64 frames of context), launched
+  directly and by replaying the captured per-window graphs (replayed twice: identical).
 """
 
 import numpy as np
@@ -46,8 +47,8 @@ def test_toy_checkpoint(gpu, reference_io):
     assert rel_err(chunked, got) < 1e-5
 
 
-@pytest.mark.parametrize("chunk", [None, 20])
-def test_full_width_one_second(gpu, chunk):
+@pytest.mark.parametrize("chunk,graph", [(None, True), (None, False), (20, True), (20, False)])
+def test_full_width_one_second(gpu, chunk, graph):
     import oracle.quant
     from cv3amd import synth
     from cv3amd.hift import DeviceHiFT
@@ -59,11 +60,14 @@ def test_full_width_one_second(gpu, chunk):
     rng = np.random.default_rng(4)
     mel = (rng.standard_normal((80, T), dtype=np.float32) * 2.0 - 5.0).astype(np.float32)
     source = np.tanh(rng.standard_normal(480 * T, dtype=np.float32) * 0.1).astype(np.float32)
-    print(f"[hift] base 512, {T} mel frames, chunk={chunk}", flush=True)
+    print(f"[hift] base 512, {T} mel frames, chunk={chunk}, graph={graph}", flush=True)
     h = _oracle_hift(cpu, T)
     want = h.decode(mel, source, chunk=chunk, context=64)
     d = DeviceHiFT(WeightStore(t, meta))
-    got = d.decode(mel, source, chunk=chunk, context=64).numpy()
+    got = d.decode(mel, source, chunk=chunk, context=64, graph=graph).numpy()
     e = rel_err(got, want)
+    if graph:  # a second replay of the captured stacks gives the same samples
+        again = d.decode(mel, source, chunk=chunk, context=64, graph=graph).numpy()
+        assert np.array_equal(again, got)
     print(f"[hift] rel err {e:.2e}", flush=True)
     assert e < 1e-4

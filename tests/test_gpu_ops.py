@@ -286,19 +286,23 @@ def test_conv1d_channels_last(dev, rng, T, k, cin, groups):
 
 
 PACKED_CASES = [
-    # cin, cout, k, dil, up, T, pad, epilogue
-    (64, 64, 11, 5, 1, 300, (50, 0), "snake"),       # HiFT stage-2 resblock conv1 + Snake
-    (64, 64, 11, 1, 1, 301, (10, 0), "residual"),    # resblock conv2 + residual
-    (128, 64, 7, 1, 3, 150, (6, 0), "none"),         # last upsampling conv (nearest x3 fused)
-    (512, 256, 16, 1, 8, 40, (15, 0), "none"),       # first upsampling conv (nearest x8 fused)
-    (256, 256, 3, 3, 1, 70, (6, 0), "leaky"),
-    (64, 18, 7, 1, 1, 200, (6, 0), "none"),          # conv_post, 18 outputs
-    (192, 100, 5, 2, 2, 33, (3, 4), "residual"),     # ragged tiles, left and right padding
+    # cin, cout, k, dil, up, T, pad, epilogue, K slices
+    (64, 64, 11, 5, 1, 300, (50, 0), "snake", 1),       # HiFT stage-2 resblock conv1 + Snake
+    (64, 64, 11, 1, 1, 301, (10, 0), "residual", 1),    # resblock conv2 + residual
+    (128, 64, 7, 1, 3, 150, (6, 0), "none", 1),         # last upsampling conv (nearest x3 fused)
+    (512, 256, 16, 1, 8, 40, (15, 0), "none", 1),       # first upsampling conv (nearest x8 fused)
+    (256, 256, 3, 3, 1, 70, (6, 0), "leaky", 1),
+    (64, 18, 7, 1, 1, 200, (6, 0), "none", 1),          # conv_post, 18 outputs
+    (192, 100, 5, 2, 2, 33, (3, 4), "residual", 1),     # ragged tiles, left and right padding
+    (256, 256, 11, 1, 1, 944, (10, 0), "snake", 4),     # 1 s-chunk stage-0 conv, split 4 ways
+    (512, 256, 16, 1, 8, 14, (15, 0), "none", 8),       # 1 s-chunk first upsampling conv, 8 ways
+    (256, 256, 11, 3, 1, 300, (30, 0), "residual", 4),  # split-K with an in-place residual
+    (128, 128, 7, 5, 1, 99, (30, 0), "leaky", 2),
 ]
 
 
-@pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi", PACKED_CASES)
-def test_conv1d_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi):
+@pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi,ks", PACKED_CASES)
+def test_conv1d_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks):
     """The stride-1 fast path with the weight repacked (out, k, in), against the oracle's
     upsample + conv1d + epilogue on (channel, time) data."""
     from cv3amd import _lib
@@ -324,10 +328,15 @@ def test_conv1d_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi):
     bd = to_device(b)
     ad = to_device(alpha)
     yd = to_device(res) if epi == "residual" else DeviceArray((cout, t_out))
-    _lib.call("conv1d_packed", xd.ptr, cin, T, T, wd.ptr, cout, k, bd.ptr, dil, pad[0], pad[1], up, yd.ptr,
-              t_out, 1, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
-              ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, t_out, 1, None)
-    assert rel_err(yd.numpy(), want) < TOL
+    ws = DeviceArray((ks * cout * t_out,)) if ks > 1 else None
+    for _ in range(2):  # the second call sees the first call's partials in the workspace
+        if epi == "residual":
+            _lib.call("copy_h2d", yd.ptr, res.ctypes.data, res.nbytes, None)
+        _lib.call("conv1d_packed", xd.ptr, cin, T, T, wd.ptr, cout, k, bd.ptr, dil, pad[0], pad[1], up, yd.ptr,
+                  t_out, 1, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
+                  ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, t_out, 1,
+                  ks, ws.ptr if ws else None, ws.size if ws else 0, None)
+        assert rel_err(yd.numpy(), want) < TOL
 
 
 def test_conv1d_packed_rejects_unaligned_channels(dev):
@@ -336,4 +345,14 @@ def test_conv1d_packed_rejects_unaligned_channels(dev):
     x, w, y = DeviceArray((80, 16)), DeviceArray((8, 5, 80)), DeviceArray((8, 16))
     with pytest.raises(NotImplementedError):
         _lib.call("conv1d_packed", x.ptr, 80, 16, 16, w.ptr, 8, 5, None, 1, 4, 0, 1, y.ptr, 16, 1, 0, 0.0,
-                  None, 1e-9, None, 0, 0, None)
+                  None, 1e-9, None, 0, 0, 1, None, 0, None)
+
+
+def test_conv1d_packed_rejects_odd_split(dev):
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray
+    x, w, y = DeviceArray((64, 16)), DeviceArray((8, 3, 64)), DeviceArray((8, 16))
+    ws = DeviceArray((2 * 8 * 16,))
+    with pytest.raises(ValueError):   # 3 taps x 2 stages = 6 stages: not 2 even slices
+        _lib.call("conv1d_packed", x.ptr, 64, 16, 16, w.ptr, 8, 3, None, 1, 2, 0, 1, y.ptr, 16, 1, 0, 0.0,
+                  None, 1e-9, None, 0, 0, 2, ws.ptr, ws.size, None)
