@@ -67,7 +67,8 @@ def parse_header(path: str = HEADER):
     return decls
 
 
-_lock = threading.Lock()
+# re-entrant: init() holds it while its call() loads the library through lib()
+_lock = threading.RLock()
 _lib = None
 _inited = False
 

@@ -46,3 +46,16 @@ def test_no_cpu_fallback_in_the_package():
             if f.endswith(".py"):
                 src = open(os.path.join(dp, f)).read()
                 assert "import oracle" not in src and "from oracle" not in src, f
+
+
+def test_init_as_the_first_library_call_does_not_deadlock():
+    """``_lib.init()`` holds the module lock while its own call loads the library; as the
+    first call of a fresh process it must return (or raise without a GPU), not block."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from cv3amd import _lib\n"
+            "try:\n    _lib.init()\nexcept Exception as e:\n    print(type(e).__name__)\n"
+            "print('returned')\n") % os.path.join(ROOT, "cosyvoice3-cpu_amd")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=60)
+    assert "returned" in r.stdout, r.stdout + r.stderr
