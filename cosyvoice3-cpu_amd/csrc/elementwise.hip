@@ -186,6 +186,79 @@ __global__ __launch_bounds__(256) void k_layer_norm4(const float* __restrict__ x
   }
 }
 
+// One wave per row for rows of at most 256 * 4 columns: each lane holds NV float4 of the
+// row (and of w / b / shift / scale), loaded up front with clamped indices and zeroed
+// past the row after the loads; mean and centred variance are wave reductions, so a
+// row needs no barrier.  Four rows per 256-thread workgroup.
+template <int NV>
+__global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict__ x, float* __restrict__ y,
+                                                         int64_t rows, int64_t cols, float eps,
+                                                         const float* __restrict__ w, const float* __restrict__ b,
+                                                         const float* __restrict__ shift,
+                                                         const float* __restrict__ scale, int64_t mod_stride,
+                                                         int64_t rows_per_group) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t c4 = cols / 4;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * cols);
+  const int64_t g = rows_per_group > 0 ? row / rows_per_group : 0;
+  const float4* sh = reinterpret_cast<const float4*>(shift ? shift + g * mod_stride : x);
+  const float4* sc = reinterpret_cast<const float4*>(scale ? scale + g * mod_stride : x);
+  const float4* w4 = reinterpret_cast<const float4*>(w ? w : x);
+  const float4* b4 = reinterpret_cast<const float4*>(b ? b : x);
+  float4 v[NV], wv[NV], bv[NV], shv[NV], scv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t j = min((int64_t)lane + 64 * i, c4 - 1);
+    v[i] = xr[j];
+    wv[i] = w4[j];
+    bv[i] = b4[j];
+    shv[i] = sh[j];
+    scv[i] = sc[j];
+  }
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i >= c4) v[i] = z;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  const float mu = wave_sum(s) / (float)cols;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (lane + 64 * i < c4) {
+      const float d0 = v[i].x - mu, d1 = v[i].y - mu, d2 = v[i].z - mu, d3 = v[i].w - mu;
+      q = fmaf(d0, d0, q);
+      q = fmaf(d1, d1, q);
+      q = fmaf(d2, d2, q);
+      q = fmaf(d3, d3, q);
+    }
+  }
+  const float den = sqrtf(wave_sum(q) / (float)cols + eps);
+  float4* yr = reinterpret_cast<float4*>(y + row * cols);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t j = lane + 64 * i;
+    if (j < c4) {
+      float o[4] = {(v[i].x - mu) / den, (v[i].y - mu) / den, (v[i].z - mu) / den, (v[i].w - mu) / den};
+      const float ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      const float bb[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
+      const float ss[4] = {shv[i].x, shv[i].y, shv[i].z, shv[i].w};
+      const float cc[4] = {scv[i].x, scv[i].y, scv[i].z, scv[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (w) o[e] = o[e] * ww[e];
+        if (b) o[e] = o[e] + bb[e];
+        if (scale) o[e] = o[e] * (1.0f + cc[e]);
+        if (shift) o[e] = o[e] + ss[e];
+      }
+      yr[j] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
 // Rotary tables.  kind 0 (DiT, dit.py:21-29,51-52): angle_f32 = f32(t * inv_f64),
 // interleaved duplicate, cos/sin in fp32.  kind 1 (Qwen2, qwen2.py:46-56):
 // angle in fp64, half-split duplicate, cos/sin in fp64 then rounded to fp32.
@@ -372,9 +445,20 @@ int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float e
   auto a16 = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
   const bool vec = cols % 4 == 0 && cols <= 4096 && a16(x) && a16(y) && a16(w) && a16(b) && a16(shift) &&
                    a16(scale) && mod_stride % 4 == 0;
-  if (vec && cols <= 1024)
-    hipLaunchKernelGGL(k_layer_norm4<1>, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, y, cols, eps, w, b,
-                       shift, scale, mod_stride, rows_per_group);
+  if (vec && cols <= 1024) {
+    const dim3 grid((unsigned)ceil_div(rows, 4));
+#define CV3_LNW(NV)                                                                                    \
+  hipLaunchKernelGGL(k_layer_norm_wave<NV>, grid, dim3(256), 0, stream_of(s), x, y, rows, cols, eps, w, b, \
+                     shift, scale, mod_stride, rows_per_group);
+    if (cols <= 256) {
+      CV3_LNW(1)
+    } else if (cols <= 512) {
+      CV3_LNW(2)
+    } else {
+      CV3_LNW(4)
+    }
+#undef CV3_LNW
+  }
   else if (vec)
     hipLaunchKernelGGL(k_layer_norm4<4>, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, y, cols, eps, w, b,
                        shift, scale, mod_stride, rows_per_group);

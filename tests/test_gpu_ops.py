@@ -70,6 +70,18 @@ def test_norms(dev, rng):
     assert rel_err(ops.layer_norm(x, w, b), ref.layer_norm(x, w, b)) < TOL
 
 
+@pytest.mark.parametrize("cols", [4, 200, 256, 260, 512, 1020, 1024, 2048])
+def test_layer_norm_widths(dev, rng, cols):
+    """Row widths on both sides of the one-wave-per-row kernel's 256 / 512 / 1024 limits,
+    with an odd row count (a partly filled last workgroup)."""
+    ops, _ = dev
+    x = (rng.normal(size=(7, cols)) * 2 - 0.5).astype(np.float32)
+    w = rng.normal(size=cols).astype(np.float32)
+    b = rng.normal(size=cols).astype(np.float32)
+    assert rel_err(ops.layer_norm(x, w, b, 1e-6), ref.layer_norm(x, w, b, 1e-6)) < TOL
+    assert rel_err(ops.layer_norm(x, None, None), ref.layer_norm(x, None, None)) < TOL
+
+
 @pytest.mark.parametrize("n,k,block", [(896, 896, 64), (128, 896, 64), (4864, 896, 64), (896, 4864, 64),
                                        (37, 200, 64), (9, 100, 64), (6144, 1024, 64)])
 def test_quantize_q8_bit_exact(dev, n, k, block):
