@@ -62,6 +62,9 @@ constexpr int QT = 64;        // queries per workgroup
 // key range is split between them.  Each wave keeps its own online softmax
 // (max, sum, output) and the two groups merge in LDS at the end:
 //   M = max(m0, m1), l = l0 e^{m0-M} + l1 e^{m1-M}, o = o0 e^{m0-M} + o1 e^{m1-M}.
+// Per tile a wave scores all 64 keys (64 MFMAs), rescales its running state once,
+// then accumulates P V (64 MFMAs).  V is staged transposed ([dim][key]) so the
+// P V operands of four consecutive keys are one 16-byte LDS read.
 __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
   __shared__ float Ks[2][KT * KS];
   __shared__ float Vs[2][KT * KS];
@@ -96,8 +99,11 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
   // The next stage's 128 K/V rows are loaded into registers while the current stage
   // is computed.  Rows past m are clamped to m - 1 (always in bounds); their scores
   // are masked to -inf below, so the loads carry no predicates.
-  // thread -> tile tid/256, keys (tid%256)/16 + 16r (r < 4), dims (tid%16)*4 .. +3
+  // K: thread -> tile tid/256, keys (tid%256)/16 + 16r (r < 4), dims (tid%16)*4 .. +3.
+  // V: thread -> tile tid/256, key tid%64, dims ((tid/64)%4)*16 .. +15, so the transposed
+  // LDS stores of one wave hit 64 consecutive keys of a dim row.
   const int ltile = tid >> 8, lkey = (tid & 255) >> 4, ld4 = (tid & 15) * 4;
+  const int vkey = tid & 63, vd = ((tid >> 6) & 3) * 16;
   float4 k0r, k1r, k2r, k3r, v0r, v1r, v2r, v3r;
 #define CV3_KV_LOAD(KOFF)                                                                        \
   {                                                                                              \
@@ -108,10 +114,11 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
     k1r = *reinterpret_cast<const float4*>(kbase + j1 * p.k_sm + ld4);                           \
     k2r = *reinterpret_cast<const float4*>(kbase + j2 * p.k_sm + ld4);                           \
     k3r = *reinterpret_cast<const float4*>(kbase + j3 * p.k_sm + ld4);                           \
-    v0r = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + ld4);                           \
-    v1r = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + ld4);                           \
-    v2r = *reinterpret_cast<const float4*>(vbase + j2 * p.v_sm + ld4);                           \
-    v3r = *reinterpret_cast<const float4*>(vbase + j3 * p.v_sm + ld4);                           \
+    const float* vr_ = vbase + min((KOFF) + ltile * KT + vkey, p.m - 1) * p.v_sm + vd;            \
+    v0r = *reinterpret_cast<const float4*>(vr_);                                                 \
+    v1r = *reinterpret_cast<const float4*>(vr_ + 4);                                             \
+    v2r = *reinterpret_cast<const float4*>(vr_ + 8);                                             \
+    v3r = *reinterpret_cast<const float4*>(vr_ + 12);                                            \
   }
   CV3_KV_LOAD((int64_t)0)
   for (int64_t st = 0; st < nstages; ++st) {
@@ -123,66 +130,76 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
     *reinterpret_cast<float4*>(&kt_[(lkey + 16) * KS + ld4]) = k1r;
     *reinterpret_cast<float4*>(&kt_[(lkey + 32) * KS + ld4]) = k2r;
     *reinterpret_cast<float4*>(&kt_[(lkey + 48) * KS + ld4]) = k3r;
-    *reinterpret_cast<float4*>(&vt_[lkey * KS + ld4]) = v0r;
-    *reinterpret_cast<float4*>(&vt_[(lkey + 16) * KS + ld4]) = v1r;
-    *reinterpret_cast<float4*>(&vt_[(lkey + 32) * KS + ld4]) = v2r;
-    *reinterpret_cast<float4*>(&vt_[(lkey + 48) * KS + ld4]) = v3r;
+    {
+      const float vv[16] = {v0r.x, v0r.y, v0r.z, v0r.w, v1r.x, v1r.y, v1r.z, v1r.w,
+                            v2r.x, v2r.y, v2r.z, v2r.w, v3r.x, v3r.y, v3r.z, v3r.w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) vt_[(vd + e) * KS + vkey] = vv[e];
+    }
     __syncthreads();
     if (st + 1 < nstages) CV3_KV_LOAD((st + 1) * 2 * KT)
     __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this stage's math
     const float* Kt = Ks[kg];
     const float* Vt = Vs[kg];
 
+    // S^T for the tile: sub-tile sub holds keys sub*16 + 4g + i (i < 4) for query column c16
+    f32x4 s[KT / 16];
 #pragma unroll
     for (int sub = 0; sub < KT / 16; ++sub) {
-      // S^T tile: rows = 16 keys, cols = 16 queries
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
       const float* krow = &Kt[(sub * 16 + c16) * KS + g * 4];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const float4 kf = *reinterpret_cast<const float4*>(krow + s4 * 16);
-        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[s4].x, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[s4].y, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[s4].z, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[s4].w, s, 0, 0, 0);
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[s4].x, s[sub], 0, 0, 0);
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[s4].y, s[sub], 0, 0, 0);
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[s4].z, s[sub], 0, 0, 0);
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[s4].w, s[sub], 0, 0, 0);
       }
-      // s[i] = score of key k0 + sub*16 + 4g + i for query qi; copy out of the
-      // accumulator and mask with selects (no divergent writes into it)
-      float sc[4];
-      float mx = -INFINITY;
+    }
+    // copy out of the accumulators and mask with selects (no divergent writes into them)
+    float sc[KT / 16][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < KT / 16; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t kj = k0 + sub * 16 + 4 * g + i;
         const bool ok = kj >= klo && kj < khi;
-        sc[i] = ok ? s[i] : -INFINITY;
-        mx = fmaxf(mx, sc[i]);
+        sc[sub][i] = ok ? s[sub][i] : -INFINITY;
+        mx = fmaxf(mx, sc[sub][i]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Branch-free so the wave-wide MFMAs below see uniform control flow: a
-      // query column with nothing visible yet keeps alpha = 1 and p = 0.
-      const float m_new = fmaxf(m_run, mx);
-      const bool none = m_new == -INFINITY;
-      const float m_use = none ? 0.f : m_new;
-      const float alpha = none ? 1.f : expf(m_run - m_new);
-      float psum = 0.f;
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // Branch-free so the wave-wide MFMAs below see uniform control flow: a query
+    // column with nothing visible yet keeps alpha = 1 and p = 0.
+    const float m_new = fmaxf(m_run, mx);
+    const bool none = m_new == -INFINITY;
+    const float m_use = none ? 0.f : m_new;
+    const float alpha = none ? 1.f : expf(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < KT / 16; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sc[i] = expf(sc[i] - m_use);
-        psum += sc[i];
+        sc[sub][i] = expf(sc[sub][i] - m_use);
+        psum += sc[sub][i];
       }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    // O^T += V^T P^T: the A operand of key group i is V^T[db*16 + c16][sub*16 + 4g + i]
+#pragma unroll
+    for (int sub = 0; sub < KT / 16; ++sub)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        oacc[db] *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float vf = Vt[(sub * 16 + 4 * g + i) * KS + db * 16 + c16];
-          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, sc[i], oacc[db], 0, 0, 0);
-        }
+        const float4 vf = *reinterpret_cast<const float4*>(&Vt[(db * 16 + c16) * KS + sub * 16 + 4 * g]);
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, sc[sub][0], oacc[db], 0, 0, 0);
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, sc[sub][1], oacc[db], 0, 0, 0);
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, sc[sub][2], oacc[db], 0, 0, 0);
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, sc[sub][3], oacc[db], 0, 0, 0);
       }
-    }
   }
 #undef CV3_KV_LOAD
   // merge the two key groups through LDS (each lane's state is per query column)
