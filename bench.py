@@ -7,7 +7,9 @@
     decoded from speech_embedding[sos] (one "step" = one token).
   * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
     fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
-    of torch.randn((1, 80, 15000), seed 0).
+    of torch.randn((1, 80, 15000), seed 0); and the same solve over 30 s (T = 1500)
+    with q8 linears (the ``flow_q8_30s`` object).
+  * HiFTNet vocoder, 10 s of audio (the ``vocoder`` object), whole and in 1 s chunks.
 
 Weights are synthetic (seeded N(0, 0.02), norms 1; cv3amd/synth.py); inputs are
 resident in HBM before the timed regions start.  Each workload reports its
@@ -264,6 +266,34 @@ def bench_flow(args, tensors, meta):
                        "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
 
 
+def bench_flow_q8(args, tensors, meta):
+    """The 30 s solve (T = 1500) with the DiT linears stored q8 (block 64, f16 scales; the
+    reference converter's balanced profile), dequantised inside the GEMM's B load."""
+    import cv3amd.quant as quant
+    from cv3amd import synth
+    from cv3amd.device import Timer, synchronize
+    from cv3amd.dit import DeviceDiT
+    from cv3amd.weights import WeightStore
+    T = 1500
+    qt = synth.quantize_store(tensors, "balanced", quant.quantize_q8)   # device quantiser
+    d = DeviceDiT(WeightStore(qt, meta, quant.QTensor))
+    mu, cond, spks, x0 = flow_inputs(T)
+    d.prepare(mu, spks, cond)
+    log("flow q8 30 s: warmup solve (captures the solve graph)")
+    d.solve(x0, graph=args.graph)
+    synchronize()
+    n = max(1, args.flow_solves - 1)
+    log(f"flow q8 30 s: timing {n} solves")
+    tm = Timer()
+    tm.start()
+    for _ in range(n):
+        d.solve(x0, graph=args.graph)
+    ms = tm.stop() / n
+    flops = d.flops_per_solve()
+    log(f"flow q8 30 s: {ms:.2f} ms/solve, RTF {ms / 1e3 / 30.0:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
+    return {"ms": ms, "flops": flops, "T": T}
+
+
 def cpu_flow(tensors, meta):
     """One estimator evaluation (22 blocks, the 10-step solve's unit) of the oracle."""
     import oracle.quant
@@ -344,6 +374,7 @@ def main():
                     help="int8 scale layout of the LM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-core baseline")
     ap.add_argument("--no-flow", action="store_true")
+    ap.add_argument("--no-flow-q8", action="store_true", help="skip the 30 s q8-weight solve")
     ap.add_argument("--no-hift", action="store_true")
     ap.add_argument("--hift-runs", type=int, default=3)
     ap.add_argument("--cpu-tokens", type=int, default=128)
@@ -370,13 +401,15 @@ def main():
     log(f"LM weights ready ({time.time() - t0:.1f} s)")
     dec = bench_decode(args, lm_t, lm_meta)
 
-    flow = None
+    flow = flow_q8 = None
     dit_t = dit_meta = None
     if not args.no_flow:
         from cv3amd import synth
         dit_t = synth.dit_tensors(depth=22)
         dit_meta = synth.dit_meta(depth=22)
         flow = bench_flow(args, dit_t, dit_meta)
+        if not args.no_flow_q8:
+            flow_q8 = bench_flow_q8(args, dit_t, dit_meta)
 
     voc = None
     hift_t = hift_meta = None
@@ -452,6 +485,15 @@ def main():
             "cpu_baseline": None if cpu_flow_s is None else {
                 "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
                 "sample": "one 22-block estimator evaluation (of the solve's 10) by the oracle, x10 extrapolated"},
+        }
+    if flow_q8 is not None:
+        line["flow_q8_30s"] = {
+            "workload": "DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
+                        "(block 64, f16 scales) dequantised in the GEMM, fp32 accumulate",
+            "ms_per_solve": round(flow_q8["ms"], 3), "rtf": round(flow_q8["ms"] / 1e3 / 30.0, 6),
+            "tflops": round(flow_q8["flops"] / (flow_q8["ms"] / 1e3) / 1e12, 2),
+            "mfma_roofline_frac": round(flow_q8["flops"] / (flow_q8["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
+            "flops_per_solve": flow_q8["flops"],
         }
     if voc is not None:
         line["vocoder"] = {
