@@ -150,7 +150,7 @@ struct RowDot {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = min(sub + i * LPR, nch - 1);
-      wv[i] = base[c];
+      wv[i] = __builtin_nontemporal_load(base + c);
       const int64_t si = srow + (int64_t)((unsigned)c / cpb);
       if constexpr (SF16)
         sc[i] = __half2float(reinterpret_cast<const __half*>(w.scales)[si]);
