@@ -421,7 +421,6 @@ struct OprojArgs {
 template <int CPL, bool SF16>
 __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   extern __shared__ float xs[];
-  __shared__ float ml[16 * NSMAX * 2];
   constexpr int LPR = 8, RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = lane / LPR, sub = lane % LPR;
@@ -446,28 +445,41 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   RowDot<LPR, CPL, SF16> rd;
   rd.load(a.w, wrow, sub, live);
   __builtin_amdgcn_sched_barrier(0);
+  // Chunk weights: thread t holds (m, l) of head t / 16, chunk t % 16.  A head's 16
+  // chunks are 16 adjacent lanes, so its max M and denominator sum_s e^{m_s - M} l_s
+  // are shuffle reductions; each weight e^{m_s - M} is computed once and shared.
+  static_assert(NSMAX == 16, "one lane per chunk in 16-lane head groups");
+  __shared__ float wl[16 * NSMAX];
+  __shared__ float dl[16];
   const int active = (int)((pos + 1 + KCH - 1) / KCH);
-  float2 mlv = make_float2(-INFINITY, 0.f);
-  if (t < a.heads * NSMAX && (t % NSMAX) < active) mlv = mlraw;
-  if (t < 16 * NSMAX) reinterpret_cast<float2*>(ml)[t] = mlv;
+  const int sl = t % NSMAX;
+  const bool valid = t < a.heads * NSMAX && sl < active;
+  const float mm = valid ? mlraw.x : -INFINITY;
+  float M = mm;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  const float wgt = valid ? expf(mm - M) : 0.f;
+  float den = valid ? mlraw.y * wgt : 0.f;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  wl[t] = wgt;
+  if (sl == 0) dl[t / NSMAX] = den;
   __syncthreads();
   if (owns) {
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < active; ++s2) M = fmaxf(M, ml[(oh * NSMAX + s2) * 2]);
-    float den = 0.f;
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int s2 = 0; s2 < NSMAX; ++s2) {
-      if (s2 < active) {
-        const float wgt = expf(ml[(oh * NSMAX + s2) * 2] - M);
-        den = fmaf(ml[(oh * NSMAX + s2) * 2 + 1], wgt, den);
-        num.x = fmaf(ov[s2].x, wgt, num.x);
-        num.y = fmaf(ov[s2].y, wgt, num.y);
-        num.z = fmaf(ov[s2].z, wgt, num.z);
-        num.w = fmaf(ov[s2].w, wgt, num.w);
+      if (s2 < active) {  // uniform: stale slots past the active count are never touched
+        const float w = wl[oh * NSMAX + s2];
+        num.x = fmaf(ov[s2].x, w, num.x);
+        num.y = fmaf(ov[s2].y, w, num.y);
+        num.z = fmaf(ov[s2].z, w, num.z);
+        num.w = fmaf(ov[s2].w, w, num.w);
       }
     }
-    reinterpret_cast<float4*>(xs + oh * a.dh)[od4] = make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+    const float dsum = dl[oh];
+    reinterpret_cast<float4*>(xs + oh * a.dh)[od4] =
+        make_float4(num.x / dsum, num.y / dsum, num.z / dsum, num.w / dsum);
   }
   // zero padding up to the staged width (chunks past the row read zeros)
   for (int64_t c = (int64_t)a.heads * a.dh + t; c < LPR * CPL * 16; c += 256) xs[c] = 0.f;
