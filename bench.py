@@ -336,12 +336,12 @@ def bench_hift(args, tensors, meta):
     mel_d, src_d = to_device(mel), to_device(source)
     out = {}
     for label, chunk in (("whole", None), ("chunked_1s", 50)):
-        d.decode(mel_d, src_d, chunk=chunk)
+        d.decode(mel_d, src_d, chunk=chunk, graph=args.graph)
         synchronize()
         tm = Timer()
         tm.start()
         for _ in range(args.hift_runs):
-            d.decode(mel_d, src_d, chunk=chunk)
+            d.decode(mel_d, src_d, chunk=chunk, graph=args.graph)
         ms = tm.stop() / args.hift_runs
         out[label] = ms
         log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
