@@ -129,6 +129,52 @@ struct VecStage {
     }
     __syncthreads();
   }
+  // Same staging with the norm folded out of the vector: xs = x * w, and the returned
+  // 1 / sqrt(mean(x^2) + eps) scales each row's dot product afterwards
+  // (W . (x * inv * w) = inv * (W . (x * w))).  The statistic's cross-wave sum rides on
+  // the staging barrier, so the dot products do not wait for a reduction.
+  __device__ __forceinline__ float finish_folded(int64_t k, int64_t kx, bool rms, float eps, float* xs, float* red) {
+    const int64_t k4 = k / 4, n4 = kx / 4;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+      if (idx >= k4) v[i] = z;
+    }
+    float ss = 0.f;
+    if (rms) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        ss = fmaf(v[i].x, v[i].x, ss);
+        ss = fmaf(v[i].y, v[i].y, ss);
+        ss = fmaf(v[i].z, v[i].z, ss);
+        ss = fmaf(v[i].w, v[i].w, ss);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
+      if (idx < n4) {
+        float4 o = v[i];
+        if (rms) {
+          o.x = o.x * w[i].x;
+          o.y = o.y * w[i].y;
+          o.z = o.z * w[i].z;
+          o.w = o.w * w[i].w;
+        }
+        reinterpret_cast<float4*>(xs)[idx] = o;
+      }
+    }
+    if (rms) {
+      ss = wave_sum(ss);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    if (!rms) return 1.f;
+    float t = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+    return 1.0f / sqrtf(t / (float)k + eps);
+  }
 };
 
 // Dot products of one row group: lanes [g*LPR, g*LPR + LPR) cover row `row`.
@@ -207,8 +253,8 @@ __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   RowDot<LPR, CPL, SF16> rd;
   rd.load(a.w, live ? wrow : a.layer_row0, sub, live);
   __builtin_amdgcn_sched_barrier(0);
-  vs.finish(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
-  const float acc = rd.dot(xs, sub);
+  const float inv = vs.finish_folded(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  const float acc = rd.dot(xs, sub) * inv;
   if (swiglu) {
     const float up = __shfl_xor(acc, LPR, 64);  // partner row group (gate <-> up)
     if (live && sub == 0 && (grp & 1) == 0) a.y[col] = (acc / (1.0f + expf(-acc))) * up;
@@ -270,8 +316,8 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   const bool upper = grp & 1;
   const int jj = (int)j + (upper ? half : 0);
   const float rc = a.cos_t[p * a.dh + jj], rs = a.sin_t[p * a.dh + jj];
-  vs.finish(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
-  float v = rd.dot(xs, sub);
+  const float inv = vs.finish_folded(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  float v = rd.dot(xs, sub) * inv;
   if (live) v += bias;
   const float other = __shfl_xor(v, LPR, 64);  // the pair partner
   if (!live || sub != 0) return;
