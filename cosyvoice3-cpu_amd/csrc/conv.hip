@@ -327,6 +327,175 @@ __global__ void k_conv_reduce(ConvFast p) {
   }
 }
 
+// Channels-last stride-1 conv (groups 1) as an implicit GEMM fed by global -> LDS DMA,
+// the structure of the linear GEMM's k_gemm_dma: C[t, co] over M = t_out time rows,
+// N = cout, K = k * cin in (tap, channel) order, weight repacked (cout, k, cin).  A BK =
+// 32 stage is 32 channels of one tap, so each A row is a 128-byte piece of one input
+// row x[(t + tap*dil - pad_l) / up] (nearest upsample fused); rows outside the padded
+// input read a static zero row instead, so the DMA needs no predicates.  Rows are
+// XOR-swizzled in LDS and the ring holds three stages (see k_gemm_dma in gemm.hip).
+__device__ float g_conv_zero_row[32];  // zero-initialised, only ever read
+
+struct ConvCL {
+  const float* x;
+  int64_t ldx;
+  int t_in, up, cin;
+  const float* w;  // [cout, k, cin]
+  int cout, k, dil, pad_l, t_out;
+  const float* bias;
+  float* y;
+  int64_t y_ts, y_cs;
+  int act;
+  float act_param;
+  const float* snake_alpha;
+  float snake_eps;
+  const float* res;
+  int64_t r_ts, r_cs;
+  float* part;  // split-K partials [ksplit, t_out, cout]
+  int ksplit;
+};
+#define CV3_VMCNT(n) (((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+struct ClSrc {
+  int r0, r1;              // this lane's two A rows (time)
+  const float* b0;         // this lane's two B rows (weight), at its chunk
+  const float* b1;
+  int lc;
+};
+
+__device__ __forceinline__ void cl_stage(const ConvCL& p, const ClSrc& s, int sg, float* as, float* bs, int w) {
+  const int cpt = p.cin / 32;
+  const int j = sg / cpt, c0 = (sg - j * cpt) * 32;
+  const int tin_up = p.t_in * p.up;
+  const int u0 = s.r0 + j * p.dil - p.pad_l, u1 = s.r1 + j * p.dil - p.pad_l;
+  const bool ok0 = s.r0 < p.t_out && u0 >= 0 && u0 < tin_up;
+  const bool ok1 = s.r1 < p.t_out && u1 >= 0 && u1 < tin_up;
+  const int q0 = ok0 ? (p.up == 1 ? u0 : (int)((unsigned)u0 / (unsigned)p.up)) : 0;
+  const int q1 = ok1 ? (p.up == 1 ? u1 : (int)((unsigned)u1 / (unsigned)p.up)) : 0;
+  const float* a0 = ok0 ? p.x + (int64_t)q0 * p.ldx + c0 + s.lc : g_conv_zero_row + s.lc;
+  const float* a1 = ok1 ? p.x + (int64_t)q1 * p.ldx + c0 + s.lc : g_conv_zero_row + s.lc;
+  __builtin_amdgcn_global_load_lds(a0, as + (w * 16) * 32, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(a1, as + (w * 16 + 8) * 32, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(s.b0 + sg * 32, bs + (w * 16) * 32, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(s.b1 + sg * 32, bs + (w * 16 + 8) * 32, 16, 0, 0);
+}
+
+__device__ __forceinline__ void cl_mma(const float* as, const float* bs, int arow, int brow, int sw, int h,
+                                       f32x16& acc) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int c = ((2 * g + h) ^ sw) * 4;
+    const float4 av = *reinterpret_cast<const float4*>(as + arow + c);
+    const float4 bv = *reinterpret_cast<const float4*>(bs + brow + c);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_conv_cl_dma(ConvCL p, int tiles_m) {
+  __shared__ float A0[2048], A1[2048], A2[2048];
+  __shared__ float B0[2048], B1[2048], B2[2048];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int m0 = (t % tiles_m) * 64, n0 = (t / tiles_m) * 64;
+  const int lr = lane >> 3;
+  const int K = p.k * p.cin;
+  ClSrc src;
+  src.lc = ((lane & 7) ^ lr) * 4;
+  src.r0 = m0 + w * 16 + lr;
+  src.r1 = src.r0 + 8;
+  src.b0 = p.w + (int64_t)min(n0 + w * 16 + lr, p.cout - 1) * K + src.lc;
+  src.b1 = p.w + (int64_t)min(n0 + w * 16 + 8 + lr, p.cout - 1) * K + src.lc;
+  const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
+  const int r32 = lane & 31, h = lane >> 5, sw = r32 & 7;
+  const int arow = (wm + r32) * 32, brow = (wn + r32) * 32;
+  const int S = K / 32 / p.ksplit;  // this workgroup's stages
+  const int sb = blockIdx.z * S;
+  f32x16 acc = {0.f};
+  cl_stage(p, src, sb, A0, B0, w);
+  cl_stage(p, src, sb + min(1, S - 1), A1, B1, w);
+#define CV3_CL_STEP(AN, BN_, AC, BC, ST)                            \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  __builtin_amdgcn_s_waitcnt(CV3_VMCNT(4));                         \
+  __builtin_amdgcn_s_barrier();                                     \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  cl_stage(p, src, sb + min((ST) + 2, S - 1), AN, BN_, w);          \
+  __builtin_amdgcn_sched_barrier(0);                                \
+  cl_mma(AC, BC, arow, brow, sw, h, acc);
+  int st = 0;
+  for (; st + 3 <= S; st += 3) {
+    CV3_CL_STEP(A2, B2, A0, B0, st)
+    CV3_CL_STEP(A0, B0, A1, B1, st + 1)
+    CV3_CL_STEP(A1, B1, A2, B2, st + 2)
+  }
+  if (st < S) {
+    CV3_CL_STEP(A2, B2, A0, B0, st)
+    if (st + 1 < S) { CV3_CL_STEP(A0, B0, A1, B1, st + 1) }
+  }
+#undef CV3_CL_STEP
+  // no DMA may still be writing this workgroup's LDS when it ends
+  __builtin_amdgcn_s_waitcnt(CV3_VMCNT(0));
+  // accumulator: reg i -> time row m0 + wm + (i/4)*8 + h*4 + i%4, output channel n0 + wn + lane%32
+  const int co = n0 + wn + r32;
+  if (co >= p.cout) return;
+  if (p.ksplit > 1) {
+    float* dst = p.part + (int64_t)blockIdx.z * p.t_out * p.cout + co;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+      if (tr < p.t_out) dst[(int64_t)tr * p.cout] = acc[i];
+    }
+    return;
+  }
+  const float bias = p.bias ? p.bias[co] : 0.f;
+  const float alpha = p.snake_alpha ? p.snake_alpha[co] : 0.f;
+  float res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tr = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), p.t_out - 1);
+    res[i] = p.res ? p.res[(int64_t)tr * p.r_ts + co * p.r_cs] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (tr < p.t_out) {
+      float v = acc[i] + bias;
+      if (p.snake_alpha) {
+        const float sn = sinf(alpha * v);
+        v = v + (1.0f / (alpha + p.snake_eps)) * (sn * sn);
+      } else {
+        v = apply_act(p.act, v, p.act_param);
+      }
+      if (p.res) v = res[i] + v;
+      p.y[(int64_t)tr * p.y_ts + co * p.y_cs] = v;
+    }
+  }
+}
+
+// Split-K epilogue of k_conv_cl_dma: slices added in order z = 0, 1, ...
+__global__ void k_conv_cl_reduce(ConvCL p) {
+  const int64_t n = (int64_t)p.t_out * p.cout;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int tr = (int)(e / p.cout), co = (int)(e - (int64_t)tr * p.cout);
+    const float r = p.res ? p.res[(int64_t)tr * p.r_ts + co * p.r_cs] : 0.f;
+    float acc = p.part[e];
+    for (int z = 1; z < p.ksplit; ++z) acc += p.part[(int64_t)z * n + e];
+    float v = acc + (p.bias ? p.bias[co] : 0.f);
+    if (p.snake_alpha) {
+      const float a = p.snake_alpha[co];
+      const float sn = sinf(a * v);
+      v = v + (1.0f / (a + p.snake_eps)) * (sn * sn);
+    } else {
+      v = apply_act(p.act, v, p.act_param);
+    }
+    if (p.res) v = r + v;
+    p.y[(int64_t)tr * p.y_ts + co * p.y_cs] = v;
+  }
+}
+
 // groups == C convolution as k shifted multiply-accumulates (ops.py:222-237)
 __global__ void k_depthwise(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
                             float* __restrict__ y, int64_t c, int64_t t_in, int64_t k, int64_t dil, int64_t pad_l,
@@ -465,6 +634,67 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
   if (ksplit > 1) {
     const int64_t n = cout * t_out;
     hipLaunchKernelGGL(k_conv_reduce, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0,
+                       stream_of(s), p);
+    CV3_LAUNCHED();
+  }
+  return CV3_OK;
+}
+
+int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
+                         int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r,
+                         int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
+                         const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
+                         int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s) {
+  CV3_REQUIRE(dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0 && cin > 0 && cout > 0, CV3_EINVAL,
+              "bad conv geometry");
+  CV3_REQUIRE(cin % 32 == 0, CV3_EUNSUPPORTED, "channels-last packed conv needs cin %% 32 == 0 (cin %lld)",
+              (long long)cin);
+  CV3_REQUIRE(((uintptr_t)x % 16) == 0 && ldx % 4 == 0 && ldx >= cin && ((uintptr_t)w_packed % 16) == 0, CV3_EINVAL,
+              "channels-last packed conv needs 16-byte aligned rows");
+  const int64_t stages = k * cin / 32;
+  CV3_REQUIRE(ksplit >= 1 && ksplit <= 16 && stages % ksplit == 0, CV3_EINVAL,
+              "ksplit %lld must divide the %lld K stages", (long long)ksplit, (long long)stages);
+  const int64_t tp = t_in * up + pad_l + pad_r;
+  const int64_t span = dilation * (k - 1) + 1;
+  const int64_t t_out = tp >= span ? tp - span + 1 : 0;
+  CV3_REQUIRE(tp < (1ll << 31) && k * cin < (1ll << 31) && dilation * k < (1ll << 31), CV3_EINVAL,
+              "channels-last packed conv sizes exceed 32-bit indexing");
+  if (t_out <= 0) return CV3_OK;
+  CV3_REQUIRE(ksplit == 1 || (workspace && workspace_floats >= ksplit * cout * t_out), CV3_EINVAL,
+              "split-K conv needs a workspace of ksplit * cout * t_out floats");
+  ConvCL p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.t_in = (int)t_in;
+  p.up = (int)up;
+  p.cin = (int)cin;
+  p.w = w_packed;
+  p.cout = (int)cout;
+  p.k = (int)k;
+  p.dil = (int)dilation;
+  p.pad_l = (int)pad_l;
+  p.t_out = (int)t_out;
+  p.bias = bias;
+  p.y = y;
+  p.y_ts = y_ts;
+  p.y_cs = y_cs;
+  p.act = act;
+  p.act_param = act_param;
+  p.snake_alpha = snake_alpha;
+  p.snake_eps = snake_eps;
+  p.res = residual;
+  p.r_ts = r_ts;
+  p.r_cs = r_cs;
+  p.part = workspace;
+  p.ksplit = (int)ksplit;
+  const int64_t tiles_m = ceil_div(t_out, 64), tiles_n = ceil_div(cout, 64);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "conv too large");
+  hipLaunchKernelGGL(k_conv_cl_dma, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
+                     stream_of(s), p, (int)tiles_m);
+  CV3_LAUNCHED();
+  if (ksplit > 1) {
+    const int64_t n = cout * t_out;
+    hipLaunchKernelGGL(k_conv_cl_reduce, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0,
                        stream_of(s), p);
     CV3_LAUNCHED();
   }

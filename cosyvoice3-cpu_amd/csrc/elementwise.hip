@@ -52,6 +52,17 @@ __global__ void k_snake(const float* __restrict__ x, const float* __restrict__ a
   }
 }
 
+// Snake on channels-last (t, c) data: the alpha of element i is alpha[i % c].
+__global__ void k_snake_cl(const float* __restrict__ x, const float* __restrict__ alpha, float* __restrict__ y,
+                           uint32_t n, uint32_t c, float eps) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const float a = alpha[i % c];
+    const float v = x[i];
+    const float s = sinf(a * v);
+    y[i] = v + (1.0f / (a + eps)) * (s * s);
+  }
+}
+
 // One workgroup per row.  softmax: e = exp(x - max), e / sum;  log: z - log(sum exp z).
 __global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ x, float* __restrict__ y, int64_t cols,
                                                       int logmode) {
@@ -419,6 +430,15 @@ int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, floa
 int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s) {
   if (c * t <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_snake, dim3(grid_for(c * t)), dim3(256), 0, stream_of(s), x, alpha, y, c, t, eps);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int cv3_snake_cl(const float* x, const float* alpha, float* y, int64_t t, int64_t c, float eps, cv3_stream_t s) {
+  CV3_REQUIRE(t >= 0 && c > 0 && t * c < (1ll << 32), CV3_EINVAL, "snake: bad shape");
+  if (t == 0) return CV3_OK;
+  hipLaunchKernelGGL(k_snake_cl, dim3(grid_for(t * c)), dim3(256), 0, stream_of(s), x, alpha, y, (uint32_t)(t * c),
+                     (uint32_t)c, eps);
   CV3_LAUNCHED();
   return CV3_OK;
 }

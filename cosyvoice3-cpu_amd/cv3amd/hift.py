@@ -1,10 +1,14 @@
 """Device-resident causal HiFTNet decode: source STFT -> conv stack -> iSTFT head.
 
 Restates cv3cpu/models/hift.py:114-210 (``_resblock``, ``_spectral``,
-``_spectral_chunked``, ``decode``) with every activation resident in HBM, in the
-reference's (channels, time) layout.  The F0 predictor and the NSF excitation
-(hift.py:56-111, float64 host code in the reference) produce the ``source``
-signal this class takes as input.
+``_spectral_chunked``, ``decode``) with every activation resident in HBM.  Inside the
+stack activations are channels-last (time, channels): a stride-1 conv is then an
+implicit GEMM whose A rows are shifted input rows, fed to LDS by DMA
+(cv3_conv1d_cl_packed).  The mel and the source STFT come in the reference's
+(channels, time) layout and are read through strides by the first convs; conv_post
+writes (channels, time) for the iSTFT head.  The F0 predictor and the NSF excitation
+(hift.py:56-111, float64 host code in the reference) produce the ``source`` signal
+this class takes as input.
 
 Per upsampling stage i (reference lines in brackets):
   leaky(x, 0.1), nearest x r_i fused into the causal ``ups`` conv      (hift.py:137-142)
@@ -36,13 +40,13 @@ def causal_pad(kernel_size: int, dilation: int = 1) -> int:
 
 def split_k(t_out: int, cout: int, stages: int) -> int:
     """K slices for the packed conv: grids under 160 tiles of 64 x 64 (a 1 s chunk's
-    256-channel stage has 60) are split until they cover about two tiles per CU; each
-    slice keeps an even number of the k*cin/32 stages."""
+    256-channel stage has 60) are split until they cover about two tiles per CU; the
+    slices divide the k*cin/32 stages evenly."""
     tiles = -(-t_out // 64) * -(-cout // 64)
     if tiles >= 160:
         return 1
-    for ks in (8, 4, 2):
-        if tiles * ks <= 512 and stages % (2 * ks) == 0:
+    for ks in (8, 6, 4, 3, 2):
+        if tiles * ks <= 512 and stages % ks == 0:
             return ks
     return 1
 
@@ -71,7 +75,7 @@ class DeviceHiFT:
         self.nk = len(self.rb_k)
         self.up_total = int(np.prod(self.rates))
         self.w = {}
-        self.wp = {}   # conv weights repacked (out, k, in) for the stride-1 fast path
+        self.wp = {}   # conv weights repacked (out, k, in) for the channels-last implicit GEMM
         self.shape = {}
         for name in weights.keys():
             if not name.startswith(prefix) or "f0_predictor" in name or "m_source" in name:
@@ -80,7 +84,7 @@ class DeviceHiFT:
             key = name[len(prefix):]
             self.w[key] = to_device(np.ascontiguousarray(arr))
             self.shape[key] = arr.shape
-            if arr.ndim == 3 and arr.shape[1] % 64 == 0:
+            if arr.ndim == 3 and arr.shape[1] % 32 == 0:
                 self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
         self.window = to_device(hann_window(self.n_fft))
         # captured spectral stacks, one per input length: (graph, mel in, source STFT in, out, arena)
@@ -105,41 +109,56 @@ class DeviceHiFT:
         return a
 
     # -- building blocks ------------------------------------------------------
-    def _conv(self, x: DeviceArray, key: str, stride: int = 1, dilation: int = 1, pad=(0, 0), up: int = 1,
+    def _conv(self, x: DeviceArray, key: str, dilation: int = 1, pad=(0, 0), up: int = 1,
               act: str = "none", act_param: float = 0.0, snake: Optional[str] = None,
-              residual: Optional[DeviceArray] = None, out: Optional[DeviceArray] = None,
-              out_col0: int = 0, out_ld: Optional[int] = None) -> DeviceArray:
-        """conv1d over (C_in, T) -> (C_out, T_out) (ops.py:165-219), with the fused
-        nearest upsample, activation / Snake and residual epilogues."""
-        cout, cin_g, k = self.shape[key + ".weight"]
-        cin, t_in = x.shape
-        if cin_g != cin:
-            raise ValueError(f"{key}: input has {cin} channels, weight expects {cin_g}")
-        span = dilation * (k - 1) + 1
-        n = max(0, (t_in * up + pad[0] + pad[1] - span) // stride + 1)
+              residual: Optional[DeviceArray] = None, out: Optional[DeviceArray] = None, out_row0: int = 0,
+              channels_first_out: bool = False) -> DeviceArray:
+        """Stride-1 conv1d (ops.py:165-219) on channels-last x (T_in, C_in) -> (T_out, C_out),
+        or (C_out, T_out) with ``channels_first_out``; nearest upsample, activation / Snake
+        and residual (channels-last) fused."""
+        cout, cin, k = self.shape[key + ".weight"]
+        t_in, c = x.shape
+        if c != cin:
+            raise ValueError(f"{key}: input has {c} channels, weight expects {cin}")
+        n = max(0, t_in * up + pad[0] + pad[1] - dilation * (k - 1))
         if out is None:
-            out = self._new((cout, n))
-        ld = out_ld if out_ld is not None else out.shape[1]
+            out = self._new((cout, n) if channels_first_out else (n, cout))
+        y_ts, y_cs = (1, out.shape[1]) if channels_first_out else (out.shape[1], 1)
         alpha = self.w[snake].ptr if snake else None
         res = residual.ptr if residual is not None else None
-        rld = residual.shape[1] if residual is not None else 0
+        r_ts = residual.shape[1] if residual is not None else 0
         wkey = key + ".weight"
-        if stride == 1 and wkey in self.wp:
+        if wkey in self.wp:   # cin % 32 == 0: the DMA implicit GEMM
             ks = split_k(n, cout, k * cin // 32)
             ws = self._new((ks * cout * n,)) if ks > 1 else None
-            _lib.call("conv1d_packed", x.ptr, cin, t_in, t_in, self.wp[wkey].ptr, cout, k,
-                      self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_col0 * F4, ld, 1,
-                      ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, ks, ws.ptr if ws else None,
+            _lib.call("conv1d_cl_packed", x.ptr, t_in, cin, cin, self.wp[wkey].ptr, cout, k,
+                      self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_ts,
+                      y_cs, ACT[act], float(act_param), alpha, 1e-9, res, r_ts, 1, ks, ws.ptr if ws else None,
                       ws.size if ws else 0, None)
-        else:
-            _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[wkey].ptr, cout, k,
-                      self.w[key + ".bias"].ptr, stride, dilation, 1, pad[0], pad[1], up, out.ptr + out_col0 * F4,
-                      ld, 1, None, ACT[act], float(act_param), alpha, 1e-9, res, rld, 1, None)
+        else:                 # narrow stacks: the generic kernel, addressed channels-last
+            _lib.call("conv1d", x.ptr, cin, t_in, 1, cin, self.w[wkey].ptr, cout, k, self.w[key + ".bias"].ptr, 1,
+                      dilation, 1, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_cs, y_ts, None,
+                      ACT[act], float(act_param), alpha, 1e-9, res, 1, r_ts, None)
+        return out
+
+    def _conv_in(self, x: DeviceArray, key: str, stride: int = 1, pad=(0, 0)) -> DeviceArray:
+        """conv1d (ops.py:165-219) from channels-first x (C_in, T_in) to channels-last output,
+        for the convs on the stack's inputs (conv_pre on the mel, the strided source_downs on
+        the source STFT), through the generic strided kernel."""
+        cout, cin, k = self.shape[key + ".weight"]
+        c, t_in = x.shape
+        if c != cin:
+            raise ValueError(f"{key}: input has {c} channels, weight expects {cin}")
+        n = max(0, (t_in + pad[0] + pad[1] - k) // stride + 1)
+        out = self._new((n, cout))
+        _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k,
+                  self.w[key + ".bias"].ptr, stride, 1, 1, pad[0], pad[1], 1, out.ptr, 1, cout, None,
+                  ACT["none"], 0.0, None, 0.0, None, 0, 0, None)
         return out
 
     def _snake(self, x: DeviceArray, key: str) -> DeviceArray:
         y = self._new(x.shape)
-        _lib.call("snake", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, None)
+        _lib.call("snake_cl", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, None)
         return y
 
     def _act(self, x: DeviceArray, name: str, param: float) -> DeviceArray:
@@ -164,29 +183,29 @@ class DeviceHiFT:
     def spectral(self, mel: DeviceArray, s_stft: DeviceArray) -> DeviceArray:
         """conv_pre .. conv_post: (80, T) -> (n_fft + 2, 120 T + 1) (hift.py:131-168)."""
         kpre = self.shape["conv_pre.weight"][2]
-        x = self._conv(mel, "conv_pre", pad=(0, causal_pad(kpre)))
+        x = self._conv_in(mel, "conv_pre", pad=(0, causal_pad(kpre)))
         downs = [1] + self.rates[::-1][:-1]
         down_cum = list(np.cumprod(downs))[::-1]
         for i, r in enumerate(self.rates):
             xl = self._act(x, "leaky", self.slope)
             k = self.shape[f"ups.{i}.weight"][2]
             cout = self.shape[f"ups.{i}.weight"][0]
-            t_up = x.shape[1] * r
+            t_up = x.shape[0] * r
             if i == len(self.rates) - 1:
-                # reflect pad (1, 0): columns 1.. hold the conv, column 0 copies column 2 (hift.py:144)
-                xu = self._new((cout, t_up + 1))
-                self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0), out=xu, out_col0=1, out_ld=t_up + 1)
+                # reflect pad (1, 0): rows 1.. hold the conv, row 0 copies row 2 (hift.py:144)
+                xu = self._new((t_up + 1, cout))
+                self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0), out=xu, out_row0=1)
                 S3 = ctypes.c_int64 * 3
-                _lib.call("copy_strided", xu.ptr + 2 * F4, xu.ptr, 1, cout, 1, S3(0, t_up + 1, 1),
-                          S3(0, t_up + 1, 1), None)
+                _lib.call("copy_strided", xu.ptr + 2 * cout * F4, xu.ptr, 1, 1, cout, S3(0, 0, 1), S3(0, 0, 1),
+                          None)
             else:
                 xu = self._conv(xl, f"ups.{i}", up=r, pad=(k - 1, 0))
             u = int(down_cum[i])
             ks = self.shape[f"source_downs.{i}.weight"][2]
             if u == 1:
-                si = self._conv(s_stft, f"source_downs.{i}", pad=(causal_pad(ks), 0))
+                si = self._conv_in(s_stft, f"source_downs.{i}", pad=(causal_pad(ks), 0))
             else:
-                si = self._conv(s_stft, f"source_downs.{i}", stride=u, pad=(u - 1, 0))
+                si = self._conv_in(s_stft, f"source_downs.{i}", stride=u, pad=(u - 1, 0))
             si = self._resblock("source_resblocks", i, si, self.src_k[i], self.src_d[i])
             if si.shape != xu.shape:
                 raise ValueError(f"stage {i}: source branch {si.shape} vs upsampled {xu.shape}")
@@ -205,7 +224,7 @@ class DeviceHiFT:
             x = acc
         x = self._act(x, "leaky", 0.01)
         kpost = self.shape["conv_post.weight"][2]
-        return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0))
+        return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0), channels_first_out=True)
 
     def _stack(self, w: int):
         """The spectral stack for a w-frame input, captured once: its staging inputs, its

@@ -131,6 +131,8 @@ int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_strea
 int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, float alpha, float beta, cv3_stream_t s);
 /* ops.snake (ops.py:77-81) over (C, T) with per-channel alpha */
 int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s);
+/* the same Snake on channels-last (t, c) data (the HiFT stack's layout, hift.py:120) */
+int cv3_snake_cl(const float* x, const float* alpha, float* y, int64_t t, int64_t c, float eps, cv3_stream_t s);
 /* ops.softmax / ops.log_softmax over the last axis (ops.py:84-93) */
 int cv3_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, int log_softmax, cv3_stream_t s);
 /* ops.rms_norm (ops.py:101-104) */
@@ -192,6 +194,16 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
                       float* y, int64_t y_cs, int64_t y_ts, int act, float act_param, const float* snake_alpha,
                       float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, int64_t ksplit,
                       float* workspace, int64_t workspace_floats, cv3_stream_t s);
+/* ops.conv1d (ops.py:165-219) for stride 1 and groups 1 on channels-last activations (the HiFT stack,
+ * hift.py:112-163): x [t_in, ldx] (cin channels), W (cout, cin, k) repacked as w_packed (cout, k, cin),
+ * y[t * y_ts + co * y_cs]; nearest upsample by `up` before the (pad_l, pad_r) zero padding; output length
+ * t_in*up + pad_l + pad_r - dilation*(k-1).  Epilogue and split-K as cv3_conv1d_packed (workspace >=
+ * ksplit*cout*t_out floats; ksplit divides k*cin/32).  Needs cin % 32 == 0 and 16-byte aligned rows. */
+int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
+                         int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r,
+                         int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
+                         const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
+                         int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s);
 /* The DiT's grouped causal conv_pos (dit.py:99-112, ops.conv1d with groups) on channels-last activations:
  * x [batch, t, ldx] (cin channels), y [batch, t, ldy] (cout channels),
  * y[b, s, co] = epi(bias[co] + sum_{j<k, c<cin/groups} W[co, c, j] x[b, s + j - pad_l, g*cin/groups + c]),

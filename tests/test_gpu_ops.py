@@ -368,3 +368,52 @@ def test_conv1d_packed_rejects_odd_split(dev):
     with pytest.raises(ValueError):   # 3 taps x 2 stages = 6 stages: not 2 even slices
         _lib.call("conv1d_packed", x.ptr, 64, 16, 16, w.ptr, 8, 3, None, 1, 2, 0, 1, y.ptr, 16, 1, 0, 0.0,
                   None, 1e-9, None, 0, 0, 2, ws.ptr, ws.size, None)
+
+
+CL_CASES = [
+    # cin, cout, k, dil, up, T, pad, epilogue, K slices, channels-first output
+    (64, 64, 11, 5, 1, 300, (50, 0), "snake", 1, False),
+    (64, 64, 11, 1, 1, 301, (10, 0), "residual", 1, False),
+    (128, 64, 7, 1, 3, 150, (6, 0), "none", 1, False),
+    (512, 256, 16, 1, 8, 40, (15, 0), "none", 2, False),
+    (256, 256, 3, 3, 1, 70, (6, 0), "leaky", 3, False),
+    (64, 18, 7, 1, 1, 200, (6, 0), "none", 1, True),         # conv_post, written (channel, time)
+    (96, 100, 5, 2, 2, 33, (3, 4), "residual", 5, False),    # ragged tiles, both pads, odd split
+    (32, 40, 1, 1, 1, 17, (0, 0), "none", 1, False),         # one stage
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi,ks,cf", CL_CASES)
+def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf):
+    """Channels-last stride-1 conv through the DMA implicit GEMM, against the oracle's
+    upsample + conv1d + epilogue on (channel, time) data."""
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray, to_device
+    x = rng.normal(size=(cin, T)).astype(np.float32)
+    w = (rng.normal(size=(cout, cin, k)) * 0.05).astype(np.float32)
+    b = (rng.normal(size=cout) * 0.05).astype(np.float32)
+    alpha = (np.abs(rng.normal(size=cout)) + 0.5).astype(np.float32)
+    xin = ref.interpolate_nearest(x, up) if up > 1 else x
+    y = ref.conv1d(xin, w, b, dilation=dil, pad=pad)
+    t_out = y.shape[1]
+    res = rng.normal(size=(cout, t_out)).astype(np.float32)
+    want = {"snake": lambda: ref.snake(y, alpha), "leaky": lambda: ref.leaky_relu(y, 0.1),
+            "residual": lambda: y + res, "none": lambda: y}[epi]()
+    xd = to_device(np.ascontiguousarray(x.T))                       # (T, cin)
+    wd = to_device(np.ascontiguousarray(w.transpose(0, 2, 1)))
+    bd, ad = to_device(b), to_device(alpha)
+    res_cl = np.ascontiguousarray(res.T)                             # (t_out, cout)
+    if cf:
+        yd, y_ts, y_cs = DeviceArray((cout, t_out)), 1, t_out
+    else:
+        yd, y_ts, y_cs = (to_device(res_cl) if epi == "residual" else DeviceArray((t_out, cout))), cout, 1
+    ws = DeviceArray((ks * cout * t_out,)) if ks > 1 else None
+    for _ in range(2):  # the second call sees the first call's partials in the workspace
+        if epi == "residual":
+            _lib.call("copy_h2d", yd.ptr, res_cl.ctypes.data, res_cl.nbytes, None)
+        _lib.call("conv1d_cl_packed", xd.ptr, T, cin, cin, wd.ptr, cout, k, bd.ptr, dil, pad[0], pad[1], up,
+                  yd.ptr, y_ts, y_cs, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
+                  ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, cout, 1,
+                  ks, ws.ptr if ws else None, ws.size if ws else 0, None)
+        got = yd.numpy() if cf else yd.numpy().T
+        assert rel_err(got, want) < TOL
