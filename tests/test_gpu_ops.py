@@ -417,3 +417,43 @@ def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf):
                   ks, ws.ptr if ws else None, ws.size if ws else 0, None)
         got = yd.numpy() if cf else yd.numpy().T
         assert rel_err(got, want) < TOL
+
+
+def test_empty_inputs_match_the_reference(dev, rng):
+    """Zero rows, zero-length convolutions and zero queries give the reference's empty shapes."""
+    ops, quant = dev
+    w = (rng.normal(size=(7, 12)) * 0.1).astype(np.float32)
+    x0 = np.zeros((0, 12), np.float32)
+    got, want = ops.linear(x0, w), ref.linear(x0, w)
+    assert got.shape == want.shape == (0, 7)
+    q, s, _ = refq.quantize_q8(w)
+    got = quant.qmatmul(x0, quant.QTensor("q8", q, s, (7, 12), 64))
+    assert got.shape == (0, 7)
+    xc = rng.normal(size=(4, 3)).astype(np.float32)
+    wc = rng.normal(size=(5, 4, 7)).astype(np.float32)
+    got, want = ops.conv1d(xc, wc), ref.conv1d(xc, wc)     # kernel longer than the input: t_out <= 0
+    assert got.shape == want.shape
+    assert ops.softmax(np.zeros((0, 5), np.float32)).shape == (0, 5)
+    assert ops.layer_norm(np.zeros((0, 8), np.float32)).shape == (0, 8)
+    qs = np.zeros((2, 0, 16), np.float32)
+    kv = rng.normal(size=(2, 5, 16)).astype(np.float32)
+    got, want = ops.sdpa(qs, kv, kv), ref.sdpa(qs, kv, kv)
+    assert got.shape == want.shape
+
+
+def test_dropin_accepts_the_reference_tuning_keywords(dev, rng):
+    """Callers pass tile_bytes / threads (qwen2.py:169, the reference's own tests); the result
+    does not depend on them."""
+    ops, quant = dev
+    x = rng.normal(size=(3, 64)).astype(np.float32)
+    w = (rng.normal(size=(40, 64)) * 0.1).astype(np.float32)
+    q, s, _ = refq.quantize_q8(w)
+    qt = quant.QTensor("q8", q, s, (40, 64), 64)
+    base = quant.qmatmul(x, qt)
+    for tb, th in ((1 << 10, 1), (1 << 22, 4)):
+        assert np.array_equal(quant.qmatmul(x, qt, tile_bytes=tb, threads=th), base)
+    xc = rng.normal(size=(4, 30)).astype(np.float32)
+    wc = rng.normal(size=(6, 4, 3)).astype(np.float32)
+    assert np.array_equal(ops.conv1d(xc, wc, tile_bytes=1 << 10), ops.conv1d(xc, wc))
+    qa = rng.normal(size=(2, 9, 16)).astype(np.float32)
+    assert np.array_equal(ops.sdpa(qa, qa, qa, tile_bytes=1 << 10), ops.sdpa(qa, qa, qa))
