@@ -136,6 +136,15 @@ def device_info():
     return {"cu_count": cu.value, "hbm_bytes": mem.value, "arch": name.value.decode()}
 
 
+def mem_stats():
+    """(bytes held by live allocations, bytes parked in the allocator's cache)."""
+    init()
+    in_use = ctypes.c_size_t()
+    cached = ctypes.c_size_t()
+    call("mem_stats", ctypes.addressof(in_use), ctypes.addressof(cached))
+    return in_use.value, cached.value
+
+
 def epilogue(act: str = "none", act_param: float = 0.0, residual=None, ld_res: int = 0,
              gate=None, gate_stride: int = 0, rows_per_gate: int = 0, rope=None):
     """Build a ``cv3_epilogue`` (pointers are ints or None).  ``rope`` is
