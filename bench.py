@@ -4,7 +4,8 @@
   * Qwen2-0.5B int8 greedy decode, batch 1 (the reported ``value``): 24 layers,
     hidden 896, 14/2 heads x 64, SwiGLU 4864, per-output-channel int8 weights with
     float32 scales, KV cache pre-filled to 512 positions of N(0, 1), K tokens
-    decoded from speech_embedding[sos] (one "step" = one token).
+    decoded from speech_embedding[sos] (one "step" = one token); and the same decode
+    with the tiny profile's q4 body layers (the ``decode_tiny`` object).
   * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
     fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
     of torch.randn((1, 80, 15000), seed 0); and the same solve over 30 s (T = 1500)
@@ -104,11 +105,11 @@ def build_lm(layers: int, profile: str):
     from cv3amd import synth
     from cv3amd.weights import WeightStore
     t = synth.qwen2_tensors(layers=layers)
-    t = synth.quantize_store(t, profile, quant.quantize_q8)   # device quantiser
+    t = synth.quantize_store(t, profile, quant.quantize_q8, quant.quantize_q4)   # device quantisers
     return t, synth.qwen2_meta(layers=layers)
 
 
-def bench_decode(args, tensors, meta):
+def bench_decode(args, tensors, meta, label: str = "decode"):
     import cv3amd.quant as quant
     from cv3amd import _lib
     from cv3amd.device import Graph, Timer, synchronize
@@ -124,7 +125,7 @@ def bench_decode(args, tensors, meta):
     v = rng.standard_normal(shape, dtype=np.float32)
     lm.fill_cache(k, v)
     sos = int(meta["speech_token_size"])
-    log(f"decode: warmup {args.warmup} tokens (captures the step graph)")
+    log(f"{label}: warmup {args.warmup} tokens (captures the step graph)")
     lm.begin(sos, PREFILL)
     for _ in range(args.warmup):
         lm.step(graph=args.graph)
@@ -132,7 +133,7 @@ def bench_decode(args, tensors, meta):
     lm.fill_cache(k, v)
     lm.begin(sos, PREFILL)
     synchronize()
-    log(f"decode: timing {args.steps} tokens")
+    log(f"{label}: timing {args.steps} tokens")
     tm = Timer()
     tm.start()
     for _ in range(args.steps):
@@ -144,7 +145,7 @@ def bench_decode(args, tensors, meta):
     avg_len = PREFILL + (args.steps - 1) / 2.0
     b = lm.bytes_per_token(int(round(avg_len)))
     per_token = b["body"] + b["kv"] + b["norms_biases"] + b["head"]
-    log(f"decode: {ms:.2f} ms for {args.steps} tokens = {tok_s:.1f} tok/s; "
+    log(f"{label}: {ms:.2f} ms for {args.steps} tokens = {tok_s:.1f} tok/s; "
         f"{per_token / 1e6:.1f} MB/token -> {per_token * tok_s / 1e9:.0f} GB/s")
 
     # Dominant kernel: the gate/up GEMV (RMSNorm prologue + SwiGLU), one layer's
@@ -167,10 +168,11 @@ def bench_decode(args, tensors, meta):
         run()
     kms = tm.stop() / (reps * layers)
     achieved = gu_bytes / (kms / 1e3)
-    log(f"decode: gate/up GEMV {kms * 1e3:.2f} us/launch, {achieved / 1e9:.0f} GB/s")
+    log(f"{label}: gate/up GEMV {kms * 1e3:.2f} us/launch, {achieved / 1e9:.0f} GB/s")
     return {
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
-        "kernel": {"name": "k_dec_gemv<8,8,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
+        "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
+                   else "k_dec_gemv<8,8,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
                    "bytes_per_launch": gu_bytes, "us_per_launch": kms * 1e3, "achieved_Bps": achieved},
     }
 
@@ -373,6 +375,7 @@ def main():
     ap.add_argument("--profile", default="per_channel", choices=["per_channel", "balanced"],
                     help="int8 scale layout of the LM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-core baseline")
+    ap.add_argument("--no-tiny", action="store_true", help="skip the q4-body (tiny profile) decode")
     ap.add_argument("--no-flow", action="store_true")
     ap.add_argument("--no-flow-q8", action="store_true", help="skip the 30 s q8-weight solve")
     ap.add_argument("--no-hift", action="store_true")
@@ -400,6 +403,13 @@ def main():
     lm_t, lm_meta = build_lm(args.layers, args.profile)
     log(f"LM weights ready ({time.time() - t0:.1f} s)")
     dec = bench_decode(args, lm_t, lm_meta)
+    tiny = None
+    if not args.no_tiny:
+        t0 = time.time()
+        tiny_t, tiny_meta = build_lm(args.layers, "tiny")
+        log(f"LM weights, tiny profile (q4 body), ready ({time.time() - t0:.1f} s)")
+        tiny = bench_decode(args, tiny_t, tiny_meta, label="decode tiny")
+        del tiny_t
 
     flow = flow_q8 = None
     dit_t = dit_meta = None
@@ -469,6 +479,19 @@ def main():
         "copy_GBps": round(copy_bps / 1e9, 1),
         "tokens_head": dec["tokens"][:8],
     }
+    if tiny is not None:
+        tk = tiny["kernel"]
+        line["decode_tiny"] = {
+            "workload": f"the same decode with the tiny profile: Qwen2 body layers q4 (block 32, f16 scales), "
+                        f"head and speech embedding q8, KV {PREFILL}->{PREFILL + args.steps}",
+            "tok_s": round(tiny["tok_s"], 2), "ms_per_token": round(tiny["ms"] / args.steps, 5),
+            "bytes_per_token": tiny["bytes_per_token"],
+            "hbm_roofline_frac": round(tiny["bytes_per_token"] * tiny["tok_s"] / HBM_PEAK, 4),
+            "roofline": {"bound": "hbm", "achieved": round(tk["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": round(tk["achieved_Bps"] / HBM_PEAK, 4), "kernel": tk["name"],
+                         "bytes_per_launch": tk["bytes_per_launch"], "us_per_launch": round(tk["us_per_launch"], 3)},
+            "tokens_head": tiny["tokens"][:8],
+        }
     if flow is not None:
         fk = flow["kernel"]
         rtf = flow["ms"] / 1e3 / AUDIO_SECONDS

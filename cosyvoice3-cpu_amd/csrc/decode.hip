@@ -19,13 +19,16 @@
 //     next  : argmax (ties to the lowest index, np.argsort(-p, stable)[0]),
 //             history[pos + 1] = id, x = speech_embedding[id], pos += 1
 //
-// The int8 GEMV (the HBM-bound part, cv3cpu/quant.py:172-204 at m = 1): a row
+// The quantised GEMV (the HBM-bound part, cv3cpu/quant.py:172-204 at m = 1): a row
 // group of LPR lanes owns one weight row; each lane streams CPL 16-byte chunks
 // of it (128 contiguous bytes per 8 lanes), issued before the activation vector
 // is staged into LDS so the two memory latencies overlap.  Codes are widened in
 // registers; per-row float32 scales are applied once after the dot product,
-// block float16 scales once per 16-code chunk (a chunk never straddles a block
-// because block % 16 == 0).
+// block float16 scales once per chunk (a chunk never straddles a block).
+// A chunk holds 16 int8 codes (q8, block % 16 == 0) or one 32-code q4 block of
+// packed nibbles (byte j: code j in the low nibble, code j + 16 in the high one,
+// stored +8; quant.py:70-86,123-131), so the tiny profile's body layers stream
+// half the bytes through the same kernels.
 #include "common.hpp"
 #include "epilogue.hpp"
 
@@ -35,11 +38,12 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-struct QW {            // one stacked int8 weight: layer l, row r at q + (l * rows + r) * kp
-  const int8_t* q;
+struct QW {            // one stacked weight: layer l, row r at q + (l * rows + r) * row_bytes
+  const int8_t* q;     // row_bytes = kp (q8) or kp / 2 (q4)
   const void* scales;  // [layers * rows, kp / block]
   int64_t rows, k, kp, block;
   int sf16;
+  int q4;
 };
 
 __device__ __forceinline__ float sc_at(const QW& w, int64_t row, int64_t kk) {
@@ -56,6 +60,38 @@ __device__ __forceinline__ float sc_chunk(const QW& w, const void* srow, unsigne
   return w.sf16 ? __half2float(reinterpret_cast<const __half*>(srow)[i]) : reinterpret_cast<const float*>(srow)[i];
 }
 
+// Chunk dot products.  q8: 16 int8 codes, each sign-extended from its byte.
+// q4: one 32-code block; word d holds codes 4d..4d+3 in its low nibbles and
+// 16+4d..16+4d+3 in its high nibbles, each stored + 8.  Flipping bit 3 of a
+// nibble n gives the 4-bit two's complement of n - 8 (n ^ 8 = n - 8 for n >= 8,
+// n + 8 = (n - 8) + 16 below); moved to the top of a byte it reads as the int8
+// 16 * (n - 8), so both nibble sets widen like q8 bytes and dot32_q4 returns
+// 16 x the chunk's dot product (the caller scales by 1/16, exactly).
+__device__ __forceinline__ float sext(uint32_t u, int lsb, int bits) {
+  return (float)((int32_t)(u << (32 - lsb - bits)) >> (32 - bits));
+}
+
+__device__ __forceinline__ float dot32_q4(const u32x4 v, const float* __restrict__ xs) {
+  const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+  float a = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float4 xl = *reinterpret_cast<const float4*>(xs + 4 * d);
+    const float4 xh = *reinterpret_cast<const float4*>(xs + 16 + 4 * d);
+    const uint32_t u = ws[d] ^ 0x88888888u;
+    const uint32_t lo = (u << 4) & 0xF0F0F0F0u, hi = u & 0xF0F0F0F0u;
+    a = fmaf(sext(lo, 0, 8), xl.x, a);
+    a = fmaf(sext(lo, 8, 8), xl.y, a);
+    a = fmaf(sext(lo, 16, 8), xl.z, a);
+    a = fmaf(sext(lo, 24, 8), xl.w, a);
+    a = fmaf(sext(hi, 0, 8), xh.x, a);
+    a = fmaf(sext(hi, 8, 8), xh.y, a);
+    a = fmaf(sext(hi, 16, 8), xh.z, a);
+    a = fmaf(sext(hi, 24, 8), xh.w, a);
+  }
+  return a;
+}
+
 __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ xs) {
   const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
   float a = 0.f;
@@ -63,10 +99,10 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ 
   for (int d = 0; d < 4; ++d) {
     const float4 xv = *reinterpret_cast<const float4*>(xs + 4 * d);
     const uint32_t u = ws[d];
-    a = fmaf((float)((int32_t)(u << 24) >> 24), xv.x, a);
-    a = fmaf((float)((int32_t)(u << 16) >> 24), xv.y, a);
-    a = fmaf((float)((int32_t)(u << 8) >> 24), xv.z, a);
-    a = fmaf((float)((int32_t)u >> 24), xv.w, a);
+    a = fmaf(sext(u, 0, 8), xv.x, a);
+    a = fmaf(sext(u, 8, 8), xv.y, a);
+    a = fmaf(sext(u, 16, 8), xv.z, a);
+    a = fmaf(sext(u, 24, 8), xv.w, a);
   }
   return a;
 }
@@ -76,7 +112,7 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float* __restrict__ 
 // load() issues every float4 load of this thread at once (NV per thread, clamped
 // indices, no predicates); kernels call it BEFORE issuing their weight stream,
 // because loads complete in issue order: a vector loaded after the weights would
-// wait for all of them.  finish() reduces, scales, writes LDS and synchronises.
+// wait for all of them.  finish_folded() writes LDS and synchronises.
 // Needs k % 4 == 0 and 16-byte aligned x / rms_w.
 template <int NV>
 struct VecStage {
@@ -92,44 +128,7 @@ struct VecStage {
       w[i] = w4[idx];
     }
   }
-  __device__ __forceinline__ void finish(int64_t k, int64_t kx, bool rms, float eps, float* xs, float* red) {
-    const int64_t k4 = k / 4, n4 = kx / 4;
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
-      if (idx >= k4) v[i] = z;
-    }
-    float inv = 1.f;
-    if (rms) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        ss = fmaf(v[i].x, v[i].x, ss);
-        ss = fmaf(v[i].y, v[i].y, ss);
-        ss = fmaf(v[i].z, v[i].z, ss);
-        ss = fmaf(v[i].w, v[i].w, ss);
-      }
-      ss = block_sum(ss, red);
-      inv = 1.0f / sqrtf(ss / (float)k + eps);
-    }
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
-      if (idx < n4) {
-        float4 o = v[i];
-        if (rms) {
-          o.x = (o.x * inv) * w[i].x;
-          o.y = (o.y * inv) * w[i].y;
-          o.z = (o.z * inv) * w[i].z;
-          o.w = (o.w * inv) * w[i].w;
-        }
-        reinterpret_cast<float4*>(xs)[idx] = o;
-      }
-    }
-    __syncthreads();
-  }
-  // Same staging with the norm folded out of the vector: xs = x * w, and the returned
+  // Stage with the norm folded out of the vector: xs = x * w, and the returned
   // 1 / sqrt(mean(x^2) + eps) scales each row's dot product afterwards
   // (W . (x * inv * w) = inv * (W . (x * w))).  The statistic's cross-wave sum rides on
   // the staging barrier, so the dot products do not wait for a reduction.
@@ -154,16 +153,14 @@ struct VecStage {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int64_t idx = threadIdx.x + (int64_t)i * blockDim.x;
-      if (idx < n4) {
-        float4 o = v[i];
-        if (rms) {
-          o.x = o.x * w[i].x;
-          o.y = o.y * w[i].y;
-          o.z = o.z * w[i].z;
-          o.w = o.w * w[i].w;
-        }
-        reinterpret_cast<float4*>(xs)[idx] = o;
+      float4 o = v[i];
+      if (rms) {
+        o.x = o.x * w[i].x;
+        o.y = o.y * w[i].y;
+        o.z = o.z * w[i].z;
+        o.w = o.w * w[i].w;
       }
+      if (idx < n4) reinterpret_cast<float4*>(xs)[idx] = o;
     }
     if (rms) {
       ss = wave_sum(ss);
@@ -177,21 +174,28 @@ struct VecStage {
   }
 };
 
+// Codes per 16-byte chunk.
+template <bool Q4>
+constexpr int kCodes = Q4 ? 32 : 16;
+
 // Dot products of one row group: lanes [g*LPR, g*LPR + LPR) cover row `row`.
 // load() issues the lane's CPL 16-byte chunks and their scales (one per chunk: the
 // per-row layout repeats the row's scale) with no predicates; dot() consumes them.
 // Chunks past the row are clamped to its last chunk and meet the zero padding of
-// the staged vector (xs is zero from K up to LPR * CPL * 16), so they add exactly
-// 0; nothing selects on a loaded value, which would wait for the load right there.
+// the staged vector (xs is zero from K up to LPR * CPL * kCodes), so they add
+// exactly 0 (q4: (n - 8) * 0); nothing selects on a loaded value, which would wait
+// for the load right there.
 // A dead row group (`row` clamped to a valid row) computes a value nobody stores.
-template <int LPR, int CPL, bool SF16>
+template <int LPR, int CPL, bool SF16, bool Q4>
 struct RowDot {
+  static constexpr int CPC = kCodes<Q4>;
   u32x4 wv[CPL];
   float sc[CPL];
   __device__ __forceinline__ void load(const QW& w, int64_t row, int sub, bool /*live*/) {
-    const u32x4* base = reinterpret_cast<const u32x4*>(w.q + row * w.kp);
-    const int nch = (int)(w.kp / 16);
-    const unsigned cpb = (unsigned)(w.block / 16);
+    const int64_t row_bytes = Q4 ? w.kp / 2 : w.kp;
+    const u32x4* base = reinterpret_cast<const u32x4*>(w.q + row * row_bytes);
+    const int nch = (int)(row_bytes / 16);
+    const unsigned cpb = (unsigned)(w.block / CPC);
     const int64_t srow = row * (w.kp / w.block);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
@@ -208,7 +212,11 @@ struct RowDot {
   __device__ __forceinline__ float dot(const float* xs, int sub) {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) acc = fmaf(dot16(wv[i], xs + (sub + i * LPR) * 16), sc[i], acc);
+    for (int i = 0; i < CPL; ++i) {
+      const float* xc = xs + (sub + i * LPR) * CPC;
+      acc = fmaf(Q4 ? dot32_q4(wv[i], xc) : dot16(wv[i], xc), sc[i], acc);
+    }
+    if (Q4) acc *= 0.0625f;
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
     return acc;
@@ -233,7 +241,7 @@ struct GemvArgs {
   int mode;
 };
 
-template <int LPR, int CPL, int MODE, bool SF16>
+template <int LPR, int CPL, int MODE, bool SF16, bool Q4>
 __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   extern __shared__ float xs[];
   __shared__ float red[4];
@@ -246,14 +254,15 @@ __global__ __launch_bounds__(256) void k_dec_gemv(GemvArgs a) {
   const int64_t col = ((int64_t)blockIdx.x * 4 + wave) * outs_per_wave + (swiglu ? grp / 2 : grp);
   const bool live = col < a.n;
   const int64_t wrow = a.layer_row0 + (swiglu ? ((grp & 1) ? col + a.n : col) : col);
-  VecStage<(LPR * CPL + 63) / 64> vs;
+  constexpr int WIDTH = LPR * CPL * kCodes<Q4>;  // staged (zero-padded) vector length
+  VecStage<(WIDTH / 4 + 255) / 256> vs;
   vs.load(a.x, a.w.k, a.rms_w);
   const float yres = MODE == 1 ? a.y[live ? col : 0] : 0.f;
   __builtin_amdgcn_sched_barrier(0);  // the vector's loads go out before the weight stream
-  RowDot<LPR, CPL, SF16> rd;
+  RowDot<LPR, CPL, SF16, Q4> rd;
   rd.load(a.w, live ? wrow : a.layer_row0, sub, live);
   __builtin_amdgcn_sched_barrier(0);
-  const float inv = vs.finish_folded(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  const float inv = vs.finish_folded(a.w.k, WIDTH, a.rms_w != nullptr, a.eps, xs, red);
   const float acc = rd.dot(xs, sub) * inv;
   if (swiglu) {
     const float up = __shfl_xor(acc, LPR, 64);  // partner row group (gate <-> up)
@@ -288,7 +297,7 @@ struct QkvArgs {
   int64_t cap;
 };
 
-template <int CPL, bool SF16>
+template <int CPL, bool SF16, bool Q4>
 __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   extern __shared__ float xs[];
   __shared__ float red[4];
@@ -304,10 +313,11 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   const int64_t r = head * a.dh + j + ((grp & 1) ? half : 0);
   const int64_t wrow = a.layer_row0 + (live ? r : 0);
   const int64_t p = *a.pos;  // issued first: the rotary tables depend on it
-  VecStage<(LPR * CPL + 63) / 64> vs;
+  constexpr int WIDTH = LPR * CPL * kCodes<Q4>;
+  VecStage<(WIDTH / 4 + 255) / 256> vs;
   vs.load(a.x, a.w.k, a.rms_w);
   __builtin_amdgcn_sched_barrier(0);
-  RowDot<LPR, CPL, SF16> rd;
+  RowDot<LPR, CPL, SF16, Q4> rd;
   rd.load(a.w, wrow, sub, live);
   const float bias = a.bias[live ? r : 0];
   __builtin_amdgcn_sched_barrier(0);
@@ -316,7 +326,7 @@ __global__ __launch_bounds__(256) void k_dec_qkv(QkvArgs a) {
   const bool upper = grp & 1;
   const int jj = (int)j + (upper ? half : 0);
   const float rc = a.cos_t[p * a.dh + jj], rs = a.sin_t[p * a.dh + jj];
-  const float inv = vs.finish_folded(a.w.k, (int64_t)LPR * CPL * 16, a.rms_w != nullptr, a.eps, xs, red);
+  const float inv = vs.finish_folded(a.w.k, WIDTH, a.rms_w != nullptr, a.eps, xs, red);
   float v = rd.dot(xs, sub) * inv;
   if (live) v += bias;
   const float other = __shfl_xor(v, LPR, 64);  // the pair partner
@@ -464,7 +474,7 @@ struct OprojArgs {
   float* x;                // residual stream, updated in place
 };
 
-template <int CPL, bool SF16>
+template <int CPL, bool SF16, bool Q4>
 __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   extern __shared__ float xs[];
   constexpr int LPR = 8, RPW = 64 / LPR;
@@ -488,7 +498,7 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
     ov[s2] = reinterpret_cast<const float4*>(a.part_o + ((int64_t)min(oh, a.heads - 1) * NSMAX + s2) * 64)
         [min(od4, d4n - 1)];
   __builtin_amdgcn_sched_barrier(0);
-  RowDot<LPR, CPL, SF16> rd;
+  RowDot<LPR, CPL, SF16, Q4> rd;
   rd.load(a.w, wrow, sub, live);
   __builtin_amdgcn_sched_barrier(0);
   // Chunk weights: thread t holds (m, l) of head t / 16, chunk t % 16.  A head's 16
@@ -511,6 +521,7 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
   wl[t] = wgt;
   if (sl == 0) dl[t / NSMAX] = den;
   __syncthreads();
+  constexpr int WIDTH = LPR * CPL * kCodes<Q4>;
   if (owns) {
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -528,7 +539,7 @@ __global__ __launch_bounds__(256) void k_dec_oproj(OprojArgs a) {
         make_float4(num.x / dsum, num.y / dsum, num.z / dsum, num.w / dsum);
   }
   // zero padding up to the staged width (chunks past the row read zeros)
-  for (int64_t c = (int64_t)a.heads * a.dh + t; c < LPR * CPL * 16; c += 256) xs[c] = 0.f;
+  for (int64_t c = (int64_t)a.heads * a.dh + t; c < WIDTH; c += 256) xs[c] = 0.f;
   __syncthreads();
   const float acc = rd.dot(xs, sub);
   if (live && sub == 0) a.x[col] = xres + acc;
@@ -625,30 +636,34 @@ QW make_qw(const cv3_qweight& w) {
   q.kp = w.kp;
   q.block = w.block;
   q.sf16 = w.scale_dtype == CV3_F16;
+  q.q4 = w.kind == CV3_KIND_Q4;
   return q;
 }
 
 int check_qw(const cv3_qweight& w, const char* what, int64_t k) {
   CV3_REQUIRE(w.q && w.scales, CV3_EINVAL, "%s: missing weight", what);
+  CV3_REQUIRE(w.kind == CV3_KIND_Q8 || w.kind == CV3_KIND_Q4, CV3_EINVAL, "%s: kind %d is neither q8 nor q4", what,
+              w.kind);
   CV3_REQUIRE(w.k == k, CV3_EINVAL, "%s: K is %lld, expected %lld", what, (long long)w.k, (long long)k);
-  CV3_REQUIRE(w.block > 0 && w.block % 16 == 0 && w.kp % w.block == 0 && w.kp >= w.k && w.kp % 16 == 0,
-              CV3_EINVAL, "%s: block %lld / padded K %lld must be multiples of 16", what, (long long)w.block,
-              (long long)w.kp);
+  const int64_t cpc = w.kind == CV3_KIND_Q4 ? 32 : 16;  // codes per 16-byte chunk
+  CV3_REQUIRE(w.block > 0 && w.block % cpc == 0 && w.kp % w.block == 0 && w.kp >= w.k && w.kp % cpc == 0,
+              CV3_EINVAL, "%s: block %lld / padded K %lld must be multiples of %lld", what, (long long)w.block,
+              (long long)w.kp, (long long)cpc);
   CV3_REQUIRE((uintptr_t)w.q % 16 == 0, CV3_EINVAL, "%s: codes must be 16-byte aligned", what);
   CV3_REQUIRE(w.scale_dtype == CV3_F16 || w.scale_dtype == CV3_F32, CV3_EINVAL, "%s: scale dtype", what);
   return CV3_OK;
 }
 
-template <int LPR, int CPL>
+template <int LPR, int CPL, bool Q4>
 void launch_gemv(const GemvArgs& a, hipStream_t st) {
   const int64_t rows_per_block = 4 * (64 / LPR) / (a.mode == 2 ? 2 : 1);
   const dim3 grid((unsigned)ceil_div(a.n, rows_per_block));
-  const size_t lds = (size_t)LPR * CPL * 16 * sizeof(float);
-#define CV3_GEMV_LAUNCH(MODE)                                                                 \
-  if (a.w.sf16)                                                                              \
-    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, true>), grid, dim3(256), lds, st, a);     \
-  else                                                                                       \
-    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, false>), grid, dim3(256), lds, st, a);
+  const size_t lds = (size_t)LPR * CPL * kCodes<Q4> * sizeof(float);
+#define CV3_GEMV_LAUNCH(MODE)                                                                  \
+  if (a.w.sf16)                                                                               \
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, true, Q4>), grid, dim3(256), lds, st, a);  \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_dec_gemv<LPR, CPL, MODE, false, Q4>), grid, dim3(256), lds, st, a);
   if (a.mode == 2) {
     CV3_GEMV_LAUNCH(2)
   } else if (a.mode == 1) {
@@ -659,23 +674,33 @@ void launch_gemv(const GemvArgs& a, hipStream_t st) {
 #undef CV3_GEMV_LAUNCH
 }
 
-// chunks per lane for a padded K, at LPR lanes per row
-int gemv(const GemvArgs& a, hipStream_t st) {
-  const int64_t nch = a.w.kp / 16;
-  if (nch <= 8 * 8) {
-    launch_gemv<8, 8>(a, st);
+// Lanes per row and 16-byte chunks per lane for a row of nch chunks.  Every
+// shape stages at most 1024 * 16 floats of vector in LDS (64 KiB).
+template <bool Q4>
+int gemv_shape(const GemvArgs& a, hipStream_t st) {
+  const int64_t nch = (Q4 ? a.w.kp / 2 : a.w.kp) / 16;
+  if (Q4 && nch <= 8 * 4) {
+    launch_gemv<8, 4, Q4>(a, st);    // q4, K <= 1024: 128 contiguous bytes per row group
+  } else if (!Q4 && a.mode == 2 && nch <= 16 * 4) {
+    launch_gemv<16, 4, Q4>(a, st);   // q8 [gate; up], K <= 1024: half the chunks per lane of 8 x 8
+  } else if (nch <= 8 * 8) {
+    launch_gemv<8, 8, Q4>(a, st);
   } else if (a.mode == 2 && nch <= 16 * 20) {
-    launch_gemv<16, 20>(a, st);  // SwiGLU pairs two row groups of one wave
+    launch_gemv<16, 20, Q4>(a, st);  // SwiGLU pairs two row groups of one wave
+  } else if (Q4 && a.mode != 2 && nch <= 64 * 3) {
+    launch_gemv<64, 3, Q4>(a, st);   // q4, K = 4864: one row per wave
   } else if (a.mode != 2 && nch <= 64 * 5) {
-    launch_gemv<64, 5>(a, st);   // e.g. K = 4864: one row per wave, 4 rows per workgroup
-  } else if (a.mode != 2 && nch <= 64 * 16) {
-    launch_gemv<64, 16>(a, st);
+    launch_gemv<64, 5, Q4>(a, st);   // q8, K = 4864: one row per wave, 4 rows per workgroup
+  } else if (a.mode != 2 && nch * kCodes<Q4> <= 64 * 16 * 16) {
+    launch_gemv<64, Q4 ? 8 : 16, Q4>(a, st);
   } else {
     return fail(CV3_EUNSUPPORTED, "decode GEMV K=%lld too large", (long long)a.w.kp);
   }
   CV3_LAUNCHED();
   return CV3_OK;
 }
+
+int gemv(const GemvArgs& a, hipStream_t st) { return a.w.q4 ? gemv_shape<true>(a, st) : gemv_shape<false>(a, st); }
 
 }  // namespace
 
@@ -697,10 +722,11 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
   if ((rc = check_qw(m->embedding, "speech_embedding", D))) return rc;
   CV3_REQUIRE(m->qkv.rows == (H + 2 * Hk) * dh && m->o.rows == D && m->gate_up.rows == 2 * I && m->down.rows == D,
               CV3_EINVAL, "stacked weight rows do not match the geometry");
-  CV3_REQUIRE(m->qkv.kp / 16 <= 8 * 8, CV3_EUNSUPPORTED, "qkv K too large for the fused rotary GEMV");
+  CV3_REQUIRE(m->qkv.kp <= 1024, CV3_EUNSUPPORTED, "qkv K too large for the fused rotary GEMV");
   CV3_REQUIRE(s->cap / KCH <= NSMAX, CV3_EUNSUPPORTED, "cache capacity above %d positions", NSMAX * KCH);
   CV3_REQUIRE(H <= 16 && dh % 4 == 0 && D % 4 == 0 && I % 4 == 0, CV3_EUNSUPPORTED, "decode geometry");
-  CV3_REQUIRE(m->o.kp / 16 <= 8 * 8, CV3_EUNSUPPORTED, "o_proj K too large");
+  CV3_REQUIRE(m->o.kp <= 1024, CV3_EUNSUPPORTED, "o_proj K too large");
+  CV3_REQUIRE(m->embedding.kind == CV3_KIND_Q8, CV3_EUNSUPPORTED, "speech_embedding must be q8");
   CV3_REQUIRE(s->workspace_floats >= kWsQ + H * NSMAX * 64 + H * NSMAX * 2 + I + 64, CV3_EINVAL,
               "workspace too small");
   hipStream_t st = stream_of(stream);
@@ -718,23 +744,34 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
     QkvArgs qa{qkv, l * qkv.rows, s->x, m->ln1 + l * D, m->eps, m->qkv_bias + l * qkv.rows, (int)H, (int)Hk,
                (int)dh, m->rope_cos, m->rope_sin, s->pos, qbuf, kc, vc, s->cap};
     const int64_t pairs = (H + 2 * Hk) * dh / 2;
-    if (qkv.sf16)
-      hipLaunchKernelGGL((k_dec_qkv<8, true>), dim3((unsigned)ceil_div(pairs, 16)), dim3(256), 64 * 16 * sizeof(float),
-                         st, qa);
-    else
-      hipLaunchKernelGGL((k_dec_qkv<8, false>), dim3((unsigned)ceil_div(pairs, 16)), dim3(256),
-                         64 * 16 * sizeof(float), st, qa);
+    const dim3 gq((unsigned)ceil_div(pairs, 16));
+    const size_t lds = 1024 * sizeof(float);  // 8 lanes x 8 q8 chunks x 16 codes = 8 x 4 q4 chunks x 32 codes
+    if (qkv.q4) {
+      if (qkv.sf16)
+        hipLaunchKernelGGL((k_dec_qkv<4, true, true>), gq, dim3(256), lds, st, qa);
+      else
+        hipLaunchKernelGGL((k_dec_qkv<4, false, true>), gq, dim3(256), lds, st, qa);
+    } else if (qkv.sf16) {
+      hipLaunchKernelGGL((k_dec_qkv<8, true, false>), gq, dim3(256), lds, st, qa);
+    } else {
+      hipLaunchKernelGGL((k_dec_qkv<8, false, false>), gq, dim3(256), lds, st, qa);
+    }
     CV3_LAUNCHED();
     AttnArgs aa{qbuf, kc, vc, (int)H, (int)Hk, (int)dh, s->cap, s->pos, scale, part_o, part_ml};
     hipLaunchKernelGGL(k_dec_attn, dim3((unsigned)(s->cap / KCH), (unsigned)Hk), dim3(512), 0, st, aa);
     CV3_LAUNCHED();
     OprojArgs oa{o, l * o.rows, D, part_o, part_ml, (int)H, (int)dh, s->pos, s->x};
-    if (o.sf16)
-      hipLaunchKernelGGL((k_dec_oproj<8, true>), dim3((unsigned)ceil_div(D, 32)), dim3(256), 64 * 16 * sizeof(float),
-                         st, oa);
-    else
-      hipLaunchKernelGGL((k_dec_oproj<8, false>), dim3((unsigned)ceil_div(D, 32)), dim3(256),
-                         64 * 16 * sizeof(float), st, oa);
+    const dim3 go((unsigned)ceil_div(D, 32));
+    if (o.q4) {
+      if (o.sf16)
+        hipLaunchKernelGGL((k_dec_oproj<4, true, true>), go, dim3(256), lds, st, oa);
+      else
+        hipLaunchKernelGGL((k_dec_oproj<4, false, true>), go, dim3(256), lds, st, oa);
+    } else if (o.sf16) {
+      hipLaunchKernelGGL((k_dec_oproj<8, true, false>), go, dim3(256), lds, st, oa);
+    } else {
+      hipLaunchKernelGGL((k_dec_oproj<8, false, false>), go, dim3(256), lds, st, oa);
+    }
     CV3_LAUNCHED();
     GemvArgs gb{gu, l * gu.rows, I, s->x, m->ln2 + l * D, m->eps, nullptr, hbuf, 2};
     if ((rc = gemv(gb, st))) return rc;
@@ -765,6 +802,7 @@ int cv3_qwen2_embed_token(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
   CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
   int rc;
   if ((rc = check_qw(m->embedding, "speech_embedding", m->hidden))) return rc;
+  CV3_REQUIRE(m->embedding.kind == CV3_KIND_Q8, CV3_EUNSUPPORTED, "speech_embedding must be q8");
   hipLaunchKernelGGL(k_dec_embed, dim3(1), dim3(256), 0, stream_of(stream), make_qw(m->embedding), s->token, s->x);
   CV3_LAUNCHED();
   return CV3_OK;

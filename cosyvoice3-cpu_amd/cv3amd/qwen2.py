@@ -32,7 +32,7 @@ c_i64, c_vp = ctypes.c_int64, ctypes.c_void_p
 
 class QWeight(ctypes.Structure):
     _fields_ = [("q", c_vp), ("scales", c_vp), ("rows", c_i64), ("k", c_i64), ("kp", c_i64), ("block", c_i64),
-                ("scale_dtype", ctypes.c_int)]
+                ("scale_dtype", ctypes.c_int), ("kind", ctypes.c_int)]
 
 
 class Model(ctypes.Structure):
@@ -58,8 +58,8 @@ def rope_tables(dim: int, theta: float, n: int):
     return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
-def _is_q8(w) -> bool:
-    return getattr(w, "kind", None) == "q8"
+def _kind(w):
+    return getattr(w, "kind", None)
 
 
 def _host(a):
@@ -67,35 +67,38 @@ def _host(a):
 
 
 class _Stacked:
-    """Rows of several q8 QTensors (per layer, in order) stacked into one device array."""
+    """Rows of several q8 or q4 QTensors (per layer, in order) stacked into one device array."""
 
     def __init__(self, per_layer: List[List[object]]):
         qs, ss = [], []
         first = per_layer[0][0]
         self.k = int(first.shape[1])
         self.block = int(first.block)
+        self.kind = _kind(first)
         sdt = np.dtype(_host(first.scales).dtype)
         for parts in per_layer:
             for w in parts:
-                if not _is_q8(w):
-                    raise ValueError("the device decode takes q8 weights (per-channel or block scales)")
-                if int(w.shape[1]) != self.k or int(w.block) != self.block or _host(w.scales).dtype != sdt:
-                    raise ValueError("stacked weights must share K, block and scale dtype")
+                if _kind(w) not in ("q8", "q4"):
+                    raise ValueError("the device decode takes q8 or q4 weights (the balanced and tiny profiles)")
+                if (int(w.shape[1]) != self.k or int(w.block) != self.block or _host(w.scales).dtype != sdt
+                        or _kind(w) != self.kind):
+                    raise ValueError("stacked weights must share kind, K, block and scale dtype")
                 qs.append(_host(w.q))
                 ss.append(_host(w.scales))
         self.rows = sum(int(w.shape[0]) for w in per_layer[0])
         q = np.concatenate(qs, axis=0)
         s = np.concatenate(ss, axis=0)
-        self.kp = int(q.shape[1])
-        if self.kp % 16 or self.block % 16:
-            raise ValueError("padded K and block must be multiples of 16")
+        self.kp = int(s.shape[1]) * self.block  # q4 rows hold kp / 2 bytes
+        cpc = 32 if self.kind == "q4" else 16
+        if self.kp % cpc or self.block % cpc:
+            raise ValueError(f"padded K and block must be multiples of {cpc}")
         self.sf16 = sdt == np.dtype(np.float16)
         self.q = to_device(np.ascontiguousarray(q))
         self.scales = to_device(np.ascontiguousarray(s))
 
     def struct(self) -> QWeight:
         return QWeight(self.q.ptr, self.scales.ptr, self.rows, self.k, self.kp, self.block,
-                       _lib.F16 if self.sf16 else _lib.F32)
+                       _lib.F16 if self.sf16 else _lib.F32, _lib.KIND_Q4 if self.kind == "q4" else _lib.KIND_Q8)
 
     @property
     def nbytes(self):

@@ -15,7 +15,8 @@ profiles follow cv3cpu/convert.py:25-49,255-265: under ``balanced`` every large
 matrix is q8 (block 64, float16 scales) except time_embed / proj_out, which are
 narrowed to float16, and conv_pos / biases / norms, which stay float32.  The
 ``per_channel`` profile is the same q8 algorithm with one float32 scale per
-output row (block = K).
+output row (block = K).  ``tiny`` is ``balanced`` with the Qwen2 body layers in
+q4 (block 32, float16 scales), as the reference's tiny profile stores them.
 """
 
 from __future__ import annotations
@@ -168,7 +169,8 @@ def choose_kind(name: str, arr: np.ndarray, profile: str) -> str:
 
     ``f32``: everything float32.  ``balanced``: q8 block 64 / float16 scales for
     large matrices, float16 for time_embed / proj_out.  ``per_channel``: like
-    balanced, with one float32 scale per output row.
+    balanced, with one float32 scale per output row.  ``tiny``: like balanced, with
+    q4 for the matrices of ``llm.model.layers.*`` (convert.py:26-27,262-263).
     """
     if profile == "f32" or arr.ndim == 1 or _KEEP_F32.search(name) or arr.size < (1 << 16):
         return "f32"
@@ -176,17 +178,26 @@ def choose_kind(name: str, arr: np.ndarray, profile: str) -> str:
         return "f16"
     if arr.ndim == 3:
         return "f32"   # grouped / conv weights stay float32 on this path
+    if profile == "tiny" and (name.startswith("llm.model.layers.") or name == "llm.model.embed_tokens"):
+        return "q4"
     return "q8"
 
 
-def quantize_store(tensors: Dict[str, np.ndarray], profile: str, quantize_q8) -> Dict[str, object]:
-    """Apply a profile: q8 entries become ``{"kind","q","scales","shape","block"}`` records,
-    float16 entries are narrowed.  ``quantize_q8(w, block, scale_dtype)`` does the work, so
-    the same inputs can be quantised by the device kernel or by a restatement."""
+def quantize_store(tensors: Dict[str, np.ndarray], profile: str, quantize_q8, quantize_q4=None) -> Dict[str, object]:
+    """Apply a profile: q8 / q4 entries become ``{"kind","q","scales","shape","block"}``
+    records, float16 entries are narrowed.  ``quantize_q8(w, block, scale_dtype)`` and
+    ``quantize_q4(w)`` do the work, so the same inputs can be quantised by the device
+    kernels or by a restatement."""
     out: Dict[str, object] = {}
     for name, arr in tensors.items():
         kind = choose_kind(name, arr, profile)
-        if kind == "q8":
+        if kind == "q4":
+            if quantize_q4 is None:
+                raise ValueError(f"profile {profile!r} needs a q4 quantiser")
+            q, s, kp = quantize_q4(arr)
+            out[name] = {"kind": "q4", "q": np.asarray(q), "scales": np.asarray(s), "shape": arr.shape,
+                         "block": 32, "orig_shape": None}
+        elif kind == "q8":
             k = arr.shape[1]
             if profile == "per_channel":
                 q, s, kp = quantize_q8(arr, k, np.float32)

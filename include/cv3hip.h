@@ -228,20 +228,23 @@ int cv3_istft(int mode, const float* a, const float* b, int64_t frames, int n_ff
               cv3_stream_t s);
 
 /* ---------------- Qwen2 decode step (cv3cpu/models/qwen2.py:139-179, cv3cpu/models/llm.py:68-77,112-123) --------- */
-/* One stacked int8 weight: `rows` rows per layer, layer l row r at q + (l * rows + r) * kp, its scales at
- * scales + (l * rows + r) * (kp / block).  Per-output-channel: block = kp, float32 scales; the reference's
- * q8 (quant.py:56-67): block = 64, float16 scales.  kp and block are multiples of 16. */
+/* One stacked quantised weight: `rows` rows per layer, layer l row r at q + (l * rows + r) * row_bytes, its
+ * scales at scales + (l * rows + r) * (kp / block).  kind CV3_KIND_Q8: int8 codes, row_bytes = kp, kp and
+ * block multiples of 16; per-output-channel is block = kp with float32 scales, the reference's q8
+ * (quant.py:56-67) block = 64 with float16 scales.  kind CV3_KIND_Q4: the reference's packed nibbles
+ * (quant.py:70-86, block 32, +8 bias, float16 scales), row_bytes = kp / 2, kp and block multiples of 32. */
 typedef struct {
   const void* q;
   const void* scales;
   int64_t rows, k, kp, block;
   int scale_dtype; /* CV3_F32 or CV3_F16 */
+  int kind;        /* CV3_KIND_Q8 or CV3_KIND_Q4 */
 } cv3_qweight;
 
 /* Device pointers of a resident Qwen2 body + CosyVoice3 LM head.  qkv stacks [q; k; v] rows per layer
  * (heads*dh + 2*kv_heads*dh), gate_up stacks [gate; up] (2*inter); qkv_bias [layers, qkv rows];
  * ln1 / ln2 [layers, hidden]; norm [hidden]; head = llm_decoder [vocab, hidden] with head_bias (may be
- * NULL); embedding = speech_embedding [vocab, hidden]; rope_cos / rope_sin [cap, head_dim] from
+ * NULL); embedding = speech_embedding [vocab, hidden] (q8); rope_cos / rope_sin [cap, head_dim] from
  * RopeCache (qwen2.py:35-61). */
 typedef struct {
   int64_t layers, hidden, heads, kv_heads, head_dim, inter;
@@ -280,7 +283,7 @@ typedef struct {
  * x = speech_embedding[id] (llm.py:121), history[pos + 1] = id, pos += 1.  Reads pos from device
  * memory, so one captured graph of this call serves every step.  The caller keeps pos + 1 < cap. */
 int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
-/* The decode step's int8 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
+/* The decode step's q8 / q4 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
  * y = W . v with v = x, or v = rms_norm(x, rms_w, eps) when rms_w is given (ops.py:101-104).
  * mode 0: y = W v + bias (bias may be NULL); 1: y += W v; 2: rows are [gate; up] (rows/2 each) and
  * y = silu(gate . v) * (up . v) (qwen2.py:175-177).  K <= 16384 (mode 2: K <= 5120). */

@@ -1,8 +1,9 @@
 """Device-resident greedy Qwen2 decode against the oracle.
 
 Both sides load the same seeded synthetic Qwen2-0.5B weights (cv3amd/synth.py),
-quantised by the oracle's quantize_q8 (bit-exact with the device quantiser, see
-test_gpu_ops.py), with the KV cache pre-filled to 512 positions of N(0, 1).
+quantised by the oracle's quantize_q8 / quantize_q4 (bit-exact with the device
+quantisers, see test_gpu_ops.py) under the per-channel, balanced (q8) and tiny
+(q4 body) profiles, with the KV cache pre-filled to 512 positions of N(0, 1).
 The oracle runs cv3cpu's Qwen2Model.forward / llm_decoder / speech_embedding
 restatement (oracle/qwen2.py, oracle/llm.py) with greedy selection.
 Bars: per-step logits within 1e-5 (max abs error over max |logit|), identical
@@ -25,7 +26,7 @@ def _setup(layers, profile, seed=0):
     from cv3amd import synth
     from cv3amd.weights import WeightStore
     t = synth.qwen2_tensors(layers=layers, seed=seed)
-    t = synth.quantize_store(t, profile, oracle.quant.quantize_q8)
+    t = synth.quantize_store(t, profile, oracle.quant.quantize_q8, oracle.quant.quantize_q4)
     meta = synth.qwen2_meta(layers=layers)
     cpu = WeightStore(t, meta, oracle.quant.QTensor)
     dev = WeightStore(t, meta, cv3amd.quant.QTensor)
@@ -47,7 +48,7 @@ def _oracle_lm(cpu, k, v, steps):
     return lm, cache
 
 
-@pytest.mark.parametrize("profile", ["per_channel", "balanced"])
+@pytest.mark.parametrize("profile", ["per_channel", "balanced", "tiny"])
 def test_decode_two_layers_logits_and_tokens(gpu, profile):
     from cv3amd.qwen2 import DeviceQwen2
     steps = 12
@@ -74,12 +75,13 @@ def test_decode_two_layers_logits_and_tokens(gpu, profile):
         assert rel_err(kc[i][:, :PREFILL + steps], cache.k[i][:, :PREFILL + steps]) < 1e-5
 
 
-def test_decode_full_depth_graph_replay(gpu):
+@pytest.mark.parametrize("profile", ["per_channel", "tiny"])
+def test_decode_full_depth_graph_replay(gpu, profile):
     """24 layers, 8 greedy tokens replayed from one captured step graph."""
     from cv3amd.qwen2 import DeviceQwen2
     steps = 8
-    cpu, dev, k, v = _setup(24, "per_channel")
-    print(f"[decode] 24 layers per-channel, {steps} steps, graph", flush=True)
+    cpu, dev, k, v = _setup(24, profile)
+    print(f"[decode] 24 layers {profile}, {steps} steps, graph", flush=True)
     lm, cache = _oracle_lm(cpu, k, v, steps)
     want = lm.greedy(lm.speech_emb([lm.sos]), cache, steps)
     d = DeviceQwen2(dev, cap=1024)

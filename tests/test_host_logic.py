@@ -66,6 +66,19 @@ def test_balanced_profile_kinds():
                        "per_channel") == "q8"
 
 
+def test_tiny_profile_kinds():
+    """tiny = balanced with the Qwen2 body layers in q4 (cv3cpu/convert.py:26-27,254-264)."""
+    from cv3amd.synth import choose_kind
+    w = np.zeros((4864, 896), np.float32)
+    assert choose_kind("llm.model.layers.3.mlp.up_proj.weight", w, "tiny") == "q4"
+    assert choose_kind("llm.model.layers.3.self_attn.k_proj.weight", np.zeros((128, 896), np.float32), "tiny") == "q4"
+    assert choose_kind("llm.model.layers.3.self_attn.k_proj.bias", np.zeros(128, np.float32), "tiny") == "f32"
+    assert choose_kind("llm.model.layers.3.post_attention_layernorm", np.ones(896, np.float32), "tiny") == "f32"
+    assert choose_kind("llm.llm_decoder.weight", np.zeros((6761, 896), np.float32), "tiny") == "q8"
+    assert choose_kind("llm.speech_embedding", np.zeros((6761, 896), np.float32), "tiny") == "q8"
+    assert choose_kind("flow.decoder.estimator.transformer_blocks.0.ff.ff.0.0.weight", w, "tiny") == "q8"
+
+
 def test_synthetic_tensors_are_seeded_per_name():
     from cv3amd.synth import dit_tensors, tensor
     a = dit_tensors(depth=1)
