@@ -347,19 +347,31 @@ def bench_hift(args, tensors, meta):
         ms = tm.stop() / args.hift_runs
         out[label] = ms
         log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
+    # mel -> waveform with the F0 predictor and the excitation on the device as well
+    for label, chunk in (("inference_whole", None), ("inference_chunked_1s", 50)):
+        d.inference(mel_d, chunk=chunk, graph=args.graph)
+        synchronize()
+        tm = Timer()
+        tm.start()
+        for _ in range(args.hift_runs):
+            d.inference(mel_d, chunk=chunk, graph=args.graph)
+        ms = tm.stop() / args.hift_runs
+        out[label] = ms
+        log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
     out["flops_whole"] = d.flops(T)
     return out
 
 
 def cpu_hift(tensors, meta):
-    """The oracle's whole-utterance decode of the same input on the host cores."""
+    """The oracle's whole-utterance inference (F0, excitation, decode) of the same mel
+    on the host cores."""
     import oracle.quant
     from oracle.hift import HiFTGenerator
     from cv3amd.weights import WeightStore
     h = HiFTGenerator(WeightStore(tensors, meta, oracle.quant.QTensor), "hift.")
-    mel, source = hift_inputs(500)
+    mel, _ = hift_inputs(500)
     t0 = time.perf_counter()
-    h.decode(mel, source)
+    h.decode(mel, h.excitation(h.f0_predict(mel).astype(np.float32)))
     return time.perf_counter() - t0
 
 
@@ -520,15 +532,21 @@ def main():
         }
     if voc is not None:
         line["vocoder"] = {
-            "workload": "causal HiFTNet decode, mel [1, 80, 500] (10 s), base 512, ups x8/x5/x3, iSTFT 16/4, fp32",
+            "workload": "causal HiFTNet, mel [1, 80, 500] (10 s), base 512, ups x8/x5/x3, iSTFT 16/4, fp32; "
+                        "ms_whole / ms_chunked_1s decode a precomputed source, ms_inference_* run mel -> waveform "
+                        "(F0 net, NSF excitation and decode) on the device",
             "ms_whole": round(voc["whole"], 3), "rtf_whole": round(voc["whole"] / 1e3 / AUDIO_SECONDS, 6),
             "ms_chunked_1s": round(voc["chunked_1s"], 3),
             "rtf_chunked_1s": round(voc["chunked_1s"] / 1e3 / AUDIO_SECONDS, 6),
+            "ms_inference_whole": round(voc["inference_whole"], 3),
+            "rtf_inference_whole": round(voc["inference_whole"] / 1e3 / AUDIO_SECONDS, 6),
+            "ms_inference_chunked_1s": round(voc["inference_chunked_1s"], 3),
             "conv_tflops_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / 1e12, 2),
             "mfma_roofline_frac_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / FP32_MFMA_PEAK, 4),
             "cpu_baseline": None if cpu_hift_s is None else {
                 "value": round(cpu_hift_s / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
-                "sample": "one whole-utterance decode of the same input by the oracle"},
+                "sample": "one whole-utterance inference (F0 net, excitation, decode) of the same mel by the "
+                          "oracle; compare with rtf_inference_whole"},
         }
     print(json.dumps(line), flush=True)
 

@@ -1,4 +1,4 @@
-"""Device-resident causal HiFTNet decode: source STFT -> conv stack -> iSTFT head.
+"""Device-resident causal HiFTNet: F0 -> NSF source -> source STFT -> conv stack -> iSTFT head.
 
 Restates cv3cpu/models/hift.py:114-210 (``_resblock``, ``_spectral``,
 ``_spectral_chunked``, ``decode``) with every activation resident in HBM.  Inside the
@@ -6,9 +6,14 @@ stack activations are channels-last (time, channels): a stride-1 conv is then an
 implicit GEMM whose A rows are shifted input rows, fed to LDS by DMA
 (cv3_conv1d_cl_packed).  The mel and the source STFT come in the reference's
 (channels, time) layout and are read through strides by the first convs; conv_post
-writes (channels, time) for the iSTFT head.  The F0 predictor and the NSF excitation
-(hift.py:56-111, float64 host code in the reference) produce the ``source`` signal
-this class takes as input.
+writes (channels, time) for the iSTFT head.
+
+``inference`` runs the whole vocoder on the device (hift.py:212-218): the F0
+predictor's five causal convs + ELU (float32, like the reference's conv1d) and its
+classifier summed in float64 (cv3_f0_classify), then the excitation
+(cv3_nsf_source: float64 harmonic phase, dither, Linear(9 -> 1), tanh), then
+``decode``.  The dither buffer is the seeded TorchMT19937 draw of hift.py:75-81,
+made once on the host replica and kept in HBM.
 
 Per upsampling stage i (reference lines in brackets):
   leaky(x, 0.1), nearest x r_i fused into the causal ``ups`` conv      (hift.py:137-142)
@@ -72,13 +77,19 @@ class DeviceHiFT:
         self.hop = int(m.get("istft_hop_len", 4))
         self.slope = float(m.get("lrelu_slope", 0.1))
         self.limit = float(m.get("audio_limit", 0.99))
+        self.sampling_rate = int(m.get("sampling_rate", 24000))
+        self.harmonics = int(m.get("nb_harmonics", 8)) + 1
+        self.nsf_alpha = float(m.get("nsf_alpha", 0.1))
+        self.nsf_sigma = float(m.get("nsf_sigma", 0.003))
+        self.nsf_threshold = float(m.get("nsf_voiced_threshold", 10.0))
+        self.noise_seed = int(m.get("noise_seed", 0))
         self.nk = len(self.rb_k)
         self.up_total = int(np.prod(self.rates))
         self.w = {}
         self.wp = {}   # conv weights repacked (out, k, in) for the channels-last implicit GEMM
         self.shape = {}
         for name in weights.keys():
-            if not name.startswith(prefix) or "f0_predictor" in name or "m_source" in name:
+            if not name.startswith(prefix) or "f0_predictor.classifier" in name or "m_source" in name:
                 continue
             arr = np.asarray(weights.get(name), np.float32)
             key = name[len(prefix):]
@@ -86,6 +97,24 @@ class DeviceHiFT:
             self.shape[key] = arr.shape
             if arr.ndim == 3 and arr.shape[1] % 32 == 0:
                 self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
+        # the F0 predictor's condnet convs sit with the stack's weights above; its
+        # classifier and the source merge (hift.py:56-72,108-110) are float32 vectors
+        self.f0_depth = 0
+        while f"f0_predictor.condnet.{self.f0_depth}.weight" in self.shape:
+            self.f0_depth += 1
+        cls = f"{prefix}f0_predictor.classifier."
+        self.f0_cls = None
+        if cls + "weight" in weights:
+            self.f0_cls = (to_device(np.asarray(weights.get(cls + "weight"), np.float32).reshape(-1)),
+                           to_device(np.asarray(weights.get(cls + "bias"), np.float32).reshape(-1)))
+        lin = f"{prefix}m_source.l_linear."
+        self.l_linear = None
+        if lin + "weight" in weights:
+            lw = np.asarray(weights.get(lin + "weight"), np.float32).reshape(-1)
+            if lw.size != self.harmonics:
+                raise ValueError(f"m_source.l_linear has {lw.size} inputs, expected {self.harmonics} harmonics")
+            self.l_linear = (to_device(lw), to_device(np.asarray(weights.get(lin + "bias"), np.float32).reshape(-1)))
+        self._noise: Optional[DeviceArray] = None
         self.window = to_device(hann_window(self.n_fft))
         # captured spectral stacks, one per input length: (graph, mel in, source STFT in, out, arena)
         self._graphs = {}
@@ -141,7 +170,8 @@ class DeviceHiFT:
                       ACT[act], float(act_param), alpha, 1e-9, res, 1, r_ts, None)
         return out
 
-    def _conv_in(self, x: DeviceArray, key: str, stride: int = 1, pad=(0, 0)) -> DeviceArray:
+    def _conv_in(self, x: DeviceArray, key: str, stride: int = 1, pad=(0, 0), act: str = "none",
+                 act_param: float = 0.0) -> DeviceArray:
         """conv1d (ops.py:165-219) from channels-first x (C_in, T_in) to channels-last output,
         for the convs on the stack's inputs (conv_pre on the mel, the strided source_downs on
         the source STFT), through the generic strided kernel."""
@@ -153,7 +183,7 @@ class DeviceHiFT:
         out = self._new((n, cout))
         _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k,
                   self.w[key + ".bias"].ptr, stride, 1, 1, pad[0], pad[1], 1, out.ptr, 1, cout, None,
-                  ACT["none"], 0.0, None, 0.0, None, 0, 0, None)
+                  ACT[act], float(act_param), None, 0.0, None, 0, 0, None)
         return out
 
     def _snake(self, x: DeviceArray, key: str) -> DeviceArray:
@@ -341,6 +371,67 @@ class DeviceHiFT:
         else:
             x = self.spectral_chunked(mel_d, s_stft, chunk, context, graph=graph)
         return self.istft_head(x)
+
+    # -- the source: F0 predictor + NSF excitation --------------------------------
+    def f0_predict(self, mel) -> DeviceArray:
+        """(80, T) mel -> (T,) F0 (hift.py:56-72), returned as the float32 values
+        inference() feeds the excitation (hift.py:216)."""
+        if not self.f0_depth or self.f0_cls is None:
+            raise ValueError("the weights hold no f0_predictor")
+        mel_d = mel if isinstance(mel, DeviceArray) else to_device(np.ascontiguousarray(mel, np.float32))
+        t = mel_d.shape[1]
+        # condnet: conv + ELU x depth, the first looking ahead (right pad), the rest causal;
+        # channels-last after the first conv, so the wide ones run as split-K DMA GEMMs
+        k0 = self.shape["f0_predictor.condnet.0.weight"][2]
+        x = self._conv_in(mel_d, "f0_predictor.condnet.0", pad=(0, causal_pad(k0)), act="elu", act_param=1.0)
+        for i in range(1, self.f0_depth):
+            k = self.shape[f"f0_predictor.condnet.{i}.weight"][2]
+            x = self._conv(x, f"f0_predictor.condnet.{i}", pad=(causal_pad(k), 0), act="elu", act_param=1.0)
+        n, c = x.shape
+        if n != t:
+            raise ValueError(f"the F0 predictor gave {n} frames for {t}")
+        f0 = DeviceArray((n,))
+        _lib.call("f0_classify", x.ptr, c, n, 1, c, self.f0_cls[0].ptr, self.f0_cls[1].ptr, f0.ptr, None)
+        return f0
+
+    def source_noise(self, n: int) -> DeviceArray:
+        """The first n rows of the [n, harmonics] dither buffer (hift.py:75-81), drawn once
+        from TorchMT19937(noise_seed) on the host replica and kept resident; a longer
+        request draws the buffer again at the new length, as the reference does."""
+        if self._noise is None or self._noise.shape[0] < n:
+            from .torch_rng import TorchMT19937
+            need = max(n, 1)
+            buf = TorchMT19937(self.noise_seed).random_float32(need * self.harmonics)
+            self._noise = to_device(buf.reshape(need, self.harmonics))
+        return self._noise
+
+    def set_source_noise(self, buf) -> None:
+        """Use a caller-supplied [n, harmonics] dither buffer (hift.py:83-88)."""
+        buf = np.ascontiguousarray(buf, np.float32)
+        if buf.ndim != 2 or buf.shape[1] != self.harmonics:
+            raise ValueError(f"dither buffer of shape {buf.shape}, expected (n, {self.harmonics})")
+        self._noise = to_device(buf)
+
+    def excitation(self, f0) -> DeviceArray:
+        """(T,) float32 F0 -> (480 T,) merged harmonic source (hift.py:90-111)."""
+        if self.l_linear is None:
+            raise ValueError("the weights hold no m_source.l_linear")
+        f0_d = f0 if isinstance(f0, DeviceArray) else to_device(np.ascontiguousarray(f0, np.float32))
+        t = f0_d.size
+        up = self.up_total * self.hop
+        noise = self.source_noise(up * t)
+        phase = DeviceArray((max(t, 1), self.harmonics), np.float64)
+        out = DeviceArray((up * t,))
+        _lib.call("nsf_source", f0_d.ptr, t, up, self.harmonics, float(self.sampling_rate), self.nsf_alpha,
+                  self.nsf_sigma, self.nsf_threshold, noise.ptr, self.l_linear[0].ptr, self.l_linear[1].ptr,
+                  phase.ptr, out.ptr, None)
+        return out
+
+    def inference(self, mel, chunk: Optional[int] = 250, context: int = 64, graph: bool = True) -> DeviceArray:
+        """(80, T) mel -> (480 T,) waveform, entirely on the device (hift.py:212-218)."""
+        mel_d = mel if isinstance(mel, DeviceArray) else to_device(np.ascontiguousarray(mel, np.float32))
+        source = self.excitation(self.f0_predict(mel_d))
+        return self.decode(mel_d, source, chunk=chunk, context=context, graph=graph)
 
     def flops(self, t: int) -> float:
         """Algorithmic conv flops of a whole-utterance decode of t mel frames."""

@@ -227,6 +227,18 @@ int cv3_istft(int mode, const float* a, const float* b, int64_t frames, int n_ff
               int center, int64_t length, float limit, float* frame_buf, float* y, int64_t* out_len_ptr,
               cv3_stream_t s);
 
+/* ---------------- HiFT source (cv3cpu/models/hift.py:56-111, 212-218) ---------------- */
+/* F0 classifier on the condnet output x (c, t) at strides (x_cs, x_ts): f0[t] = float32(|sum_c x w + b|), summed
+ * in float64 (hift.py:69-72 with inference()'s float32 cast, hift.py:216). */
+int cv3_f0_classify(const float* x, int64_t c, int64_t t, int64_t x_cs, int64_t x_ts, const float* w, const float* b,
+                    float* f0, cv3_stream_t s);
+/* HiFTGenerator.excitation (hift.py:90-111): float32 f0 [t] -> merged source [up * t].  noise [up * t, harmonics]
+ * is the dither buffer (hift.py:75-81), l_w [harmonics] / l_b [1] the m_source.l_linear weights; phase is
+ * t * harmonics doubles of caller scratch.  harmonics <= 16. */
+int cv3_nsf_source(const float* f0, int64_t t, int up, int harmonics, double sampling_rate, double alpha, double sigma,
+                   double voiced_threshold, const float* noise, const float* l_w, const float* l_b, double* phase,
+                   float* out, cv3_stream_t s);
+
 /* ---------------- Qwen2 decode step (cv3cpu/models/qwen2.py:139-179, cv3cpu/models/llm.py:68-77,112-123) --------- */
 /* One stacked quantised weight: `rows` rows per layer, layer l row r at q + (l * rows + r) * row_bytes, its
  * scales at scales + (l * rows + r) * (kp / block).  kind CV3_KIND_Q8: int8 codes, row_bytes = kp, kp and
