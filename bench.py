@@ -4,8 +4,9 @@
   * Qwen2-0.5B int8 greedy decode, batch 1 (the reported ``value``): 24 layers,
     hidden 896, 14/2 heads x 64, SwiGLU 4864, per-output-channel int8 weights with
     float32 scales, KV cache pre-filled to 512 positions of N(0, 1), K tokens
-    decoded from speech_embedding[sos] (one "step" = one token); and the same decode
-    with the tiny profile's q4 body layers (the ``decode_tiny`` object).
+    decoded from speech_embedding[sos] (one "step" = one token); the same decode with
+    the reference's sampler on the device (``sampled_tok_s``); and with the tiny
+    profile's q4 body layers (the ``decode_tiny`` object).
   * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
     fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
     of torch.randn((1, 80, 15000), seed 0); and the same solve over 30 s (T = 1500)
@@ -169,7 +170,23 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
     kms = tm.stop() / (reps * layers)
     achieved = gu_bytes / (kms / 1e3)
     log(f"{label}: gate/up GEMV {kms * 1e3:.2f} us/launch, {achieved / 1e9:.0f} GB/s")
+    # the reference's sampler (SamplingConfig defaults) on the device, stop ids held back
+    # for the whole run (strict min_len = all steps) so every timed token is decoded
+    class _Sampling:
+        top_p, top_k, win_size, tau_r, strict_min_len = 0.8, 25, 10, 0.1, True
+        rng = np.random.default_rng(0)
+    lm.fill_cache(k, v)
+    lm.generate_sampled(sos, PREFILL, args.warmup, args.warmup, _Sampling, sos, graph=args.graph)
+    lm.fill_cache(k, v)
+    synchronize()
+    tm.start()
+    sampled = lm.generate_sampled(sos, PREFILL, args.steps, args.steps, _Sampling, sos, graph=args.graph)
+    sms = tm.stop()
+    sampled_tok_s = len(sampled) / (sms / 1e3)
+    log(f"{label}: sampled (top_p 0.8, top_k 25, repetition window 10) {sms:.2f} ms for {len(sampled)} tokens "
+        f"= {sampled_tok_s:.1f} tok/s")
     return {
+        "sampled_tok_s": sampled_tok_s,
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
         "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
                    else "k_dec_gemv<8,8,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
@@ -490,6 +507,7 @@ def main():
         "cpu_baseline": cpu,
         "copy_GBps": round(copy_bps / 1e9, 1),
         "tokens_head": dec["tokens"][:8],
+        "sampled_tok_s": round(dec["sampled_tok_s"], 2),
     }
     if tiny is not None:
         tk = tiny["kernel"]

@@ -627,6 +627,456 @@ __global__ void k_dec_embed(QW emb, const int64_t* token, float* x) {
   for (int64_t c = threadIdx.x; c < emb.k; c += blockDim.x) x[c] = (float)emb.q[id * emb.kp + c] * sc_at(emb, id, c);
 }
 
+// ---------------------------------------------------------------------------
+// Sampling (cv3cpu/models/llm.py:37-49,125-149) on the device.
+//
+// NumPy's Generator draws from PCG64: a 128-bit LCG (multiplier below, the
+// stream's odd increment) whose 64-bit output is the XOR of the state's halves
+// rotated right by its top 6 bits; random() is (next >> 11) * 2^-53.  The state
+// is the Generator's own, copied in and out by the host, so the device consumes
+// exactly the draws the reference would and the host Generator continues after.
+//
+// Per token, in one 1024-thread workgroup, the reference's steps in order:
+//   logp = log_softmax(logits); below min_len the eos id (or every stop id)
+//   goes to -inf; probs = softmax(logp); the top_k entries in stable descending
+//   order (ties to the lower id); the nucleus: entries while their float64 sum
+//   is below top_p; p = probs / sum(probs) (NumPy's pairwise sum), cdf =
+//   cumsum(p) / cdf[-1], pick = first cdf > random().  If the pick occurs at
+//   least win_size * tau_r times among the last win_size tokens of this
+//   generation, it is masked and a second draw is taken from the full
+//   renormalised softmax the same way.  A stop id ends the generation: the step
+//   is recorded and later steps leave everything untouched.
+// ---------------------------------------------------------------------------
+constexpr int kSampleThreads = 1024;
+constexpr int kSamplePerThread = 8;      // vocab <= 8192, ids t*8 .. t*8+7 per thread
+constexpr int kTopKMax = 64;
+constexpr int kStopIds = 200;            // llm.py:64
+constexpr int kCandCap = (kSampleThreads / 64) * kTopKMax;  // gathered top-k candidates
+
+__device__ __forceinline__ uint64_t pcg64_next(uint64_t* st) {
+  typedef unsigned __int128 u128;
+  const u128 mult = ((u128)2549297995355413924ull << 64) | (u128)4865540595714422341ull;
+  u128 state = ((u128)st[0] << 64) | (u128)st[1];
+  const u128 inc = ((u128)st[2] << 64) | (u128)st[3];
+  state = state * mult + inc;
+  st[0] = (uint64_t)(state >> 64);
+  st[1] = (uint64_t)state;
+  const uint64_t x = (uint64_t)(state >> 64) ^ (uint64_t)state;
+  const unsigned rot = (unsigned)(state >> 122);
+  return (x >> rot) | (x << ((64u - rot) & 63u));
+}
+
+__device__ __forceinline__ double pcg64_double(uint64_t* st) {
+  return (double)(pcg64_next(st) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+__global__ void k_pcg64_random(uint64_t* pcg, int64_t n, double* out) {
+  uint64_t st[4] = {pcg[0], pcg[1], pcg[2], pcg[3]};
+  for (int64_t i = 0; i < n; ++i) out[i] = pcg64_double(st);
+  for (int i = 0; i < 4; ++i) pcg[i] = st[i];
+}
+
+struct SampleArgs {
+  NextArgs n;
+  double top_p, rep_threshold;
+  int64_t top_k, win_size, speech_token_size, min_len;
+  int strict_min_len;
+  int64_t* ctl;  // [start, stop step + 1 (0 while running), pcg state hi, lo, inc hi, lo]
+};
+
+// Wave reductions through DPP row permutations (quad swaps, half-row and row
+// mirrors: every lane ends with its 16-lane row's result) and four lane reads:
+// no LDS round trips, unlike shuffles.  Called with every lane of the wave active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  return ((uint64_t)dpp32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp32<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), lane) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+}
+// Orders one wave's LDS accesses around a point where its lanes exchange values
+// (the wave's own LDS operations complete in order; this keeps the compiler from
+// moving them and waits for the outstanding ones).  Not a workgroup barrier.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const int64_t b = __double_as_longlong(v);
+  return __longlong_as_double(((int64_t)__builtin_amdgcn_readlane((int)(b >> 32), lane) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)b, lane));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  k = max(k, dpp64<kDppXor1>(k));
+  k = max(k, dpp64<kDppXor2>(k));
+  k = max(k, dpp64<kDppHalfMirror>(k));
+  k = max(k, dpp64<kDppMirror>(k));
+  return max(max(readlane64(k, 0), readlane64(k, 16)), max(readlane64(k, 32), readlane64(k, 48)));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, __uint_as_float(dpp32<kDppXor1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp32<kDppXor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp32<kDppHalfMirror>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp32<kDppMirror>(__float_as_uint(v))));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppMirror>(__float_as_uint(v)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// (probability, id) as one integer whose order is the stable descending sort's:
+// larger probability first (non-negative floats order as their bits), then the
+// lower id.  0 marks an empty slot.
+__device__ __forceinline__ uint64_t rank_key(float p, int id) {
+  return ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0x7fffffff - id) | (1ull << 31);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return 0x7fffffff - (int)((uint32_t)k & 0x7fffffffu); }
+__device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+
+__device__ float blk_max(float v, float* red) {
+  v = wave_max_dpp(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red[0];
+  for (int w = 1; w < kSampleThreads / 64; ++w) t = fmaxf(t, red[w]);
+  return t;
+}
+
+__device__ float blk_sum(float v, float* red) {
+  v = wave_sum_dpp(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < kSampleThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+__device__ double blk_sum_d(double v, double* red) {
+  v = wave_sum_d(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < kSampleThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+// Exclusive prefix of v over the block in thread order.
+__device__ double blk_exclusive_scan_d(double v, double* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == 63) red[wave] = incl;
+  __syncthreads();
+  double base = 0.0;
+  for (int w = 0; w < wave; ++w) base += red[w];
+  return base + incl - v;
+}
+
+// softmax(sc) over the block as float32 (ops.py:84-87): e = exp(x - max), e / sum(e)
+__device__ void blk_softmax(const float* sc, float* p, float* red) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) m = fmaxf(m, sc[j]);
+  m = blk_max(m, red);
+  float e[kSamplePerThread], s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) {
+    e[j] = expf(sc[j] - m);
+    s += e[j];
+  }
+  s = blk_sum(s, red);
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) p[j] = e[j] / s;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
+  __shared__ float red[kSampleThreads / 64];
+  __shared__ double redd[kSampleThreads / 64];
+  __shared__ int redi[kSampleThreads / 64];
+  __shared__ uint64_t cand[kCandCap];
+  __shared__ float rowmax[kSampleThreads / 16];
+  __shared__ float thresh;
+  __shared__ int ncand;
+  __shared__ uint64_t sorted[64];
+  __shared__ double draw_u;
+  __shared__ int64_t pick;
+  __shared__ int resample;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t vocab = a.n.vocab;
+  const int base = tid * kSamplePerThread;
+  // the logits go out first: nothing they need has to arrive before them
+  float x[kSamplePerThread];
+  if (base + kSamplePerThread <= vocab) {
+    const float4 x0 = reinterpret_cast<const float4*>(a.n.logits + base)[0];
+    const float4 x1 = reinterpret_cast<const float4*>(a.n.logits + base)[1];
+    x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j) x[j] = base + j < vocab ? a.n.logits[base + j] : -INFINITY;
+  }
+  if (a.ctl[1] != 0) return;  // a stop id was drawn earlier: the generation is over
+  const int64_t pos = *a.n.pos, start = a.ctl[0], step = pos - start;
+  // decoded[-win_size:] of the tokens drawn so far (win_size 0 slices them all): wave 0
+  // fetches the first 64 now, while the distribution is formed
+  const int64_t w = a.win_size > 0 ? min(a.win_size, step) : step;
+  const int64_t w0 = pos - w + 1;
+  const int64_t hist0 = (wave == 0 && lane < w) ? a.n.history[w0 + lane] : -1;
+  // log_softmax (ops.py:90-93), then the eos mask of the first min_len steps
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) m = fmaxf(m, x[j]);
+  m = blk_max(m, red);
+  float z[kSamplePerThread], s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) {
+    z[j] = x[j] - m;
+    s += expf(z[j]);
+  }
+  const float ls = logf(blk_sum(s, red));
+  float sc[kSamplePerThread];
+  const bool ignore_eos = step < a.min_len;
+  const int64_t sts = a.speech_token_size;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) {
+    const int64_t id = base + j;
+    sc[j] = z[j] - ls;
+    if (id >= vocab) sc[j] = -INFINITY;
+    if (ignore_eos && (a.strict_min_len ? (id >= sts && id < sts + kStopIds) : id == sts)) sc[j] = -INFINITY;
+  }
+  float p[kSamplePerThread];
+  blk_softmax(sc, p, red);
+  // top_k in stable descending order.  A lower bound of the k-th largest
+  // probability is the k-th largest of the 64 row maxima (16 lanes x 8 ids per
+  // row): k rows hold an entry at least that large.  The entries at or above it
+  // are gathered, and wave 0 picks the k best of those (ties to the lower id).
+  // A flat distribution that leaves more candidates than the gather holds takes
+  // the exhaustive path: every wave its own k best, then wave 0 merges.
+  const int k = (int)min(a.top_k, vocab);
+  uint64_t key[kSamplePerThread];
+  float lmax = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) {
+    key[j] = base + j < vocab ? rank_key(p[j], base + j) : 0ull;
+    if (base + j < vocab) lmax = fmaxf(lmax, p[j]);
+  }
+  lmax = fmaxf(lmax, __uint_as_float(dpp32<kDppXor1>(__float_as_uint(lmax))));
+  lmax = fmaxf(lmax, __uint_as_float(dpp32<kDppXor2>(__float_as_uint(lmax))));
+  lmax = fmaxf(lmax, __uint_as_float(dpp32<kDppHalfMirror>(__float_as_uint(lmax))));
+  lmax = fmaxf(lmax, __uint_as_float(dpp32<kDppMirror>(__float_as_uint(lmax))));
+  if ((lane & 15) == 0) rowmax[wave * 4 + (lane >> 4)] = lmax;
+  if (tid == 0) ncand = 0;
+  __syncthreads();
+  if (wave == 0) {  // the k-th largest row maximum: the row whose key has k - 1 above it
+    const uint64_t rk = rank_key(rowmax[lane], lane);
+    int above = 0;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) above += readlane64(rk, q) > rk;
+    const uint64_t hit = __ballot(above == k - 1);
+    if (lane == 0) thresh = rowmax[__ffsll((unsigned long long)hit) - 1];
+  }
+  __syncthreads();
+  const float T = thresh;
+  int mine_n = 0;
+#pragma unroll
+  for (int j = 0; j < kSamplePerThread; ++j) mine_n += (key[j] != 0 && p[j] >= T);
+  if (mine_n) {
+    int slot = atomicAdd(&ncand, mine_n);
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j)
+      if (key[j] != 0 && p[j] >= T) {
+        if (slot < kCandCap) cand[slot] = key[j];
+        ++slot;
+      }
+  }
+  __syncthreads();
+  const int C = ncand;
+  constexpr int kPerLane = kCandCap / 64;
+  if (C > kCandCap) {  // uniform
+    __syncthreads();   // every gather write has landed before the slots are reused
+    for (int r = 0; r < k; ++r) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < kSamplePerThread; ++j) best = max(best, key[j]);
+      best = wave_max_u64(best);
+#pragma unroll
+      for (int j = 0; j < kSamplePerThread; ++j)
+        if (key[j] == best) key[j] = 0;
+      if (lane == 0) cand[wave * kTopKMax + r] = best;
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && C <= 64) {  // one candidate per lane: sort by counting the keys above each
+    const uint64_t ck = lane < C ? cand[lane] : 0ull;
+    int above = 0;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) above += readlane64(ck, q) > ck;
+    if (ck != 0) sorted[above] = ck;
+    wave_sync();
+  }
+  if (wave == 0) {
+    const bool all = C > kCandCap;
+    uint64_t ck[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int c = lane + 64 * j;  // gathered slot, or (wave, rank) of the exhaustive path
+      const bool ok = C > 64 && (all ? (c % kTopKMax) < k : c < C);
+      ck[j] = ok ? cand[c] : 0ull;
+    }
+    const int used = all ? kPerLane : (C + 63) / 64;  // slots per lane worth scanning
+    // entry r of the sorted head goes to lane r
+    uint64_t mine = 0;
+    if (C <= 64) mine = lane < k ? sorted[lane] : 0ull;
+    for (int r = 0; r < (C <= 64 ? 0 : k); ++r) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        if (j < used) best = max(best, ck[j]);
+      best = wave_max_u64(best);
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        if (ck[j] == best) ck[j] = 0;
+      if (lane == r) mine = best;
+    }
+    const double v = lane < k ? (double)key_p(mine) : 0.0;
+    // the nucleus: entries while the float64 running sum is below top_p (llm.py:40-45);
+    // every lane runs the same running sums on the values read from lane i
+    double cum = 0.0;
+    int n = 0;
+    for (int i = 0; i < k; ++i) {
+      if (cum >= a.top_p) break;
+      cum += readlane_d(v, i);
+      ++n;
+    }
+    if (n < 1) n = 1;  // top_p <= 0 leaves no entry (the reference's draw raises; the host rejects it)
+    // p / p.sum() with NumPy's pairwise sum (below 8 entries a running sum)
+    double tot;
+    if (n < 8) {
+      tot = 0.0;
+      for (int i = 0; i < n; ++i) tot += readlane_d(v, i);
+    } else {
+      double r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = readlane_d(v, j);
+      int i = 8;
+      for (; i < n - (n % 8); i += 8)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] += readlane_d(v, i + j);
+      tot = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+      for (; i < n; ++i) tot += readlane_d(v, i);
+    }
+    // Generator.choice: cdf = cumsum(p); cdf /= cdf[-1]; the first cdf > u
+    const double q = lane < n ? v / tot : 0.0;
+    double c = 0.0, cdf = 0.0;
+    for (int i = 0; i < n; ++i) {
+      c += readlane_d(q, i);
+      if (lane == i) cdf = c;
+    }
+    const double last = c;
+    uint64_t st[4] = {(uint64_t)a.ctl[2], (uint64_t)a.ctl[3], (uint64_t)a.ctl[4], (uint64_t)a.ctl[5]};
+    const double u = pcg64_double(st);  // every lane steps its copy; lane 0 stores it
+    const uint64_t past = __ballot(lane < n && cdf / last > u);
+    const int idx = past ? __ffsll((unsigned long long)past) - 1 : n - 1;
+    int64_t top = key_id(readlane64(mine, idx));
+    if (top < 0 || top >= vocab) top = 0;  // no finite probability at all: keep a valid row
+    // the repetition test over the window (llm.py:142-144)
+    int rep = __popcll(__ballot(hist0 == top));
+    for (int64_t q0 = w0 + 64; q0 <= pos; q0 += 64) {  // windows beyond 64 tokens
+      const int64_t qq = q0 + lane;
+      rep += __popcll(__ballot(qq <= pos && a.n.history[min(qq, pos)] == top));
+    }
+    const bool again = (double)rep >= a.rep_threshold;
+    const double u2 = again ? pcg64_double(st) : 0.0;
+    if (lane == 0) {
+      resample = again;
+      draw_u = u2;
+      pick = top;
+      for (int i = 0; i < 4; ++i) a.ctl[2 + i] = (int64_t)st[i];
+    }
+  }
+  __syncthreads();
+  if (resample) {  // uniform
+    const int64_t top = pick;
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j)
+      if (base + j == top) sc[j] = -INFINITY;
+    blk_softmax(sc, p, red);
+    double d[kSamplePerThread], tsum = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j) {
+      d[j] = (double)p[j];
+      tsum += d[j];
+    }
+    const double total = blk_sum_d(tsum, redd);
+    // cdf over ids in order: this thread's run of 8 after the sum of all earlier runs
+    double run = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j) run += d[j] / total;
+    double c = blk_exclusive_scan_d(run, redd);
+    double last = c + run;
+    __syncthreads();
+    if (tid == kSampleThreads - 1) redd[0] = last;  // cdf[-1]
+    __syncthreads();
+    last = redd[0];
+    const double u = draw_u;
+    int first = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kSamplePerThread; ++j) {
+      c += d[j] / total;
+      if (base + j < vocab && c / last > u && base + j < first) first = base + j;
+    }
+    // block minimum of the first id past u
+    for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o, 64));
+    if (lane == 0) redi[wave] = first;
+    __syncthreads();
+    if (tid == 0) {
+      int f = redi[0];
+      for (int w2 = 1; w2 < kSampleThreads / 64; ++w2) f = min(f, redi[w2]);
+      pick = f < vocab ? f : vocab - 1;
+    }
+    __syncthreads();
+  }
+  const int64_t id = pick;
+  // next input row and the bookkeeping of k_dec_next; a stop id ends the generation
+  for (int64_t cc = tid; cc < a.n.emb.k; cc += kSampleThreads)
+    a.n.x[cc] = (float)a.n.emb.q[id * a.n.emb.kp + cc] * sc_at(a.n.emb, id, cc);
+  __syncthreads();
+  if (tid == 0) {
+    a.n.history[pos + 1] = id;
+    *a.n.token = id;
+    *a.n.pos = pos + 1;
+    if (id >= sts && id < sts + kStopIds) a.ctl[1] = step + 1;
+  }
+}
+
 QW make_qw(const cv3_qweight& w) {
   QW q;
   q.q = reinterpret_cast<const int8_t*>(w.q);
@@ -706,7 +1156,9 @@ int gemv(const GemvArgs& a, hipStream_t st) { return a.w.q4 ? gemv_shape<true>(a
 
 extern "C" {
 
-int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+// One decode step: the layers, the head, then greedy selection (smp == nullptr) or the sampler.
+static int decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
+                       cv3_stream_t stream) {
   CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
   const int64_t H = m->heads, Hk = m->kv_heads, dh = m->head_dim, D = m->hidden, I = m->inter;
   CV3_REQUIRE(H > 0 && Hk > 0 && H % Hk == 0 && H / Hk <= 8, CV3_EINVAL, "heads %lld / kv heads %lld",
@@ -729,6 +1181,14 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
   CV3_REQUIRE(m->embedding.kind == CV3_KIND_Q8, CV3_EUNSUPPORTED, "speech_embedding must be q8");
   CV3_REQUIRE(s->workspace_floats >= kWsQ + H * NSMAX * 64 + H * NSMAX * 2 + I + 64, CV3_EINVAL,
               "workspace too small");
+  if (smp) {
+    CV3_REQUIRE(smp->ctl, CV3_EINVAL, "sampler: null control block");
+    CV3_REQUIRE(smp->top_k >= 1 && smp->top_k <= kTopKMax, CV3_EUNSUPPORTED, "sampler: top_k %lld (1..%d)",
+                (long long)smp->top_k, kTopKMax);
+    CV3_REQUIRE(m->head.rows <= (int64_t)kSampleThreads * kSamplePerThread, CV3_EUNSUPPORTED,
+                "sampler: vocabulary %lld above %d", (long long)m->head.rows, kSampleThreads * kSamplePerThread);
+    CV3_REQUIRE(smp->win_size >= 0 && smp->speech_token_size >= 0, CV3_EINVAL, "sampler: window / stop ids");
+  }
   hipStream_t st = stream_of(stream);
   const QW qkv = make_qw(m->qkv), o = make_qw(m->o), gu = make_qw(m->gate_up), dn = make_qw(m->down);
   const QW head = make_qw(m->head), emb = make_qw(m->embedding);
@@ -781,10 +1241,36 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
   GemvArgs gh{head, 0, head.rows, s->x, m->norm, m->eps, m->head_bias, s->logits, 0};
   if ((rc = gemv(gh, st))) return rc;
   NextArgs na{s->logits, head.rows, emb, s->x, s->pos, s->history, s->token};
-  hipLaunchKernelGGL(k_dec_next, dim3(1), dim3(1024), 0, st, na);
+  if (smp) {
+    SampleArgs sa{na, smp->top_p, smp->rep_threshold, smp->top_k, smp->win_size, smp->speech_token_size,
+                  smp->min_len, smp->strict_min_len, reinterpret_cast<int64_t*>(smp->ctl)};
+    hipLaunchKernelGGL(k_dec_sample, dim3(1), dim3(1024), 0, st, sa);
+  } else {
+    hipLaunchKernelGGL(k_dec_next, dim3(1), dim3(1024), 0, st, na);
+  }
   CV3_LAUNCHED();
   return CV3_OK;
 }
+
+int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  return decode_step(m, s, nullptr, stream);
+}
+
+int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
+                                  cv3_stream_t stream) {
+  CV3_REQUIRE(smp, CV3_EINVAL, "null sampler");
+  return decode_step(m, s, smp, stream);
+}
+
+int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream) {
+  CV3_REQUIRE(pcg && n >= 0 && (n == 0 || out), CV3_EINVAL, "pcg64: null state or output");
+  if (n == 0) return CV3_OK;
+  hipLaunchKernelGGL(k_pcg64_random, dim3(1), dim3(1), 0, stream_of(stream), reinterpret_cast<uint64_t*>(pcg), n,
+                     out);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
 
 int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
                 float* y, int mode, cv3_stream_t stream) {

@@ -44,6 +44,15 @@ class Model(ctypes.Structure):
                 ("rope_cos", c_vp), ("rope_sin", c_vp)]
 
 
+class Sampler(ctypes.Structure):
+    _fields_ = [("top_p", ctypes.c_double), ("rep_threshold", ctypes.c_double), ("top_k", c_i64),
+                ("win_size", c_i64), ("speech_token_size", c_i64), ("min_len", c_i64),
+                ("strict_min_len", ctypes.c_int), ("ctl", c_vp)]
+
+
+_M64 = (1 << 64) - 1
+
+
 class State(ctypes.Structure):
     _fields_ = [("k_cache", c_vp), ("v_cache", c_vp), ("cap", c_i64), ("pos", c_vp), ("token", c_vp),
                 ("history", c_vp), ("x", c_vp), ("logits", c_vp), ("workspace", c_vp),
@@ -161,6 +170,9 @@ class DeviceQwen2:
                            self.logits.ptr, self.workspace.ptr, nws)
         self._graph: Optional[Graph] = None
         self._pos_host = 0
+        # sampler control block: [start, stop step + 1, PCG64 state hi, lo, inc hi, lo]
+        self.ctl = DeviceArray((6,), np.int64).zero_()
+        self._sampled_graphs = {}
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
@@ -207,6 +219,67 @@ class DeviceQwen2:
         else:
             _lib.call("qwen2_decode_step", ctypes.byref(self.model), ctypes.byref(self.state), None)
         self._pos_host += 1
+
+    def step_sampled(self, smp: "Sampler", graph: bool = False):
+        """Enqueue one sampled token (no host synchronisation)."""
+        if self._pos_host + 1 >= self.cap:
+            raise ValueError("the KV cache is full")
+        if graph:
+            key = tuple(getattr(smp, f) for f, _ in Sampler._fields_)
+            g = self._sampled_graphs.get(key)
+            if g is None:
+                g = Graph()
+                with g:
+                    _lib.call("qwen2_decode_step_sampled", ctypes.byref(self.model), ctypes.byref(self.state),
+                              ctypes.byref(smp), None)
+                self._sampled_graphs[key] = g
+            g.launch()
+        else:
+            _lib.call("qwen2_decode_step_sampled", ctypes.byref(self.model), ctypes.byref(self.state),
+                      ctypes.byref(smp), None)
+        self._pos_host += 1
+
+    def generate_sampled(self, first_token: int, pos: int, max_len: int, min_len: int, sampling,
+                         speech_token_size: int, graph: bool = True, check_every: int = 16) -> List[int]:
+        """The token loop of CosyVoice3LM.generate (llm.py:104-123) with its sampler
+        (llm.py:125-149) on the device: up to max_len tokens from input
+        speech_embedding[first_token] at position pos, ending before the first stop id.
+        ``sampling`` has top_p, top_k, win_size, tau_r, strict_min_len and a NumPy
+        PCG64 Generator ``rng``, whose state the device advances exactly as the
+        reference's draws would and hands back.  The host looks for a stop every
+        ``check_every`` tokens; steps after a stop change nothing."""
+        bg = sampling.rng.bit_generator
+        st = bg.state
+        if st.get("bit_generator") != "PCG64":
+            raise ValueError("the device sampler draws from NumPy's PCG64 stream (np.random.default_rng)")
+        if pos + max_len + 1 >= self.cap:
+            raise ValueError("the generation does not fit the KV cache")
+        if not sampling.top_p > 0 or int(sampling.top_k) < 1:
+            raise ValueError("a draw needs top_p > 0 and top_k >= 1 (the nucleus would be empty)")
+        s, inc = int(st["state"]["state"]), int(st["state"]["inc"])
+        ctl = np.array([pos, 0, s >> 64, s & _M64, inc >> 64, inc & _M64], dtype=np.uint64).view(np.int64)
+        self.ctl.copy_from(ctl)
+        smp = Sampler(float(sampling.top_p), float(sampling.win_size * sampling.tau_r), int(sampling.top_k),
+                      int(sampling.win_size), int(speech_token_size), int(min_len),
+                      int(bool(getattr(sampling, "strict_min_len", False))), self.ctl.ptr)
+        self.begin(first_token, pos)
+        done = 0
+        while done < max_len:
+            n = min(check_every, max_len - done)
+            for _ in range(n):
+                self.step_sampled(smp, graph)
+            done += n
+            if int(self.ctl.numpy()[1]) != 0:
+                break
+        c = self.ctl.numpy().view(np.uint64)
+        stop = int(c[1])
+        count = stop - 1 if stop else max_len
+        new = dict(st)
+        new["state"] = {"state": (int(c[2]) << 64) | int(c[3]), "inc": (int(c[4]) << 64) | int(c[5])}
+        bg.state = new
+        ints = self.ints.numpy()
+        self._pos_host = int(ints[0])
+        return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + count]]
 
     def generate(self, first_token: int, pos: int, steps: int, graph: bool = True) -> List[int]:
         self.begin(first_token, pos)

@@ -301,6 +301,29 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
  * y = silu(gate . v) * (up . v) (qwen2.py:175-177).  K <= 16384 (mode 2: K <= 5120). */
 int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
                 float* y, int mode, cv3_stream_t stream);
+/* The sampler of CosyVoice3LM (llm.py:37-49 nucleus_sampling, llm.py:125-149 _sample) for a decode step.
+ * ctl is 6 int64 of device memory: [0] the position of the generation's first input, [1] 0 while running, set to
+ * (step + 1) when a stop id (speech_token_size .. +199) is drawn, after which steps leave the state untouched;
+ * [2..5] NumPy's PCG64 state (state high, low, increment high, low 64 bits), advanced by the draws the reference
+ * takes (one per token, two when the repetition test resamples).  rep_threshold = win_size * tau_r, formed in
+ * double as the reference compares it; steps below min_len mask the eos id (every stop id with strict_min_len).
+ * top_k 1..64, vocabulary <= 8192. */
+typedef struct {
+  double top_p;
+  double rep_threshold;
+  int64_t top_k;
+  int64_t win_size;
+  int64_t speech_token_size;
+  int64_t min_len;
+  int strict_min_len;
+  int64_t* ctl;
+} cv3_sampler;
+/* cv3_qwen2_decode_step with the token drawn by the sampler instead of the argmax (llm.py:112-123). */
+int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
+                                  cv3_stream_t stream);
+/* n doubles of Generator.random() from the PCG64 state pcg[0..3] (device, layout as in cv3_sampler.ctl[2..5]),
+ * which is advanced: the draw primitive of the sampler, exposed so its stream can be checked against NumPy. */
+int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream);
 /* x = speech_embedding[*token] (ops.py:126-144): the first input of a decode. */
 int cv3_qwen2_embed_token(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
 

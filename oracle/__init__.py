@@ -18,7 +18,8 @@ Modules
 ``dit``        DiT estimator call sequence (cv3cpu/models/dit.py)
 ``flow``       Euler CFM solver + token front (cv3cpu/models/flow.py)
 ``qwen2``      Qwen2 body with KV cache (cv3cpu/models/qwen2.py)
-``llm``        LM head, speech embedding, greedy decode (cv3cpu/models/llm.py)
+``llm``        LM head, speech embedding, sampler, greedy / sampled decode
+               (cv3cpu/models/llm.py)
 ``hift``       HiFTNet vocoder (cv3cpu/models/hift.py)
 
 How each function is pinned (golden vector, closed form, invariant or brute
@@ -43,4 +44,8 @@ PINNING = {
     "dit+flow": "frozen upstream flow_mel at toy geometry, <5e-4 (test_oracle_models)",
     "hift": "frozen upstream hift_wav at toy geometry, <2e-3; chunked==full (test_oracle_models)",
     "qwen2+llm": "frozen upstream per-step logits, <1e-3; incremental==full (test_oracle_models)",
+    "llm.sample/nucleus_sampling": "top_k=1 is the stable argmax; the nucleus cut by hand on a fixed "
+                                   "distribution; draws against numpy's own Generator.choice on the same "
+                                   "PCG64 stream; the resample never returns the masked pick; eos masks "
+                                   "(test_oracle_models)",
 }

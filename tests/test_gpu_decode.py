@@ -92,3 +92,88 @@ def test_decode_full_depth_graph_replay(gpu, profile):
     # a second run from the same state replays the same graph and the same tokens
     d.fill_cache(k, v)
     assert d.generate(lm.sos, PREFILL, steps, graph=True) == want
+
+
+def test_pcg64_stream_matches_numpy(gpu):
+    """cv3_pcg64_random against Generator.random() from the same PCG64 state, and the
+    state it leaves behind."""
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray
+    g = np.random.default_rng(20241201)
+    st = g.bit_generator.state["state"]
+    m = (1 << 64) - 1
+    pcg = DeviceArray((4,), np.int64)
+    pcg.copy_from(np.array([st["state"] >> 64, st["state"] & m, st["inc"] >> 64, st["inc"] & m],
+                           np.uint64).view(np.int64))
+    out = DeviceArray((1000,), np.float64)
+    _lib.call("pcg64_random", pcg.ptr, 1000, out.ptr, None)
+    assert np.array_equal(out.numpy(), g.random(1000))
+    c = pcg.numpy().view(np.uint64)
+    assert (int(c[0]) << 64 | int(c[1])) == g.bit_generator.state["state"]["state"]
+
+
+SAMPLING = {
+    "default": dict(top_p=0.8, top_k=25, win_size=10, tau_r=0.1),   # SamplingConfig's defaults
+    "always_resample": dict(top_p=0.8, top_k=25, win_size=10, tau_r=0.0),
+    "top1": dict(top_p=0.8, top_k=1, win_size=10, tau_r=0.1),
+    "wide": dict(top_p=0.95, top_k=64, win_size=3, tau_r=0.5),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SAMPLING))
+def test_decode_sampled_tokens_and_generator_state(gpu, name):
+    """The reference's sampler (llm.py:37-49,125-149) on the device: the same tokens as
+    the oracle's loop on the same seeded Generator, which ends in the same state."""
+    from cv3amd.qwen2 import DeviceQwen2
+    from oracle.llm import Sampling
+    max_len, min_len = 40, 4
+    cpu, dev, k, v = _setup(2, "per_channel")
+    print(f"[decode] sampled, 2 layers, {name}, {max_len} tokens", flush=True)
+    lm, cache = _oracle_lm(cpu, k, v, max_len)
+    ref = Sampling(seed=1234, **SAMPLING[name])
+    want = lm.sampled(lm.speech_emb([lm.sos]), cache, max_len, min_len, ref)
+    d = DeviceQwen2(dev, cap=1024)
+    d.fill_cache(k, v)
+    got_cfg = Sampling(seed=1234, **SAMPLING[name])
+    got = d.generate_sampled(lm.sos, PREFILL, max_len, min_len, got_cfg, lm.speech_token_size, graph=True)
+    print(f"[decode] oracle {want[:12]}...\n[decode] device {got[:12]}...", flush=True)
+    assert got == want
+    assert got_cfg.rng.bit_generator.state == ref.rng.bit_generator.state
+
+
+@pytest.mark.parametrize("strict", [False, True])
+def test_decode_sampled_stops_on_a_control_id(gpu, strict):
+    """A head bias that makes two stop ids likely: masked below min_len (only the eos id,
+    or every stop id with strict_min_len), then the generation ends on the step the
+    oracle's does, direct launches and graph replay alike."""
+    import oracle.quant
+    import cv3amd.quant
+    from cv3amd import synth
+    from cv3amd.qwen2 import DeviceQwen2
+    from cv3amd.weights import WeightStore
+    from oracle.llm import Sampling
+    t = synth.quantize_store(synth.qwen2_tensors(layers=2), "per_channel", oracle.quant.quantize_q8)
+    sts = synth.SPEECH_TOKEN_SIZE
+    bias = np.array(t["llm.llm_decoder.bias"], np.float32)
+    bias[sts] += 9.0        # eos, the id the reference masks below min_len
+    bias[sts + 5] += 4.0    # another control id: masked only with strict_min_len
+    t["llm.llm_decoder.bias"] = bias
+    meta = synth.qwen2_meta(layers=2)
+    cpu, dev = WeightStore(t, meta, oracle.quant.QTensor), WeightStore(t, meta, cv3amd.quant.QTensor)
+    rng = np.random.default_rng(100)
+    k = rng.standard_normal((2, 2, PREFILL, 64), dtype=np.float32)
+    v = rng.standard_normal((2, 2, PREFILL, 64), dtype=np.float32)
+    max_len, min_len = 48, 6
+    lm, cache = _oracle_lm(cpu, k, v, max_len)
+    ref = Sampling(seed=77, strict_min_len=strict)
+    want = lm.sampled(lm.speech_emb([lm.sos]), cache, max_len, min_len, ref)
+    print(f"[decode] stop test strict={strict}: oracle stops after {len(want)} tokens", flush=True)
+    # below min_len only strict_min_len holds the second control id back
+    assert (min_len <= len(want) < max_len) if strict else (0 < len(want) < min_len)
+    for graph in (False, True):
+        d = DeviceQwen2(dev, cap=1024)
+        d.fill_cache(k, v)
+        cfg = Sampling(seed=77, strict_min_len=strict)
+        got = d.generate_sampled(lm.sos, PREFILL, max_len, min_len, cfg, sts, graph=graph, check_every=5)
+        assert got == want
+        assert cfg.rng.bit_generator.state == ref.rng.bit_generator.state
