@@ -189,7 +189,7 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
         "sampled_tok_s": sampled_tok_s,
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
         "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
-                   else "k_dec_gemv<8,8,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
+                   else "k_dec_gemv<16,4,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
                    "bytes_per_launch": gu_bytes, "us_per_launch": kms * 1e3, "achieved_Bps": achieved},
     }
 
@@ -475,7 +475,7 @@ def main():
             cpu_flow_s = cpu_flow(dit_t, dit_meta)
             log(f"cpu baseline: {cpu_flow_s:.2f} s per evaluation")
         if voc is not None:
-            log("cpu baseline: one whole-utterance vocoder decode of the oracle")
+            log("cpu baseline: one whole-utterance vocoder inference (F0 net, excitation, decode) of the oracle")
             cpu_hift_s = cpu_hift(hift_t, hift_meta)
             log(f"cpu baseline: {cpu_hift_s:.2f} s per 10 s of audio")
 
