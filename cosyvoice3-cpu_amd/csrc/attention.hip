@@ -56,18 +56,21 @@ constexpr int KS = 68;        // LDS row stride (floats) for K and V tiles
 constexpr int QW = 16;        // queries per wave
 constexpr int QT = 64;        // queries per workgroup
 
-// 8 waves: wave w takes queries (w % 4) * 16 .. +15 of the workgroup's 64 and key
-// group kg = w / 4.  Each stage stages 2 tiles of 64 keys; key group kg works on
-// tile 2 * stage + kg, so every SIMD runs two waves (one per key group) and the
+// 4 * NKG waves: wave w takes queries (w % 4) * 16 .. +15 of the workgroup's 64 and
+// key group kg = w / 4.  Each stage stages NKG tiles of 64 keys; key group kg works
+// on tile NKG * stage + kg, so every SIMD runs NKG waves (one per key group) and the
 // key range is split between them.  Each wave keeps its own online softmax
-// (max, sum, output) and the two groups merge in LDS at the end:
-//   M = max(m0, m1), l = l0 e^{m0-M} + l1 e^{m1-M}, o = o0 e^{m0-M} + o1 e^{m1-M}.
+// (max, sum, output) and the groups merge in LDS at the end:
+//   M = max_g m_g, l = sum_g l_g e^{m_g-M}, o = sum_g o_g e^{m_g-M}.
+// NKG = 4 (1024 threads, 139 KB of LDS) hides the per-tile latency chain better on
+// long key ranges (1024 keys and up); shorter ones keep NKG = 2.
 // Per tile a wave scores all 64 keys (64 MFMAs), rescales its running state once,
 // then accumulates P V (64 MFMAs).  V is staged transposed ([dim][key]) so the
 // P V operands of four consecutive keys are one 16-byte LDS read.
-__global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
-  __shared__ float Ks[2][KT * KS];
-  __shared__ float Vs[2][KT * KS];
+template <int NKG>
+__global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
+  __shared__ float Ks[NKG][KT * KS];
+  __shared__ float Vs[NKG][KT * KS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qw = wave & 3, kg = wave >> 2;
   const int b = blockIdx.z, hq = blockIdx.y;
@@ -95,8 +98,8 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
 
   const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  const int64_t nstages = ceil_div(p.m, 2 * KT);
-  // The next stage's 128 K/V rows are loaded into registers while the current stage
+  const int64_t nstages = ceil_div(p.m, NKG * KT);
+  // The next stage's NKG * 64 K/V rows are loaded into registers while the current stage
   // is computed.  Rows past m are clamped to m - 1 (always in bounds); their scores
   // are masked to -inf below, so the loads carry no predicates.
   // K: thread -> tile tid/256, keys (tid%256)/16 + 16r (r < 4), dims (tid%16)*4 .. +3.
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
   }
   CV3_KV_LOAD((int64_t)0)
   for (int64_t st = 0; st < nstages; ++st) {
-    const int64_t k0 = st * 2 * KT + kg * KT;  // first key of this wave's tile
+    const int64_t k0 = st * NKG * KT + kg * KT;  // first key of this wave's tile
     __syncthreads();
     float* kt_ = Ks[ltile];
     float* vt_ = Vs[ltile];
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
       for (int e = 0; e < 16; ++e) vt_[(vd + e) * KS + vkey] = vv[e];
     }
     __syncthreads();
-    if (st + 1 < nstages) CV3_KV_LOAD((st + 1) * 2 * KT)
+    if (st + 1 < nstages) CV3_KV_LOAD((st + 1) * NKG * KT)
     __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this stage's math
     const float* Kt = Ks[kg];
     const float* Vt = Vs[kg];
@@ -202,11 +205,12 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
       }
   }
 #undef CV3_KV_LOAD
-  // merge the two key groups through LDS (each lane's state is per query column)
+  // merge the key groups through LDS (each lane's state is per query column)
   __syncthreads();
-  float* mb = &Ks[0][0];  // 4 waves x 64 lanes x 18 floats = 4608 <= 2 * 64 * 68
-  float* slot = mb + (qw * 64 + lane) * 18;
-  if (kg == 1) {
+  float* mb = &Ks[0][0];  // (NKG - 1) x 4 waves x 64 lanes x 18 floats <= NKG * 64 * 68
+  static_assert((NKG - 1) * 4 * 64 * 18 <= NKG * KT * KS, "merge slots fit the K tiles");
+  if (kg > 0) {
+    float* slot = mb + (((kg - 1) * 4 + qw) * 64 + lane) * 18;
     slot[0] = m_run;
     slot[1] = l_run;
 #pragma unroll
@@ -215,16 +219,24 @@ __global__ __launch_bounds__(512) void k_flash64(AttnParams p) {
       for (int i = 0; i < 4; ++i) slot[2 + db * 4 + i] = oacc[db][i];
   }
   __syncthreads();
-  if (kg == 1) return;
-  const float m1 = slot[0], l1 = slot[1];
-  const float M = fmaxf(m_run, m1);
+  if (kg > 0) return;
+  float M = m_run;
+#pragma unroll
+  for (int g2 = 1; g2 < NKG; ++g2) M = fmaxf(M, mb[(((g2 - 1) * 4 + qw) * 64 + lane) * 18]);
   const float a0 = M == -INFINITY ? 1.f : expf(m_run - M);
-  const float a1 = M == -INFINITY ? 0.f : expf(m1 - M);
-  l_run = l_run * a0 + l1 * a1;
+  l_run = l_run * a0;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < 4; ++db) oacc[db] *= a0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) oacc[db][i] = oacc[db][i] * a0 + slot[2 + db * 4 + i] * a1;
+  for (int g2 = 1; g2 < NKG; ++g2) {
+    const float* slot = mb + (((g2 - 1) * 4 + qw) * 64 + lane) * 18;
+    const float ag = M == -INFINITY ? 0.f : expf(slot[0] - M);
+    l_run += slot[1] * ag;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[db][i] += slot[2 + db * 4 + i] * ag;
+  }
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (!qvalid) return;
@@ -329,7 +341,10 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
                          (p.v_sm % 4 == 0);
   if (d == 64 && aligned16) {
     const dim3 grid((unsigned)ceil_div(n, QT), (unsigned)h, (unsigned)batch);
-    hipLaunchKernelGGL(k_flash64, grid, dim3(512), 0, st, p);
+    if (m >= 16 * KT)  // 1024 keys and up: 8 % faster at 1500 keys, no gain at 500
+      hipLaunchKernelGGL(k_flash64<4>, grid, dim3(1024), 0, st, p);
+    else
+      hipLaunchKernelGGL(k_flash64<2>, grid, dim3(512), 0, st, p);
   } else {
     const dim3 grid((unsigned)ceil_div(n, 4), (unsigned)h, (unsigned)batch);
     hipLaunchKernelGGL(k_attn_generic, grid, dim3(256), 4 * d * sizeof(float), st, p);

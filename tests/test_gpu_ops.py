@@ -230,7 +230,8 @@ def test_depthwise(dev, rng):
 
 
 @pytest.mark.parametrize("h,hk,n,m,d", [(4, 4, 23, 23, 16), (4, 2, 19, 19, 16), (16, 16, 500, 500, 64),
-                                        (14, 2, 1, 513, 64), (2, 1, 37, 37, 64), (3, 3, 70, 130, 32)])
+                                        (14, 2, 1, 513, 64), (2, 1, 37, 37, 64), (3, 3, 70, 130, 32),
+                                        (4, 2, 65, 1100, 64)])
 @pytest.mark.parametrize("mask", [None, ("causal",), ("chunk", 8, 1), ("chunk", 50, -1), ("chunk", 5, 0)])
 def test_sdpa(dev, rng, h, hk, n, m, d, mask):
     ops, _ = dev
