@@ -19,7 +19,11 @@
 // Workgroup -> tile mapping is XCD-aware: workgroups are dispatched round-robin
 // over the 8 XCDs, so linear id L runs on XCD L % 8; tile t = (L % 8) * (T / 8) +
 // L / 8 with M-tiles fastest gives each XCD whole columns of N-tiles, and each
-// weight tile is fetched into one XCD's L2 only.
+// weight tile is fetched into one XCD's L2 only.  When the activation A is larger
+// than an XCD's 4 MB L2 (the 30 s utterance: 3000 x 1024 floats), walking a column
+// would stream all of A again for every column; the register-staged kernel then
+// walks groups of 8 M-tiles across all N-tiles instead (group_m = 8), so the tiles
+// in flight share A rows and W columns (5-6 % on those GEMMs).
 #include "common.hpp"
 #include "epilogue.hpp"
 
@@ -252,14 +256,24 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16& ac
 // The GEMM kernel: 4 waves, 64 x 64 tile.  FAST (K % 64 == 0, aligned rows):
 // branch-free loads two stages ahead; otherwise one stage of guarded prefetch.
 template <int BK_KIND, bool FAST, int AMODE = A_ROWS>
-__global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast_b, int tiles_m) {
+__global__ __launch_bounds__(256) void k_gemm(GemmParams p, int fast_a, int fast_b, int tiles_m, int group_m) {
   __shared__ float As[2][BM * LDS_STRIDE];
   __shared__ float Bs[2][BN * LDS_STRIDE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = gridDim.x, L = blockIdx.x;
   const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
-  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  int tm, tn;
+  if (group_m > 0) {  // groups of group_m M-tiles, M fastest within a group, across all N-tiles
+    const int tiles_n = T / tiles_m, per_group = group_m * tiles_n, first = (t / per_group) * group_m;
+    const int rows = min(tiles_m - first, group_m), r = t % per_group;
+    tm = first + r % rows;
+    tn = r / rows;
+  } else {
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+  }
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int lrow = tid >> 3, lk = (tid & 7) * 4;
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const int r32 = lane & 31, h = lane >> 5;
@@ -563,20 +577,22 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   CV3_REQUIRE(fast || !p.epi.rope_cos, CV3_EUNSUPPORTED, "rotary epilogue needs aligned rows and K %% 64 == 0");
   // at most one 64 x 64 tile per CU: the 8-wave kernel keeps two waves per SIMD
   const bool small = tiles_m * tiles_n <= 256;
+  // A beyond one XCD's L2: walk groups of 8 M-tiles (the tile order note at the top)
+  const int group_m = m * k * (int64_t)sizeof(float) > (4ll << 20) ? 8 : 0;
   if (q8) {
     if (fast && small)
       hipLaunchKernelGGL((k_gemm8<B_Q8, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
     else if (fast)
-      hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+      hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
     else
-      hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+      hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
   } else {
     if (fast && tiles_m * tiles_n <= 512)
       hipLaunchKernelGGL(k_gemm_dma, grid, dim3(256), 0, st, p, (int)tiles_m);
     else if (fast)
-      hipLaunchKernelGGL((k_gemm<B_F32, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+      hipLaunchKernelGGL((k_gemm<B_F32, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
     else
-      hipLaunchKernelGGL((k_gemm<B_F32, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m);
+      hipLaunchKernelGGL((k_gemm<B_F32, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
   }
   CV3_LAUNCHED();
   return CV3_OK;
@@ -615,7 +631,7 @@ int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* 
                        (int)tiles_m);
   else
     hipLaunchKernelGGL((k_gemm<B_F32, true, A_CONV>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, 1,
-                       1, (int)tiles_m);
+                       1, (int)tiles_m, 0);
   CV3_LAUNCHED();
   return CV3_OK;
 }

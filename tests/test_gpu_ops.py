@@ -161,6 +161,24 @@ def test_linear_q8(dev, rng, m, k, n, block, sdt):
     assert rel_err(ops.linear(x, mine, b), ref.linear(x, theirs, b)) < TOL
 
 
+@pytest.mark.parametrize("kind,m,k,n", [("f32", 1100, 1024, 2000), ("f32", 1100, 1030, 2000),
+                                        ("q8", 1100, 1024, 1000), ("q8", 3000, 1024, 520)])
+def test_linear_large_activation(dev, rng, kind, m, k, n):
+    """Activations beyond one XCD's L2 (over 4 MB) take the grouped tile order, whose
+    last group is ragged here (18 or 47 M-tiles in groups of 8)."""
+    ops, quant = dev
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    if kind == "f32":
+        assert rel_err(ops.linear(x, w, b), ref.linear(x, w, b)) < TOL
+    else:
+        q, s, _ = refq.quantize_q8(w, 64, np.float16)
+        mine = quant.QTensor("q8", q, s, (n, k), 64)
+        theirs = refq.QTensor("q8", q, s, (n, k), 64)
+        assert rel_err(ops.linear(x, mine, b), ref.linear(x, theirs, b)) < TOL
+
+
 @pytest.mark.parametrize("m", [1, 4, 9])
 def test_linear_q4(dev, rng, m):
     ops, quant = dev
