@@ -1262,6 +1262,33 @@ int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_stat
   return decode_step(m, s, smp, stream);
 }
 
+int cv3_qwen2_select(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
+                     cv3_stream_t stream) {
+  CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
+  int rc;
+  if ((rc = check_qw(m->head, "llm_decoder", m->hidden))) return rc;
+  if ((rc = check_qw(m->embedding, "speech_embedding", m->hidden))) return rc;
+  CV3_REQUIRE(m->embedding.kind == CV3_KIND_Q8, CV3_EUNSUPPORTED, "speech_embedding must be q8");
+  const QW head = make_qw(m->head), emb = make_qw(m->embedding);
+  NextArgs na{s->logits, head.rows, emb, s->x, s->pos, s->history, s->token};
+  hipStream_t st = stream_of(stream);
+  if (smp) {
+    CV3_REQUIRE(smp->ctl, CV3_EINVAL, "sampler: null control block");
+    CV3_REQUIRE(smp->top_k >= 1 && smp->top_k <= kTopKMax, CV3_EUNSUPPORTED, "sampler: top_k %lld (1..%d)",
+                (long long)smp->top_k, kTopKMax);
+    CV3_REQUIRE(head.rows <= (int64_t)kSampleThreads * kSamplePerThread, CV3_EUNSUPPORTED,
+                "sampler: vocabulary %lld above %d", (long long)head.rows, kSampleThreads * kSamplePerThread);
+    CV3_REQUIRE(smp->win_size >= 0 && smp->speech_token_size >= 0, CV3_EINVAL, "sampler: window / stop ids");
+    SampleArgs sa{na, smp->top_p, smp->rep_threshold, smp->top_k, smp->win_size, smp->speech_token_size,
+                  smp->min_len, smp->strict_min_len, reinterpret_cast<int64_t*>(smp->ctl)};
+    hipLaunchKernelGGL(k_dec_sample, dim3(1), dim3(kSampleThreads), 0, st, sa);
+  } else {
+    hipLaunchKernelGGL(k_dec_next, dim3(1), dim3(1024), 0, st, na);
+  }
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
 int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream) {
   CV3_REQUIRE(pcg && n >= 0 && (n == 0 || out), CV3_EINVAL, "pcg64: null state or output");
   if (n == 0) return CV3_OK;

@@ -105,6 +105,17 @@ class _Stacked:
         self.q = to_device(np.ascontiguousarray(q))
         self.scales = to_device(np.ascontiguousarray(s))
 
+    def layer(self, layer: int, row0: int = 0, rows: Optional[int] = None):
+        """linear_q arguments (kind, codes, scales, scale dtype, kp, block, n) of rows
+        [row0, row0 + rows) of one layer."""
+        rows = self.rows - row0 if rows is None else rows
+        row_bytes = self.kp // 2 if self.kind == "q4" else self.kp
+        nb = self.kp // self.block
+        r = layer * self.rows + row0
+        return (_lib.KIND_Q4 if self.kind == "q4" else _lib.KIND_Q8, self.q.ptr + r * row_bytes,
+                self.scales.ptr + r * nb * (2 if self.sf16 else 4), _lib.F16 if self.sf16 else _lib.F32,
+                self.kp, self.block, rows)
+
     def struct(self) -> QWeight:
         return QWeight(self.q.ptr, self.scales.ptr, self.rows, self.k, self.kp, self.block,
                        _lib.F16 if self.sf16 else _lib.F32, _lib.KIND_Q4 if self.kind == "q4" else _lib.KIND_Q8)
@@ -220,6 +231,71 @@ class DeviceQwen2:
             _lib.call("qwen2_decode_step", ctypes.byref(self.model), ctypes.byref(self.state), None)
         self._pos_host += 1
 
+    # -- prompt prefill (the body's multi-token forward) -----------------------
+    def _linear(self, x: int, m: int, w: "_Stacked", layer: int, y: int, ldy: int, bias=None, row0: int = 0,
+                rows: Optional[int] = None, epi=None):
+        kind, q, sc, sdt, kp, block, n = w.layer(layer, row0, rows)
+        _lib.call("linear_q", kind, x, m, w.k, w.k, q, sc, sdt, kp, block, n, bias, y, ldy,
+                  ctypes.byref(epi) if epi is not None else None, None)
+
+    def prefill(self, x, pos0: int = 0):
+        """Qwen2Model.forward over T input embeddings at positions pos0 .. pos0 + T - 1
+        (qwen2.py:139-179) on the device: RMSNorm, [q; k; v] projection with bias, half-split
+        rotary, k and v appended to the cache, causal attention over the cache (mask
+        ("causal", pos0) when T > 1), o_proj + residual, RMSNorm, SwiGLU, down + residual.
+        Leaves the head logits of the last position in ``logits`` and ``pos`` at that
+        position, so ``select`` / ``generate_*_after_prefill`` draw the next token."""
+        xd = x if isinstance(x, DeviceArray) else to_device(np.ascontiguousarray(x, np.float32))
+        if xd.ndim != 2 or xd.shape[1] != self.hidden or xd.shape[0] < 1:
+            raise ValueError(f"prefill takes (T, {self.hidden}) embeddings, got {xd.shape}")
+        t = xd.shape[0]
+        if pos0 < 0 or pos0 + t >= self.cap:
+            raise ValueError("the prompt does not fit the KV cache")
+        D, H, Hk, dh, I, cap = self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter, self.cap
+        R = self.qkv.rows
+        h = DeviceArray((t, D))
+        _lib.call("copy_d2d", h.ptr, xd.ptr, t * D * 4, None)
+        n = DeviceArray((t, D))
+        qkv = DeviceArray((t, R))
+        att = DeviceArray((t, D))
+        u = DeviceArray((t, I))
+        a = DeviceArray((t, I))
+        res = _lib.epilogue(residual=h.ptr, ld_res=D)
+        swiglu = _lib.epilogue(act="silu", gate=u.ptr, gate_stride=I, rows_per_gate=1)
+        c64 = ctypes.c_int64 * 3
+        for l in range(self.layers):
+            _lib.call("rms_norm", h.ptr, self.ln1.ptr + l * D * 4, n.ptr, t, D, self.eps, None)
+            self._linear(n.ptr, t, self.qkv, l, qkv.ptr, R, bias=self.qkv_bias.ptr + l * R * 4)
+            _lib.call("rope_half", qkv.ptr, t * H, H, R, dh, self.rope_cos.ptr, self.rope_sin.ptr, pos0, None)
+            _lib.call("rope_half", qkv.ptr + H * dh * 4, t * Hk, Hk, R, dh, self.rope_cos.ptr, self.rope_sin.ptr,
+                      pos0, None)
+            for j, cache in enumerate((self.k_cache, self.v_cache)):   # rows pos0 .. of layer l
+                _lib.call("copy_strided", qkv.ptr + (H + j * Hk) * dh * 4,
+                          cache.ptr + ((l * Hk) * cap + pos0) * dh * 4, Hk, t, dh, c64(dh, R, 1),
+                          c64(cap * dh, dh, 1), None)
+            kv = l * Hk * cap * dh * 4
+            _lib.call("attention", qkv.ptr, self.k_cache.ptr + kv, self.v_cache.ptr + kv, att.ptr, 1, H, Hk, t,
+                      pos0 + t, dh, c64(0, dh, R), c64(0, cap * dh, dh), c64(0, cap * dh, dh), c64(0, dh, D),
+                      1.0 / np.sqrt(dh), 1 if t > 1 else 0, pos0, 0, None)
+            self._linear(att.ptr, t, self.o, l, h.ptr, D, epi=res)
+            _lib.call("rms_norm", h.ptr, self.ln2.ptr + l * D * 4, n.ptr, t, D, self.eps, None)
+            self._linear(n.ptr, t, self.gate_up, l, u.ptr, I, row0=I, rows=I)        # up
+            self._linear(n.ptr, t, self.gate_up, l, a.ptr, I, row0=0, rows=I, epi=swiglu)  # u * silu(gate)
+            self._linear(a.ptr, t, self.down, l, h.ptr, D, epi=res)
+        _lib.call("rms_norm", h.ptr + (t - 1) * D * 4, self.norm.ptr, n.ptr, 1, D, self.eps, None)
+        self._linear(n.ptr, 1, self.head, 0, self.logits.ptr, self.vocab,
+                     bias=self.head_bias.ptr if self.head_bias is not None else None)
+        p = np.array([pos0 + t - 1], np.int64)
+        _lib.call("copy_h2d", self.ints.ptr, p.ctypes.data, 8, None)
+        self._pos_host = pos0 + t - 1
+
+    def select(self, smp: Optional["Sampler"] = None):
+        """Draw the next token from the logits already in ``logits`` (greedy without a
+        sampler), as a decode step's last kernel does."""
+        _lib.call("qwen2_select", ctypes.byref(self.model), ctypes.byref(self.state),
+                  ctypes.byref(smp) if smp is not None else None, None)
+        self._pos_host += 1
+
     def step_sampled(self, smp: "Sampler", graph: bool = False):
         """Enqueue one sampled token (no host synchronisation)."""
         if self._pos_host + 1 >= self.cap:
@@ -239,7 +315,14 @@ class DeviceQwen2:
                       ctypes.byref(smp), None)
         self._pos_host += 1
 
-    def generate_sampled(self, first_token: int, pos: int, max_len: int, min_len: int, sampling,
+    def generate_sampled_after_prefill(self, max_len: int, min_len: int, sampling, speech_token_size: int,
+                                       graph: bool = True, check_every: int = 16) -> List[int]:
+        """generate()'s loop after ``prefill``: the first token is drawn from the prompt's
+        logits (llm.py:112-121 at i = 0), the rest by decode steps."""
+        return self.generate_sampled(None, self._pos_host, max_len, min_len, sampling, speech_token_size, graph,
+                                     check_every)
+
+    def generate_sampled(self, first_token: Optional[int], pos: int, max_len: int, min_len: int, sampling,
                          speech_token_size: int, graph: bool = True, check_every: int = 16) -> List[int]:
         """The token loop of CosyVoice3LM.generate (llm.py:104-123) with its sampler
         (llm.py:125-149) on the device: up to max_len tokens from input
@@ -247,7 +330,9 @@ class DeviceQwen2:
         ``sampling`` has top_p, top_k, win_size, tau_r, strict_min_len and a NumPy
         PCG64 Generator ``rng``, whose state the device advances exactly as the
         reference's draws would and hands back.  The host looks for a stop every
-        ``check_every`` tokens; steps after a stop change nothing."""
+        ``check_every`` tokens; steps after a stop change nothing.  ``first_token``
+        None draws the first token from the logits already present (after ``prefill``,
+        whose last position is ``pos``)."""
         bg = sampling.rng.bit_generator
         st = bg.state
         if st.get("bit_generator") != "PCG64":
@@ -262,8 +347,12 @@ class DeviceQwen2:
         smp = Sampler(float(sampling.top_p), float(sampling.win_size * sampling.tau_r), int(sampling.top_k),
                       int(sampling.win_size), int(speech_token_size), int(min_len),
                       int(bool(getattr(sampling, "strict_min_len", False))), self.ctl.ptr)
-        self.begin(first_token, pos)
         done = 0
+        if first_token is None:
+            self.select(smp)
+            done = 1
+        else:
+            self.begin(first_token, pos)
         while done < max_len:
             n = min(check_every, max_len - done)
             for _ in range(n):
@@ -280,6 +369,18 @@ class DeviceQwen2:
         ints = self.ints.numpy()
         self._pos_host = int(ints[0])
         return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + count]]
+
+    def generate_after_prefill(self, steps: int, graph: bool = True) -> List[int]:
+        """Greedy tokens after ``prefill``: the argmax of the prompt's logits, then steps - 1
+        decode steps."""
+        pos = self._pos_host
+        if pos + steps >= self.cap:
+            raise ValueError("the generation does not fit the KV cache")
+        self.select(None)
+        for _ in range(steps - 1):
+            self.step(graph)
+        ints = self.ints.numpy()
+        return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + steps]]
 
     def generate(self, first_token: int, pos: int, steps: int, graph: bool = True) -> List[int]:
         self.begin(first_token, pos)

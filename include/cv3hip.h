@@ -321,6 +321,10 @@ typedef struct {
 /* cv3_qwen2_decode_step with the token drawn by the sampler instead of the argmax (llm.py:112-123). */
 int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
                                   cv3_stream_t stream);
+/* The token selection of a decode step alone, on the logits already in s->logits: greedy (smp == NULL) or the
+ * sampler; then x = speech_embedding[id], history[pos + 1] = id, pos += 1.  After a prompt prefill that left the
+ * last position's logits and pos = that position, this draws the first speech token (llm.py:112-121, i = 0). */
+int cv3_qwen2_select(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp, cv3_stream_t stream);
 /* n doubles of Generator.random() from the PCG64 state pcg[0..3] (device, layout as in cv3_sampler.ctl[2..5]),
  * which is advanced: the draw primitive of the sampler, exposed so its stream can be checked against NumPy. */
 int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream);

@@ -177,3 +177,71 @@ def test_decode_sampled_stops_on_a_control_id(gpu, strict):
         got = d.generate_sampled(lm.sos, PREFILL, max_len, min_len, cfg, sts, graph=graph, check_every=5)
         assert got == want
         assert cfg.rng.bit_generator.state == ref.rng.bit_generator.state
+
+
+@pytest.mark.parametrize("profile", ["balanced", "tiny"])
+def test_prompt_prefill_cache_logits_and_greedy_continuation(gpu, profile):
+    """DeviceQwen2.prefill against Qwen2Model.forward over a prompt (qwen2.py:139-179): the
+    cache rows it appends and the last position's logits, for a 37-token prompt and a
+    5-token continuation on top of it (causal mask offset by the cache), then greedy
+    tokens from there."""
+    import oracle.quant
+    import cv3amd.quant
+    from cv3amd import synth
+    from cv3amd.qwen2 import DeviceQwen2
+    from cv3amd.weights import WeightStore
+    from oracle.llm import CosyVoice3LM
+    layers = 2
+    t = synth.quantize_store(synth.qwen2_tensors(layers=layers), profile, oracle.quant.quantize_q8,
+                             oracle.quant.quantize_q4)
+    meta = synth.qwen2_meta(layers=layers)
+    cpu, dev = WeightStore(t, meta, oracle.quant.QTensor), WeightStore(t, meta, cv3amd.quant.QTensor)
+    rng = np.random.default_rng(11)
+    x1 = (rng.standard_normal((37, 896), dtype=np.float32) * 0.02).astype(np.float32)
+    x2 = (rng.standard_normal((5, 896), dtype=np.float32) * 0.02).astype(np.float32)
+    lm = CosyVoice3LM(cpu, "llm.")
+    cache = lm.body.new_cache()
+    d = DeviceQwen2(dev, cap=256)
+    print(f"[decode] prefill {profile}: 37 + 5 prompt positions", flush=True)
+    for x, pos0 in ((x1, 0), (x2, 37)):
+        want = lm.head(lm.body.forward(x, cache)[-1:])[0]
+        d.prefill(x, pos0)
+        e = rel_err(d.logits.numpy(), want)
+        print(f"[decode] prefill at {pos0}: logits rel err {e:.2e}", flush=True)
+        assert e < 1e-5
+    n = len(cache)
+    kc, vc = d.k_cache.numpy(), d.v_cache.numpy()
+    for i in range(layers):
+        assert rel_err(kc[i][:, :n], cache.k[i][:, :n]) < 1e-5
+        assert rel_err(vc[i][:, :n], cache.v[i][:, :n]) < 1e-5
+    # greedy continuation: the argmax of the prompt's logits, then decode steps
+    top = int(np.argmax(want))
+    ref = [top] + lm.greedy(lm.speech_emb([top]), cache, 7)
+    got = d.generate_after_prefill(8, graph=False)
+    print(f"[decode] oracle {ref}\n[decode] device {got}", flush=True)
+    assert got == ref
+
+
+def test_prompt_prefill_then_sampled_generation(gpu):
+    """generate() end to end (llm.py:80-123) from a prompt: the oracle's loop prefills the
+    prompt in its first forward; the device prefills, draws the first token from the
+    prompt's logits and decodes the rest, on the same seeded Generator."""
+    import oracle.quant
+    from cv3amd.qwen2 import DeviceQwen2
+    from oracle.llm import Sampling
+    max_len, min_len = 30, 24   # stop ids held back (strict) for 24 draws, then allowed
+    cpu, dev, _, _ = _setup(2, "balanced")
+    rng = np.random.default_rng(12)
+    prompt = (rng.standard_normal((61, 896), dtype=np.float32) * 0.02).astype(np.float32)
+    from oracle.llm import CosyVoice3LM
+    lm = CosyVoice3LM(cpu, "llm.")
+    ref = Sampling(seed=99, strict_min_len=True)
+    want = lm.sampled(prompt, lm.body.new_cache(), max_len, min_len, ref)
+    assert len(want) >= min_len
+    d = DeviceQwen2(dev, cap=256)
+    d.prefill(prompt, 0)
+    cfg = Sampling(seed=99, strict_min_len=True)
+    got = d.generate_sampled_after_prefill(max_len, min_len, cfg, lm.speech_token_size, graph=True)
+    print(f"[decode] prompt 61: oracle {want[:10]}...\n[decode] device {got[:10]}...", flush=True)
+    assert got == want
+    assert cfg.rng.bit_generator.state == ref.rng.bit_generator.state
