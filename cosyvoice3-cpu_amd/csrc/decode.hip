@@ -1077,6 +1077,394 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// The whole decode step as one cooperative kernel (q8 weights).
+//
+// Every dependent kernel boundary of the step above costs about 4.5 us: the
+// launch, then the first loads of the next kernel.  Here one workgroup per CU runs
+// all 24 layers; the vectors that cross workgroups (x, q/k/v, attention partials,
+// x after o_proj, h) travel as 64-bit words (epoch << 32 | float bits) written and
+// polled at device scope, and each phase streams its weights into registers BEFORE
+// it waits for its input, so the weight latency overlaps the exchange (about
+// 2.2-3 us per exchange on this part).  Per layer:
+//   A  all workgroups: RMSNorm(x) -> [q; k; v] rows + bias + rotary; k, v also to
+//      the cache (read back by later tokens, after the kernel boundary)
+//   B  Hk x 8 workgroups: attention of one kv head's query heads over 128 keys
+//   C  64 workgroups: merge the partials, o_proj rows + residual -> x_mid
+//   D  all workgroups: RMSNorm(x_mid) -> [gate; up] pairs -> h = silu(g) * u
+//   E  128 workgroups: down rows + residual -> x for the next layer
+// then the head rows, and (greedy) the argmax, speech_embedding row and
+// bookkeeping by workgroup 0.  Every buffer is double-buffered by layer parity:
+// it is rewritten two layers later, after phase D, which needs every workgroup,
+// so all of its readers are done.  Epochs are (launch counter * 256 + layer * 8 +
+// phase; the host counts launches), so no word left by another phase, layer or
+// launch can match.  Every
+// wait is bounded: a word that does not arrive sets the error flag and the
+// workgroups leave, each within one wait.
+// ---------------------------------------------------------------------------
+constexpr int kPT = 512;                 // threads per workgroup
+constexpr int kPKeys = 128;              // keys per attention item
+constexpr int kPChunks = 8;              // attention items per kv head: cache <= 1024 positions
+constexpr int kPOproj = 64;              // workgroups of phase C
+constexpr int kPDown = 128;              // workgroups of phase E
+constexpr int kPSpin = 1 << 18;          // polls (each with a short sleep) before a wait gives up
+constexpr int kPPart = 66;               // words per attention partial: m, l, o[64]
+
+struct PersistArgs {
+  QW qkv, o, gu, dn, head, emb;
+  const float *ln1, *ln2, *norm, *qkv_bias, *head_bias, *rope_cos, *rope_sin;
+  int layers, D, H, Hk, dh, I;
+  float eps, scale;
+  float *k_cache, *v_cache;
+  int64_t cap;
+  int64_t *pos, *token, *history;
+  float *x, *logits;
+  uint64_t *xb, *qkvb, *pb, *mb, *hb, *arg;  // exchange words, two sets each
+  int64_t* err;                              // set when a wait gives up
+  uint32_t epoch_base;                       // launch counter * 256, from the host
+  int select;                                // 1: greedy argmax + next input here
+};
+
+__device__ __forceinline__ void ll_put(uint64_t* p, float v, uint32_t e) {
+  __hip_atomic_store(p, ((uint64_t)e << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The workgroup reads words [0, n) carrying epoch e into dst (LDS), eight per
+// thread per batch.  False for every thread (and the error flag set) if a word
+// never arrives.  A wait also ends early once another workgroup has set the
+// flag, so one missing word ends the launch within about one wait.
+__device__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err) {
+  bool ok = true;
+  for (int b0 = 0; b0 < n && ok; b0 += kPT * 8) {
+    uint64_t w[8];
+    bool got = false;
+    for (int spins = 0; spins < kPSpin; ++spins) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = b0 + (int)threadIdx.x + kPT * j;
+        w[j] = idx < n ? __hip_atomic_load(src + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : ((uint64_t)e << 32);
+      }
+      got = true;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) got = got && (uint32_t)(w[j] >> 32) == e;
+      if (got) break;
+      if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int idx = b0 + (int)threadIdx.x + kPT * j;
+      if (idx < n) dst[idx] = __uint_as_float((uint32_t)w[j]);
+    }
+    ok = !__syncthreads_or(!got);
+  }
+  if (!ok && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(err), 1ull);
+  return ok;
+}
+
+template <bool SF16>
+__global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
+  __shared__ __align__(16) float xin[1024];   // a phase's input vector, raw
+  __shared__ __align__(16) float xmid[1024];  // x after o_proj (phase D keeps it for E)
+  __shared__ __align__(16) float xs[5120];    // staged (normed, zero-padded) vector of the dot products
+  __shared__ __align__(16) float big[18432];  // phase B: K^T, V, q, p; phase C: partials
+  __shared__ float red[16];
+  __shared__ float hb_val[8], hb_w[8];
+  __shared__ int hb_i[8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps per-wave indices scalar
+  const int G = gridDim.x, w = blockIdx.x;
+  const int D = a.D, H = a.H, Hk = a.Hk, dh = a.dh, I = a.I;
+  const int R = (H + 2 * Hk) * dh;  // [q; k; v] rows per layer
+  const int GQ = H / Hk;            // query heads per kv head
+  const uint32_t base = a.epoch_base;
+  const int64_t pos = *a.pos;
+  const int nact = (int)((pos + kPKeys) / kPKeys);  // attention items per kv head in use
+  const int half = dh / 2;
+  // zero the staging tails once: the dot products read xs up to 64 chunks per row
+  for (int i = tid; i < 5120; i += kPT) xs[i] = 0.f;
+  __syncthreads();
+
+  for (int l = 0; l < a.layers; ++l) {
+    const int par = l & 1;
+    const uint32_t E = base + (uint32_t)l * 8u;
+    // ---- A: [q; k; v] pairs (rows head*dh + j and + half) ----
+    {
+      const int npairs = R / 2;
+      const int p = w + G * wave;  // one pair per wave
+      const bool live = p < npairs;
+      const int hd = (live ? p : 0) / half, j = (live ? p : 0) % half;
+      const int r0 = hd * dh + j, r1 = r0 + half;
+      RowDot<64, 1, SF16, false> d0, d1;
+      d0.load(a.qkv, (int64_t)l * R + r0, lane, live);
+      d1.load(a.qkv, (int64_t)l * R + r1, lane, live);
+      const float c0 = a.rope_cos[pos * dh + j], s0 = a.rope_sin[pos * dh + j];
+      const float c1 = a.rope_cos[pos * dh + j + half], s1 = a.rope_sin[pos * dh + j + half];
+      const float b0 = a.qkv_bias[(int64_t)l * R + r0], b1 = a.qkv_bias[(int64_t)l * R + r1];
+      if (l == 0) {
+        for (int i = tid; i < D; i += kPT) xin[i] = a.x[i];
+        __syncthreads();
+      } else if (!ll_get(a.xb + (par ^ 1) * D, D, E - 8u + 4u, xin, a.err)) {
+        return;
+      }
+      VecStage<1> vs;
+      vs.load(xin, D, a.ln1 + (int64_t)l * D);
+      const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
+      float v0 = d0.dot(xs, lane) * inv + b0;
+      float v1 = d1.dot(xs, lane) * inv + b1;
+      if (live && lane == 0) {
+        if (hd < H + Hk) {  // rotary on q and k: x cos + rotate_half(x) sin
+          const float o0 = v0 * c0 + (-v1) * s0, o1 = v1 * c1 + v0 * s1;
+          v0 = o0;
+          v1 = o1;
+        }
+        ll_put(a.qkvb + par * R + r0, v0, E);
+        ll_put(a.qkvb + par * R + r1, v1, E);
+        if (hd >= H) {  // k or v head: the cache row at pos
+          const int kvh = hd - H;
+          float* cache = kvh < Hk ? a.k_cache : a.v_cache;
+          const int gh = kvh < Hk ? kvh : kvh - Hk;
+          float* row = cache + (((int64_t)l * Hk + gh) * a.cap + pos) * dh;
+          row[j] = v0;
+          row[j + half] = v1;
+        }
+      }
+      __syncthreads();  // xs is reused below
+    }
+    // ---- B: attention items (kv head g, 128-key chunk c) ----
+    if (w < Hk * kPChunks && (w % kPChunks) < nact) {
+      const int g = w / kPChunks, c = w % kPChunks;
+      const int64_t k0 = (int64_t)c * kPKeys;
+      const int nk = (int)min((int64_t)kPKeys, pos + 1 - k0);  // keys in this chunk (the last may be pos)
+      float* Kt = big;                      // [dh][kPKeys + 1]
+      float* Vs = big + 64 * (kPKeys + 1);  // [kPKeys][dh]
+      float* qs = Vs + kPKeys * 64;         // [GQ][dh]
+      float* ps = qs + 8 * 64;              // [GQ][kPKeys]
+      const float* kb = a.k_cache + ((int64_t)l * Hk + g) * a.cap * dh;
+      const float* vb = a.v_cache + ((int64_t)l * Hk + g) * a.cap * dh;
+      // cache rows before pos (written by earlier launches): 128 keys x 16 float4 = 4 per thread
+      float4 kr[4], vr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = tid + kPT * r, key = idx >> 4, d4 = idx & 15;
+        const int64_t row = min(k0 + key, pos > 0 ? pos - 1 : 0);
+        kr[r] = reinterpret_cast<const float4*>(kb + row * dh)[d4];
+        vr[r] = reinterpret_cast<const float4*>(vb + row * dh)[d4];
+      }
+      // q of the group's heads and the new k, v row
+      float* qkvl = xs;  // scratch: q [GQ*dh], then k [dh], v [dh]
+      if (!ll_get(a.qkvb + par * R + g * GQ * dh, GQ * dh, E, qkvl, a.err)) return;
+      if (!ll_get(a.qkvb + par * R + (H + g) * dh, dh, E, qkvl + GQ * dh, a.err)) return;
+      if (!ll_get(a.qkvb + par * R + (H + Hk + g) * dh, dh, E, qkvl + GQ * dh + dh, a.err)) return;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = tid + kPT * r, key = idx >> 4, d = (idx & 15) * 4;
+        float4 kk = kr[r], vv = vr[r];
+        if (k0 + key == pos) {  // the new row comes from this launch's exchange
+          kk = make_float4(qkvl[GQ * dh + d], qkvl[GQ * dh + d + 1], qkvl[GQ * dh + d + 2], qkvl[GQ * dh + d + 3]);
+          vv = make_float4(qkvl[GQ * dh + dh + d], qkvl[GQ * dh + dh + d + 1], qkvl[GQ * dh + dh + d + 2],
+                           qkvl[GQ * dh + dh + d + 3]);
+        }
+        if (key >= nk) kk = vv = make_float4(0.f, 0.f, 0.f, 0.f);
+        Kt[(d + 0) * (kPKeys + 1) + key] = kk.x;
+        Kt[(d + 1) * (kPKeys + 1) + key] = kk.y;
+        Kt[(d + 2) * (kPKeys + 1) + key] = kk.z;
+        Kt[(d + 3) * (kPKeys + 1) + key] = kk.w;
+        reinterpret_cast<float4*>(Vs + key * 64)[d / 4] = vv;
+      }
+      for (int i = tid; i < GQ * dh; i += kPT) qs[i] = qkvl[i] * a.scale;  // (q * scale) first (ops.py:292)
+      __syncthreads();
+      if (wave < GQ) {
+        const int h = wave;
+        float sv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int key = lane + 64 * u;
+          float t = 0.f;
+#pragma unroll 16
+          for (int d = 0; d < 64; ++d) t = fmaf(qs[h * 64 + d], Kt[d * (kPKeys + 1) + key], t);
+          sv[u] = key < nk ? t : -INFINITY;
+        }
+        float m = fmaxf(sv[0], sv[1]);
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float p0 = expf(sv[0] - m), p1 = expf(sv[1] - m);
+        float lsum = p0 + p1;
+        for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+        ps[h * kPKeys + lane] = p0;
+        ps[h * kPKeys + lane + 64] = p1;
+        wave_sync();  // the wave reads back every lane's p
+        float ov = 0.f;  // dim = lane
+#pragma unroll 16
+        for (int key = 0; key < kPKeys; ++key) ov = fmaf(ps[h * kPKeys + key], Vs[key * 64 + lane], ov);
+        uint64_t* out = a.pb + (size_t)par * kPChunks * H * kPPart + ((size_t)c * H + g * GQ + h) * kPPart;
+        if (lane == 0) {
+          ll_put(out, m, E + 1u);
+          ll_put(out + 1, lsum, E + 1u);
+        }
+        ll_put(out + 2 + lane, ov, E + 1u);
+      }
+      __syncthreads();  // big and xs are reused below
+    }
+    // ---- C: merge + o_proj rows + residual -> x_mid ----
+    if (w < kPOproj) {
+      const int rows = (D + kPOproj - 1) / kPOproj, rbeg = w * rows;
+      RowDot<64, 1, SF16, false> d0, d1;
+      const int ra = rbeg + wave, rb = rbeg + wave + 8;
+      const bool la = wave < rows && ra < D, lb = wave + 8 < rows && rb < D;
+      d0.load(a.o, (int64_t)l * D + (la ? ra : 0), lane, la);
+      d1.load(a.o, (int64_t)l * D + (lb ? rb : 0), lane, lb);
+      float* part = big;  // [nact][H][66]
+      if (!ll_get(a.pb + (size_t)par * kPChunks * H * kPPart, nact * H * kPPart, E + 1u, part, a.err)) return;
+      float* xr = xmid;   // x_in of this WG's rows
+      if (l == 0) {
+        for (int i = tid; i < rows && rbeg + i < D; i += kPT) xr[i] = a.x[rbeg + i];
+        __syncthreads();
+      } else if (!ll_get(a.xb + (par ^ 1) * D + rbeg, min(rows, D - rbeg), E - 8u + 4u, xr, a.err)) {
+        return;
+      }
+      // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den
+      for (int i = tid; i < 1024; i += kPT) {
+        if (i >= H * dh) {  // the o_proj dot reads the staged vector up to 1024
+          xs[i] = 0.f;
+          continue;
+        }
+        const int h = i / dh, d = i % dh;
+        float M = -INFINITY;
+        for (int c = 0; c < nact; ++c) M = fmaxf(M, part[(c * H + h) * kPPart]);
+        float num = 0.f, den = 0.f;
+        for (int c = 0; c < nact; ++c) {
+          const float* pc = part + (c * H + h) * kPPart;
+          const float wgt = expf(pc[0] - M);
+          den = fmaf(pc[1], wgt, den);
+          num = fmaf(pc[2 + d], wgt, num);
+        }
+        xs[i] = num / den;
+      }
+      __syncthreads();
+      const float va = d0.dot(xs, lane), vb2 = d1.dot(xs, lane);
+      if (lane == 0) {
+        if (la) ll_put(a.mb + par * D + ra, xr[wave] + va, E + 2u);
+        if (lb) ll_put(a.mb + par * D + rb, xr[wave + 8] + vb2, E + 2u);
+      }
+      __syncthreads();
+    }
+    // ---- D: [gate; up] pairs -> h ----
+    {
+      // balanced split: every workgroup owns at least one pair (I >= G), so phase E's
+      // wait for all of h is also a wait for every workgroup to be done with layer l
+      const int jbeg = (int)((int64_t)w * I / G), per = (int)((int64_t)(w + 1) * I / G) - jbeg;
+      RowDot<64, 1, SF16, false> dg[3], du[3];
+      int jj[3];
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        jj[t] = jbeg + wave + 8 * t;
+        const bool live = wave + 8 * t < per && jj[t] < I;
+        const int64_t jr = live ? jj[t] : jbeg;
+        dg[t].load(a.gu, (int64_t)l * 2 * I + min(jr, (int64_t)I - 1), lane, live);
+        du[t].load(a.gu, (int64_t)l * 2 * I + I + min(jr, (int64_t)I - 1), lane, live);
+      }
+      if (!ll_get(a.mb + par * D, D, E + 2u, xmid, a.err)) return;
+      VecStage<1> vs;
+      vs.load(xmid, D, a.ln2 + (int64_t)l * D);
+      const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const float gv = dg[t].dot(xs, lane) * inv, uv = du[t].dot(xs, lane) * inv;
+        if (lane == 0 && wave + 8 * t < per && jj[t] < I)
+          ll_put(a.hb + (size_t)par * I + jj[t], (gv / (1.0f + expf(-gv))) * uv, E + 3u);
+      }
+      __syncthreads();  // xs is restaged below
+    }
+    // ---- E: down rows + residual -> x of the next layer ----
+    if (w < kPDown && w * ((D + kPDown - 1) / kPDown) < D) {  // only workgroups that own rows wait
+      const int rows = (D + kPDown - 1) / kPDown, r = w * rows + wave;
+      const bool live = wave < rows && r < D;
+      RowDot<64, 5, SF16, false> dd;
+      dd.load(a.dn, (int64_t)l * D + (live ? r : 0), lane, live);
+      for (int i = I + tid; i < 1024; i += kPT) xs[i] = 0.f;  // the staged tail past I must be zero
+      if (!ll_get(a.hb + (size_t)par * I, I, E + 3u, xs, a.err)) return;  // xs[I..5120) stays zero
+      const float v = dd.dot(xs, lane);
+      if (live && lane == 0) ll_put(a.xb + par * D + r, xmid[r] + v, E + 4u);
+      __syncthreads();
+    }
+  }
+  // ---- head rows, then the greedy pick ----
+  const uint32_t EH = base + (uint32_t)a.layers * 8u;
+  {
+    const int V = (int)a.head.rows, per = (V + G - 1) / G, rbeg = w * per;
+    RowDot<64, 1, SF16, false> dh4[4];
+    int rr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      rr[t] = rbeg + wave + 8 * t;
+      const bool live = wave + 8 * t < per && rr[t] < V;
+      dh4[t].load(a.head, live ? rr[t] : 0, lane, live);
+    }
+    const int lp = (a.layers - 1) & 1;
+    if (!ll_get(a.xb + lp * D, D, EH - 8u + 4u, xin, a.err)) return;
+    VecStage<1> vs;
+    vs.load(xin, D, a.norm);
+    const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float v = dh4[t].dot(xs, lane) * inv + (a.head_bias && rr[t] < V ? a.head_bias[min(rr[t], V - 1)] : 0.f);
+      if (wave + 8 * t < per && rr[t] < V) {
+        if (lane == 0) a.logits[rr[t]] = v;
+        if (v > best) {  // rows ascend within the wave
+          best = v;
+          bidx = rr[t];
+        }
+      }
+    }
+    if (lane == 0) {
+      hb_val[wave] = best;
+      hb_i[wave] = bidx;
+    }
+    __syncthreads();
+    if (!a.select) return;
+    if (tid == 0) {
+      float b = hb_val[0];
+      int bi = hb_i[0];
+      for (int k = 1; k < kPT / 64; ++k)
+        if (hb_val[k] > b || (hb_val[k] == b && hb_i[k] < bi)) {
+          b = hb_val[k];
+          bi = hb_i[k];
+        }
+      ll_put(a.arg + 2 * w, b, EH);
+      ll_put(a.arg + 2 * w + 1, __int_as_float(bi), EH);
+    }
+    if (w != 0) return;
+    float* cand = big;
+    if (!ll_get(a.arg, 2 * G, EH, cand, a.err)) return;
+    if (tid == 0) {
+      float b = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int k = 0; k < G; ++k) {
+        const float v = cand[2 * k];
+        const int i = __float_as_int(cand[2 * k + 1]);
+        if (v > b || (v == b && i < bi)) {
+          b = v;
+          bi = i;
+        }
+      }
+      if (bi < 0 || bi >= V) bi = 0;  // all-NaN logits: keep a valid row
+      hb_i[0] = bi;
+    }
+    __syncthreads();
+    const int64_t id = hb_i[0];
+    for (int64_t cc = tid; cc < a.emb.k; cc += kPT)
+      a.x[cc] = (float)a.emb.q[id * a.emb.kp + cc] * sc_at(a.emb, id, cc);
+    if (tid == 0) {
+      a.history[pos + 1] = id;
+      *a.token = id;
+      *a.pos = pos + 1;
+    }
+  }
+}
+
 QW make_qw(const cv3_qweight& w) {
   QW q;
   q.q = reinterpret_cast<const int8_t*>(w.q);
@@ -1260,6 +1648,107 @@ int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_stat
                                   cv3_stream_t stream) {
   CV3_REQUIRE(smp, CV3_EINVAL, "null sampler");
   return decode_step(m, s, smp, stream);
+}
+
+static int64_t persist_words(const cv3_qwen2_model* m, int workgroups) {
+  const int64_t D = m->hidden, R = (m->heads + 2 * m->kv_heads) * m->head_dim;
+  return 2 * D + 2 * R + 2 * (int64_t)kPChunks * m->heads * kPPart + 2 * D + 2 * m->inter + 2 * (int64_t)workgroups;
+}
+
+int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words) {
+  CV3_REQUIRE(m && words && workgroups > 0, CV3_EINVAL, "null model or output, or no workgroups");
+  *words = persist_words(m, workgroups);
+  return CV3_OK;
+}
+
+int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,
+                                     int select, cv3_stream_t stream) {
+  CV3_REQUIRE(m && s && p, CV3_EINVAL, "null model, state or exchange block");
+  const int64_t H = m->heads, Hk = m->kv_heads, dh = m->head_dim, D = m->hidden, I = m->inter;
+  CV3_REQUIRE(H > 0 && Hk > 0 && H % Hk == 0 && H / Hk <= 8 && dh == 64 && H * dh == D, CV3_EUNSUPPORTED,
+              "persistent step: heads %lld / kv heads %lld / head dim %lld", (long long)H, (long long)Hk,
+              (long long)dh);
+  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= 5120 && I >= kPDown, CV3_EUNSUPPORTED,
+              "persistent step: hidden %lld / inter %lld", (long long)D, (long long)I);
+  CV3_REQUIRE(m->layers > 0 && m->layers * 8 + 8 <= 256, CV3_EUNSUPPORTED, "persistent step: %lld layers (at most 31)",
+              (long long)m->layers);
+  CV3_REQUIRE(s->cap > 0 && s->cap <= (int64_t)kPChunks * kPKeys, CV3_EUNSUPPORTED,
+              "persistent step: cache capacity above %d positions", kPChunks * kPKeys);
+  int rc;
+  if ((rc = check_qw(m->qkv, "qkv", D))) return rc;
+  if ((rc = check_qw(m->o, "o_proj", D))) return rc;
+  if ((rc = check_qw(m->gate_up, "gate_up", D))) return rc;
+  if ((rc = check_qw(m->down, "down", I))) return rc;
+  if ((rc = check_qw(m->head, "llm_decoder", D))) return rc;
+  if ((rc = check_qw(m->embedding, "speech_embedding", D))) return rc;
+  const cv3_qweight* all[6] = {&m->qkv, &m->o, &m->gate_up, &m->down, &m->head, &m->embedding};
+  for (const cv3_qweight* w : all)
+    CV3_REQUIRE(w->kind == CV3_KIND_Q8 && w->scale_dtype == m->qkv.scale_dtype, CV3_EUNSUPPORTED,
+                "persistent step: q8 weights with one scale dtype");
+  CV3_REQUIRE(m->qkv.rows == (H + 2 * Hk) * dh && m->o.rows == D && m->gate_up.rows == 2 * I && m->down.rows == D &&
+                  m->embedding.rows >= m->head.rows,
+              CV3_EINVAL, "stacked weight rows do not match the geometry");
+  int dev = 0, cus = 0;
+  CV3_HIP(hipGetDevice(&dev));
+  CV3_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const bool sf16 = m->qkv.scale_dtype == CV3_F16;
+  const void* fn = sf16 ? (const void*)k_dec_persist<true> : (const void*)k_dec_persist<false>;
+  int per_cu = 0;
+  CV3_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPT, 0));
+  const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
+  CV3_REQUIRE(G >= kPDown && G <= per_cu * cus && G <= I, CV3_EUNSUPPORTED,
+              "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G, kPDown, per_cu * cus,
+              (long long)I);
+  CV3_REQUIRE((H + 2 * Hk) * dh / 2 <= 8LL * G && I <= 24LL * G && m->head.rows <= 32LL * G &&
+                  Hk * kPChunks <= G,
+              CV3_EUNSUPPORTED, "persistent step: too few workgroups for the geometry");
+  CV3_REQUIRE(p->words && p->err && p->words_len >= persist_words(m, G), CV3_EINVAL,
+              "persistent step: exchange words missing or too few");
+  CV3_REQUIRE(p->epoch_base != 0, CV3_EINVAL, "persistent step: epoch base 0 is the cleared state");
+  PersistArgs a{};
+  a.qkv = make_qw(m->qkv);
+  a.o = make_qw(m->o);
+  a.gu = make_qw(m->gate_up);
+  a.dn = make_qw(m->down);
+  a.head = make_qw(m->head);
+  a.emb = make_qw(m->embedding);
+  a.ln1 = m->ln1;
+  a.ln2 = m->ln2;
+  a.norm = m->norm;
+  a.qkv_bias = m->qkv_bias;
+  a.head_bias = m->head_bias;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.layers = (int)m->layers;
+  a.D = (int)D;
+  a.H = (int)H;
+  a.Hk = (int)Hk;
+  a.dh = (int)dh;
+  a.I = (int)I;
+  a.eps = m->eps;
+  a.scale = 1.0f / sqrtf((float)dh);
+  a.k_cache = s->k_cache;
+  a.v_cache = s->v_cache;
+  a.cap = s->cap;
+  a.pos = s->pos;
+  a.token = s->token;
+  a.history = s->history;
+  a.x = s->x;
+  a.logits = s->logits;
+  const int64_t R = (H + 2 * Hk) * dh;
+  uint64_t* wds = p->words;
+  a.xb = wds;
+  a.qkvb = a.xb + 2 * D;
+  a.pb = a.qkvb + 2 * R;
+  a.mb = a.pb + 2 * (int64_t)kPChunks * H * kPPart;
+  a.hb = a.mb + 2 * D;
+  a.arg = a.hb + 2 * I;
+  a.err = p->err;
+  a.epoch_base = p->epoch_base;
+  a.select = select ? 1 : 0;
+  void* args[] = {&a};
+  CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));
+  return CV3_OK;
 }
 
 int cv3_qwen2_select(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,

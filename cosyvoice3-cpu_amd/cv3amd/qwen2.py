@@ -44,6 +44,11 @@ class Model(ctypes.Structure):
                 ("rope_cos", c_vp), ("rope_sin", c_vp)]
 
 
+class Persist(ctypes.Structure):
+    _fields_ = [("words", c_vp), ("words_len", c_i64), ("err", c_vp), ("epoch_base", ctypes.c_uint32),
+                ("workgroups", ctypes.c_int)]
+
+
 class Sampler(ctypes.Structure):
     _fields_ = [("top_p", ctypes.c_double), ("rep_threshold", ctypes.c_double), ("top_k", c_i64),
                 ("win_size", c_i64), ("speech_token_size", c_i64), ("min_len", c_i64),
@@ -184,6 +189,7 @@ class DeviceQwen2:
         # sampler control block: [start, stop step + 1, PCG64 state hi, lo, inc hi, lo]
         self.ctl = DeviceArray((6,), np.int64).zero_()
         self._sampled_graphs = {}
+        self._persist: Optional[Persist] = None   # exchange words of the one-launch step, made on first use
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
@@ -379,6 +385,42 @@ class DeviceQwen2:
         self.select(None)
         for _ in range(steps - 1):
             self.step(graph)
+        ints = self.ints.numpy()
+        return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + steps]]
+
+    # -- the whole step as one cooperative launch --------------------------
+    def step_persistent(self, select: bool = True):
+        """Enqueue one token as a single cooperative launch (cv3_qwen2_decode_step_persistent):
+        greedy selection inside (``select``), or logits only for ``select_sampled``."""
+        if self._pos_host + 1 >= self.cap:
+            raise ValueError("the KV cache is full")
+        if self._persist is None:
+            n = ctypes.c_int64()
+            _lib.call("qwen2_persist_words", ctypes.byref(self.model), 256, _lib.ptr(n))
+            self._pwords = DeviceArray((n.value,), np.int64).zero_()
+            self._perr = DeviceArray((1,), np.int64).zero_()
+            self._persist = Persist(self._pwords.ptr, n.value, self._perr.ptr, 0, 0)
+        p = self._persist
+        base = (p.epoch_base + 256) & 0xFFFFFFFF
+        if base == 0:   # the launch counter wrapped: clear the words so no old epoch can match
+            self._pwords.zero_()
+            base = 256
+        p.epoch_base = base
+        _lib.call("qwen2_decode_step_persistent", ctypes.byref(self.model), ctypes.byref(self.state),
+                  ctypes.byref(p), 1 if select else 0, None)
+        self._pos_host += 1 if select else 0
+
+    def persistent_error(self) -> bool:
+        """True if a launch of the one-launch step gave up waiting (its results are invalid)."""
+        return self._persist is not None and int(self._perr.numpy()[0]) != 0
+
+    def generate_persistent(self, first_token: int, pos: int, steps: int) -> List[int]:
+        """Greedy tokens with the one-launch step; raises if a launch gave up."""
+        self.begin(first_token, pos)
+        for _ in range(steps):
+            self.step_persistent(True)
+        if self.persistent_error():
+            raise RuntimeError("the one-launch decode step gave up waiting for an exchange")
         ints = self.ints.numpy()
         return [int(t) for t in ints[2 + pos + 1: 2 + pos + 1 + steps]]
 

@@ -321,6 +321,22 @@ typedef struct {
 /* cv3_qwen2_decode_step with the token drawn by the sampler instead of the argmax (llm.py:112-123). */
 int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
                                   cv3_stream_t stream);
+/* The decode step as ONE cooperative launch (q8 weights, head dim 64, cache <= 1024 positions): one workgroup
+ * per CU runs every layer; vectors crossing workgroups travel as (epoch, value) words in `words` (device memory
+ * of *words uint64 from cv3_qwen2_persist_words; zeroed at allocation, then whatever earlier launches left),
+ * with every wait bounded: a word that never arrives sets *err (device int64, caller clears it) and the launch
+ * ends early.  epoch_base must differ between launches (count launches, times 256, never 0).  select 1: the
+ * greedy pick and bookkeeping of cv3_qwen2_decode_step; select 0: logits only (then cv3_qwen2_select). */
+typedef struct {
+  uint64_t* words;
+  int64_t words_len;
+  int64_t* err;
+  uint32_t epoch_base;
+  int workgroups; /* 0: one per CU, at most 256 */
+} cv3_persist;
+int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words);
+int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,
+                                     int select, cv3_stream_t stream);
 /* The token selection of a decode step alone, on the logits already in s->logits: greedy (smp == NULL) or the
  * sampler; then x = speech_embedding[id], history[pos + 1] = id, pos += 1.  After a prompt prefill that left the
  * last position's logits and pos = that position, this draws the first speech token (llm.py:112-121, i = 0). */

@@ -1,0 +1,115 @@
+"""The one-launch decode step (cv3_qwen2_decode_step_persistent) against the oracle.
+
+Same seeded synthetic Qwen2-0.5B weights as test_gpu_decode.py, q8 under the
+per-channel (float32 scales) and balanced (block 64, float16 scales) profiles.
+Bars: per-step logits within 1e-5 (max abs error over max |logit|) of the
+oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
+layers the tokens equal the five-kernel step's and the logits agree within 1e-5.
+Positions cover an empty cache (one attention chunk), a start just below the
+128-key chunk boundary, and 512 cached positions (five chunks).
+"""
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(layers, profile, n, seed=0):
+    import oracle.quant
+    import cv3amd.quant
+    from cv3amd import synth
+    from cv3amd.weights import WeightStore
+    t = synth.qwen2_tensors(layers=layers, seed=seed)
+    t = synth.quantize_store(t, profile, oracle.quant.quantize_q8, oracle.quant.quantize_q4)
+    meta = synth.qwen2_meta(layers=layers)
+    cpu = WeightStore(t, meta, oracle.quant.QTensor)
+    dev = WeightStore(t, meta, cv3amd.quant.QTensor)
+    rng = np.random.default_rng(200 + seed)
+    k = rng.standard_normal((layers, 2, n, 64), dtype=np.float32)
+    v = rng.standard_normal((layers, 2, n, 64), dtype=np.float32)
+    return cpu, dev, k, v
+
+
+def _oracle_lm(cpu, k, v, n, steps):
+    from oracle.llm import CosyVoice3LM
+    lm = CosyVoice3LM(cpu, "llm.")
+    cache = lm.body.new_cache()
+    cache._reserve(n + steps + 1)
+    for i in range(lm.cfg.num_hidden_layers):
+        cache.k[i][:, :n] = k[i]
+        cache.v[i][:, :n] = v[i]
+    cache.length = n
+    return lm, cache
+
+
+@pytest.mark.parametrize("profile,n,steps", [("per_channel", 512, 10), ("balanced", 0, 6),
+                                             ("balanced", 122, 10)])
+def test_persistent_step_logits_and_tokens(gpu, profile, n, steps):
+    from cv3amd.qwen2 import DeviceQwen2
+    cpu, dev, k, v = _setup(2, profile, n)
+    print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps", flush=True)
+    lm, cache = _oracle_lm(cpu, k, v, n, steps)
+    d = DeviceQwen2(dev, cap=1024)
+    if n:
+        d.fill_cache(k, v)
+    d.begin(lm.sos, n)
+    x = lm.speech_emb([lm.sos])
+    for s in range(steps):
+        want = lm.head(lm.body.forward(x, cache)[-1:])[0]
+        top = int(np.argmax(want))
+        x = lm.speech_emb([top])
+        d.step_persistent()
+        got = d.logits.numpy()
+        assert not d.persistent_error(), f"step {s}: a wait gave up"
+        e = rel_err(got, want)
+        print(f"[persist] step {s} token {top} logits rel err {e:.2e}", flush=True)
+        assert e < 1e-5, f"step {s}"
+        assert int(d.ints.numpy()[2 + n + 1 + s]) == top
+        assert int(d.ints.numpy()[0]) == n + 1 + s
+    kc, vc = d.k_cache.numpy(), d.v_cache.numpy()
+    for i in range(2):
+        assert rel_err(kc[i][:, :n + steps], cache.k[i][:, :n + steps]) < 1e-5
+        assert rel_err(vc[i][:, :n + steps], cache.v[i][:, :n + steps]) < 1e-5
+
+
+def test_persistent_full_depth_matches_five_kernel_step(gpu):
+    """24 layers: the one-launch step and the five-kernel step give the same tokens."""
+    from cv3amd.qwen2 import DeviceQwen2
+    n, steps = 300, 16
+    _, dev, k, v = _setup(24, "balanced", n)
+    print(f"[persist] 24 layers, {n} cached, {steps} steps", flush=True)
+    a = DeviceQwen2(dev, cap=1024)
+    a.fill_cache(k, v)
+    want = []
+    a.begin(1, n)
+    for _ in range(steps):
+        a.step(graph=False)
+        want.append(a.logits.numpy())
+    want_tok = [int(t) for t in a.ints.numpy()[2 + n + 1: 2 + n + 1 + steps]]
+    b = DeviceQwen2(dev, cap=1024)
+    b.fill_cache(k, v)
+    b.begin(1, n)
+    for s in range(steps):
+        b.step_persistent()
+        e = rel_err(b.logits.numpy(), want[s])
+        print(f"[persist] step {s} logits rel err vs five-kernel step {e:.2e}", flush=True)
+        assert e < 1e-5, f"step {s}"
+    assert not b.persistent_error()
+    got_tok = [int(t) for t in b.ints.numpy()[2 + n + 1: 2 + n + 1 + steps]]
+    assert got_tok == want_tok
+    assert rel_err(b.k_cache.numpy(), a.k_cache.numpy()) < 1e-5
+    # and generate_persistent replays the same sequence from the same start
+    b.fill_cache(k, v)
+    assert b.generate_persistent(1, n, steps) == want_tok
+
+
+def test_persistent_step_rejects_q4(gpu):
+    from cv3amd.qwen2 import DeviceQwen2
+    _, dev, _, _ = _setup(2, "tiny", 0)
+    d = DeviceQwen2(dev, cap=1024)
+    d.begin(1, 0)
+    with pytest.raises(NotImplementedError):
+        d.step_persistent()
