@@ -4,9 +4,11 @@
   * Qwen2-0.5B int8 greedy decode, batch 1 (the reported ``value``): 24 layers,
     hidden 896, 14/2 heads x 64, SwiGLU 4864, per-output-channel int8 weights with
     float32 scales, KV cache pre-filled to 512 positions of N(0, 1), K tokens
-    decoded from speech_embedding[sos] (one "step" = one token); the same decode with
-    the reference's sampler on the device (``sampled_tok_s``); and with the tiny
-    profile's q4 body layers (the ``decode_tiny`` object).
+    decoded from speech_embedding[sos] (one "step" = one token), each token one
+    cooperative launch of the whole step (``--decode-step kernels``: five kernels per
+    layer, whose rate is reported beside it in ``five_kernel_step``); the same decode
+    with the reference's sampler on the device (``sampled_tok_s``); and with the tiny
+    profile's q4 body layers (the ``decode_tiny`` object, five-kernel step).
   * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
     fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
     of torch.randn((1, 80, 15000), seed 0); and the same solve over 30 s (T = 1500)
@@ -126,28 +128,44 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
     v = rng.standard_normal(shape, dtype=np.float32)
     lm.fill_cache(k, v)
     sos = int(meta["speech_token_size"])
-    log(f"{label}: warmup {args.warmup} tokens (captures the step graph)")
-    lm.begin(sos, PREFILL)
-    for _ in range(args.warmup):
-        lm.step(graph=args.graph)
-    synchronize()
-    lm.fill_cache(k, v)
-    lm.begin(sos, PREFILL)
-    synchronize()
-    log(f"{label}: timing {args.steps} tokens")
+    # the one-launch step takes q8 weights; the q4 body (tiny profile) runs the five-kernel step
+    persistent = args.decode_step == "persistent" and lm.gate_up.kind == "q8"
+    lm.cooperative = args.cooperative
     tm = Timer()
-    tm.start()
-    for _ in range(args.steps):
-        lm.step(graph=args.graph)
-    ms = tm.stop()
-    synchronize()
-    tokens = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + args.steps]]
+
+    def timed_tokens(one_launch: bool):
+        """Warm up, then time args.steps greedy tokens from the same cache and start."""
+        what = "one-launch step" if one_launch else "five-kernel step"
+        log(f"{label}: {what}: warmup {args.warmup} tokens")
+        lm.fill_cache(k, v)
+        lm.begin(sos, PREFILL)
+        for _ in range(args.warmup):
+            lm.step_persistent() if one_launch else lm.step(graph=args.graph)
+        synchronize()
+        lm.fill_cache(k, v)
+        lm.begin(sos, PREFILL)
+        synchronize()
+        log(f"{label}: {what}: timing {args.steps} tokens")
+        tm.start()
+        for _ in range(args.steps):
+            lm.step_persistent() if one_launch else lm.step(graph=args.graph)
+        ms_ = tm.stop()
+        synchronize()
+        if one_launch and lm.persistent_error():
+            raise RuntimeError("the one-launch decode step gave up waiting for an exchange")
+        toks = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + args.steps]]
+        log(f"{label}: {what}: {ms_:.2f} ms for {args.steps} tokens = {args.steps / (ms_ / 1e3):.1f} tok/s")
+        return ms_, toks
+
+    ms_k, tokens_k = timed_tokens(False)
+    ms, tokens = timed_tokens(True) if persistent else (ms_k, tokens_k)
+    if tokens != tokens_k:
+        raise RuntimeError("the one-launch and five-kernel steps chose different tokens")
     tok_s = args.steps / (ms / 1e3)
     avg_len = PREFILL + (args.steps - 1) / 2.0
     b = lm.bytes_per_token(int(round(avg_len)))
     per_token = b["body"] + b["kv"] + b["norms_biases"] + b["head"]
-    log(f"{label}: {ms:.2f} ms for {args.steps} tokens = {tok_s:.1f} tok/s; "
-        f"{per_token / 1e6:.1f} MB/token -> {per_token * tok_s / 1e9:.0f} GB/s")
+    log(f"{label}: {tok_s:.1f} tok/s; {per_token / 1e6:.1f} MB/token -> {per_token * tok_s / 1e9:.0f} GB/s")
 
     # Dominant kernel: the gate/up GEMV (RMSNorm prologue + SwiGLU), one layer's
     # [gate; up] = 2 x 4864 x 896 int8 + scales per launch.  Timed back-to-back
@@ -176,18 +194,26 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
         top_p, top_k, win_size, tau_r, strict_min_len = 0.8, 25, 10, 0.1, True
         rng = np.random.default_rng(0)
     lm.fill_cache(k, v)
-    lm.generate_sampled(sos, PREFILL, args.warmup, args.warmup, _Sampling, sos, graph=args.graph)
+    lm.generate_sampled(sos, PREFILL, args.warmup, args.warmup, _Sampling, sos, graph=args.graph,
+                        persistent=persistent)
     lm.fill_cache(k, v)
     synchronize()
     tm.start()
-    sampled = lm.generate_sampled(sos, PREFILL, args.steps, args.steps, _Sampling, sos, graph=args.graph)
+    sampled = lm.generate_sampled(sos, PREFILL, args.steps, args.steps, _Sampling, sos, graph=args.graph,
+                                  persistent=persistent)
     sms = tm.stop()
     sampled_tok_s = len(sampled) / (sms / 1e3)
     log(f"{label}: sampled (top_p 0.8, top_k 25, repetition window 10) {sms:.2f} ms for {len(sampled)} tokens "
         f"= {sampled_tok_s:.1f} tok/s")
+    sf16 = lm.gate_up.sf16
     return {
-        "sampled_tok_s": sampled_tok_s,
+        "sampled_tok_s": sampled_tok_s, "persistent": persistent,
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
+        "five_kernel_tok_s": args.steps / (ms_k / 1e3),
+        # the one-launch step is a single kernel per token: its bytes are the token's
+        "step_kernel": {"name": f"k_dec_persist<{'true' if sf16 else 'false'}> (the whole decode step)",
+                        "bytes_per_launch": per_token, "us_per_launch": ms / args.steps * 1e3,
+                        "achieved_Bps": per_token / (ms / args.steps / 1e3)},
         "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
                    else "k_dec_gemv<16,4,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
                    "bytes_per_launch": gu_bytes, "us_per_launch": kms * 1e3, "achieved_Bps": achieved},
@@ -410,6 +436,12 @@ def main():
     ap.add_argument("--no-hift", action="store_true")
     ap.add_argument("--hift-runs", type=int, default=3)
     ap.add_argument("--cpu-tokens", type=int, default=128)
+    ap.add_argument("--decode-step", choices=("persistent", "kernels"), default="persistent",
+                    help="the decode step the reported value times: one cooperative launch per token, or "
+                         "five kernels per layer (replayed from a graph unless --no-graph)")
+    ap.add_argument("--cooperative", action="store_true",
+                    help="launch the one-launch step with hipLaunchCooperativeKernel (guaranteed co-residency, "
+                         "about 20 us more per token) instead of an ordinary launch")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
     args = ap.parse_args()
@@ -480,9 +512,12 @@ def main():
             log(f"cpu baseline: {cpu_hift_s:.2f} s per 10 s of audio")
 
     kern = dec["kernel"]
+    step_k = dec["step_kernel"] if dec["persistent"] else kern
     line = {
         "metric": METRIC,
-        "launch_mode": "hip-graph replay" if args.graph else "direct launches",
+        "decode_step": (("one cooperative launch" if args.cooperative else "one kernel launch") + " per token")
+        if dec["persistent"] else "five kernels per layer",
+        "launch_mode": "direct launches" if dec["persistent"] or not args.graph else "hip-graph replay",
         "value": round(dec["tok_s"], 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -500,10 +535,17 @@ def main():
                    "decode_tokens": args.steps, "kv_prefill": PREFILL},
         "hbm_roofline_frac": round(dec["bytes_per_token"] * dec["tok_s"] / HBM_PEAK, 4),
         "bytes_per_token": dec["bytes_per_token"],
-        "roofline": {"bound": "hbm", "achieved": round(kern["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(kern["achieved_Bps"] / HBM_PEAK, 4), "traffic": None,
-                     "kernel": kern["name"], "bytes_per_launch": kern["bytes_per_launch"],
-                     "us_per_launch": round(kern["us_per_launch"], 3)},
+        "roofline": {"bound": "hbm", "achieved": round(step_k["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(step_k["achieved_Bps"] / HBM_PEAK, 4), "traffic": None,
+                     "kernel": step_k["name"], "bytes_per_launch": step_k["bytes_per_launch"],
+                     "us_per_launch": round(step_k["us_per_launch"], 3)},
+        "five_kernel_step": {
+            "tok_s": round(dec["five_kernel_tok_s"], 2),
+            "launch_mode": "hip-graph replay" if args.graph else "direct launches",
+            "roofline": {"bound": "hbm", "achieved": round(kern["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": round(kern["achieved_Bps"] / HBM_PEAK, 4), "traffic": None,
+                         "kernel": kern["name"], "bytes_per_launch": kern["bytes_per_launch"],
+                         "us_per_launch": round(kern["us_per_launch"], 3)}},
         "cpu_baseline": cpu,
         "copy_GBps": round(copy_bps / 1e9, 1),
         "tokens_head": dec["tokens"][:8],

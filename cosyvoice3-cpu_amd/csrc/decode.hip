@@ -1082,33 +1082,44 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
 //
 // Every dependent kernel boundary of the step above costs about 4.5 us: the
 // launch, then the first loads of the next kernel.  Here one workgroup per CU runs
-// all 24 layers; the vectors that cross workgroups (x, q/k/v, attention partials,
+// all layers; the vectors that cross workgroups (x, q/k/v, attention partials,
 // x after o_proj, h) travel as 64-bit words (epoch << 32 | float bits) written and
-// polled at device scope, and each phase streams its weights into registers BEFORE
-// it waits for its input, so the weight latency overlaps the exchange (about
-// 2.2-3 us per exchange on this part).  Per layer:
-//   A  all workgroups: RMSNorm(x) -> [q; k; v] rows + bias + rotary; k, v also to
-//      the cache (read back by later tokens, after the kernel boundary)
-//   B  Hk x 8 workgroups: attention of one kv head's query heads over 128 keys
+// polled at device scope, and each phase issues its weight (and cache) loads
+// BEFORE it waits for its input, so their latency overlaps the exchange.  Per layer:
+//   A  all workgroups: RMSNorm(x) -> [q; k; v] row pairs + bias + rotary; k, v
+//      also to the cache (read back by later tokens, after the kernel boundary)
+//   B  H x 8 workgroups: one query head over one 128-key chunk of the cache
+//      (flash-decoding partial: max, sum, unnormalised output)
 //   C  64 workgroups: merge the partials, o_proj rows + residual -> x_mid
 //   D  all workgroups: RMSNorm(x_mid) -> [gate; up] pairs -> h = silu(g) * u
 //   E  128 workgroups: down rows + residual -> x for the next layer
 // then the head rows, and (greedy) the argmax, speech_embedding row and
-// bookkeeping by workgroup 0.  Every buffer is double-buffered by layer parity:
-// it is rewritten two layers later, after phase D, which needs every workgroup,
-// so all of its readers are done.  Epochs are (launch counter * 256 + layer * 8 +
-// phase; the host counts launches), so no word left by another phase, layer or
-// launch can match.  Every
-// wait is bounded: a word that does not arrive sets the error flag and the
-// workgroups leave, each within one wait.
+// bookkeeping by workgroup 0.
+//
+// Reuse of the exchange words: every buffer is double-buffered by layer parity,
+// so a word of layer l is rewritten in layer l + 2.  Phase D splits the [gate;
+// up] pairs so that every workgroup owns at least one (inter >= workgroups), and
+// phase E waits for all of h; so once any workgroup is in layer l + 1, every
+// workgroup has finished phase D of layer l, and with it every read of a layer-l
+// word except phase E's own, which end before x of layer l exists (only the
+// workgroups that own down rows wait in E).  The next writer of any layer-l word
+// has passed layer l + 1.  Epochs are launch counter * 256 + layer * 8 + phase
+// (the host counts launches and clears the words when the counter wraps), so no
+// word left by another phase, layer or launch matches.  Every wait is bounded: a
+// word that does not arrive sets the error flag, and every other wait ends
+// within 256 polls of seeing it.
 // ---------------------------------------------------------------------------
 constexpr int kPT = 512;                 // threads per workgroup
 constexpr int kPKeys = 128;              // keys per attention item
-constexpr int kPChunks = 8;              // attention items per kv head: cache <= 1024 positions
+constexpr int kPChunks = 8;              // attention items per head: cache <= 1024 positions
 constexpr int kPOproj = 64;              // workgroups of phase C
 constexpr int kPDown = 128;              // workgroups of phase E
 constexpr int kPSpin = 1 << 18;          // polls (each with a short sleep) before a wait gives up
 constexpr int kPPart = 66;               // words per attention partial: m, l, o[64]
+// Replicas of the exchanged vectors that many workgroups poll (x: all, x_mid: all,
+// h: 128, partials: 64): workgroup w reads replica w % n, so each copy of a word
+// has a few dozen readers instead of hundreds polling one cache line.
+constexpr int kRX = 8, kRM = 8, kRH = 4, kRP = 2;
 
 struct PersistArgs {
   QW qkv, o, gu, dn, head, emb;
@@ -1119,7 +1130,8 @@ struct PersistArgs {
   int64_t cap;
   int64_t *pos, *token, *history;
   float *x, *logits;
-  uint64_t *xb, *qkvb, *pb, *mb, *hb, *arg;  // exchange words, two sets each
+  uint64_t *xb, *qkvb, *pb, *mb, *hb, *arg;  // exchange words, two sets each (arg: one)
+  int64_t sx, sp, sm, sh;                    // words between replicas of x, partials, x_mid, h
   int64_t* err;                              // set when a wait gives up
   uint32_t epoch_base;                       // launch counter * 256, from the host
   int select;                                // 1: greedy argmax + next input here
@@ -1129,31 +1141,45 @@ __device__ __forceinline__ void ll_put(uint64_t* p, float v, uint32_t e) {
   __hip_atomic_store(p, ((uint64_t)e << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The workgroup reads words [0, n) carrying epoch e into dst (LDS), eight per
-// thread per batch.  False for every thread (and the error flag set) if a word
-// never arrives.  A wait also ends early once another workgroup has set the
-// flag, so one missing word ends the launch within about one wait.
-__device__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err) {
+// The workgroup reads the words of up to three ranges (n0 words at s0, then n1 at
+// s1, n2 at s2), all carrying epoch e, into dst[0 .. n0 + n1 + n2) in LDS: NW
+// words per thread per poll, so a wait of up to NW * 512 words is one round trip.
+// False for every thread (and the error flag set) if a word never arrives; a wait
+// also ends early once another workgroup has set the flag.
+template <int NW>
+__device__ bool ll_get(const uint64_t* s0, int n0, const uint64_t* s1, int n1, const uint64_t* s2, int n2,
+                       uint32_t e, float* dst, int64_t* err) {
+  const int n = n0 + n1 + n2;
   bool ok = true;
-  for (int b0 = 0; b0 < n && ok; b0 += kPT * 8) {
-    uint64_t w[8];
+  for (int b0 = 0; b0 < n && ok; b0 += kPT * NW) {
+    const uint64_t* src[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      const int idx = b0 + (int)threadIdx.x + kPT * j;
+      src[j] = idx < n0 ? s0 + idx : idx < n0 + n1 ? s1 + (idx - n0) : s2 + (idx - n0 - n1);
+    }
+    uint64_t w[NW];
     bool got = false;
     for (int spins = 0; spins < kPSpin; ++spins) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < NW; ++j) {
         const int idx = b0 + (int)threadIdx.x + kPT * j;
-        w[j] = idx < n ? __hip_atomic_load(src + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : ((uint64_t)e << 32);
+        w[j] = idx < n ? __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ((uint64_t)e << 32);
       }
       got = true;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) got = got && (uint32_t)(w[j] >> 32) == e;
+      for (int j = 0; j < NW; ++j) got = got && (uint32_t)(w[j] >> 32) == e;
       if (got) break;
       if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-      __builtin_amdgcn_s_sleep(1);
+      // back off after a few misses: hundreds of workgroups polling the same words
+      // slow every exchange down
+      if (spins < 8)
+        __builtin_amdgcn_s_sleep(1);
+      else
+        __builtin_amdgcn_s_sleep(20);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NW; ++j) {
       const int idx = b0 + (int)threadIdx.x + kPT * j;
       if (idx < n) dst[idx] = __uint_as_float((uint32_t)w[j]);
     }
@@ -1162,16 +1188,90 @@ __device__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64
   if (!ok && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(err), 1ull);
   return ok;
 }
+template <int NW>
+__device__ __forceinline__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err) {
+  return ll_get<NW>(src, n, nullptr, 0, nullptr, 0, e, dst, err);
+}
+
+// Dot product of one weight row spread over the whole wave (64 lanes x CPL
+// chunks), reduced through DPP: every lane gets the sum.
+template <int CPL, bool SF16>
+__device__ __forceinline__ float wdot(const RowDot<64, CPL, SF16, false>& rd, const float* xs, int lane) {
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) acc = fmaf(dot16(rd.wv[i], xs + (lane + i * 64) * 16), rd.sc[i], acc);
+  return wave_sum_dpp(acc);
+}
+// The same for K <= 1024 with the lane's 16 staged values already in registers
+// (a wave computing several rows reads its slice of the vector once).
+struct XSlice {
+  float v[16];
+  __device__ __forceinline__ void load(const float* xs, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(v)[i] = reinterpret_cast<const float4*>(xs + lane * 16)[i];
+  }
+};
+template <bool SF16>
+__device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, false>& rd, const XSlice& x) {
+  return wave_sum_dpp(fmaf(dot16(rd.wv[0], x.v), rd.sc[0], 0.f));
+}
+
+// RMSNorm staging with the norm weight loaded ahead (thread t owns float4 t):
+// xs[0, 1024) = x * w, zero past D; returns 1 / sqrt(mean(x^2) + eps), which
+// scales each row's dot product afterwards.  x is in LDS.
+struct NormStage {
+  float4 w;
+  __device__ __forceinline__ void prefetch(const float* g, int D) {
+    const int t = threadIdx.x;
+    w = t < D / 4 ? reinterpret_cast<const float4*>(g)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red) {
+    const int t = threadIdx.x;
+    const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float ss = 0.f;
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+    if (t < 256) reinterpret_cast<float4*>(xs)[t] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+    ss = wave_sum_dpp(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPT / 64; ++i) tot += red[i];
+    return 1.0f / sqrtf(tot / (float)D + eps);
+  }
+};
+
+// A workgroup with nothing to produce before a wait (phase D outside the o_proj
+// workgroups, phase A outside the down workgroups) sleeps through about three
+// quarters of its previous layer's wait before polling: the layers take the same
+// time, and hundreds of idle workgroups polling the same words from the start
+// slow the exchange for everyone.  `prev` is that wait in wall-clock ticks
+// (0: poll at once), capped.
+__device__ __forceinline__ uint64_t idle_wait(uint64_t t0, uint64_t prev) {
+  const uint64_t target = min(prev, (uint64_t)4000) * 3 / 4;
+  while (wall_clock64() - t0 < target) __builtin_amdgcn_s_sleep(10);
+  return t0;
+}
+
+// float -> unsigned with the same order (NaN lowest), for an argmax key
+__device__ __forceinline__ uint32_t ord_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return f != f ? 0u : (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
 template <bool SF16>
 __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
-  __shared__ __align__(16) float xin[1024];   // a phase's input vector, raw
+  __shared__ __align__(16) float xin[1024];   // x of the layer (raw), for A's norm and C's residual
   __shared__ __align__(16) float xmid[1024];  // x after o_proj (phase D keeps it for E)
   __shared__ __align__(16) float xs[5120];    // staged (normed, zero-padded) vector of the dot products
-  __shared__ __align__(16) float big[18432];  // phase B: K^T, V, q, p; phase C: partials
+  __shared__ __align__(16) float big[8192];   // phase B: q, k, v, per-wave partials; C: partials
   __shared__ float red[16];
-  __shared__ float hb_val[8], hb_w[8];
+  __shared__ float hb_val[8];
   __shared__ int hb_i[8];
+  __shared__ uint64_t hb_key[8];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps per-wave indices scalar
   const int G = gridDim.x, w = blockIdx.x;
@@ -1180,161 +1280,198 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   const int GQ = H / Hk;            // query heads per kv head
   const uint32_t base = a.epoch_base;
   const int64_t pos = *a.pos;
-  const int nact = (int)((pos + kPKeys) / kPKeys);  // attention items per kv head in use
+  const int nact = (int)((pos + kPKeys) / kPKeys);  // attention chunks in use
   const int half = dh / 2;
-  // zero the staging tails once: the dot products read xs up to 64 chunks per row
+  const int rowsC = (D + kPOproj - 1) / kPOproj, rowsE = (D + kPDown - 1) / kPDown;
+  const bool isB = w < H * kPChunks && (w % kPChunks) < nact;
+  const bool isC = w < kPOproj, isE = w < kPDown && w * rowsE < D;  // only workgroups that own rows wait in E
+  // phase A's pair of this wave and its rotary factors (the same in every layer)
+  const int npairs = R / 2;
+  const int pA = w + G * wave;
+  const bool liveA = pA < npairs;
+  const int hdA = (liveA ? pA : 0) / half, jA = (liveA ? pA : 0) % half;
+  const int r0A = hdA * dh + jA, r1A = r0A + half;
+  const float c0 = a.rope_cos[pos * dh + jA], s0 = a.rope_sin[pos * dh + jA];
+  const float c1 = a.rope_cos[pos * dh + jA + half], s1 = a.rope_sin[pos * dh + jA + half];
+  // phase C's rows, phase D's pairs (every workgroup owns at least one: I >= G), phase E's row
+  const int raC = w * rowsC + wave, rbC = w * rowsC + wave + 8;
+  const bool laC = isC && wave < rowsC && raC < D, lbC = isC && wave + 8 < rowsC && rbC < D;
+  const int jbeg = (int)((int64_t)w * I / G), perD = (int)((int64_t)(w + 1) * I / G) - jbeg;
+  const int rE = w * rowsE + wave;
+  const bool liveE = isE && wave < rowsE && rE < D;
+
+  // Weight loads: each phase issues its own just before its wait, so they arrive
+  // while it polls.  (Loads complete in issue order, so a poll also waits for
+  // every load issued before it; issuing the next phase's weights any earlier
+  // holds up this phase's wait or its compute.)
+  RowDot<64, 1, SF16, false> dA0, dA1, dC0, dC1, dg[3], du[3];
+  RowDot<64, 5, SF16, false> dd;
+  NormStage ns1, ns2;
+  float bA0, bA1;
+  auto load_A = [&](int l) {
+    dA0.load(a.qkv, (int64_t)l * R + r0A, lane, liveA);
+    dA1.load(a.qkv, (int64_t)l * R + r1A, lane, liveA);
+    bA0 = a.qkv_bias[(int64_t)l * R + r0A];
+    bA1 = a.qkv_bias[(int64_t)l * R + r1A];
+    ns1.prefetch(a.ln1 + (int64_t)l * D, D);
+  };
+  auto load_C = [&](int l) {
+    dC0.load(a.o, (int64_t)l * D + (laC ? raC : 0), lane, laC);
+    dC1.load(a.o, (int64_t)l * D + (lbC ? rbC : 0), lane, lbC);
+  };
+  auto load_D = [&](int l) {
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      const bool live = wave + 8 * t < perD;
+      const int64_t jr = live ? jbeg + wave + 8 * t : jbeg;
+      dg[t].load(a.gu, (int64_t)l * 2 * I + jr, lane, live);
+      du[t].load(a.gu, (int64_t)l * 2 * I + I + jr, lane, live);
+    }
+    ns2.prefetch(a.ln2 + (int64_t)l * D, D);
+  };
+  auto load_E = [&](int l) { dd.load(a.dn, (int64_t)l * D + (liveE ? rE : 0), lane, liveE); };
+
+  // the dot products read xs up to 64 chunks per row: the tail past 1024 stays zero
   for (int i = tid; i < 5120; i += kPT) xs[i] = 0.f;
+  load_A(0);
   __syncthreads();
+  uint64_t waitA = 0, waitD = 0;  // the idle workgroups' previous waits (wall-clock ticks)
 
   for (int l = 0; l < a.layers; ++l) {
     const int par = l & 1;
     const uint32_t E = base + (uint32_t)l * 8u;
     // ---- A: [q; k; v] pairs (rows head*dh + j and + half) ----
     {
-      const int npairs = R / 2;
-      const int p = w + G * wave;  // one pair per wave
-      const bool live = p < npairs;
-      const int hd = (live ? p : 0) / half, j = (live ? p : 0) % half;
-      const int r0 = hd * dh + j, r1 = r0 + half;
-      RowDot<64, 1, SF16, false> d0, d1;
-      d0.load(a.qkv, (int64_t)l * R + r0, lane, live);
-      d1.load(a.qkv, (int64_t)l * R + r1, lane, live);
-      const float c0 = a.rope_cos[pos * dh + j], s0 = a.rope_sin[pos * dh + j];
-      const float c1 = a.rope_cos[pos * dh + j + half], s1 = a.rope_sin[pos * dh + j + half];
-      const float b0 = a.qkv_bias[(int64_t)l * R + r0], b1 = a.qkv_bias[(int64_t)l * R + r1];
-      if (l == 0) {
+      if (l == 0) {  // its weights went out before the loop
         for (int i = tid; i < D; i += kPT) xin[i] = a.x[i];
         __syncthreads();
-      } else if (!ll_get(a.xb + (par ^ 1) * D, D, E - 8u + 4u, xin, a.err)) {
-        return;
+      } else {
+        load_A(l);
+        const uint64_t t0 = isE ? 0 : idle_wait(wall_clock64(), waitA);
+        if (!ll_get<2>(a.xb + ((par ^ 1) * kRX + w % kRX) * a.sx, D, E - 8u + 4u, xin, a.err)) return;
+        if (!isE) waitA = wall_clock64() - t0;
       }
-      VecStage<1> vs;
-      vs.load(xin, D, a.ln1 + (int64_t)l * D);
-      const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
-      float v0 = d0.dot(xs, lane) * inv + b0;
-      float v1 = d1.dot(xs, lane) * inv + b1;
-      if (live && lane == 0) {
-        if (hd < H + Hk) {  // rotary on q and k: x cos + rotate_half(x) sin
+      const float inv = ns1.stage(xin, D, a.eps, xs, red);
+      XSlice xv;
+      xv.load(xs, lane);
+      float v0 = wdot(dA0, xv) * inv + bA0;
+      float v1 = wdot(dA1, xv) * inv + bA1;
+      if (liveA && lane == 0) {
+        if (hdA < H + Hk) {  // rotary on q and k: x cos + rotate_half(x) sin
           const float o0 = v0 * c0 + (-v1) * s0, o1 = v1 * c1 + v0 * s1;
           v0 = o0;
           v1 = o1;
         }
-        ll_put(a.qkvb + par * R + r0, v0, E);
-        ll_put(a.qkvb + par * R + r1, v1, E);
-        if (hd >= H) {  // k or v head: the cache row at pos
-          const int kvh = hd - H;
+        ll_put(a.qkvb + par * R + r0A, v0, E);
+        ll_put(a.qkvb + par * R + r1A, v1, E);
+        if (hdA >= H) {  // k or v head: the cache row at pos
+          const int kvh = hdA - H;
           float* cache = kvh < Hk ? a.k_cache : a.v_cache;
           const int gh = kvh < Hk ? kvh : kvh - Hk;
           float* row = cache + (((int64_t)l * Hk + gh) * a.cap + pos) * dh;
-          row[j] = v0;
-          row[j + half] = v1;
+          row[jA] = v0;
+          row[jA + half] = v1;
         }
       }
       __syncthreads();  // xs is reused below
     }
-    // ---- B: attention items (kv head g, 128-key chunk c) ----
-    if (w < Hk * kPChunks && (w % kPChunks) < nact) {
-      const int g = w / kPChunks, c = w % kPChunks;
+    // ---- B: attention item (query head h, 128-key chunk c) ----
+    if (isB) {
+      const int h = w / kPChunks, c = w % kPChunks, g = h / GQ;
       const int64_t k0 = (int64_t)c * kPKeys;
-      const int nk = (int)min((int64_t)kPKeys, pos + 1 - k0);  // keys in this chunk (the last may be pos)
-      float* Kt = big;                      // [dh][kPKeys + 1]
-      float* Vs = big + 64 * (kPKeys + 1);  // [kPKeys][dh]
-      float* qs = Vs + kPKeys * 64;         // [GQ][dh]
-      float* ps = qs + 8 * 64;              // [GQ][kPKeys]
       const float* kb = a.k_cache + ((int64_t)l * Hk + g) * a.cap * dh;
       const float* vb = a.v_cache + ((int64_t)l * Hk + g) * a.cap * dh;
-      // cache rows before pos (written by earlier launches): 128 keys x 16 float4 = 4 per thread
-      float4 kr[4], vr[4];
+      const int64_t last = pos > 0 ? pos - 1 : 0;  // rows before pos come from earlier launches
+      // scores: wave `wave` has keys k0 + 16 wave + lane / 4, a quarter (16 dims) per lane
+      const int64_t key = k0 + 16 * wave + (lane >> 2);
+      const int qd = (lane & 3) * 16;
+      float4 kr[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int idx = tid + kPT * r, key = idx >> 4, d4 = idx & 15;
-        const int64_t row = min(k0 + key, pos > 0 ? pos - 1 : 0);
-        kr[r] = reinterpret_cast<const float4*>(kb + row * dh)[d4];
-        vr[r] = reinterpret_cast<const float4*>(vb + row * dh)[d4];
-      }
-      // q of the group's heads and the new k, v row
-      float* qkvl = xs;  // scratch: q [GQ*dh], then k [dh], v [dh]
-      if (!ll_get(a.qkvb + par * R + g * GQ * dh, GQ * dh, E, qkvl, a.err)) return;
-      if (!ll_get(a.qkvb + par * R + (H + g) * dh, dh, E, qkvl + GQ * dh, a.err)) return;
-      if (!ll_get(a.qkvb + par * R + (H + Hk + g) * dh, dh, E, qkvl + GQ * dh + dh, a.err)) return;
+      for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(kb + min(key, last) * dh + qd)[i];
+      // values: the wave's 16 keys, dim = lane
+      float vr[16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int idx = tid + kPT * r, key = idx >> 4, d = (idx & 15) * 4;
-        float4 kk = kr[r], vv = vr[r];
-        if (k0 + key == pos) {  // the new row comes from this launch's exchange
-          kk = make_float4(qkvl[GQ * dh + d], qkvl[GQ * dh + d + 1], qkvl[GQ * dh + d + 2], qkvl[GQ * dh + d + 3]);
-          vv = make_float4(qkvl[GQ * dh + dh + d], qkvl[GQ * dh + dh + d + 1], qkvl[GQ * dh + dh + d + 2],
-                           qkvl[GQ * dh + dh + d + 3]);
-        }
-        if (key >= nk) kk = vv = make_float4(0.f, 0.f, 0.f, 0.f);
-        Kt[(d + 0) * (kPKeys + 1) + key] = kk.x;
-        Kt[(d + 1) * (kPKeys + 1) + key] = kk.y;
-        Kt[(d + 2) * (kPKeys + 1) + key] = kk.z;
-        Kt[(d + 3) * (kPKeys + 1) + key] = kk.w;
-        reinterpret_cast<float4*>(Vs + key * 64)[d / 4] = vv;
+      for (int t = 0; t < 16; ++t) vr[t] = vb[min(k0 + 16 * wave + t, last) * dh + lane];
+      float* qkv = big;  // q [dh], k [dh], v [dh] of this layer
+      if (!ll_get<1>(a.qkvb + par * R + h * dh, dh, a.qkvb + par * R + (H + g) * dh, dh,
+                     a.qkvb + par * R + (H + Hk + g) * dh, dh, E, qkv, a.err))
+        return;
+      if (key == pos) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(qkv + dh + qd)[i];
       }
-      for (int i = tid; i < GQ * dh; i += kPT) qs[i] = qkvl[i] * a.scale;  // (q * scale) first (ops.py:292)
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 q4 = reinterpret_cast<const float4*>(qkv + qd)[i];
+        // (q * scale) first (ops.py:292)
+        s = fmaf(q4.x * a.scale, kr[i].x, s);
+        s = fmaf(q4.y * a.scale, kr[i].y, s);
+        s = fmaf(q4.z * a.scale, kr[i].z, s);
+        s = fmaf(q4.w * a.scale, kr[i].w, s);
+      }
+      s += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(s)));
+      s += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(s)));
+      s = key <= pos ? s : -INFINITY;
+      const float mw = wave_max_dpp(s);  // the wave's 16 keys
+      const float p = mw == -INFINITY ? 0.f : expf(s - mw);
+      const float lw = wave_sum_dpp((lane & 3) == 0 ? p : 0.f);
+      float o = 0.f;  // dim = lane
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int64_t kt = k0 + 16 * wave + t;
+        const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 4 * t));
+        const float vt = kt == pos ? qkv[2 * dh + lane] : vr[t];
+        o = kt <= pos ? fmaf(pt, vt, o) : o;
+      }
+      float* ow = big + 4 * dh;  // [8 waves][dh], then m, l per wave
+      ow[wave * dh + lane] = o;
+      if (lane == 0) {
+        ow[8 * dh + wave] = mw;
+        ow[8 * dh + 8 + wave] = lw;
+      }
       __syncthreads();
-      if (wave < GQ) {
-        const int h = wave;
-        float sv[2];
+      if (wave == 0) {
+        float M = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int key = lane + 64 * u;
-          float t = 0.f;
-#pragma unroll 16
-          for (int d = 0; d < 64; ++d) t = fmaf(qs[h * 64 + d], Kt[d * (kPKeys + 1) + key], t);
-          sv[u] = key < nk ? t : -INFINITY;
+        for (int i = 0; i < 8; ++i) M = fmaxf(M, ow[8 * dh + i]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float mi = ow[8 * dh + i];
+          const float f = mi == -INFINITY ? 0.f : expf(mi - M);
+          L = fmaf(ow[8 * dh + 8 + i], f, L);
+          O = fmaf(ow[i * dh + lane], f, O);
         }
-        float m = fmaxf(sv[0], sv[1]);
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        const float p0 = expf(sv[0] - m), p1 = expf(sv[1] - m);
-        float lsum = p0 + p1;
-        for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
-        ps[h * kPKeys + lane] = p0;
-        ps[h * kPKeys + lane + 64] = p1;
-        wave_sync();  // the wave reads back every lane's p
-        float ov = 0.f;  // dim = lane
-#pragma unroll 16
-        for (int key = 0; key < kPKeys; ++key) ov = fmaf(ps[h * kPKeys + key], Vs[key * 64 + lane], ov);
-        uint64_t* out = a.pb + (size_t)par * kPChunks * H * kPPart + ((size_t)c * H + g * GQ + h) * kPPart;
-        if (lane == 0) {
-          ll_put(out, m, E + 1u);
-          ll_put(out + 1, lsum, E + 1u);
+#pragma unroll
+        for (int rr = 0; rr < kRP; ++rr) {
+          uint64_t* out = a.pb + (par * kRP + rr) * a.sp + ((int64_t)c * H + h) * kPPart;
+          if (lane == 0) {
+            ll_put(out, M, E + 1u);
+            ll_put(out + 1, L, E + 1u);
+          }
+          ll_put(out + 2 + lane, O, E + 1u);
         }
-        ll_put(out + 2 + lane, ov, E + 1u);
       }
-      __syncthreads();  // big and xs are reused below
+      __syncthreads();  // big is reused below
     }
     // ---- C: merge + o_proj rows + residual -> x_mid ----
-    if (w < kPOproj) {
-      const int rows = (D + kPOproj - 1) / kPOproj, rbeg = w * rows;
-      RowDot<64, 1, SF16, false> d0, d1;
-      const int ra = rbeg + wave, rb = rbeg + wave + 8;
-      const bool la = wave < rows && ra < D, lb = wave + 8 < rows && rb < D;
-      d0.load(a.o, (int64_t)l * D + (la ? ra : 0), lane, la);
-      d1.load(a.o, (int64_t)l * D + (lb ? rb : 0), lane, lb);
+    if (isC) {
+      load_C(l);
       float* part = big;  // [nact][H][66]
-      if (!ll_get(a.pb + (size_t)par * kPChunks * H * kPPart, nact * H * kPPart, E + 1u, part, a.err)) return;
-      float* xr = xmid;   // x_in of this WG's rows
-      if (l == 0) {
-        for (int i = tid; i < rows && rbeg + i < D; i += kPT) xr[i] = a.x[rbeg + i];
-        __syncthreads();
-      } else if (!ll_get(a.xb + (par ^ 1) * D + rbeg, min(rows, D - rbeg), E - 8u + 4u, xr, a.err)) {
-        return;
-      }
+      if (!ll_get<16>(a.pb + (par * kRP + w % kRP) * a.sp, nact * H * kPPart, E + 1u, part, a.err)) return;
       // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den
       for (int i = tid; i < 1024; i += kPT) {
         if (i >= H * dh) {  // the o_proj dot reads the staged vector up to 1024
           xs[i] = 0.f;
           continue;
         }
-        const int h = i / dh, d = i % dh;
+        const int hh = i / dh, d = i % dh;
         float M = -INFINITY;
-        for (int c = 0; c < nact; ++c) M = fmaxf(M, part[(c * H + h) * kPPart]);
+        for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, part[(cc * H + hh) * kPPart]);
         float num = 0.f, den = 0.f;
-        for (int c = 0; c < nact; ++c) {
-          const float* pc = part + (c * H + h) * kPPart;
+        for (int cc = 0; cc < nact; ++cc) {
+          const float* pc = part + (cc * H + hh) * kPPart;
           const float wgt = expf(pc[0] - M);
           den = fmaf(pc[1], wgt, den);
           num = fmaf(pc[2 + d], wgt, num);
@@ -1342,50 +1479,41 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         xs[i] = num / den;
       }
       __syncthreads();
-      const float va = d0.dot(xs, lane), vb2 = d1.dot(xs, lane);
-      if (lane == 0) {
-        if (la) ll_put(a.mb + par * D + ra, xr[wave] + va, E + 2u);
-        if (lb) ll_put(a.mb + par * D + rb, xr[wave + 8] + vb2, E + 2u);
+      XSlice xv;
+      xv.load(xs, lane);
+      const float va = wdot(dC0, xv), vb2 = wdot(dC1, xv);
+      if (lane < kRM) {  // lane i writes replica i
+        if (laC) ll_put(a.mb + (par * kRM + lane) * a.sm + raC, xin[raC] + va, E + 2u);
+        if (lbC) ll_put(a.mb + (par * kRM + lane) * a.sm + rbC, xin[rbC] + vb2, E + 2u);
       }
       __syncthreads();
     }
     // ---- D: [gate; up] pairs -> h ----
     {
-      // balanced split: every workgroup owns at least one pair (I >= G), so phase E's
-      // wait for all of h is also a wait for every workgroup to be done with layer l
-      const int jbeg = (int)((int64_t)w * I / G), per = (int)((int64_t)(w + 1) * I / G) - jbeg;
-      RowDot<64, 1, SF16, false> dg[3], du[3];
-      int jj[3];
+      load_D(l);
+      const uint64_t t0 = isC ? 0 : idle_wait(wall_clock64(), waitD);
+      if (!ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)) return;
+      if (!isC) waitD = wall_clock64() - t0;
+      const float inv = ns2.stage(xmid, D, a.eps, xs, red);
+      XSlice xv;
+      xv.load(xs, lane);
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        jj[t] = jbeg + wave + 8 * t;
-        const bool live = wave + 8 * t < per && jj[t] < I;
-        const int64_t jr = live ? jj[t] : jbeg;
-        dg[t].load(a.gu, (int64_t)l * 2 * I + min(jr, (int64_t)I - 1), lane, live);
-        du[t].load(a.gu, (int64_t)l * 2 * I + I + min(jr, (int64_t)I - 1), lane, live);
-      }
-      if (!ll_get(a.mb + par * D, D, E + 2u, xmid, a.err)) return;
-      VecStage<1> vs;
-      vs.load(xmid, D, a.ln2 + (int64_t)l * D);
-      const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
-#pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        const float gv = dg[t].dot(xs, lane) * inv, uv = du[t].dot(xs, lane) * inv;
-        if (lane == 0 && wave + 8 * t < per && jj[t] < I)
-          ll_put(a.hb + (size_t)par * I + jj[t], (gv / (1.0f + expf(-gv))) * uv, E + 3u);
+        if (wave + 8 * t < perD) {  // uniform per wave
+          const float gv = wdot(dg[t], xv) * inv, uv = wdot(du[t], xv) * inv;
+          if (lane < kRH)
+            ll_put(a.hb + (par * kRH + lane) * a.sh + jbeg + wave + 8 * t, (gv / (1.0f + expf(-gv))) * uv, E + 3u);
+        }
       }
       __syncthreads();  // xs is restaged below
     }
     // ---- E: down rows + residual -> x of the next layer ----
-    if (w < kPDown && w * ((D + kPDown - 1) / kPDown) < D) {  // only workgroups that own rows wait
-      const int rows = (D + kPDown - 1) / kPDown, r = w * rows + wave;
-      const bool live = wave < rows && r < D;
-      RowDot<64, 5, SF16, false> dd;
-      dd.load(a.dn, (int64_t)l * D + (live ? r : 0), lane, live);
+    if (isE) {
+      load_E(l);
       for (int i = I + tid; i < 1024; i += kPT) xs[i] = 0.f;  // the staged tail past I must be zero
-      if (!ll_get(a.hb + (size_t)par * I, I, E + 3u, xs, a.err)) return;  // xs[I..5120) stays zero
-      const float v = dd.dot(xs, lane);
-      if (live && lane == 0) ll_put(a.xb + par * D + r, xmid[r] + v, E + 4u);
+      if (!ll_get<10>(a.hb + (par * kRH + w % kRH) * a.sh, I, E + 3u, xs, a.err)) return;
+      const float v = wdot(dd, xs, lane);
+      if (liveE && lane < kRX) ll_put(a.xb + (par * kRX + lane) * a.sx + rE, xmid[rE] + v, E + 4u);
       __syncthreads();
     }
   }
@@ -1394,28 +1522,36 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   {
     const int V = (int)a.head.rows, per = (V + G - 1) / G, rbeg = w * per;
     RowDot<64, 1, SF16, false> dh4[4];
-    int rr[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      rr[t] = rbeg + wave + 8 * t;
-      const bool live = wave + 8 * t < per && rr[t] < V;
-      dh4[t].load(a.head, live ? rr[t] : 0, lane, live);
+      const int rr = rbeg + wave + 8 * t;
+      const bool live = wave + 8 * t < per && rr < V;
+      dh4[t].load(a.head, live ? rr : 0, lane, live);
+    }
+    NormStage ns;
+    ns.prefetch(a.norm, D);
+    float hbias[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rr = rbeg + wave + 8 * t;
+      hbias[t] = a.head_bias && rr < V ? a.head_bias[rr] : 0.f;
     }
     const int lp = (a.layers - 1) & 1;
-    if (!ll_get(a.xb + lp * D, D, EH - 8u + 4u, xin, a.err)) return;
-    VecStage<1> vs;
-    vs.load(xin, D, a.norm);
-    const float inv = vs.finish_folded(D, 1024, true, a.eps, xs, red);
+    if (!ll_get<2>(a.xb + (lp * kRX + w % kRX) * a.sx, D, EH - 8u + 4u, xin, a.err)) return;
+    const float inv = ns.stage(xin, D, a.eps, xs, red);
+    XSlice xv;
+    xv.load(xs, lane);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float v = dh4[t].dot(xs, lane) * inv + (a.head_bias && rr[t] < V ? a.head_bias[min(rr[t], V - 1)] : 0.f);
-      if (wave + 8 * t < per && rr[t] < V) {
-        if (lane == 0) a.logits[rr[t]] = v;
+      const int rr = rbeg + wave + 8 * t;
+      if (wave + 8 * t < per && rr < V) {  // uniform per wave
+        const float v = wdot(dh4[t], xv) * inv + hbias[t];
+        if (lane == 0) a.logits[rr] = v;
         if (v > best) {  // rows ascend within the wave
           best = v;
-          bidx = rr[t];
+          bidx = rr;
         }
       }
     }
@@ -1438,23 +1574,19 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     }
     if (w != 0) return;
     float* cand = big;
-    if (!ll_get(a.arg, 2 * G, EH, cand, a.err)) return;
-    if (tid == 0) {
-      float b = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int k = 0; k < G; ++k) {
-        const float v = cand[2 * k];
-        const int i = __float_as_int(cand[2 * k + 1]);
-        if (v > b || (v == b && i < bi)) {
-          b = v;
-          bi = i;
-        }
-      }
-      if (bi < 0 || bi >= V) bi = 0;  // all-NaN logits: keep a valid row
-      hb_i[0] = bi;
-    }
+    if (!ll_get<1>(a.arg, 2 * G, EH, cand, a.err)) return;
+    // argmax over the workgroups' candidates: larger value, then the lower row
+    uint64_t k = 0;
+    if (tid < G) k = ((uint64_t)ord_bits(cand[2 * tid]) << 32) | (0xffffffffu - (uint32_t)__float_as_int(cand[2 * tid + 1]));
+    k = wave_max_u64(k);
+    if (lane == 0) hb_key[wave] = k;
     __syncthreads();
-    const int64_t id = hb_i[0];
+    uint64_t kb = hb_key[0];
+#pragma unroll
+    for (int i = 1; i < kPT / 64; ++i) kb = max(kb, hb_key[i]);
+    int bi = (int)(0xffffffffu - (uint32_t)kb);
+    if (bi < 0 || bi >= V) bi = 0;  // all-NaN logits: keep a valid row
+    const int64_t id = bi;
     for (int64_t cc = tid; cc < a.emb.k; cc += kPT)
       a.x[cc] = (float)a.emb.q[id * a.emb.kp + cc] * sc_at(a.emb, id, cc);
     if (tid == 0) {
@@ -1650,9 +1782,14 @@ int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_stat
   return decode_step(m, s, smp, stream);
 }
 
+// Words between replicas of an n-word vector: whole 4 KiB pages plus 512 bytes,
+// so the copies start in different channels.
+static int64_t replica_stride(int64_t n) { return (n + 511) / 512 * 512 + 64; }
+
 static int64_t persist_words(const cv3_qwen2_model* m, int workgroups) {
   const int64_t D = m->hidden, R = (m->heads + 2 * m->kv_heads) * m->head_dim;
-  return 2 * D + 2 * R + 2 * (int64_t)kPChunks * m->heads * kPPart + 2 * D + 2 * m->inter + 2 * (int64_t)workgroups;
+  return 2 * kRX * replica_stride(D) + 2 * R + 2 * kRP * replica_stride((int64_t)kPChunks * m->heads * kPPart) +
+         2 * kRM * replica_stride(D) + 2 * kRH * replica_stride(m->inter) + 2 * (int64_t)workgroups;
 }
 
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words) {
@@ -1700,7 +1837,7 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
               "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G, kPDown, per_cu * cus,
               (long long)I);
   CV3_REQUIRE((H + 2 * Hk) * dh / 2 <= 8LL * G && I <= 24LL * G && m->head.rows <= 32LL * G &&
-                  Hk * kPChunks <= G,
+                  H * kPChunks <= G && H * kPChunks * kPPart <= 8192,
               CV3_EUNSUPPORTED, "persistent step: too few workgroups for the geometry");
   CV3_REQUIRE(p->words && p->err && p->words_len >= persist_words(m, G), CV3_EINVAL,
               "persistent step: exchange words missing or too few");
@@ -1737,17 +1874,29 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   a.logits = s->logits;
   const int64_t R = (H + 2 * Hk) * dh;
   uint64_t* wds = p->words;
+  a.sx = replica_stride(D);
+  a.sp = replica_stride((int64_t)kPChunks * H * kPPart);
+  a.sm = replica_stride(D);
+  a.sh = replica_stride(I);
   a.xb = wds;
-  a.qkvb = a.xb + 2 * D;
+  a.qkvb = a.xb + 2 * kRX * a.sx;
   a.pb = a.qkvb + 2 * R;
-  a.mb = a.pb + 2 * (int64_t)kPChunks * H * kPPart;
-  a.hb = a.mb + 2 * D;
-  a.arg = a.hb + 2 * I;
+  a.mb = a.pb + 2 * kRP * a.sp;
+  a.hb = a.mb + 2 * kRM * a.sm;
+  a.arg = a.hb + 2 * kRH * a.sh;
   a.err = p->err;
   a.epoch_base = p->epoch_base;
   a.select = select ? 1 : 0;
-  void* args[] = {&a};
-  CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));
+  if (p->cooperative) {
+    void* args[] = {&a};
+    CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));
+  } else {
+    if (sf16)
+      hipLaunchKernelGGL(k_dec_persist<true>, dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    else
+      hipLaunchKernelGGL(k_dec_persist<false>, dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    CV3_LAUNCHED();
+  }
   return CV3_OK;
 }
 

@@ -46,7 +46,7 @@ class Model(ctypes.Structure):
 
 class Persist(ctypes.Structure):
     _fields_ = [("words", c_vp), ("words_len", c_i64), ("err", c_vp), ("epoch_base", ctypes.c_uint32),
-                ("workgroups", ctypes.c_int)]
+                ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int)]
 
 
 class Sampler(ctypes.Structure):
@@ -190,6 +190,9 @@ class DeviceQwen2:
         self.ctl = DeviceArray((6,), np.int64).zero_()
         self._sampled_graphs = {}
         self._persist: Optional[Persist] = None   # exchange words of the one-launch step, made on first use
+        # the one-launch step's launch: ordinary (the device runs nothing else meanwhile) or
+        # hipLaunchCooperativeKernel, which guarantees co-residency at ~20 us more per token
+        self.cooperative = False
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
@@ -302,11 +305,16 @@ class DeviceQwen2:
                   ctypes.byref(smp) if smp is not None else None, None)
         self._pos_host += 1
 
-    def step_sampled(self, smp: "Sampler", graph: bool = False):
-        """Enqueue one sampled token (no host synchronisation)."""
+    def step_sampled(self, smp: "Sampler", graph: bool = False, persistent: bool = False):
+        """Enqueue one sampled token (no host synchronisation); ``persistent`` runs the
+        body and head as one cooperative launch (cv3_qwen2_decode_step_persistent), then
+        the draw (cv3_qwen2_select)."""
         if self._pos_host + 1 >= self.cap:
             raise ValueError("the KV cache is full")
-        if graph:
+        if persistent:
+            self.step_persistent(select=False)
+            _lib.call("qwen2_select", ctypes.byref(self.model), ctypes.byref(self.state), ctypes.byref(smp), None)
+        elif graph:
             key = tuple(getattr(smp, f) for f, _ in Sampler._fields_)
             g = self._sampled_graphs.get(key)
             if g is None:
@@ -322,14 +330,16 @@ class DeviceQwen2:
         self._pos_host += 1
 
     def generate_sampled_after_prefill(self, max_len: int, min_len: int, sampling, speech_token_size: int,
-                                       graph: bool = True, check_every: int = 16) -> List[int]:
+                                       graph: bool = True, check_every: int = 16,
+                                       persistent: bool = False) -> List[int]:
         """generate()'s loop after ``prefill``: the first token is drawn from the prompt's
         logits (llm.py:112-121 at i = 0), the rest by decode steps."""
         return self.generate_sampled(None, self._pos_host, max_len, min_len, sampling, speech_token_size, graph,
-                                     check_every)
+                                     check_every, persistent)
 
     def generate_sampled(self, first_token: Optional[int], pos: int, max_len: int, min_len: int, sampling,
-                         speech_token_size: int, graph: bool = True, check_every: int = 16) -> List[int]:
+                         speech_token_size: int, graph: bool = True, check_every: int = 16,
+                         persistent: bool = False) -> List[int]:
         """The token loop of CosyVoice3LM.generate (llm.py:104-123) with its sampler
         (llm.py:125-149) on the device: up to max_len tokens from input
         speech_embedding[first_token] at position pos, ending before the first stop id.
@@ -338,7 +348,8 @@ class DeviceQwen2:
         reference's draws would and hands back.  The host looks for a stop every
         ``check_every`` tokens; steps after a stop change nothing.  ``first_token``
         None draws the first token from the logits already present (after ``prefill``,
-        whose last position is ``pos``)."""
+        whose last position is ``pos``).  ``persistent`` decodes with the one-launch step
+        (q8 weights) instead of the five-kernel step."""
         bg = sampling.rng.bit_generator
         st = bg.state
         if st.get("bit_generator") != "PCG64":
@@ -362,10 +373,12 @@ class DeviceQwen2:
         while done < max_len:
             n = min(check_every, max_len - done)
             for _ in range(n):
-                self.step_sampled(smp, graph)
+                self.step_sampled(smp, graph, persistent)
             done += n
             if int(self.ctl.numpy()[1]) != 0:
                 break
+        if persistent and self.persistent_error():
+            raise RuntimeError("the one-launch decode step gave up waiting for an exchange")
         c = self.ctl.numpy().view(np.uint64)
         stop = int(c[1])
         count = stop - 1 if stop else max_len
@@ -390,8 +403,9 @@ class DeviceQwen2:
 
     # -- the whole step as one cooperative launch --------------------------
     def step_persistent(self, select: bool = True):
-        """Enqueue one token as a single cooperative launch (cv3_qwen2_decode_step_persistent):
-        greedy selection inside (``select``), or logits only for ``select_sampled``."""
+        """Enqueue one token as a single launch of the whole step (cv3_qwen2_decode_step_persistent,
+        cooperative if ``self.cooperative``): greedy selection inside (``select``), or logits only,
+        for the sampler (``step_sampled(persistent=True)``)."""
         if self._pos_host + 1 >= self.cap:
             raise ValueError("the KV cache is full")
         if self._persist is None:
@@ -399,8 +413,9 @@ class DeviceQwen2:
             _lib.call("qwen2_persist_words", ctypes.byref(self.model), 256, _lib.ptr(n))
             self._pwords = DeviceArray((n.value,), np.int64).zero_()
             self._perr = DeviceArray((1,), np.int64).zero_()
-            self._persist = Persist(self._pwords.ptr, n.value, self._perr.ptr, 0, 0)
+            self._persist = Persist(self._pwords.ptr, n.value, self._perr.ptr, 0, 0, 0)
         p = self._persist
+        p.cooperative = 1 if self.cooperative else 0
         base = (p.epoch_base + 256) & 0xFFFFFFFF
         if base == 0:   # the launch counter wrapped: clear the words so no old epoch can match
             self._pwords.zero_()

@@ -321,18 +321,24 @@ typedef struct {
 /* cv3_qwen2_decode_step with the token drawn by the sampler instead of the argmax (llm.py:112-123). */
 int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
                                   cv3_stream_t stream);
-/* The decode step as ONE cooperative launch (q8 weights, head dim 64, cache <= 1024 positions): one workgroup
- * per CU runs every layer; vectors crossing workgroups travel as (epoch, value) words in `words` (device memory
- * of *words uint64 from cv3_qwen2_persist_words; zeroed at allocation, then whatever earlier launches left),
- * with every wait bounded: a word that never arrives sets *err (device int64, caller clears it) and the launch
- * ends early.  epoch_base must differ between launches (count launches, times 256, never 0).  select 1: the
- * greedy pick and bookkeeping of cv3_qwen2_decode_step; select 0: logits only (then cv3_qwen2_select). */
+/* The decode step of cv3_qwen2_decode_step (Qwen2Model.forward, qwen2.py:139-179; llm_decoder, llm.py:74-77;
+ * the argmax and next input, llm.py:121,138) as ONE kernel launch (q8 weights, head dim 64, cache <= 1024
+ * positions): one workgroup per CU runs every layer; vectors crossing workgroups travel as (epoch, value) words
+ * in `words` (device memory of *words uint64 from cv3_qwen2_persist_words; zeroed at allocation, then whatever
+ * earlier launches left), with every wait bounded: a word that never arrives sets *err (device int64, caller
+ * clears it) and the launch ends early, its results invalid.  epoch_base must differ between launches (count
+ * launches, times 256, never 0; clear `words` when the count wraps).  select 1: the greedy pick and bookkeeping
+ * of cv3_qwen2_decode_step; select 0: logits only (then cv3_qwen2_select).  The workgroups must all be resident
+ * at once: cooperative 1 launches with hipLaunchCooperativeKernel, which guarantees that or fails; cooperative 0
+ * launches ordinarily (about 20 us less per token), for a device with nothing else running: a workgroup that
+ * cannot start shows up as *err, not as a hang.  One such launch at a time per device. */
 typedef struct {
   uint64_t* words;
   int64_t words_len;
   int64_t* err;
   uint32_t epoch_base;
-  int workgroups; /* 0: one per CU, at most 256 */
+  int workgroups;  /* 0: one per CU, at most 256 */
+  int cooperative; /* 1: hipLaunchCooperativeKernel; 0: ordinary launch */
 } cv3_persist;
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words);
 int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,

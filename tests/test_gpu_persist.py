@@ -6,7 +6,8 @@ Bars: per-step logits within 1e-5 (max abs error over max |logit|) of the
 oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
 layers the tokens equal the five-kernel step's and the logits agree within 1e-5.
 Positions cover an empty cache (one attention chunk), a start just below the
-128-key chunk boundary, and 512 cached positions (five chunks).
+128-key chunk boundary, and 512 cached positions (five chunks); ordinary and
+cooperative launches.
 """
 
 import numpy as np
@@ -45,14 +46,15 @@ def _oracle_lm(cpu, k, v, n, steps):
     return lm, cache
 
 
-@pytest.mark.parametrize("profile,n,steps", [("per_channel", 512, 10), ("balanced", 0, 6),
-                                             ("balanced", 122, 10)])
-def test_persistent_step_logits_and_tokens(gpu, profile, n, steps):
+@pytest.mark.parametrize("profile,n,steps,cooperative", [("per_channel", 512, 10, False), ("balanced", 0, 6, False),
+                                                         ("balanced", 122, 10, False), ("per_channel", 300, 6, True)])
+def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative):
     from cv3amd.qwen2 import DeviceQwen2
     cpu, dev, k, v = _setup(2, profile, n)
-    print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps", flush=True)
+    print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps, cooperative={cooperative}", flush=True)
     lm, cache = _oracle_lm(cpu, k, v, n, steps)
     d = DeviceQwen2(dev, cap=1024)
+    d.cooperative = cooperative
     if n:
         d.fill_cache(k, v)
     d.begin(lm.sos, n)
@@ -113,3 +115,59 @@ def test_persistent_step_rejects_q4(gpu):
     d.begin(1, 0)
     with pytest.raises(NotImplementedError):
         d.step_persistent()
+
+
+@pytest.mark.parametrize("strict", [False, True])
+def test_persistent_sampled_generation(gpu, strict):
+    """The one-launch step followed by the device sampler: the oracle's sampled tokens and
+    Generator state (llm.py:104-149), including a stop on a control id (a head bias makes
+    the eos id and another stop id likely; min_len holds back the eos id, or every stop
+    id with strict_min_len)."""
+    import oracle.quant
+    import cv3amd.quant
+    from cv3amd import synth
+    from cv3amd.qwen2 import DeviceQwen2
+    from cv3amd.weights import WeightStore
+    from oracle.llm import Sampling
+    n, max_len, min_len = 512, 48, 6
+    t = synth.quantize_store(synth.qwen2_tensors(layers=2), "per_channel", oracle.quant.quantize_q8)
+    sts = synth.SPEECH_TOKEN_SIZE
+    bias = np.array(t["llm.llm_decoder.bias"], np.float32)
+    bias[sts] += 9.0
+    bias[sts + 5] += 4.0
+    t["llm.llm_decoder.bias"] = bias
+    meta = synth.qwen2_meta(layers=2)
+    cpu, dev = WeightStore(t, meta, oracle.quant.QTensor), WeightStore(t, meta, cv3amd.quant.QTensor)
+    rng = np.random.default_rng(100)
+    k = rng.standard_normal((2, 2, n, 64), dtype=np.float32)
+    v = rng.standard_normal((2, 2, n, 64), dtype=np.float32)
+    lm, cache = _oracle_lm(cpu, k, v, n, max_len)
+    ref = Sampling(seed=77, strict_min_len=strict)
+    want = lm.sampled(lm.speech_emb([lm.sos]), cache, max_len, min_len, ref)
+    print(f"[persist] sampled, strict={strict}: oracle stops after {len(want)} tokens", flush=True)
+    assert (min_len <= len(want) < max_len) if strict else (0 < len(want) < min_len)
+    d = DeviceQwen2(dev, cap=1024)
+    d.fill_cache(k, v)
+    cfg = Sampling(seed=77, strict_min_len=strict)
+    got = d.generate_sampled(lm.sos, n, max_len, min_len, cfg, sts, check_every=5, persistent=True)
+    assert got == want
+    assert cfg.rng.bit_generator.state == ref.rng.bit_generator.state
+
+
+def test_persistent_sampled_long_run_matches_five_kernel_step(gpu):
+    """40 draws with SamplingConfig's defaults over 24 layers: the same tokens and
+    Generator state as the five-kernel sampled step."""
+    from cv3amd.qwen2 import DeviceQwen2
+    from oracle.llm import Sampling
+    n, max_len = 200, 40
+    _, dev, k, v = _setup(24, "balanced", n)
+    out = []
+    for persistent in (False, True):
+        d = DeviceQwen2(dev, cap=1024)
+        d.fill_cache(k, v)
+        cfg = Sampling(seed=5)
+        toks = d.generate_sampled(1, n, max_len, 0, cfg, 6561, persistent=persistent)
+        out.append((toks, cfg.rng.bit_generator.state))
+    print(f"[persist] sampled 24 layers: {out[0][0][:10]}...", flush=True)
+    assert out[0][0] == out[1][0]
+    assert out[0][1] == out[1][1]
