@@ -1193,14 +1193,29 @@ __device__ __forceinline__ bool ll_get(const uint64_t* src, int n, uint32_t e, f
   return ll_get<NW>(src, n, nullptr, 0, nullptr, 0, e, dst, err);
 }
 
+// Wave sum in every lane without lane reads: DPP within each 16-lane row, then the
+// row-pair and half swaps of gfx950 (v_permlane16_swap / v_permlane32_swap).  The
+// additions group as ((row0 + row1) + (row2 + row3)), as in wave_sum_dpp, so the
+// two give the same bits.
+__device__ __forceinline__ float wave_sum_swap(float v) {
+  v += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp32<kDppMirror>(__float_as_uint(v)));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Dot product of one weight row spread over the whole wave (64 lanes x CPL
-// chunks), reduced through DPP: every lane gets the sum.
+// chunks), reduced across the wave: every lane gets the sum.
 template <int CPL, bool SF16>
 __device__ __forceinline__ float wdot(const RowDot<64, CPL, SF16, false>& rd, const float* xs, int lane) {
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) acc = fmaf(dot16(rd.wv[i], xs + (lane + i * 64) * 16), rd.sc[i], acc);
-  return wave_sum_dpp(acc);
+  return wave_sum_swap(acc);
 }
 // The same for K <= 1024 with the lane's 16 staged values already in registers
 // (a wave computing several rows reads its slice of the vector once).
@@ -1213,7 +1228,7 @@ struct XSlice {
 };
 template <bool SF16>
 __device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, false>& rd, const XSlice& x) {
-  return wave_sum_dpp(fmaf(dot16(rd.wv[0], x.v), rd.sc[0], 0.f));
+  return wave_sum_swap(fmaf(dot16(rd.wv[0], x.v), rd.sc[0], 0.f));
 }
 
 // RMSNorm staging with the norm weight loaded ahead (thread t owns float4 t):
@@ -1234,7 +1249,7 @@ struct NormStage {
     ss = fmaf(v.z, v.z, ss);
     ss = fmaf(v.w, v.w, ss);
     if (t < 256) reinterpret_cast<float4*>(xs)[t] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
-    ss = wave_sum_dpp(ss);
+    ss = wave_sum_swap(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
     float tot = 0.f;
@@ -1378,25 +1393,25 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     // ---- B: attention item (query head h, 128-key chunk c) ----
     if (isB) {
       const int h = w / kPChunks, c = w % kPChunks, g = h / GQ;
-      const int64_t k0 = (int64_t)c * kPKeys;
       const float* kb = a.k_cache + ((int64_t)l * Hk + g) * a.cap * dh;
       const float* vb = a.v_cache + ((int64_t)l * Hk + g) * a.cap * dh;
-      const int64_t last = pos > 0 ? pos - 1 : 0;  // rows before pos come from earlier launches
-      // scores: wave `wave` has keys k0 + 16 wave + lane / 4, a quarter (16 dims) per lane
-      const int64_t key = k0 + 16 * wave + (lane >> 2);
+      const int ipos = (int)pos, last = ipos > 0 ? ipos - 1 : 0;  // rows before pos come from earlier launches
+      // scores: wave `wave` has keys kw + lane / 4, a quarter (16 dims) per lane
+      const int kw = c * kPKeys + 16 * wave;
+      const int key = kw + (lane >> 2);
       const int qd = (lane & 3) * 16;
       float4 kr[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(kb + min(key, last) * dh + qd)[i];
-      // values: the wave's 16 keys, dim = lane
+      for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(kb + (int64_t)min(key, last) * dh + qd)[i];
+      // values: the wave's 16 keys, dim = lane (keys past pos read row `last`: finite, and weighted 0)
       float vr[16];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) vr[t] = vb[min(k0 + 16 * wave + t, last) * dh + lane];
+      for (int t = 0; t < 16; ++t) vr[t] = vb[(int64_t)min(kw + t, last) * dh + lane];
       float* qkv = big;  // q [dh], k [dh], v [dh] of this layer
       if (!ll_get<1>(a.qkvb + par * R + h * dh, dh, a.qkvb + par * R + (H + g) * dh, dh,
                      a.qkvb + par * R + (H + Hk + g) * dh, dh, E, qkv, a.err))
         return;
-      if (key == pos) {
+      if (key == ipos) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(qkv + dh + qd)[i];
       }
@@ -1412,17 +1427,17 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       }
       s += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(s)));
       s += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(s)));
-      s = key <= pos ? s : -INFINITY;
+      s = key <= ipos ? s : -INFINITY;
       const float mw = wave_max_dpp(s);  // the wave's 16 keys
-      const float p = mw == -INFINITY ? 0.f : expf(s - mw);
-      const float lw = wave_sum_dpp((lane & 3) == 0 ? p : 0.f);
-      float o = 0.f;  // dim = lane
+      const float p = mw == -INFINITY ? 0.f : expf(s - mw);  // 0 for keys past pos
+      const float lw = wave_sum_swap((lane & 3) == 0 ? p : 0.f);
+      const float vnew = qkv[2 * dh + lane];  // v of this token
+      const int tn = ipos - kw;               // its slot in the wave's keys (may lie outside 0..15)
+      float o = 0.f;                          // dim = lane
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        const int64_t kt = k0 + 16 * wave + t;
         const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 4 * t));
-        const float vt = kt == pos ? qkv[2 * dh + lane] : vr[t];
-        o = kt <= pos ? fmaf(pt, vt, o) : o;
+        o = fmaf(pt, t == tn ? vnew : vr[t], o);
       }
       float* ow = big + 4 * dh;  // [8 waves][dh], then m, l per wave
       ow[wave * dh + lane] = o;
@@ -1460,23 +1475,26 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       load_C(l);
       float* part = big;  // [nact][H][66]
       if (!ll_get<16>(a.pb + (par * kRP + w % kRP) * a.sp, nact * H * kPPart, E + 1u, part, a.err)) return;
-      // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den
-      for (int i = tid; i < 1024; i += kPT) {
-        if (i >= H * dh) {  // the o_proj dot reads the staged vector up to 1024
-          xs[i] = 0.f;
-          continue;
-        }
-        const int hh = i / dh, d = i % dh;
+      // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den;
+      // the chunk weights e^{m_c - M} / den, one thread per (chunk, head) = part index,
+      // into xmid (free until D)
+      if (tid < nact * H) {
+        const int hh = tid % H;
         float M = -INFINITY;
         for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, part[(cc * H + hh) * kPPart]);
-        float num = 0.f, den = 0.f;
-        for (int cc = 0; cc < nact; ++cc) {
-          const float* pc = part + (cc * H + hh) * kPPart;
-          const float wgt = expf(pc[0] - M);
-          den = fmaf(pc[1], wgt, den);
-          num = fmaf(pc[2 + d], wgt, num);
+        float den = 0.f;
+        for (int cc = 0; cc < nact; ++cc)
+          den = fmaf(part[(cc * H + hh) * kPPart + 1], expf(part[(cc * H + hh) * kPPart] - M), den);
+        xmid[tid] = expf(part[tid * kPPart] - M) / den;
+      }
+      __syncthreads();
+      for (int i = tid; i < 1024; i += kPT) {
+        float att = 0.f;  // the o_proj dot reads the staged vector up to 1024: zero past H dh
+        if (i < H * dh) {
+          const int hh = i / dh, d = i % dh;
+          for (int cc = 0; cc < nact; ++cc) att = fmaf(part[(cc * H + hh) * kPPart + 2 + d], xmid[cc * H + hh], att);
         }
-        xs[i] = num / den;
+        xs[i] = att;
       }
       __syncthreads();
       XSlice xv;
