@@ -232,6 +232,12 @@ int cv3_event_record(void* ev, cv3_stream_t s) {
   return CV3_OK;
 }
 
+int cv3_stream_wait_event(cv3_stream_t s, void* ev) {
+  CV3_REQUIRE(ev, CV3_EINVAL, "null event");
+  CV3_HIP(hipStreamWaitEvent(stream_of(s), reinterpret_cast<hipEvent_t>(ev), 0));
+  return CV3_OK;
+}
+
 int cv3_event_elapsed_ms(void* ev0, void* ev1, float* ms) {
   CV3_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev1)));
   CV3_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(ev0), reinterpret_cast<hipEvent_t>(ev1)));

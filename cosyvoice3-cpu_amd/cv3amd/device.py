@@ -183,6 +183,53 @@ class Timer:
             pass
 
 
+class Stream:
+    """A non-blocking stream of default priority (work on it runs beside the thread's own)."""
+
+    def __init__(self):
+        _lib.init()
+        h = ctypes.c_void_p()
+        _lib.call("stream_create", ctypes.addressof(h))
+        self.handle = h.value
+
+    def wait(self, event: "Event"):
+        """Later work on this stream waits for the event's last recorded point."""
+        _lib.call("stream_wait_event", self.handle, event.handle)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                _lib.lib().cv3_stream_destroy(ctypes.c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+class Event:
+    """A HIP event, recorded on a stream (None: the calling thread's)."""
+
+    def __init__(self):
+        _lib.init()
+        h = ctypes.c_void_p()
+        _lib.call("event_create", ctypes.addressof(h))
+        self.handle = h.value
+
+    def record(self, stream: "Optional[Stream]" = None) -> "Event":
+        _lib.call("event_record", self.handle, stream.handle if stream is not None else None)
+        return self
+
+    def __del__(self):
+        try:
+            if self.handle:
+                _lib.lib().cv3_event_destroy(ctypes.c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+def wait_event(event: Event):
+    """Later work on the calling thread's stream waits for the event."""
+    _lib.call("stream_wait_event", None, event.handle)
+
+
 class Graph:
     """A captured sequence of launches on the calling thread's stream."""
 
@@ -203,8 +250,8 @@ class Graph:
             self.exec = x.value
         return False
 
-    def launch(self):
-        _lib.call("graph_launch", self.exec, None)
+    def launch(self, stream: "Optional[Stream]" = None):
+        _lib.call("graph_launch", self.exec, stream.handle if stream is not None else None)
 
     def __del__(self):
         try:

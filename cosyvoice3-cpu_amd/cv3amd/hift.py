@@ -27,15 +27,16 @@ epilogue -> causal conv with the residual x added in its epilogue  (hift.py:114-
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import List, Optional
 
 import numpy as np
 
 from . import _lib
-from .device import DeviceArray, Graph, to_device
+from .device import DeviceArray, Event, Graph, Stream, to_device, wait_event
 
 ACT = _lib.ACT
 F4 = 4
+WINDOW_STREAMS = 4   # vocoder windows replayed side by side (one stream each, default priority)
 
 
 def causal_pad(kernel_size: int, dilation: int = 1) -> int:
@@ -118,6 +119,7 @@ class DeviceHiFT:
         self.window = to_device(hann_window(self.n_fft))
         # captured spectral stacks, one per input length: (graph, mel in, source STFT in, out, arena)
         self._graphs = {}
+        self._streams: List[Stream] = []
         self._arena = None       # while recording or capturing: every intermediate of the stack
         self._arena_i = -1       # >= 0 while capturing: the next arena entry to hand out
 
@@ -256,11 +258,12 @@ class DeviceHiFT:
         kpost = self.shape["conv_post.weight"][2]
         return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0), channels_first_out=True)
 
-    def _stack(self, w: int):
-        """The spectral stack for a w-frame input, captured once: its staging inputs, its
-        output and the graph.  Recorded eagerly first (on zeroed inputs), then captured
-        with the recorded intermediates (see ``_new``)."""
-        g = self._graphs.get(w)
+    def _stack(self, w: int, slot: int = 0):
+        """The spectral stack for a w-frame input, captured once per (w, slot): its staging
+        inputs, its output and the graph (each slot owns its buffers, so windows on
+        different streams run side by side).  Recorded eagerly first (on zeroed inputs),
+        then captured with the recorded intermediates (see ``_new``)."""
+        g = self._graphs.get((w, slot))
         if g is None:
             mel_w = DeviceArray((self.shape["conv_pre.weight"][1], w))
             st_w = DeviceArray((self.n_fft + 2, w * self.up_total + 1))
@@ -278,26 +281,29 @@ class DeviceHiFT:
                 g = (graph, mel_w, st_w, out, self._arena)
             finally:
                 self._arena, self._arena_i = None, -1
-            self._graphs[w] = g
+            self._graphs[(w, slot)] = g
         return g
 
-    def spectral_graph(self, mel: DeviceArray, s_stft: DeviceArray, c0: int = 0, c1: Optional[int] = None):
-        """spectral() of mel[:, c0:c1] and its source STFT columns by graph replay; returns the
-        stack's own output buffer, valid until the next replay of the same length."""
+    def spectral_graph(self, mel: DeviceArray, s_stft: DeviceArray, c0: int = 0, c1: Optional[int] = None,
+                       slot: int = 0, stream: Optional[Stream] = None):
+        """spectral() of mel[:, c0:c1] and its source STFT columns by graph replay on ``stream``
+        (None: the calling thread's); returns the stack's own output buffer, valid until the
+        next replay of the same (length, slot)."""
         t = mel.shape[1]
         c1 = t if c1 is None else c1
         w = c1 - c0
-        graph, mel_w, st_w, out, _ = self._stack(w)
+        graph, mel_w, st_w, out, _ = self._stack(w, slot)
         S3 = ctypes.c_int64 * 3
         up = self.up_total
-        _lib.call("copy_strided", mel.ptr + c0 * F4, mel_w.ptr, 1, mel.shape[0], w, S3(0, t, 1), S3(0, w, 1), None)
+        sh = stream.handle if stream is not None else None
+        _lib.call("copy_strided", mel.ptr + c0 * F4, mel_w.ptr, 1, mel.shape[0], w, S3(0, t, 1), S3(0, w, 1), sh)
         fs = s_stft.shape[1]
         f0, f1 = c0 * up, min(fs, c1 * up + 1)
         if f1 - f0 != st_w.shape[1]:
             raise ValueError(f"source STFT has {fs} frames, expected {t * up + 1}")
         _lib.call("copy_strided", s_stft.ptr + f0 * F4, st_w.ptr, 1, s_stft.shape[0], f1 - f0, S3(0, fs, 1),
-                  S3(0, f1 - f0, 1), None)
-        graph.launch()
+                  S3(0, f1 - f0, 1), sh)
+        graph.launch(stream)
         return out
 
     def spectral_chunked(self, mel: DeviceArray, s_stft: DeviceArray, chunk: int, context: int,
@@ -310,7 +316,18 @@ class DeviceHiFT:
         nout = self.n_fft + 2
         out = DeviceArray((nout, t * up + 1))
         S3 = ctypes.c_int64 * 3
-        for m0 in range(0, t, chunk):
+        starts = list(range(0, t, chunk))
+        # graph replay: the windows are independent, so they run side by side on up to
+        # WINDOW_STREAMS streams (window i on stream i mod n), each with its own captured
+        # stack; the thread's stream waits for all of them before anything reads `out`
+        streams = self._window_streams(min(WINDOW_STREAMS, len(starts))) if graph else []
+        if streams:
+            for i, m0 in enumerate(starts):  # build (record + capture) every stack first, on this stream
+                self._stack(min(t, m0 + chunk + look) - max(0, m0 - context), i % len(streams))
+            ready = Event().record()
+            for st in streams:
+                st.wait(ready)
+        for i, m0 in enumerate(starts):
             m1 = min(t, m0 + chunk)
             c0 = max(0, m0 - context)
             c1 = min(t, m1 + look)
@@ -318,9 +335,11 @@ class DeviceHiFT:
             take = (m1 - m0) * up
             src0, dst0, n = (0, 0, 1 + take) if m0 == 0 else (1 + lead, 1 + m0 * up, take)
             if graph:
-                sub = self.spectral_graph(mel, s_stft, c0, c1)
+                slot = i % len(streams)
+                st = streams[slot]
+                sub = self.spectral_graph(mel, s_stft, c0, c1, slot=slot, stream=st)
                 _lib.call("copy_strided", sub.ptr + src0 * F4, out.ptr + dst0 * F4, 1, nout, n,
-                          S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), None)
+                          S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), st.handle)
                 continue
             sub_mel = DeviceArray((mel.shape[0], c1 - c0))
             _lib.call("copy_strided", mel.ptr + c0 * F4, sub_mel.ptr, 1, mel.shape[0], c1 - c0,
@@ -333,7 +352,14 @@ class DeviceHiFT:
             sub = self.spectral(sub_mel, sub_s)
             _lib.call("copy_strided", sub.ptr + src0 * F4, out.ptr + dst0 * F4, 1, nout, n,
                       S3(0, sub.shape[1], 1), S3(0, t * up + 1, 1), None)
+        for st in streams:
+            wait_event(Event().record(st))
         return out
+
+    def _window_streams(self, n: int) -> List[Stream]:
+        while len(self._streams) < n:
+            self._streams.append(Stream())
+        return self._streams[:n]
 
     def source_stft(self, source: DeviceArray) -> DeviceArray:
         """(n_fft + 2, frames) real / imaginary stack of the source STFT (hift.py:198-199)."""

@@ -86,6 +86,9 @@ int cv3_device_sync(void);
 int cv3_event_create(void** ev);
 int cv3_event_destroy(void* ev);
 int cv3_event_record(void* ev, cv3_stream_t s);
+/* Work enqueued on s after this call waits for ev's last recorded point (no counterpart in the reference:
+ * orders work across streams, e.g. vocoder windows run side by side). */
+int cv3_stream_wait_event(cv3_stream_t s, void* ev);
 int cv3_event_elapsed_ms(void* ev0, void* ev1, float* ms);
 int cv3_graph_begin(cv3_stream_t s);
 int cv3_graph_end(cv3_stream_t s, void** exec);
