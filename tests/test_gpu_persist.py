@@ -7,7 +7,9 @@ oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
 layers the tokens equal the five-kernel step's and the logits agree within 1e-5.
 Positions cover an empty cache (one attention chunk), a start just below the
 128-key chunk boundary, and 512 cached positions (five chunks); ordinary and
-cooperative launches.
+cooperative launches.  Failure handling is forced from the host: a preset error
+flag (every wait gives up within its bounded polls, the host raises) and the
+launch counter's wrap.
 """
 
 import numpy as np
@@ -171,3 +173,45 @@ def test_persistent_sampled_long_run_matches_five_kernel_step(gpu):
     print(f"[persist] sampled 24 layers: {out[0][0][:10]}...", flush=True)
     assert out[0][0] == out[1][0]
     assert out[0][1] == out[1][1]
+
+
+def test_persistent_error_flag_ends_the_launch_and_raises(gpu):
+    """A flag already set (as after a wait that gave up) makes every wait of the next launch
+    give up within 256 polls: the launch ends normally, and the host raises."""
+    from cv3amd.qwen2 import DeviceQwen2
+    _, dev, k, v = _setup(2, "per_channel", 64)
+    d = DeviceQwen2(dev, cap=1024)
+    d.fill_cache(k, v)
+    d.begin(1, 64)
+    d.step_persistent()                      # allocates the exchange words and the flag
+    assert not d.persistent_error()
+    d._perr.copy_from(np.ones(1, np.int64))  # the host sets the flag
+    d.step_persistent()
+    assert d.persistent_error()
+    with pytest.raises(RuntimeError):
+        d.generate_persistent(1, 64, 2)
+
+
+def test_persistent_epoch_counter_wrap(gpu):
+    """The launch counter wraps at 2^32 / 256 launches: the host clears the words and starts
+    again at 256; the tokens stay the oracle's."""
+    from cv3amd.qwen2 import DeviceQwen2
+    n, steps = 200, 6
+    cpu, dev, k, v = _setup(2, "per_channel", n)
+    lm, cache = _oracle_lm(cpu, k, v, n, steps)
+    x = lm.speech_emb([lm.sos])
+    want = []
+    for _ in range(steps):
+        top = int(np.argmax(lm.head(lm.body.forward(x, cache)[-1:])[0]))
+        want.append(top)
+        x = lm.speech_emb([top])
+    d = DeviceQwen2(dev, cap=1024)
+    d.fill_cache(k, v)
+    d.begin(lm.sos, n)
+    d.step_persistent()
+    d._persist.epoch_base = 0xFFFFFF00 - 256   # the next launch takes the last base, the one after wraps
+    for _ in range(steps - 1):
+        d.step_persistent()
+    assert d._persist.epoch_base == 256 * (steps - 2)
+    assert not d.persistent_error()
+    assert [int(t) for t in d.ints.numpy()[2 + n + 1: 2 + n + 1 + steps]] == want
