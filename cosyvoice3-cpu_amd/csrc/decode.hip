@@ -1209,38 +1209,48 @@ __device__ __forceinline__ float wave_sum_swap(float v) {
 }
 
 // Dot product of one weight row spread over the whole wave (64 lanes x CPL
-// chunks), reduced across the wave: every lane gets the sum.
-template <int CPL, bool SF16>
-__device__ __forceinline__ float wdot(const RowDot<64, CPL, SF16, false>& rd, const float* xs, int lane) {
+// chunks of 16 int8 codes, or of 32 q4 codes), reduced across the wave: every lane
+// gets the sum.  (q4: the chunk dots carry the codes x 16, undone once here.)
+template <int CPL, bool SF16, bool Q4>
+__device__ __forceinline__ float wdot(const RowDot<64, CPL, SF16, Q4>& rd, const float* xs, int lane) {
+  constexpr int CPC = kCodes<Q4>;
   float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) acc = fmaf(dot16(rd.wv[i], xs + (lane + i * 64) * 16), rd.sc[i], acc);
+  for (int i = 0; i < CPL; ++i) {
+    const float* xc = xs + (lane + i * 64) * CPC;
+    acc = fmaf(Q4 ? dot32_q4(rd.wv[i], xc) : dot16(rd.wv[i], xc), rd.sc[i], acc);
+  }
+  if (Q4) acc *= 0.0625f;
   return wave_sum_swap(acc);
 }
-// The same for K <= 1024 with the lane's 16 staged values already in registers
-// (a wave computing several rows reads its slice of the vector once).
+// The same for one chunk per lane (K <= 64 chunks) with the lane's staged values
+// already in registers (a wave computing several rows reads its slice once).
+template <int CPC>
 struct XSlice {
-  float v[16];
+  float v[CPC];
   __device__ __forceinline__ void load(const float* xs, int lane) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(v)[i] = reinterpret_cast<const float4*>(xs + lane * 16)[i];
+    for (int i = 0; i < CPC / 4; ++i)
+      reinterpret_cast<float4*>(v)[i] = reinterpret_cast<const float4*>(xs + lane * CPC)[i];
   }
 };
-template <bool SF16>
-__device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, false>& rd, const XSlice& x) {
-  return wave_sum_swap(fmaf(dot16(rd.wv[0], x.v), rd.sc[0], 0.f));
+template <bool SF16, bool Q4>
+__device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, Q4>& rd, const XSlice<kCodes<Q4>>& x) {
+  const float acc = fmaf(Q4 ? dot32_q4(rd.wv[0], x.v) : dot16(rd.wv[0], x.v), rd.sc[0], 0.f);
+  return wave_sum_swap(Q4 ? acc * 0.0625f : acc);
 }
 
 // RMSNorm staging with the norm weight loaded ahead (thread t owns float4 t):
-// xs[0, 1024) = x * w, zero past D; returns 1 / sqrt(mean(x^2) + eps), which
-// scales each row's dot product afterwards.  x is in LDS.
+// xs[0, width) = x * w, zero past D (width 1024 or 2048: what a one-chunk-per-lane
+// row of q8 or q4 codes reads); returns 1 / sqrt(mean(x^2) + eps), which scales each
+// row's dot product afterwards.  x is in LDS.
 struct NormStage {
   float4 w;
   __device__ __forceinline__ void prefetch(const float* g, int D) {
     const int t = threadIdx.x;
     w = t < D / 4 ? reinterpret_cast<const float4*>(g)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red) {
+  __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red, int width) {
     const int t = threadIdx.x;
     const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
     float ss = 0.f;
@@ -1248,7 +1258,7 @@ struct NormStage {
     ss = fmaf(v.y, v.y, ss);
     ss = fmaf(v.z, v.z, ss);
     ss = fmaf(v.w, v.w, ss);
-    if (t < 256) reinterpret_cast<float4*>(xs)[t] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+    if (t < width / 4) reinterpret_cast<float4*>(xs)[t] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
     ss = wave_sum_swap(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
@@ -1277,11 +1287,17 @@ __device__ __forceinline__ uint32_t ord_bits(float f) {
   return f != f ? 0u : (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-template <bool SF16>
+// Q4: the body's matrices are q4 (32 codes per 16-byte chunk); the head and the
+// speech embedding stay q8, as the reference's converter stores them.
+template <bool SF16, bool Q4>
 __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
+  constexpr int CPC = kCodes<Q4>;       // codes per chunk of the body rows
+  constexpr int kStage = 64 * CPC;      // staged width of a one-chunk-per-lane body row
+  constexpr int kDownCPL = Q4 ? 3 : 5;  // chunks per lane of a down row
+  constexpr int kXs = 64 * kDownCPL * CPC;
   __shared__ __align__(16) float xin[1024];   // x of the layer (raw), for A's norm and C's residual
   __shared__ __align__(16) float xmid[1024];  // x after o_proj (phase D keeps it for E)
-  __shared__ __align__(16) float xs[5120];    // staged (normed, zero-padded) vector of the dot products
+  __shared__ __align__(16) float xs[kXs];     // staged (normed, zero-padded) vector of the dot products
   __shared__ __align__(16) float big[8192];   // phase B: q, k, v, per-wave partials; C: partials
   __shared__ float red[16];
   __shared__ float hb_val[8];
@@ -1319,8 +1335,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   // while it polls.  (Loads complete in issue order, so a poll also waits for
   // every load issued before it; issuing the next phase's weights any earlier
   // holds up this phase's wait or its compute.)
-  RowDot<64, 1, SF16, false> dA0, dA1, dC0, dC1, dg[3], du[3];
-  RowDot<64, 5, SF16, false> dd;
+  RowDot<64, 1, SF16, Q4> dA0, dA1, dC0, dC1, dg[3], du[3];
+  RowDot<64, kDownCPL, SF16, Q4> dd;
   NormStage ns1, ns2;
   float bA0, bA1;
   auto load_A = [&](int l) {
@@ -1346,8 +1362,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   };
   auto load_E = [&](int l) { dd.load(a.dn, (int64_t)l * D + (liveE ? rE : 0), lane, liveE); };
 
-  // the dot products read xs up to 64 chunks per row: the tail past 1024 stays zero
-  for (int i = tid; i < 5120; i += kPT) xs[i] = 0.f;
+  // the dot products read xs up to 64 chunks per lane row: the tail past what a phase stages stays zero
+  for (int i = tid; i < kXs; i += kPT) xs[i] = 0.f;
   load_A(0);
   __syncthreads();
   uint64_t waitA = 0, waitD = 0;  // the idle workgroups' previous waits (wall-clock ticks)
@@ -1366,8 +1382,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         if (!ll_get<2>(a.xb + ((par ^ 1) * kRX + w % kRX) * a.sx, D, E - 8u + 4u, xin, a.err)) return;
         if (!isE) waitA = wall_clock64() - t0;
       }
-      const float inv = ns1.stage(xin, D, a.eps, xs, red);
-      XSlice xv;
+      const float inv = ns1.stage(xin, D, a.eps, xs, red, kStage);
+      XSlice<CPC> xv;
       xv.load(xs, lane);
       float v0 = wdot(dA0, xv) * inv + bA0;
       float v1 = wdot(dA1, xv) * inv + bA1;
@@ -1488,8 +1504,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         xmid[tid] = expf(part[tid * kPPart] - M) / den;
       }
       __syncthreads();
-      for (int i = tid; i < 1024; i += kPT) {
-        float att = 0.f;  // the o_proj dot reads the staged vector up to 1024: zero past H dh
+      for (int i = tid; i < kStage; i += kPT) {
+        float att = 0.f;  // the o_proj dot reads the staged vector up to kStage: zero past H dh
         if (i < H * dh) {
           const int hh = i / dh, d = i % dh;
           for (int cc = 0; cc < nact; ++cc) att = fmaf(part[(cc * H + hh) * kPPart + 2 + d], xmid[cc * H + hh], att);
@@ -1497,7 +1513,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         xs[i] = att;
       }
       __syncthreads();
-      XSlice xv;
+      XSlice<CPC> xv;
       xv.load(xs, lane);
       const float va = wdot(dC0, xv), vb2 = wdot(dC1, xv);
       if (lane < kRM) {  // lane i writes replica i
@@ -1512,8 +1528,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       const uint64_t t0 = isC ? 0 : idle_wait(wall_clock64(), waitD);
       if (!ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)) return;
       if (!isC) waitD = wall_clock64() - t0;
-      const float inv = ns2.stage(xmid, D, a.eps, xs, red);
-      XSlice xv;
+      const float inv = ns2.stage(xmid, D, a.eps, xs, red, kStage);
+      XSlice<CPC> xv;
       xv.load(xs, lane);
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
@@ -1528,7 +1544,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     // ---- E: down rows + residual -> x of the next layer ----
     if (isE) {
       load_E(l);
-      for (int i = I + tid; i < 1024; i += kPT) xs[i] = 0.f;  // the staged tail past I must be zero
+      for (int i = I + tid; i < kStage; i += kPT) xs[i] = 0.f;  // the staged tail past I must be zero
       if (!ll_get<10>(a.hb + (par * kRH + w % kRH) * a.sh, I, E + 3u, xs, a.err)) return;
       const float v = wdot(dd, xs, lane);
       if (liveE && lane < kRX) ll_put(a.xb + (par * kRX + lane) * a.sx + rE, xmid[rE] + v, E + 4u);
@@ -1556,8 +1572,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     }
     const int lp = (a.layers - 1) & 1;
     if (!ll_get<2>(a.xb + (lp * kRX + w % kRX) * a.sx, D, EH - 8u + 4u, xin, a.err)) return;
-    const float inv = ns.stage(xin, D, a.eps, xs, red);
-    XSlice xv;
+    const float inv = ns.stage(xin, D, a.eps, xs, red, kStage);
+    XSlice<16> xv;
     xv.load(xs, lane);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
@@ -1823,7 +1839,8 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   CV3_REQUIRE(H > 0 && Hk > 0 && H % Hk == 0 && H / Hk <= 8 && dh == 64 && H * dh == D, CV3_EUNSUPPORTED,
               "persistent step: heads %lld / kv heads %lld / head dim %lld", (long long)H, (long long)Hk,
               (long long)dh);
-  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= 5120 && I >= kPDown, CV3_EUNSUPPORTED,
+  const bool q4 = m->qkv.kind == CV3_KIND_Q4;
+  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= (q4 ? 6144 : 5120) && I >= kPDown, CV3_EUNSUPPORTED,
               "persistent step: hidden %lld / inter %lld", (long long)D, (long long)I);
   CV3_REQUIRE(m->layers > 0 && m->layers * 8 + 8 <= 256, CV3_EUNSUPPORTED, "persistent step: %lld layers (at most 31)",
               (long long)m->layers);
@@ -1836,10 +1853,17 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   if ((rc = check_qw(m->down, "down", I))) return rc;
   if ((rc = check_qw(m->head, "llm_decoder", D))) return rc;
   if ((rc = check_qw(m->embedding, "speech_embedding", D))) return rc;
-  const cv3_qweight* all[6] = {&m->qkv, &m->o, &m->gate_up, &m->down, &m->head, &m->embedding};
-  for (const cv3_qweight* w : all)
-    CV3_REQUIRE(w->kind == CV3_KIND_Q8 && w->scale_dtype == m->qkv.scale_dtype, CV3_EUNSUPPORTED,
-                "persistent step: q8 weights with one scale dtype");
+  // the body's four matrices share one kind (q8, or q4 with float16 scales); the head and the
+  // speech embedding are q8; one scale dtype throughout
+  const cv3_qweight* body[4] = {&m->qkv, &m->o, &m->gate_up, &m->down};
+  for (const cv3_qweight* w : body)
+    CV3_REQUIRE(w->kind == m->qkv.kind && (w->kind == CV3_KIND_Q8 || w->kind == CV3_KIND_Q4) &&
+                    w->scale_dtype == m->qkv.scale_dtype,
+                CV3_EUNSUPPORTED, "persistent step: body weights of one int8 or q4 kind and one scale dtype");
+  CV3_REQUIRE(m->head.kind == CV3_KIND_Q8 && m->embedding.kind == CV3_KIND_Q8 &&
+                  m->head.scale_dtype == m->qkv.scale_dtype && m->embedding.scale_dtype == m->qkv.scale_dtype &&
+                  (!q4 || m->qkv.scale_dtype == CV3_F16),
+              CV3_EUNSUPPORTED, "persistent step: q8 head and embedding with the body's scale dtype (f16 for q4)");
   CV3_REQUIRE(m->qkv.rows == (H + 2 * Hk) * dh && m->o.rows == D && m->gate_up.rows == 2 * I && m->down.rows == D &&
                   m->embedding.rows >= m->head.rows,
               CV3_EINVAL, "stacked weight rows do not match the geometry");
@@ -1847,7 +1871,9 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   CV3_HIP(hipGetDevice(&dev));
   CV3_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   const bool sf16 = m->qkv.scale_dtype == CV3_F16;
-  const void* fn = sf16 ? (const void*)k_dec_persist<true> : (const void*)k_dec_persist<false>;
+  const void* fn = q4     ? (const void*)k_dec_persist<true, true>
+                   : sf16 ? (const void*)k_dec_persist<true, false>
+                          : (const void*)k_dec_persist<false, false>;
   int per_cu = 0;
   CV3_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPT, 0));
   const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
@@ -1909,10 +1935,12 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
     void* args[] = {&a};
     CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));
   } else {
-    if (sf16)
-      hipLaunchKernelGGL(k_dec_persist<true>, dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    if (q4)
+      hipLaunchKernelGGL((k_dec_persist<true, true>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    else if (sf16)
+      hipLaunchKernelGGL((k_dec_persist<true, false>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
     else
-      hipLaunchKernelGGL(k_dec_persist<false>, dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+      hipLaunchKernelGGL((k_dec_persist<false, false>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
     CV3_LAUNCHED();
   }
   return CV3_OK;

@@ -1,7 +1,8 @@
 """The one-launch decode step (cv3_qwen2_decode_step_persistent) against the oracle.
 
 Same seeded synthetic Qwen2-0.5B weights as test_gpu_decode.py, q8 under the
-per-channel (float32 scales) and balanced (block 64, float16 scales) profiles.
+per-channel (float32 scales) and balanced (block 64, float16 scales) profiles, and
+the tiny profile's q4 body (head and embedding q8).
 Bars: per-step logits within 1e-5 (max abs error over max |logit|) of the
 oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
 layers the tokens equal the five-kernel step's and the logits agree within 1e-5.
@@ -49,7 +50,8 @@ def _oracle_lm(cpu, k, v, n, steps):
 
 
 @pytest.mark.parametrize("profile,n,steps,cooperative", [("per_channel", 512, 10, False), ("balanced", 0, 6, False),
-                                                         ("balanced", 122, 10, False), ("per_channel", 300, 6, True)])
+                                                         ("balanced", 122, 10, False), ("per_channel", 300, 6, True),
+                                                         ("tiny", 300, 8, False)])
 def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative):
     from cv3amd.qwen2 import DeviceQwen2
     cpu, dev, k, v = _setup(2, profile, n)
@@ -79,12 +81,13 @@ def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative):
         assert rel_err(vc[i][:, :n + steps], cache.v[i][:, :n + steps]) < 1e-5
 
 
-def test_persistent_full_depth_matches_five_kernel_step(gpu):
+@pytest.mark.parametrize("profile", ["balanced", "tiny"])
+def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
     """24 layers: the one-launch step and the five-kernel step give the same tokens."""
     from cv3amd.qwen2 import DeviceQwen2
     n, steps = 300, 16
-    _, dev, k, v = _setup(24, "balanced", n)
-    print(f"[persist] 24 layers, {n} cached, {steps} steps", flush=True)
+    _, dev, k, v = _setup(24, profile, n)
+    print(f"[persist] 24 layers, profile={profile}, {n} cached, {steps} steps", flush=True)
     a = DeviceQwen2(dev, cap=1024)
     a.fill_cache(k, v)
     want = []
@@ -110,11 +113,15 @@ def test_persistent_full_depth_matches_five_kernel_step(gpu):
     assert b.generate_persistent(1, n, steps) == want_tok
 
 
-def test_persistent_step_rejects_q4(gpu):
+def test_persistent_step_rejects_too_few_workgroups(gpu):
+    """The host checks the launch before it is made: 64 workgroups cannot hold phase E's
+    128 down-row workgroups."""
     from cv3amd.qwen2 import DeviceQwen2
-    _, dev, _, _ = _setup(2, "tiny", 0)
+    _, dev, _, _ = _setup(2, "per_channel", 0)
     d = DeviceQwen2(dev, cap=1024)
     d.begin(1, 0)
+    d.step_persistent()
+    d._persist.workgroups = 64
     with pytest.raises(NotImplementedError):
         d.step_persistent()
 
