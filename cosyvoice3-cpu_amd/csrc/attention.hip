@@ -52,6 +52,7 @@ __device__ __forceinline__ void visible_keys(const AttnParams& p, int64_t qi, in
 }
 
 constexpr int KT = 64;        // keys per LDS tile
+constexpr float kLog2E = 1.4426950408889634f;
 constexpr int KS = 68;        // LDS row stride (floats) for K and V tiles
 constexpr int QW = 16;        // queries per wave
 constexpr int QT = 64;        // queries per workgroup
@@ -67,6 +68,9 @@ constexpr int QT = 64;        // queries per workgroup
 // Per tile a wave scores all 64 keys (64 MFMAs), rescales its running state once,
 // then accumulates P V (64 MFMAs).  V is staged transposed ([dim][key]) so the
 // P V operands of four consecutive keys are one 16-byte LDS read.
+// Scores are kept in base-2 units: q is scaled by log2(e) after the reference's
+// (q * scale), so every exponential is one v_exp_f32 (2^x) instead of an expf
+// range reduction; e^{s - m} = 2^{s log2 e - m log2 e}, to within a few ulp.
 template <int NKG>
 __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
   __shared__ float Ks[NKG][KT * KS];
@@ -88,7 +92,8 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
     const float4 t = qvalid ? *reinterpret_cast<const float4*>(qrow + s4 * 16 + g * 4) : make_float4(0, 0, 0, 0);
-    qf[s4] = f32x4{t.x * p.scale, t.y * p.scale, t.z * p.scale, t.w * p.scale};
+    qf[s4] = f32x4{(t.x * p.scale) * kLog2E, (t.y * p.scale) * kLog2E, (t.z * p.scale) * kLog2E,
+                   (t.w * p.scale) * kLog2E};
   }
 
   f32x4 oacc[4];
@@ -179,13 +184,13 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
     const float m_new = fmaxf(m_run, mx);
     const bool none = m_new == -INFINITY;
     const float m_use = none ? 0.f : m_new;
-    const float alpha = none ? 1.f : expf(m_run - m_new);
+    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
     float psum = 0.f;
 #pragma unroll
     for (int sub = 0; sub < KT / 16; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sc[sub][i] = expf(sc[sub][i] - m_use);
+        sc[sub][i] = __builtin_amdgcn_exp2f(sc[sub][i] - m_use);
         psum += sc[sub][i];
       }
     l_run = l_run * alpha + psum;
@@ -223,14 +228,14 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
   float M = m_run;
 #pragma unroll
   for (int g2 = 1; g2 < NKG; ++g2) M = fmaxf(M, mb[(((g2 - 1) * 4 + qw) * 64 + lane) * 18]);
-  const float a0 = M == -INFINITY ? 1.f : expf(m_run - M);
+  const float a0 = M == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - M);
   l_run = l_run * a0;
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] *= a0;
 #pragma unroll
   for (int g2 = 1; g2 < NKG; ++g2) {
     const float* slot = mb + (((g2 - 1) * 4 + qw) * 64 + lane) * 18;
-    const float ag = M == -INFINITY ? 0.f : expf(slot[0] - M);
+    const float ag = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(slot[0] - M);
     l_run += slot[1] * ag;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
