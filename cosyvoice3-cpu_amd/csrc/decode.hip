@@ -1146,9 +1146,12 @@ __device__ __forceinline__ void ll_put(uint64_t* p, float v, uint32_t e) {
 // words per thread per poll, so a wait of up to NW * 512 words is one round trip.
 // False for every thread (and the error flag set) if a word never arrives; a wait
 // also ends early once another workgroup has set the flag.
-template <int NW>
+struct Ident {
+  __device__ __forceinline__ int operator()(int i) const { return i; }
+};
+template <int NW, class Map = Ident>
 __device__ bool ll_get(const uint64_t* s0, int n0, const uint64_t* s1, int n1, const uint64_t* s2, int n2,
-                       uint32_t e, float* dst, int64_t* err) {
+                       uint32_t e, float* dst, int64_t* err, Map map = Map()) {
   const int n = n0 + n1 + n2;
   bool ok = true;
   for (int b0 = 0; b0 < n && ok; b0 += kPT * NW) {
@@ -1181,17 +1184,19 @@ __device__ bool ll_get(const uint64_t* s0, int n0, const uint64_t* s1, int n1, c
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
       const int idx = b0 + (int)threadIdx.x + kPT * j;
-      if (idx < n) dst[idx] = __uint_as_float((uint32_t)w[j]);
+      if (idx < n) dst[map(idx)] = __uint_as_float((uint32_t)w[j]);
     }
     ok = !__syncthreads_or(!got);
   }
   if (!ok && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(err), 1ull);
   return ok;
 }
-template <int NW>
-__device__ __forceinline__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err) {
-  return ll_get<NW>(src, n, nullptr, 0, nullptr, 0, e, dst, err);
+template <int NW, class Map = Ident>
+__device__ __forceinline__ bool ll_get(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err,
+                                       Map map = Map()) {
+  return ll_get<NW, Map>(src, n, nullptr, 0, nullptr, 0, e, dst, err, map);
 }
+
 
 // Wave sum in every lane without lane reads: DPP within each 16-lane row, then the
 // row-pair and half swaps of gfx950 (v_permlane16_swap / v_permlane32_swap).  The
@@ -1238,6 +1243,32 @@ template <bool SF16, bool Q4>
 __device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, Q4>& rd, const XSlice<kCodes<Q4>>& x) {
   const float acc = fmaf(Q4 ? dot32_q4(rd.wv[0], x.v) : dot16(rd.wv[0], x.v), rd.sc[0], 0.f);
   return wave_sum_swap(Q4 ? acc * 0.0625f : acc);
+}
+
+// Chunk-transposed staging for rows of NCH chunks of CPC codes (one chunk per lane and
+// per 64-lane step): the f-th float4 of chunk c sits at float4 slot f NCH + c, so the
+// 64 lanes of a wave, reading the same f of chunks c .. c + 63, read 64 consecutive
+// float4s (no LDS bank conflicts; the natural layout puts them 4 CPC bytes apart).
+template <int CPC, int NCH>
+struct ChunkT {
+  __device__ __forceinline__ int operator()(int k) const {
+    return ((((k >> 2) & (CPC / 4 - 1)) * NCH + k / CPC) << 2) | (k & 3);
+  }
+};
+template <int CPL, bool SF16, bool Q4>
+__device__ __forceinline__ float wdot_t(const RowDot<64, CPL, SF16, Q4>& rd, const float* xs, int lane) {
+  constexpr int CPC = kCodes<Q4>, NCH = 64 * CPL;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    float xc[CPC];
+#pragma unroll
+    for (int f = 0; f < CPC / 4; ++f)
+      reinterpret_cast<float4*>(xc)[f] = reinterpret_cast<const float4*>(xs)[f * NCH + lane + i * 64];
+    acc = fmaf(Q4 ? dot32_q4(rd.wv[i], xc) : dot16(rd.wv[i], xc), rd.sc[i], acc);
+  }
+  if (Q4) acc *= 0.0625f;
+  return wave_sum_swap(acc);
 }
 
 // RMSNorm staging with the norm weight loaded ahead (thread t owns float4 t):
@@ -1544,9 +1575,12 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     // ---- E: down rows + residual -> x of the next layer ----
     if (isE) {
       load_E(l);
-      for (int i = I + tid; i < kStage; i += kPT) xs[i] = 0.f;  // the staged tail past I must be zero
-      if (!ll_get<10>(a.hb + (par * kRH + w % kRH) * a.sh, I, E + 3u, xs, a.err)) return;
-      const float v = wdot(dd, xs, lane);
+      // h staged chunk-transposed; the slots of k >= I must be zero (other phases stage
+      // their vectors over part of this range)
+      const ChunkT<CPC, 64 * kDownCPL> tmap;
+      for (int k = I + tid; k < 64 * kDownCPL * CPC; k += kPT) xs[tmap(k)] = 0.f;
+      if (!ll_get<10>(a.hb + (par * kRH + w % kRH) * a.sh, I, E + 3u, xs, a.err, tmap)) return;
+      const float v = wdot_t(dd, xs, lane);
       if (liveE && lane < kRX) ll_put(a.xb + (par * kRX + lane) * a.sx + rE, xmid[rE] + v, E + 4u);
       __syncthreads();
     }
