@@ -1110,6 +1110,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
 // within 256 polls of seeing it.
 // ---------------------------------------------------------------------------
 constexpr int kPT = 512;                 // threads per workgroup
+constexpr float kLog2E = 1.4426950408889634f;
 constexpr int kPKeys = 128;              // keys per attention item
 constexpr int kPChunks = 8;              // attention items per head: cache <= 1024 positions
 constexpr int kPOproj = 64;              // workgroups of phase C
@@ -1462,21 +1463,23 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(qkv + dh + qd)[i];
       }
+      // scores in base-2 units, (q * scale) first (ops.py:292), then q * log2(e): the
+      // softmax weights e^{s - m} become single v_exp_f32 (2^x); the partials' m are in
+      // the same units, which only the merge below reads
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float4 q4 = reinterpret_cast<const float4*>(qkv + qd)[i];
-        // (q * scale) first (ops.py:292)
-        s = fmaf(q4.x * a.scale, kr[i].x, s);
-        s = fmaf(q4.y * a.scale, kr[i].y, s);
-        s = fmaf(q4.z * a.scale, kr[i].z, s);
-        s = fmaf(q4.w * a.scale, kr[i].w, s);
+        s = fmaf((q4.x * a.scale) * kLog2E, kr[i].x, s);
+        s = fmaf((q4.y * a.scale) * kLog2E, kr[i].y, s);
+        s = fmaf((q4.z * a.scale) * kLog2E, kr[i].z, s);
+        s = fmaf((q4.w * a.scale) * kLog2E, kr[i].w, s);
       }
       s += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(s)));
       s += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(s)));
       s = key <= ipos ? s : -INFINITY;
       const float mw = wave_max_dpp(s);  // the wave's 16 keys
-      const float p = mw == -INFINITY ? 0.f : expf(s - mw);  // 0 for keys past pos
+      const float p = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mw);  // 0 for keys past pos
       const float lw = wave_sum_swap((lane & 3) == 0 ? p : 0.f);
       const float vnew = qkv[2 * dh + lane];  // v of this token
       const int tn = ipos - kw;               // its slot in the wave's keys (may lie outside 0..15)
@@ -1501,7 +1504,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float mi = ow[8 * dh + i];
-          const float f = mi == -INFINITY ? 0.f : expf(mi - M);
+          const float f = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
           L = fmaf(ow[8 * dh + 8 + i], f, L);
           O = fmaf(ow[i * dh + lane], f, O);
         }
@@ -1531,8 +1534,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, part[(cc * H + hh) * kPPart]);
         float den = 0.f;
         for (int cc = 0; cc < nact; ++cc)
-          den = fmaf(part[(cc * H + hh) * kPPart + 1], expf(part[(cc * H + hh) * kPPart] - M), den);
-        xmid[tid] = expf(part[tid * kPPart] - M) / den;
+          den = fmaf(part[(cc * H + hh) * kPPart + 1], __builtin_amdgcn_exp2f(part[(cc * H + hh) * kPPart] - M), den);
+        xmid[tid] = __builtin_amdgcn_exp2f(part[tid * kPPart] - M) / den;
       }
       __syncthreads();
       for (int i = tid; i < kStage; i += kPT) {
