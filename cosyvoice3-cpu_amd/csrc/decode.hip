@@ -1118,9 +1118,10 @@ constexpr int kPDown = 128;              // workgroups of phase E
 constexpr int kPSpin = 1 << 18;          // polls (each with a short sleep) before a wait gives up
 constexpr int kPPart = 66;               // words per attention partial: m, l, o[64]
 // Replicas of the exchanged vectors that many workgroups poll (x: all, x_mid: all,
-// h: 128, partials: 64): workgroup w reads replica w % n, so each copy of a word
-// has a few dozen readers instead of hundreds polling one cache line.
-constexpr int kRX = 8, kRM = 8, kRH = 4, kRP = 2;
+// h: 128): workgroup w reads replica w % n.  Measured with the throttled polling
+// below: one copy is 2 % slower, 4 and 8 copies no faster or slower (the producers'
+// extra stores sit on their critical path).
+constexpr int kRX = 2, kRM = 2, kRH = 2, kRP = 1;
 
 struct PersistArgs {
   QW qkv, o, gu, dn, head, emb;
