@@ -1092,7 +1092,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
 //      (flash-decoding partial: max, sum, unnormalised output)
 //   C  128 workgroups: merge the partials, o_proj rows + residual -> x_mid
 //   D  all workgroups: RMSNorm(x_mid) -> [gate; up] pairs -> h = silu(g) * u
-//   E  128 workgroups: down rows + residual -> x for the next layer
+//   E  up to 256 workgroups (224 at hidden 896): down rows + residual -> x for the next layer
 // then the head rows, and (greedy) the argmax, speech_embedding row and
 // bookkeeping by workgroup 0.
 //
@@ -1114,7 +1114,7 @@ constexpr float kLog2E = 1.4426950408889634f;
 constexpr int kPKeys = 128;              // keys per attention item
 constexpr int kPChunks = 8;              // attention items per head: cache <= 1024 positions
 constexpr int kPOproj = 128;             // workgroups of phase C (64: 4 % slower, 192 and 256: 2-3 %)
-constexpr int kPDown = 128;              // workgroups of phase E
+constexpr int kPDown = 256;              // workgroups of phase E, at most (128: 2 % slower)
 constexpr int kPSpin = 1 << 18;          // polls (each with a short sleep) before a wait gives up
 constexpr int kPPart = 66;               // words per attention partial: m, l, o[64]
 // Replicas of the exchanged vectors that many workgroups poll (x: all, x_mid: all,
@@ -1346,9 +1346,10 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   const int64_t pos = *a.pos;
   const int nact = (int)((pos + kPKeys) / kPKeys);  // attention chunks in use
   const int half = dh / 2;
-  const int rowsC = (D + kPOproj - 1) / kPOproj, rowsE = (D + kPDown - 1) / kPDown;
+  const int nE = min(kPDown, G);  // phase E's workgroups
+  const int rowsC = (D + kPOproj - 1) / kPOproj, rowsE = (D + nE - 1) / nE;
   const bool isB = w < H * kPChunks && (w % kPChunks) < nact;
-  const bool isC = w < kPOproj, isE = w < kPDown && w * rowsE < D;  // only workgroups that own rows wait in E
+  const bool isC = w < kPOproj, isE = w < nE && w * rowsE < D;  // only workgroups that own rows wait in E
   // phase A's pair of this wave and its rotary factors (the same in every layer)
   const int npairs = R / 2;
   const int pA = w + G * wave;
@@ -1878,7 +1879,7 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
               "persistent step: heads %lld / kv heads %lld / head dim %lld", (long long)H, (long long)Hk,
               (long long)dh);
   const bool q4 = m->qkv.kind == CV3_KIND_Q4;
-  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= (q4 ? 6144 : 5120) && I >= kPDown, CV3_EUNSUPPORTED,
+  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= (q4 ? 6144 : 5120) && I >= kPOproj, CV3_EUNSUPPORTED,
               "persistent step: hidden %lld / inter %lld", (long long)D, (long long)I);
   CV3_REQUIRE(m->layers > 0 && m->layers * 8 + 8 <= 256, CV3_EUNSUPPORTED, "persistent step: %lld layers (at most 31)",
               (long long)m->layers);
@@ -1915,8 +1916,10 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   int per_cu = 0;
   CV3_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPT, 0));
   const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
-  CV3_REQUIRE(G >= kPDown && G <= per_cu * cus && G <= I, CV3_EUNSUPPORTED,
-              "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G, kPDown, per_cu * cus,
+  // phase C needs kPOproj workgroups; phase E at most 8 rows (one per wave) on min(kPDown, G)
+  CV3_REQUIRE(G >= kPOproj && G <= per_cu * cus && G <= I && (D + std::min(kPDown, G) - 1) / std::min(kPDown, G) <= 8,
+              CV3_EUNSUPPORTED, "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G,
+              kPOproj, per_cu * cus,
               (long long)I);
   CV3_REQUIRE((H + 2 * Hk) * dh / 2 <= 8LL * G && I <= 24LL * G && m->head.rows <= 32LL * G &&
                   H * kPChunks <= G && H * kPChunks * kPPart <= 8192,
