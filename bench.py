@@ -3,23 +3,25 @@
 
   * Qwen2-0.5B int8 greedy decode, batch 1 (the reported ``value``): 24 layers,
     hidden 896, 14/2 heads x 64, SwiGLU 4864, per-output-channel int8 weights with
-    float32 scales, KV cache pre-filled to 512 positions of N(0, 1), K tokens
-    decoded from speech_embedding[sos] (one "step" = one token), each token one
-    cooperative launch of the whole step (``--decode-step kernels``: five kernels per
-    layer, whose rate is reported beside it in ``five_kernel_step``); the same decode
-    with the reference's sampler on the device (``sampled_tok_s``); and with the tiny
-    profile's q4 body layers (the ``decode_tiny`` object).
+    float32 scales, KV cache pre-filled to 512 positions of N(0, 1).  One step is one
+    whole decode: 256 greedy tokens from speech_embedding[sos], KV 512 -> 768, each
+    token one launch of the whole decode step (``--decode-step kernels``: five kernels
+    per layer, whose rate is reported beside it in ``five_kernel_step``); the same
+    decode with the reference's sampler on the device (``sampled_tok_s``); and with
+    the tiny profile's q4 body layers (the ``decode_tiny`` object).
   * DiT flow decoder, 10 s of audio (the ``flow`` object): 22 blocks x [2, 500, 1024]
     fp32, 10 Euler steps with classifier-free guidance, noise from the host replica
-    of torch.randn((1, 80, 15000), seed 0); and the same solve over 30 s (T = 1500)
-    with q8 linears (the ``flow_q8_30s`` object).
+    of torch.randn((1, 80, 15000), seed 0), checked against its pinned SHA-256; and
+    the same solve over 30 s (T = 1500) with q8 linears, per-output-channel float32
+    scales (``flow_q8_30s``) and block-64 float16 scales (``flow_q8_30s_block64``).
   * HiFTNet vocoder, 10 s of audio (the ``vocoder`` object), whole and in 1 s chunks.
 
 Weights are synthetic (seeded N(0, 0.02), norms 1; cv3amd/synth.py); inputs are
 resident in HBM before the timed regions start.  Each workload reports its
 dominant kernel against the MI355X roofline (HBM 8 TB/s for the int8 GEMV, fp32
-matrix 157.3 TFLOP/s for the DiT GEMM), timed live with HIP events, and the
-oracle's NumPy restatement timed on the host cores on a bounded sample.
+matrix 157.3 TFLOP/s for the DiT GEMM), timed live with HIP events, next to the
+measured device copy rate and fp32 MFMA probe rate, and the oracle's NumPy
+restatement timed on the host cores on a bounded sample.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -43,8 +45,12 @@ import numpy as np  # noqa: E402
 METRIC = "DiT flow RTF (10 s, CFG) + int8 LM decode tok/s, each as % of roofline"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
-PREFILL = 512
+PREFILL = 512             # KV cache positions pre-filled before each decode
+DECODE_TOKENS = 256       # tokens per decode: KV 512 -> 768
 AUDIO_SECONDS = 10.0       # 500 mel frames at 50 Hz
+# SHA-256 of torch.randn((1, 80, 15000)) under seed 0 as float32 bytes: the flow's initial noise
+# (cv3cpu/models/flow.py:16,36-43).  tests/test_oracle_rng.py pins it to the oracle's replica.
+NOISE_SHA256 = "ca8eb3b705dfa463ec872b622bd82459b5790c00f88f2529d993e40233bae482"
 
 
 def log(msg: str):
@@ -87,6 +93,22 @@ def copy_bandwidth(nbytes: int = 256 << 20, reps: int = 10) -> float:
     return 2.0 * nbytes / (ms / 1e3)
 
 
+def mfma_peak(cu_count: int, iters: int = 20000) -> float:
+    """fp32 matrix-core rate (flop/s) the device sustains on register operands
+    (cv3_mfma_peak_f32): the measured ceiling beside the published 157.3 TFLOP/s."""
+    from cv3amd import _lib
+    from cv3amd.device import DeviceArray, Timer, synchronize
+    out = DeviceArray((cu_count * 512,))
+    flops = ctypes.c_double()
+    _lib.call("mfma_peak_f32", 1000, cu_count, out.ptr, ctypes.addressof(flops), None)   # clocks up
+    synchronize()
+    tm = Timer()
+    tm.start()
+    _lib.call("mfma_peak_f32", iters, cu_count, out.ptr, ctypes.addressof(flops), None)
+    ms = tm.stop()
+    return flops.value / (ms / 1e3)
+
+
 def replayer(graph: bool, enqueue):
     """A callable that enqueues ``enqueue``'s launches: replayed from one captured HIP
     graph, or issued directly (the mode used under the kernel-trace profiler)."""
@@ -112,13 +134,19 @@ def build_lm(layers: int, profile: str):
     return t, synth.qwen2_meta(layers=layers)
 
 
-def bench_decode(args, tensors, meta, label: str = "decode"):
+def bench_decode(args, tensors, meta, label: str = "decode", decodes: int = None, warmup: int = None):
+    """Greedy decodes of DECODE_TOKENS tokens from the KV cache pre-filled to PREFILL positions.
+    One step = one whole decode: begin at position PREFILL with speech_embedding[sos], then
+    DECODE_TOKENS tokens.  A decode only writes cache rows PREFILL and up, and each token reads
+    the rows below its own position, so every decode sees the same pre-filled cache."""
     import cv3amd.quant as quant
     from cv3amd import _lib
     from cv3amd.device import Graph, Timer, synchronize
     from cv3amd.qwen2 import DeviceQwen2
     from cv3amd.weights import WeightStore
 
+    decodes = args.steps if decodes is None else decodes
+    warmup = args.warmup if warmup is None else warmup
     store = WeightStore(tensors, meta, quant.QTensor)
     layers = meta["qwen2"]["num_hidden_layers"]
     lm = DeviceQwen2(store, cap=1024)
@@ -132,41 +160,42 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
     lm.cooperative = args.cooperative
     tm = Timer()
 
-    def timed_tokens(one_launch: bool):
-        """Warm up, then time args.steps greedy tokens from the same cache and start."""
+    def one_decode(one_launch: bool):
+        lm.begin(sos, PREFILL)
+        for _ in range(DECODE_TOKENS):
+            lm.step_persistent() if one_launch else lm.step(graph=args.graph)
+
+    def timed_decodes(one_launch: bool, n: int, w: int):
+        """w untimed decodes, then n timed ones; returns (ms per decode, tokens of the last)."""
         what = "one-launch step" if one_launch else "five-kernel step"
-        log(f"{label}: {what}: warmup {args.warmup} tokens")
-        lm.fill_cache(k, v)
-        lm.begin(sos, PREFILL)
-        for _ in range(args.warmup):
-            lm.step_persistent() if one_launch else lm.step(graph=args.graph)
+        log(f"{label}: {what}: {w} warmup + {n} timed decodes of {DECODE_TOKENS} tokens from KV {PREFILL}")
+        for _ in range(w):
+            one_decode(one_launch)
         synchronize()
-        lm.fill_cache(k, v)
-        lm.begin(sos, PREFILL)
-        synchronize()
-        log(f"{label}: {what}: timing {args.steps} tokens")
         tm.start()
-        for _ in range(args.steps):
-            lm.step_persistent() if one_launch else lm.step(graph=args.graph)
-        ms_ = tm.stop()
+        for _ in range(n):
+            one_decode(one_launch)
+        ms_ = tm.stop() / n
         synchronize()
         if one_launch and lm.persistent_error():
             raise RuntimeError("the one-launch decode step gave up waiting for an exchange")
-        toks = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + args.steps]]
-        log(f"{label}: {what}: {ms_:.2f} ms for {args.steps} tokens = {args.steps / (ms_ / 1e3):.1f} tok/s")
+        toks = [int(t) for t in lm.ints.numpy()[2 + PREFILL + 1: 2 + PREFILL + 1 + DECODE_TOKENS]]
+        log(f"{label}: {what}: {ms_:.2f} ms per decode = {DECODE_TOKENS / (ms_ / 1e3):.1f} tok/s")
         return ms_, toks
 
-    ms_k, tokens_k = timed_tokens(False)
-    ms, tokens = timed_tokens(True) if persistent else (ms_k, tokens_k)
+    side = max(1, min(decodes, 3))     # the step not reported as the value: a shorter sample
+    if persistent:
+        ms, tokens = timed_decodes(True, decodes, warmup)
+        ms_k, tokens_k = timed_decodes(False, side, 1)
+    else:
+        ms_k, tokens_k = timed_decodes(False, decodes, warmup)
+        ms, tokens = ms_k, tokens_k
     if tokens != tokens_k:
         raise RuntimeError("the one-launch and five-kernel steps chose different tokens")
-    # report the faster step (the one-launch step wins on q8; on the q4 body the nibble unpacking
-    # makes its compute-bound phases slower than the five-kernel step)
-    if persistent and ms_k < ms:
-        persistent, ms = False, ms_k
-    tok_s = args.steps / (ms / 1e3)
-    avg_len = PREFILL + (args.steps - 1) / 2.0
-    b = lm.bytes_per_token(int(round(avg_len)))
+    tok_s = DECODE_TOKENS / (ms / 1e3)
+    # algorithmic bytes averaged over the decode's tokens: token s reads PREFILL + s + 1 cache rows
+    parts = [lm.bytes_per_token(PREFILL + s) for s in range(DECODE_TOKENS)]
+    b = {key: sum(p[key] for p in parts) / DECODE_TOKENS for key in parts[0]}
     per_token = b["body"] + b["kv"] + b["norms_biases"] + b["head"]
     log(f"{label}: {tok_s:.1f} tok/s; {per_token / 1e6:.1f} MB/token -> {per_token * tok_s / 1e9:.0f} GB/s")
 
@@ -196,13 +225,10 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
     class _Sampling:
         top_p, top_k, win_size, tau_r, strict_min_len = 0.8, 25, 10, 0.1, True
         rng = np.random.default_rng(0)
-    lm.fill_cache(k, v)
-    lm.generate_sampled(sos, PREFILL, args.warmup, args.warmup, _Sampling, sos, graph=args.graph,
-                        persistent=persistent)
-    lm.fill_cache(k, v)
+    lm.generate_sampled(sos, PREFILL, 8, 8, _Sampling, sos, graph=args.graph, persistent=persistent)
     synchronize()
     tm.start()
-    sampled = lm.generate_sampled(sos, PREFILL, args.steps, args.steps, _Sampling, sos, graph=args.graph,
+    sampled = lm.generate_sampled(sos, PREFILL, DECODE_TOKENS, DECODE_TOKENS, _Sampling, sos, graph=args.graph,
                                   persistent=persistent)
     sms = tm.stop()
     sampled_tok_s = len(sampled) / (sms / 1e3)
@@ -212,12 +238,12 @@ def bench_decode(args, tensors, meta, label: str = "decode"):
     return {
         "sampled_tok_s": sampled_tok_s, "persistent": persistent,
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
-        "five_kernel_tok_s": args.steps / (ms_k / 1e3),
+        "five_kernel_tok_s": DECODE_TOKENS / (ms_k / 1e3), "decodes": decodes,
         # the one-launch step is a single kernel per token: its bytes are the token's
         "step_kernel": {"name": f"k_dec_persist<{'true' if sf16 else 'false'}, "
                                 f"{'true' if lm.gate_up.kind == 'q4' else 'false'}> (the whole decode step)",
-                        "bytes_per_launch": per_token, "us_per_launch": ms / args.steps * 1e3,
-                        "achieved_Bps": per_token / (ms / args.steps / 1e3)},
+                        "bytes_per_launch": per_token, "us_per_launch": ms / DECODE_TOKENS * 1e3,
+                        "achieved_Bps": per_token / (ms / DECODE_TOKENS / 1e3)},
         "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
                    else "k_dec_gemv<16,4,2> (RMSNorm + [gate;up] int8 GEMV + SwiGLU)",
                    "bytes_per_launch": gu_bytes, "us_per_launch": kms * 1e3, "achieved_Bps": achieved},
@@ -243,8 +269,8 @@ def cpu_decode(tensors, meta, n_tokens: int):
         cache.v[i][:, :PREFILL] = v[i]
     cache.length = PREFILL
     x = lm.speech_emb([lm.sos])
-    logits = lm.head(lm.body.forward(x, cache)[-1:])[0]   # warm-up token
-    x = lm.speech_emb([int(np.argmax(logits))])
+    logits0 = lm.head(lm.body.forward(x, cache)[-1:])[0]   # warm-up token
+    x = lm.speech_emb([int(np.argmax(logits0))])
     t0 = time.perf_counter()
     toks = []
     for _ in range(n_tokens):
@@ -253,7 +279,7 @@ def cpu_decode(tensors, meta, n_tokens: int):
         toks.append(top)
         x = lm.speech_emb([top])
     dt = time.perf_counter() - t0
-    return n_tokens / dt, dt
+    return n_tokens / dt, dt, [int(np.argmax(logits0))] + toks
 
 
 # ---------------------------------------------------------------------------
@@ -261,13 +287,17 @@ def cpu_decode(tensors, meta, n_tokens: int):
 # ---------------------------------------------------------------------------
 
 def flow_inputs(T: int):
+    import hashlib
     from cv3amd.torch_rng import randn
     rng = np.random.default_rng(0)
     mu = rng.standard_normal((1, 80, T), dtype=np.float32)
     cond = rng.standard_normal((1, 80, T), dtype=np.float32)
     spks = rng.standard_normal((1, 80), dtype=np.float32)
-    x0 = randn((1, 80, 15000), 0)[:, :, :T]            # flow.py:16-17,36-43
-    return mu, cond, spks, np.ascontiguousarray(x0)
+    noise = randn((1, 80, 15000), 0)                      # flow.py:16-17,36-43
+    digest = hashlib.sha256(np.ascontiguousarray(noise, np.float32).tobytes()).hexdigest()
+    if digest != NOISE_SHA256:
+        raise RuntimeError(f"the host torch.randn replica drew different ODE noise on this host (sha256 {digest})")
+    return mu, cond, spks, np.ascontiguousarray(noise[:, :, :T])
 
 
 def bench_flow(args, tensors, meta):
@@ -315,31 +345,33 @@ def bench_flow(args, tensors, meta):
                        "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
 
 
-def bench_flow_q8(args, tensors, meta):
-    """The 30 s solve (T = 1500) with the DiT linears stored q8 (block 64, f16 scales; the
-    reference converter's balanced profile), dequantised inside the GEMM's B load."""
+def bench_flow_q8(args, tensors, meta, profile: str):
+    """The 30 s solve (T = 1500) with the DiT linears stored q8, dequantised inside the GEMM's
+    B load: ``per_channel`` (one float32 scale per output row) or ``balanced`` (block 64,
+    float16 scales; the reference converter's default profile)."""
     import cv3amd.quant as quant
     from cv3amd import synth
     from cv3amd.device import Timer, synchronize
     from cv3amd.dit import DeviceDiT
     from cv3amd.weights import WeightStore
     T = 1500
-    qt = synth.quantize_store(tensors, "balanced", quant.quantize_q8)   # device quantiser
+    qt = synth.quantize_store(tensors, profile, quant.quantize_q8)   # device quantiser
     d = DeviceDiT(WeightStore(qt, meta, quant.QTensor))
     mu, cond, spks, x0 = flow_inputs(T)
     d.prepare(mu, spks, cond)
-    log("flow q8 30 s: warmup solve (captures the solve graph)")
+    log(f"flow q8 ({profile}) 30 s: warmup solve (captures the solve graph)")
     d.solve(x0, graph=args.graph)
     synchronize()
     n = max(1, args.flow_solves - 1)
-    log(f"flow q8 30 s: timing {n} solves")
+    log(f"flow q8 ({profile}) 30 s: timing {n} solves")
     tm = Timer()
     tm.start()
     for _ in range(n):
         d.solve(x0, graph=args.graph)
     ms = tm.stop() / n
     flops = d.flops_per_solve()
-    log(f"flow q8 30 s: {ms:.2f} ms/solve, RTF {ms / 1e3 / 30.0:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
+    log(f"flow q8 ({profile}) 30 s: {ms:.2f} ms/solve, RTF {ms / 1e3 / 30.0:.2e}, "
+        f"{flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
     return {"ms": ms, "flops": flops, "T": T}
 
 
@@ -427,8 +459,9 @@ def cpu_hift(tensors, meta):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256, help="decode tokens timed")
-    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens first")
+    ap.add_argument("--steps", type=int, default=10,
+                    help=f"timed steps; one step is one greedy decode of {DECODE_TOKENS} tokens from KV {PREFILL}")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed decodes first")
     ap.add_argument("--flow-solves", type=int, default=3)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--profile", default="per_channel", choices=["per_channel", "balanced"],
@@ -453,8 +486,8 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is "
               "described in DESIGN.md and is not measured", file=sys.stderr)
         sys.exit(2)
-    if PREFILL + args.warmup + args.steps + 1 >= 1024 or PREFILL + args.steps + 1 >= 1024:
-        sys.exit("decode length does not fit the 1024-position cache")
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be at least 1 and --warmup at least 0")
 
     from cv3amd import _lib
     _lib.lib()
@@ -464,6 +497,9 @@ def main():
 
     copy_bps = copy_bandwidth()
     log(f"device copy: {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")
+    mfma_fps = mfma_peak(info["cu_count"])
+    log(f"fp32 MFMA probe: {mfma_fps / 1e12:.1f} TFLOP/s (v_mfma_f32_32x32x2f32 on registers, "
+        f"{info['cu_count']} workgroups x 8 waves)")
     t0 = time.time()
     lm_t, lm_meta = build_lm(args.layers, args.profile)
     log(f"LM weights ready ({time.time() - t0:.1f} s)")
@@ -473,7 +509,8 @@ def main():
         t0 = time.time()
         tiny_t, tiny_meta = build_lm(args.layers, "tiny")
         log(f"LM weights, tiny profile (q4 body), ready ({time.time() - t0:.1f} s)")
-        tiny = bench_decode(args, tiny_t, tiny_meta, label="decode tiny")
+        tiny = bench_decode(args, tiny_t, tiny_meta, label="decode tiny", decodes=max(1, min(args.steps, 3)),
+                            warmup=1)
         del tiny_t
 
     flow = flow_q8 = None
@@ -484,7 +521,7 @@ def main():
         dit_meta = synth.dit_meta(depth=22)
         flow = bench_flow(args, dit_t, dit_meta)
         if not args.no_flow_q8:
-            flow_q8 = bench_flow_q8(args, dit_t, dit_meta)
+            flow_q8 = {p: bench_flow_q8(args, dit_t, dit_meta, p) for p in ("per_channel", "balanced")}
 
     voc = None
     hift_t = hift_meta = None
@@ -500,11 +537,14 @@ def main():
     cpu_hift_s = None
     if not args.no_cpu:
         log(f"cpu baseline: oracle decode of {args.cpu_tokens} tokens on {cores} host cores")
-        cpu_tok_s, cpu_dt = cpu_decode(lm_t, lm_meta, args.cpu_tokens)
+        cpu_tok_s, cpu_dt, cpu_toks = cpu_decode(lm_t, lm_meta, args.cpu_tokens)
         log(f"cpu baseline: {cpu_tok_s:.2f} tok/s ({cpu_dt:.1f} s)")
+        if cpu_toks != dec["tokens"][:len(cpu_toks)]:
+            raise RuntimeError("the oracle's greedy tokens differ from the device decode's")
         cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-               "sample": f"{args.cpu_tokens} greedy tokens of the same 24-layer per-channel int8 decode "
-                         f"(KV 513..{PREFILL + args.cpu_tokens}) by the oracle's NumPy restatement, "
+               "sample": f"tokens 2..{args.cpu_tokens + 1} of the same 24-layer per-channel int8 greedy decode "
+                         f"(KV {PREFILL + 1}->{PREFILL + 1 + args.cpu_tokens}, after one untimed token) by the "
+                         f"oracle's NumPy restatement, its tokens identical to the device's; "
                          f"OpenBLAS threads = {cores}, host '{cpu_model()}'"}
         if flow is not None:
             log("cpu baseline: one 22-block estimator evaluation of the oracle")
@@ -527,7 +567,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dec["ms"] / args.steps, 5),
+        "ms_per_step": round(dec["ms"], 4),
+        "ms_per_token": round(dec["ms"] / DECODE_TOKENS, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -535,8 +576,9 @@ def main():
         else "f32 (int8 weights, block-64 f16 scales)",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) KV prefill)",
         "config": {"workload": f"Qwen2-0.5B greedy decode, batch 1, {args.layers} layers, hidden 896, 14/2 heads x 64, "
-                               f"SwiGLU 4864, int8 {args.profile}, KV {PREFILL}->{PREFILL + args.steps}",
-                   "decode_tokens": args.steps, "kv_prefill": PREFILL},
+                               f"SwiGLU 4864, int8 {args.profile}; one step = one decode of {DECODE_TOKENS} "
+                               f"tokens, KV {PREFILL}->{PREFILL + DECODE_TOKENS}",
+                   "decode_tokens": DECODE_TOKENS, "kv_prefill": PREFILL},
         "hbm_roofline_frac": round(dec["bytes_per_token"] * dec["tok_s"] / HBM_PEAK, 4),
         "bytes_per_token": dec["bytes_per_token"],
         "roofline": {"bound": "hbm", "achieved": round(step_k["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
@@ -552,6 +594,7 @@ def main():
                          "us_per_launch": round(kern["us_per_launch"], 3)}},
         "cpu_baseline": cpu,
         "copy_GBps": round(copy_bps / 1e9, 1),
+        "mfma_f32_probe_TFLOPs": round(mfma_fps / 1e12, 2),
         "tokens_head": dec["tokens"][:8],
         "sampled_tok_s": round(dec["sampled_tok_s"], 2),
     }
@@ -560,9 +603,10 @@ def main():
         tsk = tiny["step_kernel"] if tiny["persistent"] else tk
         line["decode_tiny"] = {
             "workload": f"the same decode with the tiny profile: Qwen2 body layers q4 (block 32, f16 scales), "
-                        f"head and speech embedding q8, KV {PREFILL}->{PREFILL + args.steps}",
+                        f"head and speech embedding q8, KV {PREFILL}->{PREFILL + DECODE_TOKENS}",
+            "decodes_timed": tiny["decodes"],
             "decode_step": "one kernel launch per token" if tiny["persistent"] else "five kernels per layer",
-            "tok_s": round(tiny["tok_s"], 2), "ms_per_token": round(tiny["ms"] / args.steps, 5),
+            "tok_s": round(tiny["tok_s"], 2), "ms_per_token": round(tiny["ms"] / DECODE_TOKENS, 5),
             "five_kernel_tok_s": round(tiny["five_kernel_tok_s"], 2),
             "bytes_per_token": tiny["bytes_per_token"],
             "hbm_roofline_frac": round(tiny["bytes_per_token"] * tiny["tok_s"] / HBM_PEAK, 4),
@@ -594,14 +638,17 @@ def main():
                 "sample": "one 22-block estimator evaluation (of the solve's 10) by the oracle, x10 extrapolated"},
         }
     if flow_q8 is not None:
-        line["flow_q8_30s"] = {
-            "workload": "DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
-                        "(block 64, f16 scales) dequantised in the GEMM, fp32 accumulate",
-            "ms_per_solve": round(flow_q8["ms"], 3), "rtf": round(flow_q8["ms"] / 1e3 / 30.0, 6),
-            "tflops": round(flow_q8["flops"] / (flow_q8["ms"] / 1e3) / 1e12, 2),
-            "mfma_roofline_frac": round(flow_q8["flops"] / (flow_q8["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
-            "flops_per_solve": flow_q8["flops"],
-        }
+        scales = {"per_channel": "per-output-channel int8 + float32 scales",
+                  "balanced": "block-64 int8 + float16 scales (the converter's balanced profile)"}
+        for prof, fq in flow_q8.items():
+            line["flow_q8_30s" if prof == "per_channel" else "flow_q8_30s_block64"] = {
+                "workload": f"DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
+                            f"({scales[prof]}) dequantised in the GEMM, fp32 accumulate",
+                "ms_per_solve": round(fq["ms"], 3), "rtf": round(fq["ms"] / 1e3 / 30.0, 6),
+                "tflops": round(fq["flops"] / (fq["ms"] / 1e3) / 1e12, 2),
+                "mfma_roofline_frac": round(fq["flops"] / (fq["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
+                "flops_per_solve": fq["flops"],
+            }
     if voc is not None:
         line["vocoder"] = {
             "workload": "causal HiFTNet, mel [1, 80, 500] (10 s), base 512, ups x8/x5/x3, iSTFT 16/4, fp32; "

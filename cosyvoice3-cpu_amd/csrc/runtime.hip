@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <cstdarg>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -27,33 +28,70 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// Set once by cv3_shutdown: later frees and destroys become no-ops, so objects the
+// host language releases during its own teardown never touch a torn-down runtime.
+static std::atomic<bool> g_shut{false};
+
+static std::mutex g_mu;                          // allocator, stream and graph registries
 static thread_local hipStream_t g_tls_stream = nullptr;
+static std::vector<hipStream_t> g_thread_streams;  // every per-thread stream, for cv3_shutdown
 
 hipStream_t stream_of(cv3_stream_t s) {
   if (s) return reinterpret_cast<hipStream_t>(s);
   if (!g_tls_stream) {
     // Default priority only: streams of different priorities are avoided.
-    if (hipStreamCreateWithFlags(&g_tls_stream, hipStreamNonBlocking) != hipSuccess) g_tls_stream = nullptr;
+    hipStream_t h = nullptr;
+    if (hipStreamCreateWithFlags(&h, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_thread_streams.push_back(h);
+    g_tls_stream = h;
   }
   return g_tls_stream;
+}
+
+static bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusActive;
 }
 
 // ---------------------------------------------------------------------------
 // Caching allocator.  hipFree synchronises the whole device, so the drop-in
 // per-op path (which allocates temporaries on every call) keeps freed blocks in
-// size-class free lists.  A freed block remembers an event recorded on the
-// freeing thread's stream; a later allocation from another stream waits on it.
+// size-class free lists.
+//
+// Stream safety: a block remembers the stream it was allocated on (its home) and
+// every other stream it was used on (cv3_record_stream).  Freeing records one
+// event on each of those streams and on the freeing thread's stream; a later
+// allocation from a different stream waits for all of them, so a block is never
+// handed out while a kernel on any of its streams may still touch it.
+//
+// Graph capture: a block freed while the freeing thread's stream is capturing is
+// still referenced by the graph being built.  It stays allocated and belongs to
+// that graph from cv3_graph_end on; cv3_graph_destroy returns it to the cache
+// behind the graph's last launch.  Allocation during capture reuses only blocks
+// whose pending frees were all recorded on the capturing stream itself (no
+// cross-stream wait inside a capture); a captured graph is launched on its
+// capture stream, or after that stream has been synchronised.
 // ---------------------------------------------------------------------------
 struct Block {
   size_t size;
-  hipEvent_t ready;
-  hipStream_t stream;
+  hipStream_t home;
+  std::vector<hipStream_t> users;                          // streams besides home
+  std::vector<hipEvent_t> events;                          // event pool, grows to #streams
+  std::vector<std::pair<hipStream_t, hipEvent_t>> pending;  // recorded at the last free
 };
 
-static std::mutex g_mu;
 static std::multimap<size_t, void*> g_free;            // size class -> ptr
 static std::unordered_map<void*, Block> g_blocks;      // every live or cached block
 static size_t g_in_use = 0, g_cached = 0;
+static thread_local std::vector<void*> g_tls_deferred;  // freed during this thread's capture
+
+struct GraphExec {
+  hipGraphExec_t exec;
+  std::vector<void*> owned;   // blocks freed while it was being captured
+  hipStream_t last;           // stream of its last launch
+};
+static std::unordered_map<GraphExec*, bool> g_graphs;
 
 static size_t size_class(size_t b) {
   if (b <= 256) return 256;
@@ -66,6 +104,31 @@ static size_t size_class(size_t b) {
   return (b + g - 1) / g * g;
 }
 
+// Records the block's pending events on `streams` and parks it in the free list.
+// Caller holds g_mu.
+static int release_locked(void* ptr, Block& b, const std::vector<hipStream_t>& streams) {
+  b.pending.clear();
+  for (size_t i = 0; i < streams.size(); ++i) {
+    if (i == b.events.size()) {
+      hipEvent_t ev;
+      CV3_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+      b.events.push_back(ev);
+    }
+    CV3_HIP(hipEventRecord(b.events[i], streams[i]));
+    b.pending.emplace_back(streams[i], b.events[i]);
+  }
+  g_free.emplace(b.size, ptr);
+  g_in_use -= b.size;
+  g_cached += b.size;
+  return CV3_OK;
+}
+
+static void add_stream(std::vector<hipStream_t>& v, hipStream_t s) {
+  for (hipStream_t x : v)
+    if (x == s) return;
+  v.push_back(s);
+}
+
 }  // namespace cv3
 
 using namespace cv3;
@@ -75,6 +138,7 @@ extern "C" {
 const char* cv3_last_error(void) { return g_error.c_str(); }
 
 int cv3_init(int device) {
+  CV3_REQUIRE(!g_shut.load(), CV3_EINVAL, "the library has been shut down");
   int n = 0;
   CV3_HIP(hipGetDeviceCount(&n));
   CV3_REQUIRE(n > 0, CV3_EHIP, "no HIP device is visible");
@@ -99,16 +163,27 @@ int cv3_device_info(int* cu_count, int64_t* hbm_bytes, char* name, int name_len)
 
 int cv3_malloc(void** ptr, size_t bytes) {
   CV3_REQUIRE(ptr, CV3_EINVAL, "null output pointer");
+  CV3_REQUIRE(!g_shut.load(), CV3_EINVAL, "the library has been shut down");
   const size_t sz = size_class(bytes ? bytes : 1);
   hipStream_t cur = stream_of(nullptr);
+  CV3_REQUIRE(cur, CV3_EHIP, "could not create the calling thread's stream");
+  const bool cap = capturing(cur);
   {
     std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_free.find(sz);
-    if (it != g_free.end()) {
+    auto range = g_free.equal_range(sz);
+    for (auto it = range.first; it != range.second; ++it) {
       void* p = it->second;
-      g_free.erase(it);
       Block& b = g_blocks[p];
-      if (b.stream != cur) hipStreamWaitEvent(cur, b.ready, 0);
+      bool ok = true;
+      if (cap)
+        for (auto& pe : b.pending) ok = ok && pe.first == cur;
+      if (!ok) continue;
+      for (auto& pe : b.pending)
+        if (pe.first != cur) CV3_HIP(hipStreamWaitEvent(cur, pe.second, 0));
+      g_free.erase(it);
+      b.pending.clear();
+      b.home = cur;
+      b.users.clear();
       g_cached -= sz;
       g_in_use += sz;
       *ptr = p;
@@ -117,44 +192,58 @@ int cv3_malloc(void** ptr, size_t bytes) {
   }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, sz);
-  if (e != hipSuccess) {
+  if (e != hipSuccess && !cap) {
     // Out of memory: release the cache and try once more.
     cv3_empty_cache();
     (void)hipGetLastError();
     e = hipMalloc(&p, sz);
   }
   if (e != hipSuccess) return fail(CV3_EHIP, "hipMalloc(%zu) failed: %s", sz, hipGetErrorString(e));
-  hipEvent_t ev;
-  CV3_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   std::lock_guard<std::mutex> lk(g_mu);
-  g_blocks[p] = Block{sz, ev, cur};
+  g_blocks[p] = Block{sz, cur, {}, {}, {}};
   g_in_use += sz;
   *ptr = p;
   return CV3_OK;
 }
 
+int cv3_record_stream(void* ptr, cv3_stream_t s) {
+  if (!ptr || g_shut.load()) return CV3_OK;
+  hipStream_t st = stream_of(s);
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_blocks.find(ptr);
+  CV3_REQUIRE(it != g_blocks.end(), CV3_EINVAL, "cv3_record_stream of a pointer not from cv3_malloc");
+  if (st != it->second.home) add_stream(it->second.users, st);
+  return CV3_OK;
+}
+
 int cv3_free(void* ptr) {
-  if (!ptr) return CV3_OK;
+  if (!ptr || g_shut.load()) return CV3_OK;
   hipStream_t cur = stream_of(nullptr);
+  CV3_REQUIRE(cur, CV3_EHIP, "could not create the calling thread's stream");
+  if (capturing(cur)) {   // the graph being captured may still refer to it
+    std::lock_guard<std::mutex> lk(g_mu);
+    CV3_REQUIRE(g_blocks.count(ptr), CV3_EINVAL, "cv3_free of a pointer not from cv3_malloc");
+    g_tls_deferred.push_back(ptr);
+    return CV3_OK;
+  }
   std::lock_guard<std::mutex> lk(g_mu);
   auto it = g_blocks.find(ptr);
   CV3_REQUIRE(it != g_blocks.end(), CV3_EINVAL, "cv3_free of a pointer not from cv3_malloc");
   Block& b = it->second;
-  b.stream = cur;
-  CV3_HIP(hipEventRecord(b.ready, cur));
-  g_free.emplace(b.size, ptr);
-  g_in_use -= b.size;
-  g_cached += b.size;
-  return CV3_OK;
+  std::vector<hipStream_t> streams{b.home};
+  for (hipStream_t u : b.users) add_stream(streams, u);
+  add_stream(streams, cur);
+  return release_locked(ptr, b, streams);
 }
 
 int cv3_empty_cache(void) {
+  if (g_shut.load()) return CV3_OK;
   std::lock_guard<std::mutex> lk(g_mu);
   for (auto& kv : g_free) {
     auto it = g_blocks.find(kv.second);
     if (it != g_blocks.end()) {
-      hipEventSynchronize(it->second.ready);
-      hipEventDestroy(it->second.ready);
+      for (auto& pe : it->second.pending) hipEventSynchronize(pe.second);
+      for (hipEvent_t ev : it->second.events) hipEventDestroy(ev);
       g_cached -= it->second.size;
       g_blocks.erase(it);
     }
@@ -201,7 +290,7 @@ int cv3_stream_create(cv3_stream_t* s) {
 }
 
 int cv3_stream_destroy(cv3_stream_t s) {
-  if (s) CV3_HIP(hipStreamDestroy(reinterpret_cast<hipStream_t>(s)));
+  if (s && !g_shut.load()) CV3_HIP(hipStreamDestroy(reinterpret_cast<hipStream_t>(s)));
   return CV3_OK;
 }
 
@@ -223,7 +312,7 @@ int cv3_event_create(void** ev) {
 }
 
 int cv3_event_destroy(void* ev) {
-  if (ev) CV3_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  if (ev && !g_shut.load()) CV3_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
   return CV3_OK;
 }
 
@@ -245,28 +334,88 @@ int cv3_event_elapsed_ms(void* ev0, void* ev1, float* ms) {
 }
 
 int cv3_graph_begin(cv3_stream_t s) {
+  CV3_REQUIRE(g_tls_deferred.empty(), CV3_EINVAL, "a capture is already in progress on this thread");
   CV3_HIP(hipStreamBeginCapture(stream_of(s), hipStreamCaptureModeThreadLocal));
   return CV3_OK;
 }
 
 int cv3_graph_end(cv3_stream_t s, void** exec) {
   hipGraph_t g = nullptr;
-  CV3_HIP(hipStreamEndCapture(stream_of(s), &g));
+  hipStream_t st = stream_of(s);
+  std::vector<void*> owned;
+  owned.swap(g_tls_deferred);
+  hipError_t e = hipStreamEndCapture(st, &g);
   hipGraphExec_t x = nullptr;
-  hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
-  if (e != hipSuccess) return fail(CV3_EHIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
-  *exec = x;
+  if (e == hipSuccess) {
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+  }
+  if (e != hipSuccess) {
+    // nothing was captured for good: the deferred blocks go back behind the stream
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (void* p : owned) {
+      auto it = g_blocks.find(p);
+      if (it != g_blocks.end()) release_locked(p, it->second, {it->second.home, st});
+    }
+    return fail(CV3_EHIP, "graph capture failed: %s", hipGetErrorString(e));
+  }
+  GraphExec* w = new GraphExec{x, std::move(owned), st};
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_graphs[w] = true;
+  *exec = w;
   return CV3_OK;
 }
 
 int cv3_graph_launch(void* exec, cv3_stream_t s) {
-  CV3_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), stream_of(s)));
+  CV3_REQUIRE(exec, CV3_EINVAL, "null graph");
+  GraphExec* w = reinterpret_cast<GraphExec*>(exec);
+  hipStream_t st = stream_of(s);
+  CV3_HIP(hipGraphLaunch(w->exec, st));
+  w->last = st;
   return CV3_OK;
 }
 
 int cv3_graph_destroy(void* exec) {
-  if (exec) CV3_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)));
+  if (!exec || g_shut.load()) return CV3_OK;
+  GraphExec* w = reinterpret_cast<GraphExec*>(exec);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_graphs.erase(w)) return fail(CV3_EINVAL, "cv3_graph_destroy of an unknown graph");
+  for (void* p : w->owned) {   // behind the graph's last launch
+    auto it = g_blocks.find(p);
+    if (it != g_blocks.end()) {
+      std::vector<hipStream_t> streams{it->second.home};
+      for (hipStream_t u : it->second.users) add_stream(streams, u);
+      add_stream(streams, w->last);
+      release_locked(p, it->second, streams);
+    }
+  }
+  hipError_t e = hipGraphExecDestroy(w->exec);
+  delete w;
+  if (e != hipSuccess) return fail(CV3_EHIP, "hipGraphExecDestroy failed: %s", hipGetErrorString(e));
+  return CV3_OK;
+}
+
+int cv3_shutdown(void) {
+  if (g_shut.exchange(true)) return CV3_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return CV3_OK;   // the runtime was never brought up
+  hipDeviceSynchronize();
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& kv : g_graphs) {
+    hipGraphExecDestroy(kv.first->exec);
+    delete kv.first;
+  }
+  g_graphs.clear();
+  for (auto& kv : g_blocks) {
+    for (hipEvent_t ev : kv.second.events) hipEventDestroy(ev);
+    hipFree(kv.first);
+  }
+  g_blocks.clear();
+  g_free.clear();
+  g_in_use = g_cached = 0;
+  for (hipStream_t st : g_thread_streams) hipStreamDestroy(st);
+  g_thread_streams.clear();
+  g_tls_stream = nullptr;
   return CV3_OK;
 }
 

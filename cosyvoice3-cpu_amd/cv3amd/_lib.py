@@ -11,6 +11,7 @@ There is no CPU fallback: if the library is missing, or no GPU is visible,
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import re
@@ -118,13 +119,24 @@ def call(name: str, *args):
 
 
 def init(device: int = 0):
-    """Select the device once per process (raises if no GPU is visible)."""
+    """Select the device once per process (raises if no GPU is visible).  Registers
+    :func:`shutdown` to run at interpreter exit."""
     global _inited
     if not _inited:
         with _lock:
             if not _inited:
                 call("init", device)
+                atexit.register(shutdown)
                 _inited = True
+
+
+def shutdown():
+    """Release every device object the library holds (graphs, blocks, per-thread streams)
+    after synchronising the device.  Runs from ``atexit``, i.e. before the interpreter
+    tears down the objects that own those handles and before the HIP runtime's own
+    exit handlers; device arrays, events and graphs released after it are no-ops."""
+    if _lib is not None and _inited:
+        _lib.cv3_shutdown()
 
 
 def device_info():

@@ -120,6 +120,13 @@ class DeviceArray:
             _lib.call("copy_h2d", self.ptr, a.ctypes.data, a.nbytes, None)
         return self
 
+    def record_stream(self, stream) -> "DeviceArray":
+        """Declare that work on ``stream`` (a :class:`Stream`) uses this array, so its block
+        is not reused before that work is done."""
+        if stream is not None:
+            _lib.call("record_stream", self._block.ptr, stream.handle)
+        return self
+
     def zero_(self) -> "DeviceArray":
         if self.nbytes:
             _lib.call("fill_zero", self.ptr, self.nbytes, None)

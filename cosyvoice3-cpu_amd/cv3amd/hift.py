@@ -120,6 +120,7 @@ class DeviceHiFT:
         # captured spectral stacks, one per input length: (graph, mel in, source STFT in, out, arena)
         self._graphs = {}
         self._streams: List[Stream] = []
+        self._recorded = set()   # (width, slot, stream) whose stack buffers are recorded on the stream
         self._arena = None       # while recording or capturing: every intermediate of the stack
         self._arena_i = -1       # >= 0 while capturing: the next arena entry to hand out
 
@@ -292,10 +293,15 @@ class DeviceHiFT:
         t = mel.shape[1]
         c1 = t if c1 is None else c1
         w = c1 - c0
-        graph, mel_w, st_w, out, _ = self._stack(w, slot)
+        graph, mel_w, st_w, out, arena = self._stack(w, slot)
         S3 = ctypes.c_int64 * 3
         up = self.up_total
         sh = stream.handle if stream is not None else None
+        if sh is not None and (w, slot, sh) not in self._recorded:
+            # the stack's buffers are used on that stream: their blocks wait for it when freed
+            for a in (mel_w, st_w, out, *arena):
+                a.record_stream(stream)
+            self._recorded.add((w, slot, sh))
         _lib.call("copy_strided", mel.ptr + c0 * F4, mel_w.ptr, 1, mel.shape[0], w, S3(0, t, 1), S3(0, w, 1), sh)
         fs = s_stft.shape[1]
         f0, f1 = c0 * up, min(fs, c1 * up + 1)
@@ -327,6 +333,7 @@ class DeviceHiFT:
             ready = Event().record()
             for st in streams:
                 st.wait(ready)
+                out.record_stream(st)
         for i, m0 in enumerate(starts):
             m1 = min(t, m0 + chunk)
             c0 = max(0, m0 - context)

@@ -16,6 +16,7 @@ writeable array is re-uploaded on every call because it may change.
 
 from __future__ import annotations
 
+import threading
 import weakref
 from dataclasses import dataclass
 from typing import Dict, Optional
@@ -39,6 +40,7 @@ class DeviceQ:
 
 
 _CACHE: Dict[int, object] = {}
+_UPLOAD = threading.Lock()   # one upload per weight object when several threads miss at once
 
 
 def _remember(obj, value):
@@ -53,6 +55,12 @@ def device_qtensor(qt) -> DeviceQ:
     hit = _CACHE.get(id(qt))
     if hit is not None:
         return hit
+    with _UPLOAD:
+        hit = _CACHE.get(id(qt))
+        return hit if hit is not None else _upload_qtensor(qt)
+
+
+def _upload_qtensor(qt) -> DeviceQ:
     kind = {"q8": _lib.KIND_Q8, "q4": _lib.KIND_Q4}[qt.kind]
     sdt = np.dtype(qt.scales.dtype)
     sc_code = _lib.F16 if sdt == np.float16 else _lib.F32
@@ -71,7 +79,9 @@ def device_f32(arr) -> DeviceArray:
         hit = _CACHE.get(id(arr))
         if hit is not None:
             return hit
-        return _remember(arr, to_device(arr, np.float32))
+        with _UPLOAD:
+            hit = _CACHE.get(id(arr))
+            return hit if hit is not None else _remember(arr, to_device(arr, np.float32))
     return to_device(np.asarray(arr), np.float32)
 
 

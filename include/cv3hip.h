@@ -72,7 +72,10 @@ const char* cv3_last_error(void);
 int cv3_init(int device);
 int cv3_device_info(int* cu_count, int64_t* hbm_bytes, char* arch_name, int name_len);
 int cv3_malloc(void** ptr, size_t bytes); /* stream-aware caching allocator */
-int cv3_free(void* ptr);
+int cv3_free(void* ptr);    /* behind every stream the block was used on; deferred to the graph if capturing */
+/* Marks a block as used on stream s too, so its free waits for s (no counterpart in the reference, whose
+ * arrays are host memory: the device analogue of a tensor used on a second stream). */
+int cv3_record_stream(void* ptr, cv3_stream_t s);
 int cv3_empty_cache(void);
 int cv3_mem_stats(size_t* in_use, size_t* cached);
 int cv3_copy_h2d(void* dst, const void* src, size_t bytes, cv3_stream_t s); /* returns when done */
@@ -94,6 +97,14 @@ int cv3_graph_begin(cv3_stream_t s);
 int cv3_graph_end(cv3_stream_t s, void** exec);
 int cv3_graph_launch(void* exec, cv3_stream_t s);
 int cv3_graph_destroy(void* exec);
+/* Synchronises the device and releases every graph, cached or live block and per-thread stream; afterwards
+ * frees and destroys are no-ops (no counterpart in the reference: called once at process exit, before the
+ * HIP runtime's own teardown). */
+int cv3_shutdown(void);
+/* fp32 matrix-core rate probe: workgroups x 512 threads, each wave `iters` rounds of four independent
+ * v_mfma_f32_32x32x2f32 on registers; *flops = the flops issued; out holds workgroups*512 floats (no
+ * counterpart in the reference: the measured ceiling beside the published 157.3 TFLOP/s). */
+int cv3_mfma_peak_f32(int64_t iters, int64_t workgroups, float* out, double* flops, cv3_stream_t s);
 
 /* ---------------- host RNG (cv3cpu/torch_rng.py; host memory, host code) ---------------- */
 int cv3_mt_create(uint64_t seed, void** gen);                   /* TorchMT19937.__init__  torch_rng.py:30 */

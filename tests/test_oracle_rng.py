@@ -57,12 +57,36 @@ def _lib_normal(seed, n):
     return out
 
 
+def _check_library_against_oracle(torch_rng_golden, seed, n):
+    got = _lib_normal(seed, n)
+    ref = randn((n,), seed)
+    assert got.dtype == ref.dtype and np.array_equal(got, ref), \
+        f"{int((got != ref).sum())} of {n} samples differ, max {np.abs(got - ref).max():.3g}"
+    key = {5: "5", 17: "17", 1000: "1000", 80 * 15000: "1x80x15000"}[n]
+    _check(torch_rng_golden[f"randn_{seed}_{key}"], got.reshape(torch_rng_golden[f"randn_{seed}_{key}"]["shape"]))
+
+
 @pytest.mark.parametrize("seed", [0, 42])
 @pytest.mark.parametrize("n", [5, 17, 1000, 80 * 15000])
 def test_library_host_rng_matches_oracle(torch_rng_golden, seed, n):
-    """The shipped host RNG (C++ in libcv3hip.so, no GPU needed) reproduces the oracle."""
-    got = _lib_normal(seed, n)
-    ref = randn((n,), seed)
-    assert np.abs(got - ref).max() <= 1e-6
-    key = {5: "5", 17: "17", 1000: "1000", 80 * 15000: "1x80x15000"}[n]
-    _check(torch_rng_golden[f"randn_{seed}_{key}"], got.reshape(torch_rng_golden[f"randn_{seed}_{key}"]["shape"]))
+    """The shipped host RNG (C++ in libcv3hip.so, no GPU needed) reproduces the oracle
+    bit for bit, including the ODE noise torch.randn((1, 80, 15000)) of seed 0."""
+    _check_library_against_oracle(torch_rng_golden, seed, n)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 42])
+@pytest.mark.parametrize("n", [17, 80 * 15000])
+def test_library_host_rng_matches_oracle_on_the_gpu_host(torch_rng_golden, seed, n):
+    """The same bit-identity on the host that runs the device workloads (its libm
+    and NumPy draw the noise the flow solve starts from)."""
+    _check_library_against_oracle(torch_rng_golden, seed, n)
+
+
+def test_bench_noise_digest_is_the_oracles():
+    """The SHA-256 bench.py checks the host's ODE noise against is the oracle's
+    torch.randn((1, 80, 15000)) of seed 0, which the frozen torch samples pin above."""
+    import hashlib
+    import bench
+    got = hashlib.sha256(np.ascontiguousarray(randn((1, 80, 15000), 0), np.float32).tobytes()).hexdigest()
+    assert got == bench.NOISE_SHA256
