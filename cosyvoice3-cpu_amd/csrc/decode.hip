@@ -29,6 +29,8 @@
 // packed nibbles (byte j: code j in the low nibble, code j + 16 in the high one,
 // stored +8; quant.py:70-86,123-131), so the tiny profile's body layers stream
 // half the bytes through the same kernels.
+#include <mutex>
+
 #include "common.hpp"
 #include "epilogue.hpp"
 
@@ -1853,6 +1855,72 @@ int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_stat
                                   cv3_stream_t stream) {
   CV3_REQUIRE(smp, CV3_EINVAL, "null sampler");
   return decode_step(m, s, smp, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The decode step without a caller workspace: its q / attention-partial /
+// SwiGLU buffers live in a fixed device array, so a caller that cannot
+// allocate (graph capture, a serving loop that forbids hipMalloc) still gets a
+// step.  Nothing in that scratch must start at zero: every piece a kernel reads
+// was written earlier in the same step (q and h by their GEMVs, the partials of
+// chunks 0..pos/64 by the attention kernel, and only those are merged).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kScratchInterMax = 16384;
+constexpr int64_t kScratchFloats = kWsQ + 16 * NSMAX * 64 + ((16 * NSMAX * 2 + 3) / 4) * 4 + kScratchInterMax + 64;
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices] = {};   // per device: the device address of `scratch`
+
+// The device address of this device's copy of `scratch` (looked up once per device, with
+// that device current); nullptr and the error text set on failure.
+float* scratch_of_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    fail(CV3_EHIP, "decode scratch: no current device below %d", kScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(CV3_EHIP, "hipGetSymbolAddress(decode scratch) failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+namespace cv3 {
+// Called by cv3_init with the selected device current.
+int decode_scratch_setup() { return scratch_of_current_device() ? CV3_OK : CV3_EHIP; }
+}  // namespace cv3
+
+extern "C" {
+
+int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
+  const int64_t H = m->heads, I = m->inter;
+  CV3_REQUIRE(H > 0 && H <= 16 && I > 0 && I <= kScratchInterMax, CV3_EINVAL,
+              "decode step without workspace: %lld heads and intermediate size %lld exceed its fixed scratch "
+              "(at most 16 heads and an intermediate size of %lld, %lld floats)",
+              (long long)H, (long long)I, (long long)kScratchInterMax, (long long)kScratchFloats);
+  float* ws = scratch_of_current_device();
+  if (!ws) return CV3_EHIP;
+  cv3_qwen2_state t = *s;
+  t.workspace = ws;
+  t.workspace_floats = kScratchFloats;
+  return decode_step(m, &t, nullptr, stream);
 }
 
 // Words between replicas of an n-word vector: whole 4 KiB pages plus 512 bytes,

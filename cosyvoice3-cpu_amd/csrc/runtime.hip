@@ -36,6 +36,8 @@ static std::mutex g_mu;                          // allocator, stream and graph 
 static thread_local hipStream_t g_tls_stream = nullptr;
 static std::vector<hipStream_t> g_thread_streams;  // every per-thread stream, for cv3_shutdown
 
+int decode_scratch_setup();   // decode.hip: looks up its fixed scratch on the current device
+
 hipStream_t stream_of(cv3_stream_t s) {
   if (s) return reinterpret_cast<hipStream_t>(s);
   if (!g_tls_stream) {
@@ -145,7 +147,7 @@ int cv3_init(int device) {
   CV3_REQUIRE(device >= 0 && device < n, CV3_EINVAL, "device %d out of range (have %d)", device, n);
   CV3_HIP(hipSetDevice(device));
   CV3_HIP(hipFree(nullptr));
-  return CV3_OK;
+  return decode_scratch_setup();
 }
 
 int cv3_device_info(int* cu_count, int64_t* hbm_bytes, char* name, int name_len) {

@@ -309,6 +309,13 @@ typedef struct {
  * x = speech_embedding[id] (llm.py:121), history[pos + 1] = id, pos += 1.  Reads pos from device
  * memory, so one captured graph of this call serves every step.  The caller keeps pos + 1 < cap. */
 int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
+/* cv3_qwen2_decode_step without a caller workspace, for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc): no counterpart in the reference.  s->workspace and
+ * s->workspace_floats are ignored; the step's scratch is a fixed device array of the library (137.5 KB, held
+ * on each device until the process ends), so it allocates nothing.  Geometries beyond that scratch (more than
+ * 16 heads, or an intermediate size above 16384) are rejected.  Every call on one device shares the array:
+ * calls that overlap on one device race. */
+int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
 /* The decode step's q8 / q4 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
  * y = W . v with v = x, or v = rms_norm(x, rms_w, eps) when rms_w is given (ops.py:101-104).
  * mode 0: y = W v + bias (bias may be NULL); 1: y += W v; 2: rows are [gate; up] (rows/2 each) and
