@@ -375,6 +375,119 @@ def bench_flow_q8(args, tensors, meta, profile: str):
     return {"ms": ms, "flops": flops, "T": T}
 
 
+def bench_dit_kernels(args):
+    """Each launch of one DiT block at the 10 s solve's shapes (T = 500, CFG batch 2), timed alone:
+    `reps` back-to-back launches of the same kernel, replayed from a captured graph, on the buffers
+    a real estimator evaluation left behind; then the 30 s q8 GEMMs (block-64 / f16 weights).
+    For profiling single kernels (rocprofv3 --pmc passes) and for the per-kernel roofline table."""
+    import ctypes
+    import math
+    import cv3amd.quant as quant
+    from cv3amd import _lib, synth
+    from cv3amd.device import Timer, synchronize
+    from cv3amd.dit import DeviceDiT
+    from cv3amd.weights import WeightStore
+    T, B = 500, 2
+    info = _lib.device_info()
+    copy_bps = copy_bandwidth()   # also the known-size kernel the traffic counters are scaled by
+    log(f"dit kernels: device copy {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")
+    peak = mfma_peak(info["cu_count"])
+    log(f"dit kernels: fp32 MFMA probe {peak / 1e12:.1f} TFLOP/s (k_mfma_peak, the matrix-core busy reference)")
+    tensors, meta = synth.dit_tensors(depth=2), synth.dit_meta(depth=2)
+    d = DeviceDiT(WeightStore(tensors, meta, quant.QTensor))
+    mu, cond, spks, x0 = flow_inputs(T)
+    d.prepare(mu, spks, cond)
+    d.solve(x0, graph=False)
+    synchronize()
+    D, H, dh, F = d.dim, d.heads, d.dim_head, d.ff_dim
+    BT = B * T
+    f4 = 4
+    S3 = ctypes.c_int64 * 3
+    qs = S3(T * 3 * D, dh, 3 * D)
+    os_ = S3(T * D, dh, D)
+    scale = float(np.float32(1.0 / math.sqrt(dh)))
+    rope_epi = _lib.epilogue(rope=(d.cos.ptr, d.sin.ptr, T, D, dh, 2 * D))
+    g = d.mods.ptr   # any AdaLN row: the timing does not depend on its values
+    res_epi = _lib.epilogue(residual=d.h.ptr, ld_res=D, gate=g, gate_stride=0, rows_per_gate=1)
+    k = d.conv_k
+    mish = _lib.epilogue("mish")
+    launches = {
+        "layer_norm + AdaLN [1000, 1024]": (
+            lambda: _lib.call("layer_norm", d.h.ptr, d.n.ptr, BT, D, 1e-6, None, None, g, g + D * f4, 0, 0, None),
+            None),
+        f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T + rotary": (
+            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D, rope_epi), 2.0 * BT * 3 * D * D),
+        f"flash attention B={B} H={H} T={T} d={dh}": (
+            lambda: _lib.call("attention", d.qkvb.ptr, d.qkvb.ptr + D * f4, d.qkvb.ptr + 2 * D * f4, d.att.ptr,
+                              B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None), 4.0 * B * H * T * T * dh),
+        f"out GEMM [{BT}, {D}] x [{D}, {D}]^T + gated residual": (
+            lambda: d.out[0](d.att.ptr, BT, D, d.z1.ptr, D, res_epi), 2.0 * BT * D * D),
+        f"ff1 GEMM [{BT}, {D}] x [{F}, {D}]^T + GELU": (
+            lambda: d.ff1[0](d.n.ptr, BT, D, d.ffb.ptr, F, _lib.epilogue("gelu_tanh")), 2.0 * BT * F * D),
+        f"ff2 GEMM [{BT}, {F}] x [{D}, {F}]^T + gated residual": (
+            lambda: d.ff2[0](d.ffb.ptr, BT, F, d.z1.ptr, D, res_epi), 2.0 * BT * D * F),
+        f"grouped causal conv k={k} groups={d.conv_groups} [{B}, {T}, {D}] + Mish": (
+            lambda: _lib.call("conv1d_cl", d.h.ptr, B, T, D, D, d.conv_w[0].ptr, D, k, d.conv_groups, k - 1,
+                              d.conv_b[0].ptr, d.z1.ptr, D, ctypes.byref(mish), None),
+            2.0 * BT * D * (D // d.conv_groups) * k),
+    }
+    out = {}
+    reps = args.kernel_reps
+    tm = Timer()
+    for name, (fn, flops) in launches.items():
+        run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
+        run()
+        synchronize()
+        tm.start()
+        for _ in range(5):
+            run()
+        us = tm.stop() / (5 * reps) * 1e3
+        rate = flops / (us * 1e-6) / 1e12 if flops else None
+        log(f"dit kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / 157.3:.1%} of fp32 MFMA peak)"
+                                                   if rate else ""))
+        out[name] = {"us": round(us, 2), "tflops": round(rate, 2) if rate else None}
+    # the 30 s solve's q8 GEMMs (int8 B dequantised on its way into LDS), block-64 / f16 scales
+    T3 = 1500
+    BT3 = B * T3
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((BT3, F), dtype=np.float32)
+    from cv3amd.device import to_device, DeviceArray
+    a_d = to_device(a)
+    for (n, kk, label) in ((3 * D, D, "QKV"), (F, D, "ff1"), (D, D, "out"), (D, F, "ff2")):
+        w = to_device(rng.standard_normal((n, kk), dtype=np.float32) * np.float32(0.02))
+        qd, sd, kp = quant.quantize_q8(w, 64, np.float16)   # device quantiser
+        y = DeviceArray((BT3, n), np.float32)
+        fn = lambda: _lib.call("linear_q", _lib.KIND_Q8, a_d.ptr, BT3, kk, F, qd.ptr, sd.ptr, _lib.F16, kp, 64, n,
+                               None, y.ptr, n, None, None)
+        run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
+        run()
+        synchronize()
+        tm.start()
+        for _ in range(5):
+            run()
+        us = tm.stop() / (5 * reps) * 1e3
+        rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
+        name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T (block 64, f16 scales)"
+        log(f"dit kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / 157.3:.1%})")
+        out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
+    out["mfma_probe_tflops"] = round(peak / 1e12, 2)
+    if args.kernel_solve:
+        # the whole 10 s solve (22 blocks, 10 steps, CFG) for the end-to-end figure
+        del d
+        t22, m22 = synth.dit_tensors(depth=22), synth.dit_meta(depth=22)
+        d = DeviceDiT(WeightStore(t22, m22, quant.QTensor))
+        d.prepare(mu, spks, cond)
+        d.solve(x0, graph=args.graph)
+        synchronize()
+        tm.start()
+        for _ in range(3):
+            d.solve(x0, graph=args.graph)
+        ms = tm.stop() / 3
+        log(f"dit kernels: 10 s solve {ms:.2f} ms ({d.flops_per_solve() / (ms / 1e3) / 1e12:.1f} TFLOP/s)")
+        out["solve_10s_ms"] = round(ms, 3)
+    return out
+
+
 def cpu_flow(tensors, meta):
     """One estimator evaluation (22 blocks, the 10-step solve's unit) of the oracle."""
     import oracle.quant
@@ -479,6 +592,12 @@ def main():
     ap.add_argument("--cooperative", action="store_true",
                     help="launch the one-launch step with hipLaunchCooperativeKernel (guaranteed co-residency, "
                          "about 20 us more per token) instead of an ordinary launch")
+    ap.add_argument("--dit-kernels", action="store_true",
+                    help="time each DiT block launch alone at the 10 s shapes (and the 30 s q8 GEMMs), print "
+                         "them as one JSON line and exit: for per-kernel rooflines and rocprofv3 counter passes")
+    ap.add_argument("--kernel-reps", type=int, default=20, help="launches per replay in --dit-kernels")
+    ap.add_argument("--no-kernel-solve", dest="kernel_solve", action="store_false",
+                    help="--dit-kernels without the closing 22-block solve")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
     args = ap.parse_args()
@@ -494,6 +613,9 @@ def main():
     _lib.init(0)
     info = _lib.device_info()
     log(f"device {info['arch']} with {info['cu_count']} CUs")
+    if args.dit_kernels:
+        print(json.dumps({"dit_kernels": bench_dit_kernels(args)}), flush=True)
+        return
 
     copy_bps = copy_bandwidth()
     log(f"device copy: {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")

@@ -71,20 +71,31 @@ constexpr int QT = 64;        // queries per workgroup
 // Scores are kept in base-2 units: q is scaled by log2(e) after the reference's
 // (q * scale), so every exponential is one v_exp_f32 (2^x) instead of an expf
 // range reduction; e^{s - m} = 2^{s log2 e - m log2 e}, to within a few ulp.
+//
+// The grid is one-dimensional, nq query tiles x h heads x batch.  Workgroup w runs on XCD w % 8
+// (round-robin dispatch), and each XCD has its own L2: when the tile count divides by 8, XCD x
+// takes the x-th eighth of the tiles in (batch, head)-major order, so each head's K / V rows
+// are fetched into one L2 and re-read from there by that head's query tiles (otherwise every
+// XCD would hold a query tile of every head and fetch all of K / V).
 template <int NKG>
-__global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
+__global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p, int nq) {
   __shared__ float Ks[NKG][KT * KS];
   __shared__ float Vs[NKG][KT * KS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qw = wave & 3, kg = wave >> 2;
-  const int b = blockIdx.z, hq = blockIdx.y;
+  const int ntiles = (int)gridDim.x;
+  const int wg = (int)blockIdx.x;
+  const int tile = (ntiles & 7) == 0 ? (wg & 7) * (ntiles >> 3) + (wg >> 3) : wg;
+  const int qt = tile % nq, bh = tile / nq;
+  const int b = bh / p.h, hq = bh % p.h;
   const int hkv = hq / (p.h / p.hk);
-  const int64_t q0 = (int64_t)blockIdx.x * QT + qw * QW;
+  const int64_t q0 = (int64_t)qt * QT + qw * QW;
   const int c16 = lane & 15, g = lane >> 4;
   const int64_t qi = q0 + c16;
   const bool qvalid = qi < p.n;
-  int64_t klo, khi;
-  visible_keys(p, qi, klo, khi);
+  int64_t klo64, khi64;
+  visible_keys(p, qi, klo64, khi64);
+  const int klo = (int)klo64, khi = (int)khi64;  // the host bounds m below 2^31 - 64
 
   // Q fragments, pre-scaled like the reference's (q * scale) (ops.py:292)
   f32x4 qf[4];
@@ -130,7 +141,7 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
   }
   CV3_KV_LOAD((int64_t)0)
   for (int64_t st = 0; st < nstages; ++st) {
-    const int64_t k0 = st * NKG * KT + kg * KT;  // first key of this wave's tile
+    const int k0i = (int)(st * NKG * KT + kg * KT);  // first key of this wave's tile
     __syncthreads();
     float* kt_ = Ks[ltile];
     float* vt_ = Vs[ltile];
@@ -151,19 +162,24 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
     const float* Vt = Vs[kg];
 
     // S^T for the tile: sub-tile sub holds keys sub*16 + 4g + i (i < 4) for query column c16
+    // the four sub-tiles' accumulators are independent: consecutive MFMAs go to different ones
     f32x4 s[KT / 16];
 #pragma unroll
-    for (int sub = 0; sub < KT / 16; ++sub) {
-      s[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float* krow = &Kt[(sub * 16 + c16) * KS + g * 4];
+    for (int sub = 0; sub < KT / 16; ++sub) s[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 kf = *reinterpret_cast<const float4*>(krow + s4 * 16);
-        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[s4].x, s[sub], 0, 0, 0);
-        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[s4].y, s[sub], 0, 0, 0);
-        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[s4].z, s[sub], 0, 0, 0);
-        s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[s4].w, s[sub], 0, 0, 0);
-      }
+    for (int s4 = 0; s4 < 4; ++s4) {
+      float4 kf[KT / 16];
+#pragma unroll
+      for (int sub = 0; sub < KT / 16; ++sub)
+        kf[sub] = *reinterpret_cast<const float4*>(&Kt[(sub * 16 + c16) * KS + g * 4 + s4 * 16]);
+#pragma unroll
+      for (int sub = 0; sub < KT / 16; ++sub) s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[sub].x, qf[s4].x, s[sub], 0, 0, 0);
+#pragma unroll
+      for (int sub = 0; sub < KT / 16; ++sub) s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[sub].y, qf[s4].y, s[sub], 0, 0, 0);
+#pragma unroll
+      for (int sub = 0; sub < KT / 16; ++sub) s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[sub].z, qf[s4].z, s[sub], 0, 0, 0);
+#pragma unroll
+      for (int sub = 0; sub < KT / 16; ++sub) s[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[sub].w, qf[s4].w, s[sub], 0, 0, 0);
     }
     // copy out of the accumulators and mask with selects (no divergent writes into them)
     float sc[KT / 16][4];
@@ -172,7 +188,7 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
     for (int sub = 0; sub < KT / 16; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t kj = k0 + sub * 16 + 4 * g + i;
+        const int kj = k0i + sub * 16 + 4 * g + i;
         const bool ok = kj >= klo && kj < khi;
         sc[sub][i] = ok ? s[sub][i] : -INFINITY;
         mx = fmaxf(mx, sc[sub][i]);
@@ -199,15 +215,20 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p) {
     for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
     // O^T += V^T P^T: the A operand of key group i is V^T[db*16 + c16][sub*16 + 4g + i]
 #pragma unroll
-    for (int sub = 0; sub < KT / 16; ++sub)
+    for (int sub = 0; sub < KT / 16; ++sub) {
+      float4 vf[4];
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const float4 vf = *reinterpret_cast<const float4*>(&Vt[(db * 16 + c16) * KS + sub * 16 + 4 * g]);
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, sc[sub][0], oacc[db], 0, 0, 0);
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, sc[sub][1], oacc[db], 0, 0, 0);
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, sc[sub][2], oacc[db], 0, 0, 0);
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, sc[sub][3], oacc[db], 0, 0, 0);
-      }
+      for (int db = 0; db < 4; ++db)
+        vf[db] = *reinterpret_cast<const float4*>(&Vt[(db * 16 + c16) * KS + sub * 16 + 4 * g]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[db].x, sc[sub][0], oacc[db], 0, 0, 0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[db].y, sc[sub][1], oacc[db], 0, 0, 0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[db].z, sc[sub][2], oacc[db], 0, 0, 0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[db].w, sc[sub][3], oacc[db], 0, 0, 0);
+    }
   }
 #undef CV3_KV_LOAD
   // merge the key groups through LDS (each lane's state is per query column)
@@ -345,11 +366,14 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
                          (p.k_sh % 4 == 0) && (p.k_sm % 4 == 0) && (p.v_sb % 4 == 0) && (p.v_sh % 4 == 0) &&
                          (p.v_sm % 4 == 0);
   if (d == 64 && aligned16) {
-    const dim3 grid((unsigned)ceil_div(n, QT), (unsigned)h, (unsigned)batch);
+    CV3_REQUIRE(m < (1ll << 31) - 4 * 64, CV3_EUNSUPPORTED, "attention over 2^31 keys or more");
+    const int64_t nq = ceil_div(n, QT);
+    CV3_REQUIRE(nq * h * batch < (int64_t)1 << 31, CV3_EUNSUPPORTED, "attention grid too large");
+    const dim3 grid((unsigned)(nq * h * batch));
     if (m >= 16 * KT)  // 1024 keys and up: 8 % faster at 1500 keys, no gain at 500
-      hipLaunchKernelGGL(k_flash64<4>, grid, dim3(1024), 0, st, p);
+      hipLaunchKernelGGL(k_flash64<4>, grid, dim3(1024), 0, st, p, (int)nq);
     else
-      hipLaunchKernelGGL(k_flash64<2>, grid, dim3(512), 0, st, p);
+      hipLaunchKernelGGL(k_flash64<2>, grid, dim3(512), 0, st, p, (int)nq);
   } else {
     const dim3 grid((unsigned)ceil_div(n, 4), (unsigned)h, (unsigned)batch);
     hipLaunchKernelGGL(k_attn_generic, grid, dim3(256), 4 * d * sizeof(float), st, p);

@@ -360,7 +360,7 @@ struct ClSrc {
   int r0, r1;              // this lane's two A rows (time)
   const float* b0;         // this lane's two B rows (weight), at its chunk
   const float* b1;
-  int lc;
+  int lc, lc8;             // chunk offsets of rows r0 and r1 (the swizzle of k_gemm_dma)
 };
 
 __device__ __forceinline__ void cl_stage(const ConvCL& p, const ClSrc& s, int sg, float* as, float* bs, int w) {
@@ -373,7 +373,7 @@ __device__ __forceinline__ void cl_stage(const ConvCL& p, const ClSrc& s, int sg
   const int q0 = ok0 ? (p.up == 1 ? u0 : (int)((unsigned)u0 / (unsigned)p.up)) : 0;
   const int q1 = ok1 ? (p.up == 1 ? u1 : (int)((unsigned)u1 / (unsigned)p.up)) : 0;
   const float* a0 = ok0 ? p.x + (int64_t)q0 * p.ldx + c0 + s.lc : g_conv_zero_row + s.lc;
-  const float* a1 = ok1 ? p.x + (int64_t)q1 * p.ldx + c0 + s.lc : g_conv_zero_row + s.lc;
+  const float* a1 = ok1 ? p.x + (int64_t)q1 * p.ldx + c0 + s.lc8 : g_conv_zero_row + s.lc8;
   __builtin_amdgcn_global_load_lds(a0, as + (w * 16) * 32, 16, 0, 0);
   __builtin_amdgcn_global_load_lds(a1, as + (w * 16 + 8) * 32, 16, 0, 0);
   __builtin_amdgcn_global_load_lds(s.b0 + sg * 32, bs + (w * 16) * 32, 16, 0, 0);
@@ -404,13 +404,14 @@ __global__ __launch_bounds__(256) void k_conv_cl_dma(ConvCL p, int tiles_m) {
   const int lr = lane >> 3;
   const int K = p.k * p.cin;
   ClSrc src;
-  src.lc = ((lane & 7) ^ lr) * 4;
+  src.lc = ((lane & 7) ^ (lr >> 1)) * 4;
+  src.lc8 = src.lc ^ 16;
   src.r0 = m0 + w * 16 + lr;
   src.r1 = src.r0 + 8;
   src.b0 = p.w + (int64_t)min(n0 + w * 16 + lr, p.cout - 1) * K + src.lc;
-  src.b1 = p.w + (int64_t)min(n0 + w * 16 + 8 + lr, p.cout - 1) * K + src.lc;
+  src.b1 = p.w + (int64_t)min(n0 + w * 16 + 8 + lr, p.cout - 1) * K + src.lc8;
   const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
-  const int r32 = lane & 31, h = lane >> 5, sw = r32 & 7;
+  const int r32 = lane & 31, h = lane >> 5, sw = (r32 >> 1) & 7;
   const int arow = (wm + r32) * 32, brow = (wn + r32) * 32;
   const int S = K / 32 / p.ksplit;  // this workgroup's stages
   const int sb = blockIdx.z * S;

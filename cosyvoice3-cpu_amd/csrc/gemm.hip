@@ -220,20 +220,31 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16& ac
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = acc[i] + bv;
   if (e.rope_cos) {  // uniform branch, shuffles inside
-    const int64_t cp = col % e.rope_period;
-    const bool rot = col < e.rope_limit && cp < e.rope_width;
-    float cs[16], sn[16];
+    // 32-bit index arithmetic (the host bounds the table and the row count): one modulo for
+    // the lane's first row, then row i % rope_rows = base + offset_i, less rope_rows once
+    // when rope_rows exceeds the 27-row spread of the 16 registers (else a modulo each)
+    const uint32_t rr = (uint32_t)e.rope_rows, rw = (uint32_t)e.rope_width;
+    const uint32_t cp = (uint32_t)col % (uint32_t)e.rope_period;
+    const bool rot = col < e.rope_limit && cp < rw;
+    // most waves hold no rotated column (the DiT rotates 2 x 64 of 3072): skip the table
+    // loads and shuffles there (a wave-uniform branch, so the shuffles stay whole-wave)
+    if (__any(rot)) {
+      const uint32_t first = (uint32_t)(r0 + h * 4) % rr;
+      float cs[16], sn[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t row = min(r0 + (i >> 2) * 8 + h * 4 + (i & 3), p.m - 1);
-      const int64_t ti = (row % e.rope_rows) * e.rope_width + (rot ? cp : 0);
-      cs[i] = e.rope_cos[ti];
-      sn[i] = e.rope_sin[ti];
-    }
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t off = (uint32_t)((i >> 2) * 8 + (i & 3));
+        uint32_t tr = first + off;
+        tr = rr > 27u ? (tr >= rr ? tr - rr : tr) : tr % rr;
+        const uint32_t ti = tr * rw + (rot ? cp : 0u);
+        cs[i] = e.rope_cos[ti];
+        sn[i] = e.rope_sin[ti];
+      }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float other = __shfl_xor(v[i], 1, 64);
-      if (rot) v[i] = (col & 1) ? v[i] * cs[i] + other * sn[i] : v[i] * cs[i] + (-other) * sn[i];
+      for (int i = 0; i < 16; ++i) {
+        const float other = __shfl_xor(v[i], 1, 64);
+        if (rot) v[i] = (col & 1) ? v[i] * cs[i] + other * sn[i] : v[i] * cs[i] + (-other) * sn[i];
+      }
     }
   }
   float g[16], res[16];
@@ -455,8 +466,12 @@ __global__ __launch_bounds__(512) void k_gemm8(GemmParams p, int tiles_m) {
 //
 // A DMA writes 64 lanes x 16 B contiguously; lane l of a wave's load covers tile
 // row r = base + l / 8 and slot l % 8, and fetches the row's 16-byte chunk
-// (l % 8) ^ (r % 8).  Chunk c of row r therefore sits at r * 32 + ((c ^ (r % 8)) * 4)
-// floats, which spreads the eight rows an MFMA read touches over all banks.
+// (l % 8) ^ sw(r) with sw(r) = (r / 2) % 8.  Chunk c of row r therefore sits at
+// r * 32 + ((c ^ sw(r)) * 4) floats.  A 16-byte read is served 16 lanes at a time from
+// a 256-byte bank window, which holds two 128-byte rows: rows r and r + 1 fall in its
+// two halves and (r / 2) % 8 differs across the 8 row pairs of 16 consecutive rows, so
+// the 16 rows a read touches hit 16 distinct 16-byte slots.  (Swizzling by r % 8 gave
+// rows r and r + 8 the same slot: half the LDS cycles were bank-conflict stalls.)
 //
 // Per step: wait until this wave's DMA of the current stage has landed (vmcnt:
 // loads complete in order), barrier (every wave's DMA has landed and every wave
@@ -504,15 +519,16 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmParams p, int tiles_m) {
   const int T = gridDim.x, L = blockIdx.x;
   const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
   const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
-  const int lr = lane >> 3, lc = ((lane & 7) ^ lr) * 4;
+  // rows w*16 + lr (sw = lr / 2) and w*16 + 8 + lr (sw = 4 + lr / 2: the chunk index ^ 4)
+  const int lr = lane >> 3, lc = ((lane & 7) ^ (lr >> 1)) * 4, lc8 = lc ^ 16;
   const float* b = reinterpret_cast<const float*>(p.b);
   DmaSrc src;
   src.a0 = p.a + min(m0 + w * 16 + lr, p.m - 1) * p.lda + lc;
-  src.a1 = p.a + min(m0 + w * 16 + 8 + lr, p.m - 1) * p.lda + lc;
+  src.a1 = p.a + min(m0 + w * 16 + 8 + lr, p.m - 1) * p.lda + lc8;
   src.b0 = b + min(n0 + w * 16 + lr, p.n - 1) * p.ldb + lc;
-  src.b1 = b + min(n0 + w * 16 + 8 + lr, p.n - 1) * p.ldb + lc;
+  src.b1 = b + min(n0 + w * 16 + 8 + lr, p.n - 1) * p.ldb + lc8;
   const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
-  const int r32 = lane & 31, h = lane >> 5, sw = r32 & 7;
+  const int r32 = lane & 31, h = lane >> 5, sw = (r32 >> 1) & 7;
   const int arow = (wm + r32) * BK, brow = (wn + r32) * BK;
   const int64_t S = p.k / BK;
   f32x16 acc = {0.f};
@@ -575,6 +591,10 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   // the branch-free kernel: whole K stages and aligned rows for both operands
   const bool fast = fast_a && fast_b && k % (2 * BK) == 0;
   CV3_REQUIRE(fast || !p.epi.rope_cos, CV3_EUNSUPPORTED, "rotary epilogue needs aligned rows and K %% 64 == 0");
+  CV3_REQUIRE(!p.epi.rope_cos || (p.epi.rope_rows > 0 && p.epi.rope_period > 0 && p.epi.rope_width > 0 &&
+                                  p.epi.rope_rows * p.epi.rope_width < (1ll << 31) && m + 64 < (1ll << 31) &&
+                                  n < (1ll << 31)),
+              CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
   // at most one 64 x 64 tile per CU: the 8-wave kernel keeps two waves per SIMD
   const bool small = tiles_m * tiles_n <= 256;
   // A beyond one XCD's L2: walk groups of 8 M-tiles (the tile order note at the top)
