@@ -1,8 +1,10 @@
 // fp32 GEMM on the CDNA4 matrix cores: C[m, n] = epi(A[m, :k] . W[n, :k]),
 // both operands K-contiguous (the reference's (out, in) weight layout,
 // cv3cpu/ops.py:121-123).  Used for every multi-row linear (the DiT's
-// projections, cv3cpu/quant.py:165-170) and, with an int8 B operand dequantised
-// on its way into LDS, for q8 weights (cv3cpu/quant.py:176-190).
+// projections, cv3cpu/quant.py:165-170) and, with a quantised B operand
+// dequantised on its way into LDS, for q8 and q4 weights (cv3cpu/quant.py:176-204):
+// each code becomes the float32 (code * scale) the reference's dequantisation
+// forms (quant.py:70-86), so only the summation order differs from it.
 //
 // Tiling: a 256-thread workgroup owns a BM x BN = 64 x 64 output tile; each of
 // its four waves owns a 32 x 32 quadrant computed with v_mfma_f32_32x32x2_f32
@@ -39,7 +41,17 @@ struct Stage {
   float4 a0, a1, b0, b1;
 };
 
-enum { B_F32 = 0, B_Q8 = 1 };
+enum { B_F32 = 0, B_Q8 = 1, B_Q4 = 2 };
+
+// q4 (cv3cpu/quant.py:70-86): blocks of 32 codes in 16 bytes, byte j holding code j in its
+// low nibble and code j + 16 in its high nibble, +8 biased, one float16 scale per block.
+// A GEMM stage (BK = 32, k0 % 32 == 0) is one block, so a thread's four consecutive k
+// (lk % 4 == 0) are four nibbles of one aligned 32-bit word, all low (lk < 16) or all high.
+__device__ __forceinline__ float4 q4_word(uint32_t w, int lk, float s) {
+  const uint32_t v = lk >= 16 ? (w >> 4) : w;
+  return make_float4((float)((int)(v & 0xF) - 8) * s, (float)((int)((v >> 8) & 0xF) - 8) * s,
+                     (float)((int)((v >> 16) & 0xF) - 8) * s, (float)((int)((v >> 24) & 0xF) - 8) * s);
+}
 
 struct GemmParams {
   const float* a;
@@ -89,6 +101,20 @@ __device__ __forceinline__ float4 load_b(const GemmParams& p, int64_t row, int64
     float t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[i] = (kk + i < p.k) ? src[i] : 0.f;
+    return make_float4(t[0], t[1], t[2], t[3]);
+  } else if constexpr (BK_KIND == B_Q4) {
+    // kk = k0 + lk: block kk / 32, byte (kk % 16) of it, nibble half by kk % 32 >= 16
+    const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.b) + row * p.ldb + (kk >> 5) * 16;
+    const int lk = (int)(kk & 31);
+    const float s = __half2float(reinterpret_cast<const __half*>(p.scales)[row * p.nb + (kk >> 5)]);
+    if (fast) return q4_word(*reinterpret_cast<const uint32_t*>(blk + (lk & 15)), lk, s);
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = lk + i;  // within the block (lk % 4 == 0, so c < 32)
+      const uint8_t byte = blk[c & 15];
+      t[i] = (kk + i < p.k) ? (float)((int)((c >= 16 ? byte >> 4 : byte) & 0xF) - 8) * s : 0.f;
+    }
     return make_float4(t[0], t[1], t[2], t[3]);
   } else {
     const int8_t* src = reinterpret_cast<const int8_t*>(p.b) + row * p.ldb + kk;
@@ -144,6 +170,9 @@ __device__ __forceinline__ BRow b_row(const GemmParams& p, int64_t row, int lk) 
   if constexpr (BK_KIND == B_F32) {
     r.codes = reinterpret_cast<const float*>(p.b) + row * p.ldb + lk;
     r.scales = nullptr;
+  } else if constexpr (BK_KIND == B_Q4) {
+    r.codes = reinterpret_cast<const uint8_t*>(p.b) + row * p.ldb + (lk & 15);
+    r.scales = reinterpret_cast<const __half*>(p.scales) + row * p.nb;
   } else {
     r.codes = reinterpret_cast<const int8_t*>(p.b) + row * p.ldb + lk;
     r.scales = p.sf16 ? (const void*)(reinterpret_cast<const __half*>(p.scales) + row * p.nb)
@@ -157,6 +186,10 @@ template <int BK_KIND>
 __device__ __forceinline__ float4 load_b_fast(const GemmParams& p, const BRow& r, int64_t koff) {
   if constexpr (BK_KIND == B_F32) {
     return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(r.codes) + koff);
+  } else if constexpr (BK_KIND == B_Q4) {
+    // koff % 32 == 0: block koff / 32 starts at byte koff / 2
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(r.codes) + (koff >> 1));
+    return q4_word(w, r.lk, __half2float(reinterpret_cast<const __half*>(r.scales)[koff >> 5]));
   } else {
     const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(r.codes) + koff);
     const uint32_t si = ((uint32_t)koff + (uint32_t)r.lk) / (uint32_t)p.block;
@@ -562,9 +595,12 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmParams p, int tiles_m) {
 
 namespace cv3 {
 
-int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb, const void* scales,
-         bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
-         const cv3_epilogue* epi, hipStream_t st) {
+int gemm(int bkind, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb,
+         const void* scales, bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c,
+         int64_t ldc, const cv3_epilogue* epi, hipStream_t st) {
+  CV3_REQUIRE(bkind == B_F32 || bkind == B_Q8 || bkind == B_Q4, CV3_EINVAL, "unknown GEMM operand kind %d", bkind);
+  CV3_REQUIRE(bkind != B_Q4 || (block == 32 && sf16), CV3_EUNSUPPORTED,
+              "q4 GEMM needs 32-code blocks with float16 scales");
   GemmParams p{};
   p.a = a;
   p.lda = lda;
@@ -582,8 +618,9 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   p.ldc = ldc;
   p.epi = epi ? *epi : cv3_epilogue{};
   const int fast_a = ((uintptr_t)a % 16 == 0) && (lda % 4 == 0);
-  const int fast_b = q8 ? (((uintptr_t)b % 4 == 0) && (ldb % 4 == 0) && (block % 4 == 0))
-                        : (((uintptr_t)b % 16 == 0) && (ldb % 4 == 0));
+  const int fast_b = bkind == B_Q8   ? (((uintptr_t)b % 4 == 0) && (ldb % 4 == 0) && (block % 4 == 0))
+                     : bkind == B_Q4 ? (((uintptr_t)b % 4 == 0) && (ldb % 4 == 0))
+                                     : (((uintptr_t)b % 16 == 0) && (ldb % 4 == 0));
   const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
   const dim3 grid((unsigned)(tiles_m * tiles_n));
@@ -599,13 +636,20 @@ int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void*
   const bool small = tiles_m * tiles_n <= 256;
   // A beyond one XCD's L2: walk groups of 8 M-tiles (the tile order note at the top)
   const int group_m = m * k * (int64_t)sizeof(float) > (4ll << 20) ? 8 : 0;
-  if (q8) {
+  if (bkind == B_Q8) {
     if (fast && small)
       hipLaunchKernelGGL((k_gemm8<B_Q8, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
     else if (fast)
       hipLaunchKernelGGL((k_gemm<B_Q8, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
     else
       hipLaunchKernelGGL((k_gemm<B_Q8, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
+  } else if (bkind == B_Q4) {
+    if (fast && small)
+      hipLaunchKernelGGL((k_gemm8<B_Q4, A_ROWS>), grid, dim3(512), 0, st, p, (int)tiles_m);
+    else if (fast)
+      hipLaunchKernelGGL((k_gemm<B_Q4, true>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
+    else
+      hipLaunchKernelGGL((k_gemm<B_Q4, false>), grid, dim3(256), 0, st, p, fast_a, fast_b, (int)tiles_m, group_m);
   } else {
     if (fast && tiles_m * tiles_n <= 512)
       hipLaunchKernelGGL(k_gemm_dma, grid, dim3(256), 0, st, p, (int)tiles_m);

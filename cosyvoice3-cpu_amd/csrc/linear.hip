@@ -1,15 +1,16 @@
 // ops.linear / quant.qmatmul entry points (cv3cpu/ops.py:121-123,
 // cv3cpu/quant.py:156-204): GEMV for up to four activation rows, the MFMA GEMM
-// above that.
+// above that (fp32, q8 and q4 weights alike).
 #include "common.hpp"
 
 namespace cv3 {
 int gemv(int wk, bool sf16, bool swiglu, const float* x, int64_t m, int64_t k, int64_t ldx, const void* w,
          int64_t ldw_bytes, const void* scales, int64_t nb, int64_t block, int64_t n, const float* bias, float* y,
          int64_t ldy, const cv3_epilogue* epi, const float* rms_w, float rms_eps, hipStream_t st);
-int gemm(bool q8, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb, const void* scales,
-         bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
-         const cv3_epilogue* epi, hipStream_t st);
+// bkind: 0 fp32, 1 q8, 2 q4 weights
+int gemm(int bkind, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb,
+         const void* scales, bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c,
+         int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
 }  // namespace cv3
 
 using namespace cv3;
@@ -27,7 +28,7 @@ int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const floa
   const bool rope = epi && epi->rope_cos;  // the rotary epilogue lives in the GEMM only
   if (m <= kGemvRows && !rope)
     return gemv(0, false, false, x, m, k, ldx, w, ldw * 4, nullptr, 1, k, n, bias, y, ldy, epi, nullptr, 0.f, st);
-  return gemm(false, x, m, k, ldx, w, ldw, nullptr, false, 1, k, n, bias, y, ldy, epi, st);
+  return gemm(0, x, m, k, ldx, w, ldw, nullptr, false, 1, k, n, bias, y, ldy, epi, st);
 }
 
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
@@ -46,23 +47,13 @@ int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, co
   if (kind == CV3_KIND_Q8) {
     if (m <= kGemvRows && !rope)
       return gemv(1, sf16, false, x, m, k, ldx, q, kp, scales, nb, block, n, bias, y, ldy, epi, nullptr, 0.f, st);
-    return gemm(true, x, m, k, ldx, q, kp, scales, sf16, nb, block, n, bias, y, ldy, epi, st);
+    return gemm(1, x, m, k, ldx, q, kp, scales, sf16, nb, block, n, bias, y, ldy, epi, st);
   }
-  // q4: GEMV directly; many rows go through the GEMV four rows at a time
-  for (int64_t r = 0; r < m; r += kGemvRows) {
-    const int64_t mm = std::min<int64_t>(kGemvRows, m - r);
-    cv3_epilogue e = epi ? *epi : cv3_epilogue{};
-    if (e.residual) e.residual += r * e.ld_res;
-    if (e.gate && e.rows_per_gate > 0) {
-      // gate rows are indexed by absolute row; shift by whole gate groups only
-      CV3_REQUIRE(r % e.rows_per_gate == 0 || e.rows_per_gate >= m, CV3_EINVAL, "q4 gate grouping");
-      e.gate += (r / e.rows_per_gate) * e.gate_stride;
-    }
-    int rc = gemv(2, true, false, x + r * ldx, mm, k, ldx, q, kp / 2, scales, nb, block, n, bias, y + r * ldy, ldy,
-                  &e, nullptr, 0.f, st);
-    if (rc) return rc;
-  }
-  return CV3_OK;
+  // q4 (32-code blocks, float16 scales): the GEMV for the decode regime, the GEMM above it
+  CV3_REQUIRE(block == 32, CV3_EUNSUPPORTED, "q4 weights need 32-code blocks (got %lld)", (long long)block);
+  if (m <= kGemvRows)
+    return gemv(2, true, false, x, m, k, ldx, q, kp / 2, scales, nb, block, n, bias, y, ldy, epi, nullptr, 0.f, st);
+  return gemm(2, x, m, k, ldx, q, kp / 2, scales, true, nb, block, n, bias, y, ldy, epi, st);
 }
 
 }  // extern "C"

@@ -179,14 +179,29 @@ def test_linear_large_activation(dev, rng, kind, m, k, n):
         assert rel_err(ops.linear(x, mine, b), ref.linear(x, theirs, b)) < TOL
 
 
-@pytest.mark.parametrize("m", [1, 4, 9])
-def test_linear_q4(dev, rng, m):
+@pytest.mark.parametrize("m", [1, 4, 9, 64, 300])
+@pytest.mark.parametrize("k,n", [(896, 300), (896, 4864), (4864, 896), (100, 9), (1024, 1024), (130, 70)])
+def test_linear_q4(dev, rng, m, k, n):
+    """q4 weights: the GEMV up to 4 rows, the MFMA GEMM (nibbles dequantised on their way
+    into LDS) above: branch-free (K % 64 == 0) and guarded (ragged K) stages, the
+    8-wave kernel (at most 256 tiles) and the 4-wave one."""
     ops, quant = dev
-    w = (rng.normal(size=(300, 896)) * 0.02).astype(np.float32)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
     q, s, _ = refq.quantize_q4(w)
-    x = rng.normal(size=(m, 896)).astype(np.float32)
-    assert rel_err(ops.linear(x, quant.QTensor("q4", q, s, (300, 896), 32)),
-                   ref.linear(x, refq.QTensor("q4", q, s, (300, 896), 32))) < TOL
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    assert rel_err(ops.linear(x, quant.QTensor("q4", q, s, (n, k), 32), b),
+                   ref.linear(x, refq.QTensor("q4", q, s, (n, k), 32), b)) < TOL
+
+
+def test_linear_q4_large(dev, rng):
+    """1000 activation rows through [2048, 1024] q4 weights: the DiT ff1 shape."""
+    ops, quant = dev
+    w = (rng.normal(size=(2048, 1024)) * 0.02).astype(np.float32)
+    q, s, _ = refq.quantize_q4(w)
+    x = rng.normal(size=(1000, 1024)).astype(np.float32)
+    assert rel_err(ops.linear(x, quant.QTensor("q4", q, s, (2048, 1024), 32)),
+                   ref.linear(x, refq.QTensor("q4", q, s, (2048, 1024), 32))) < TOL
 
 
 def test_embedding(dev, rng):
