@@ -44,6 +44,13 @@ import numpy as np  # noqa: E402
 
 METRIC = "DiT flow RTF (10 s, CFG) + int8 LM decode tok/s, each as % of roofline"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+# HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
+# device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
+# the one-launch decode step (24 layers, per-channel int8, KV 512: 410.0 MB read + 12.4 MB written)
+# and the fused QKV GEMM of the 10 s solve (46.8 MB + 12.3 MB).  Counters cannot be read inside
+# this process, so these are the measured figures for exactly these kernels and shapes.
+TRAFFIC_DECODE_STEP = 422.4e6
+TRAFFIC_QKV_GEMM = 59.1e6
 FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
 PREFILL = 512             # KV cache positions pre-filled before each decode
 DECODE_TOKENS = 256       # tokens per decode: KV 512 -> 768
@@ -375,24 +382,50 @@ def bench_flow_q8(args, tensors, meta, profile: str):
     return {"ms": ms, "flops": flops, "T": T}
 
 
-def bench_dit_kernels(args):
-    """Each launch of one DiT block at the 10 s solve's shapes (T = 500, CFG batch 2), timed alone:
-    `reps` back-to-back launches of the same kernel, replayed from a captured graph, on the buffers
-    a real estimator evaluation left behind; then the 30 s q8 GEMMs (block-64 / f16 weights).
-    For profiling single kernels (rocprofv3 --pmc passes) and for the per-kernel roofline table."""
+def bench_kernels(args):
+    """The roofline kernels one by one, for per-kernel tables and rocprofv3 counter passes:
+    16 tokens of the one-launch decode step (24 layers, per-channel int8, KV 512), each launch of
+    one DiT block at the 10 s solve's shapes (T = 500, CFG batch 2) timed alone (`reps`
+    back-to-back launches of the same kernel, replayed from a captured graph unless --no-graph,
+    on the buffers a real estimator evaluation left behind), the 30 s q8 GEMMs (block-64 / f16
+    weights), one whole-utterance vocoder inference (10 s), then optionally the whole 10 s
+    solve.  The five-kernel decode step is left out (its kernels have their own bench lines)."""
     import ctypes
     import math
     import cv3amd.quant as quant
     from cv3amd import _lib, synth
-    from cv3amd.device import Timer, synchronize
+    from cv3amd.device import Timer, synchronize, to_device, DeviceArray
     from cv3amd.dit import DeviceDiT
     from cv3amd.weights import WeightStore
     T, B = 500, 2
     info = _lib.device_info()
     copy_bps = copy_bandwidth()   # also the known-size kernel the traffic counters are scaled by
-    log(f"dit kernels: device copy {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")
+    log(f"kernels: device copy {copy_bps / 1e9:.0f} GB/s (read + write of 256 MiB)")
     peak = mfma_peak(info["cu_count"])
-    log(f"dit kernels: fp32 MFMA probe {peak / 1e12:.1f} TFLOP/s (k_mfma_peak, the matrix-core busy reference)")
+    log(f"kernels: fp32 MFMA probe {peak / 1e12:.1f} TFLOP/s (k_mfma_peak, the matrix-core busy reference)")
+    out = {"mfma_probe_tflops": round(peak / 1e12, 2)}
+    # the one-launch decode step
+    from cv3amd.qwen2 import DeviceQwen2
+    lm_t, lm_meta = build_lm(args.layers, args.profile)
+    lm = DeviceQwen2(WeightStore(lm_t, lm_meta, quant.QTensor), cap=1024)
+    rng = np.random.default_rng(0)
+    kv_shape = (args.layers, lm.kv_heads, PREFILL, lm.head_dim)
+    lm.fill_cache(rng.standard_normal(kv_shape, dtype=np.float32), rng.standard_normal(kv_shape, dtype=np.float32))
+    lm.begin(int(lm_meta["speech_token_size"]), PREFILL)
+    for _ in range(4):
+        lm.step_persistent()
+    synchronize()
+    tm = Timer()
+    tm.start()
+    for _ in range(16):
+        lm.step_persistent()
+    us = tm.stop() / 16 * 1e3
+    if lm.persistent_error():
+        raise RuntimeError("the one-launch decode step gave up waiting")
+    nbytes = sum(lm.bytes_per_token(PREFILL + 12).values())   # the timed tokens' midpoint (KV 524)
+    log(f"kernels: one-launch decode step {us:.1f} us per token ({nbytes / (us * 1e-6) / 1e9:.0f} GB/s)")
+    out["decode_step_us"] = round(us, 2)
+    del lm, lm_t
     tensors, meta = synth.dit_tensors(depth=2), synth.dit_meta(depth=2)
     d = DeviceDiT(WeightStore(tensors, meta, quant.QTensor))
     mu, cond, spks, x0 = flow_inputs(T)
@@ -431,9 +464,7 @@ def bench_dit_kernels(args):
                               d.conv_b[0].ptr, d.z1.ptr, D, ctypes.byref(mish), None),
             2.0 * BT * D * (D // d.conv_groups) * k),
     }
-    out = {}
     reps = args.kernel_reps
-    tm = Timer()
     for name, (fn, flops) in launches.items():
         run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
         run()
@@ -443,7 +474,7 @@ def bench_dit_kernels(args):
             run()
         us = tm.stop() / (5 * reps) * 1e3
         rate = flops / (us * 1e-6) / 1e12 if flops else None
-        log(f"dit kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / 157.3:.1%} of fp32 MFMA peak)"
+        log(f"kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / 157.3:.1%} of fp32 MFMA peak)"
                                                    if rate else ""))
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2) if rate else None}
     # the 30 s solve's q8 GEMMs (int8 B dequantised on its way into LDS), block-64 / f16 scales
@@ -451,7 +482,6 @@ def bench_dit_kernels(args):
     BT3 = B * T3
     rng = np.random.default_rng(0)
     a = rng.standard_normal((BT3, F), dtype=np.float32)
-    from cv3amd.device import to_device, DeviceArray
     a_d = to_device(a)
     for (n, kk, label) in ((3 * D, D, "QKV"), (F, D, "ff1"), (D, D, "out"), (D, F, "ff2")):
         w = to_device(rng.standard_normal((n, kk), dtype=np.float32) * np.float32(0.02))
@@ -468,9 +498,20 @@ def bench_dit_kernels(args):
         us = tm.stop() / (5 * reps) * 1e3
         rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
         name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T (block 64, f16 scales)"
-        log(f"dit kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / 157.3:.1%})")
+        log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / 157.3:.1%})")
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
-    out["mfma_probe_tflops"] = round(peak / 1e12, 2)
+    # one whole-utterance vocoder inference (F0 net, excitation, decode; its convs are k_conv_cl_dma)
+    from cv3amd.hift import DeviceHiFT
+    h = DeviceHiFT(WeightStore(synth.hift_tensors(base=512), synth.hift_meta()))
+    mel_d = to_device(hift_inputs(500)[0])
+    h.inference(mel_d, graph=args.graph)
+    synchronize()
+    tm.start()
+    h.inference(mel_d, graph=args.graph)
+    ms = tm.stop()
+    log(f"kernels: vocoder inference, 10 s whole: {ms:.2f} ms")
+    out["vocoder_inference_ms"] = round(ms, 3)
+    del h
     if args.kernel_solve:
         # the whole 10 s solve (22 blocks, 10 steps, CFG) for the end-to-end figure
         del d
@@ -483,7 +524,7 @@ def bench_dit_kernels(args):
         for _ in range(3):
             d.solve(x0, graph=args.graph)
         ms = tm.stop() / 3
-        log(f"dit kernels: 10 s solve {ms:.2f} ms ({d.flops_per_solve() / (ms / 1e3) / 1e12:.1f} TFLOP/s)")
+        log(f"kernels: 10 s solve {ms:.2f} ms ({d.flops_per_solve() / (ms / 1e3) / 1e12:.1f} TFLOP/s)")
         out["solve_10s_ms"] = round(ms, 3)
     return out
 
@@ -592,12 +633,13 @@ def main():
     ap.add_argument("--cooperative", action="store_true",
                     help="launch the one-launch step with hipLaunchCooperativeKernel (guaranteed co-residency, "
                          "about 20 us more per token) instead of an ordinary launch")
-    ap.add_argument("--dit-kernels", action="store_true",
-                    help="time each DiT block launch alone at the 10 s shapes (and the 30 s q8 GEMMs), print "
-                         "them as one JSON line and exit: for per-kernel rooflines and rocprofv3 counter passes")
-    ap.add_argument("--kernel-reps", type=int, default=20, help="launches per replay in --dit-kernels")
+    ap.add_argument("--kernels", action="store_true",
+                    help="time the roofline kernels one by one (one-launch decode tokens, each DiT block launch at "
+                         "the 10 s shapes, the 30 s q8 GEMMs, a vocoder inference), print them as one JSON line "
+                         "and exit: for per-kernel rooflines and rocprofv3 counter passes")
+    ap.add_argument("--kernel-reps", type=int, default=20, help="launches per replay in --kernels")
     ap.add_argument("--no-kernel-solve", dest="kernel_solve", action="store_false",
-                    help="--dit-kernels without the closing 22-block solve")
+                    help="--kernels without the closing 22-block 10 s solve")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
     args = ap.parse_args()
@@ -613,8 +655,8 @@ def main():
     _lib.init(0)
     info = _lib.device_info()
     log(f"device {info['arch']} with {info['cu_count']} CUs")
-    if args.dit_kernels:
-        print(json.dumps({"dit_kernels": bench_dit_kernels(args)}), flush=True)
+    if args.kernels:
+        print(json.dumps({"kernels": bench_kernels(args)}), flush=True)
         return
 
     copy_bps = copy_bandwidth()
@@ -704,7 +746,9 @@ def main():
         "hbm_roofline_frac": round(dec["bytes_per_token"] * dec["tok_s"] / HBM_PEAK, 4),
         "bytes_per_token": dec["bytes_per_token"],
         "roofline": {"bound": "hbm", "achieved": round(step_k["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(step_k["achieved_Bps"] / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(step_k["achieved_Bps"] / HBM_PEAK, 4),
+                     "traffic": TRAFFIC_DECODE_STEP if (dec["persistent"] and args.profile == "per_channel"
+                                                         and args.layers == 24 and not args.cooperative) else None,
                      "kernel": step_k["name"], "bytes_per_launch": step_k["bytes_per_launch"],
                      "us_per_launch": round(step_k["us_per_launch"], 3)},
         "five_kernel_step": {
@@ -753,7 +797,7 @@ def main():
             "flops_per_solve": flow["flops"],
             "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
                          "peak": FP32_MFMA_PEAK / 1e12, "unit": "TFLOP/s",
-                         "frac": round(fk["achieved_flops"] / FP32_MFMA_PEAK, 4), "traffic": None,
+                         "frac": round(fk["achieved_flops"] / FP32_MFMA_PEAK, 4), "traffic": TRAFFIC_QKV_GEMM,
                          "kernel": fk["name"], "us_per_launch": round(fk["us_per_launch"], 2)},
             "cpu_baseline": None if cpu_flow_s is None else {
                 "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
