@@ -59,89 +59,126 @@ def read_header(fh) -> tuple:
     return head, meta, 8 + n
 
 
+class _Record:
+    """One logical tensor of the file: where its bytes are, how to read them, and the
+    host object once something asked for it."""
+
+    __slots__ = ("name", "dtype", "shape", "span", "scales", "quant", "obj")
+
+    def __init__(self, name: str, info: Dict[str, Any], data0: int, size: int):
+        a, b = info["data_offsets"]
+        if not (0 <= a <= b and data0 + b <= size):
+            raise ValueError(f"{name}: byte range {a}..{b} outside the file")
+        self.name = name
+        self.dtype = info["dtype"]
+        self.shape = tuple(int(x) for x in info["shape"])
+        self.span = (data0 + a, b - a)       # absolute file offset, bytes
+        self.scales: Optional["_Record"] = None
+        self.quant: Optional[Dict[str, Any]] = None
+        self.obj = None
+
+    def spans(self):
+        yield self.span
+        if self.scales is not None:
+            yield self.scales.span
+
+    def nbytes(self) -> int:
+        return sum(n for _, n in self.spans())
+
+
 class DeviceWeightFile:
-    """Read side of the reference weight file; ``get(name)`` is an ndarray or a QTensor."""
+    """Read side of the reference weight file; ``get(name)`` is an ndarray or a QTensor.
+
+    The header is parsed once into a table of records, one per logical tensor in file
+    order, each holding its payload's and (quantised) its scales' byte spans.  Every query
+    reads that table; materialised objects live on their records, so dropping a stage is
+    clearing its records, and evicting it advises exactly the stage's own byte runs."""
 
     def __init__(self, path: str, qtensor_cls=None):
         from .quant import QTensor
         self.path = path
         self._qcls = qtensor_cls or QTensor
         self._fh = open(path, "rb")
-        self._index, metadata, self._data0 = read_header(self._fh)
-        self._size = os.fstat(self._fh.fileno()).st_size
+        index, metadata, data0 = read_header(self._fh)
+        size = os.fstat(self._fh.fileno()).st_size
         self._map = mmap.mmap(self._fh.fileno(), 0, access=mmap.ACCESS_READ)
         blob = json.loads(metadata.get(METADATA_KEY, "{}"))
         self.meta: Dict[str, Any] = blob.get("meta", {})
-        self._quant: Dict[str, Dict[str, Any]] = blob.get("quant", {})
-        for name, info in self._index.items():
-            a, b = info["data_offsets"]
-            if not (0 <= a <= b and self._data0 + b <= self._size):
-                raise ValueError(f"{name}: byte range {a}..{b} outside the file")
-        self._names = [k for k in self._index if not k.endswith(SCALES_SUFFIX)]
-        self._cache: Dict[str, Any] = {}
+        quant: Dict[str, Dict[str, Any]] = blob.get("quant", {})
+        all_records = {k: _Record(k, v, data0, size) for k, v in index.items()}
+        # a scales entry belongs to the tensor it is named after; it is not a tensor of its own
+        self._rec: Dict[str, _Record] = {}
+        for name, r in all_records.items():
+            if name.endswith(SCALES_SUFFIX):
+                continue
+            r.quant = quant.get(name)
+            if r.quant is not None:
+                r.scales = all_records.get(name + SCALES_SUFFIX)
+                if r.scales is None:
+                    raise ValueError(f"{name}: quantised, but the file has no {name + SCALES_SUFFIX}")
+            self._rec[name] = r
+        # orphan scales entries still count towards the file's bytes
+        owned = {id(r.scales) for r in self._rec.values() if r.scales is not None}
+        self._orphans = [r for k, r in all_records.items() if k.endswith(SCALES_SUFFIX) and id(r) not in owned]
+
+    def _under(self, prefix: str):
+        return (r for k, r in self._rec.items() if k.startswith(prefix))
+
+    def _record(self, name: str) -> _Record:
+        r = self._rec.get(name)
+        if r is None:
+            raise KeyError(name)
+        return r
 
     # -- introspection ------------------------------------------------------
     def keys(self) -> Iterable[str]:
-        return list(self._names)
+        return list(self._rec)
 
     def __contains__(self, name: str) -> bool:
-        return name in self._index and not name.endswith(SCALES_SUFFIX)
+        return name in self._rec
 
     def entry(self, name: str) -> Dict[str, Any]:
-        if name not in self:
-            raise KeyError(name)
-        q = self._quant.get(name)
-        nbytes = self._nbytes(name)
-        if q is not None:
-            return {"kind": q["kind"], "shape": list(q["shape"]), "block": q["block"], "mshape": list(q["mshape"]),
-                    "nbytes": nbytes + self._nbytes(name + SCALES_SUFFIX)}
-        info = self._index[name]
-        return {"kind": _RAW_KINDS.get(info["dtype"], info["dtype"].lower()), "shape": list(info["shape"]),
-                "nbytes": nbytes}
-
-    def _nbytes(self, name: str) -> int:
-        a, b = self._index[name]["data_offsets"]
-        return b - a
+        """Storage kind, logical shape and bytes on disk (payload plus scales)."""
+        r = self._record(name)
+        if r.quant is None:
+            return {"kind": _RAW_KINDS.get(r.dtype, r.dtype.lower()), "shape": list(r.shape), "nbytes": r.nbytes()}
+        q = r.quant
+        return {"kind": q["kind"], "shape": list(q["shape"]), "block": q["block"], "mshape": list(q["mshape"]),
+                "nbytes": r.nbytes()}
 
     def total_bytes(self) -> int:
-        return sum(self._nbytes(k) for k in self._index)
+        return sum(r.nbytes() for r in self._rec.values()) + sum(r.nbytes() for r in self._orphans)
 
     def stage_bytes(self, prefix: str) -> int:
-        return sum(self._nbytes(k) for k in self._index if k.startswith(prefix))
+        return sum(r.nbytes() for r in self._under(prefix)) + sum(
+            r.nbytes() for r in self._orphans if r.name.startswith(prefix))
 
     # -- access ---------------------------------------------------------------
-    def _array(self, name: str) -> np.ndarray:
-        info = self._index[name]
-        a, b = info["data_offsets"]
-        shape = tuple(int(s) for s in info["shape"])
-        if info["dtype"] == "BF16":  # widened to float32: numpy has no bfloat16
-            raw = np.frombuffer(self._map, np.dtype("<u2"), (b - a) // 2, self._data0 + a)
-            return _frozen((raw.astype(np.uint32) << 16).view(np.float32).reshape(shape))
-        dt = _DTYPES.get(info["dtype"])
+    def _view(self, r: _Record) -> np.ndarray:
+        off, n = r.span
+        if r.dtype == "BF16":  # widened to float32: numpy has no bfloat16
+            raw = np.frombuffer(self._map, np.dtype("<u2"), n // 2, off)
+            return _frozen((raw.astype(np.uint32) << 16).view(np.float32).reshape(r.shape))
+        dt = _DTYPES.get(r.dtype)
         if dt is None:
-            raise ValueError(f"{name}: unsupported safetensors dtype {info['dtype']}")
-        count = (b - a) // dt.itemsize
-        if count != int(np.prod(shape)):
-            raise ValueError(f"{name}: {b - a} bytes do not hold {shape} x {info['dtype']}")
-        arr = np.frombuffer(self._map, dt, count, self._data0 + a).reshape(shape)
+            raise ValueError(f"{r.name}: unsupported safetensors dtype {r.dtype}")
+        if n != int(np.prod(r.shape)) * dt.itemsize:
+            raise ValueError(f"{r.name}: {n} bytes do not hold {r.shape} x {r.dtype}")
+        arr = np.frombuffer(self._map, dt, n // dt.itemsize, off).reshape(r.shape)
         if dt.itemsize > 1 and arr.ctypes.data % dt.itemsize:
             arr = _frozen(np.array(arr, copy=True))  # a misaligned view would take NumPy's slow path
         return arr
 
     def get(self, name: str):
-        hit = self._cache.get(name)
-        if hit is not None:
-            return hit
-        if name not in self:
-            raise KeyError(name)
-        q = self._quant.get(name)
-        if q is None:
-            out = self._array(name)
-        else:
-            out = self._qcls(q["kind"], self._array(name), self._array(name + SCALES_SUFFIX), tuple(q["mshape"]),
-                             int(q["block"]), tuple(q["shape"]))
-        self._cache[name] = out
-        return out
+        r = self._record(name)
+        if r.obj is None:
+            if r.quant is None:
+                r.obj = self._view(r)
+            else:
+                q = r.quant
+                r.obj = self._qcls(q["kind"], self._view(r), self._view(r.scales), tuple(q["mshape"]),
+                                   int(q["block"]), tuple(q["shape"]))
+        return r.obj
 
     def get_f32(self, name: str) -> np.ndarray:
         """float32 copy; a quantised entry comes back as its (N, K) matrix (io/weights.py:167-170)."""
@@ -149,23 +186,22 @@ class DeviceWeightFile:
         return t.dequant() if hasattr(t, "dequant") else np.asarray(t, dtype=np.float32)
 
     def subset(self, prefix: str) -> Dict[str, Any]:
-        n = len(prefix)
-        return {k[n:]: self.get(k) for k in self._names if k.startswith(prefix)}
+        """The tensors under ``prefix``, keyed by the rest of their names."""
+        cut = len(prefix)
+        return {r.name[cut:]: self.get(r.name) for r in list(self._under(prefix))}
 
     # -- lifetime -------------------------------------------------------------
     def upload(self, prefix: str = "") -> int:
         """Copy every tensor under ``prefix`` into HBM now, one pass per stage, for the
         per-op path (``cv3amd.ops`` finds the copies by host object); returns the bytes
-        uploaded.  The copies live as long as the host objects this file caches, i.e.
+        uploaded.  The copies live as long as the host objects this file holds, i.e.
         until ``release`` / ``evict``.  The model harnesses need no upload: they lay a
         stage's weights out themselves (fused QKV, stacked layers) as they are built."""
         from .weights import device_f32, device_qtensor
         total = 0
-        for k in self._names:
-            if not k.startswith(prefix):
-                continue
-            t = self.get(k)
-            if hasattr(t, "scales"):
+        for r in list(self._under(prefix)):
+            t = self.get(r.name)
+            if r.quant is not None:
                 device_qtensor(t)
                 total += t.nbytes
             else:
@@ -174,31 +210,37 @@ class DeviceWeightFile:
 
     def release(self, prefix: str = "") -> None:
         """Drop the host objects under ``prefix``; their device copies go with them."""
-        for k in [k for k in self._cache if k.startswith(prefix)]:
-            del self._cache[k]
+        for r in self._under(prefix):
+            r.obj = None
 
     def evict(self, prefix: str = "") -> int:
-        """``release`` plus MADV_DONTNEED on the mapped pages of every tensor under
-        ``prefix`` (io/weights.py:182-205); returns the bytes handed back."""
-        lo = hi = None
-        for name, info in self._index.items():
-            if name.startswith(prefix):
-                a, b = info["data_offsets"]
-                lo = a if lo is None else min(lo, a)
-                hi = b if hi is None else max(hi, b)
+        """``release``, then hand back to the kernel (MADV_DONTNEED) the whole pages that
+        only the stage's own bytes cover (io/weights.py:182-205: the per-stage lifetime).
+        The stage's payload and scales spans are merged into maximal contiguous runs and
+        each run's page-aligned interior is advised, so a tensor of another stage stored
+        between two of this stage's keeps its pages.  Returns the bytes handed back."""
+        spans = [sp for r in self._under(prefix) for sp in r.spans()]
+        spans += [r.span for r in self._orphans if r.name.startswith(prefix)]
+        spans.sort()
         self.release(prefix)
-        if lo is None:
-            return 0
+        runs = []
+        for off, n in spans:
+            if runs and off <= runs[-1][1]:
+                runs[-1][1] = max(runs[-1][1], off + n)
+            else:
+                runs.append([off, off + n])
         page = mmap.PAGESIZE
-        start = (self._data0 + lo + page - 1) // page * page
-        end = (self._data0 + hi) // page * page
-        if end <= start or not hasattr(self._map, "madvise"):
-            return 0
-        self._map.madvise(mmap.MADV_DONTNEED, start, end - start)
-        return end - start
+        freed = 0
+        for lo, hi in runs:
+            first = -(-lo // page) * page
+            last = hi - hi % page
+            if last > first and hasattr(self._map, "madvise"):
+                self._map.madvise(mmap.MADV_DONTNEED, first, last - first)
+                freed += last - first
+        return freed
 
     def close(self) -> None:
-        self._cache.clear()
+        self.release()
         try:
             self._map.close()
         except BufferError:

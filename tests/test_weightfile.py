@@ -178,3 +178,22 @@ def test_evict_releases_pages_and_rereads(tmp_path):
         assert again is not first  # the cached object went with the pages
         assert np.array_equal(oq.qmatmul(x, again), before)
         assert f.evict("nothing.") == 0
+
+
+def test_evict_spares_other_stages_between(tmp_path):
+    """A stage's tensors stored around another stage's: eviction advises only the stage's
+    own byte runs (each run's whole pages), never the pages of the tensor in between."""
+    import mmap
+    rng = np.random.default_rng(4)
+    p = tmp_path / "interleaved.safetensors"
+    big = lambda: rng.normal(size=(512, 2048)).astype(np.float32)   # 4 MiB each
+    write_weight_file(str(p), {"a.first": big(), "b.middle": big(), "a.last": big()})
+    with _open(p) as f:
+        middle = np.array(f.get("b.middle"))
+        freed = f.evict("a.")
+        page = mmap.PAGESIZE
+        # two runs of 4 MiB each: at most their sizes, at least their whole interior pages
+        assert 2 * (4 << 20) - 2 * 2 * page <= freed <= 2 * (4 << 20)
+        assert f.evict("b.") <= 4 << 20
+        assert np.array_equal(np.asarray(f.get("b.middle")), middle)
+        assert f.stage_bytes("a.") == 2 * (4 << 20) and f.total_bytes() == 3 * (4 << 20)
