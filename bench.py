@@ -450,6 +450,8 @@ def bench_kernels(args):
             None),
         f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T + rotary": (
             lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D, rope_epi), 2.0 * BT * 3 * D * D),
+        f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T, bias only": (
+            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D), 2.0 * BT * 3 * D * D),
         f"flash attention B={B} H={H} T={T} d={dh}": (
             lambda: _lib.call("attention", d.qkvb.ptr, d.qkvb.ptr + D * f4, d.qkvb.ptr + 2 * D * f4, d.att.ptr,
                               B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None), 4.0 * B * H * T * T * dh),
@@ -768,8 +770,10 @@ def main():
         tk = tiny["kernel"]
         tsk = tiny["step_kernel"] if tiny["persistent"] else tk
         line["decode_tiny"] = {
-            "workload": f"the same decode with the tiny profile: Qwen2 body layers q4 (block 32, f16 scales), "
-                        f"head and speech embedding q8, KV {PREFILL}->{PREFILL + DECODE_TOKENS}",
+            "workload": f"the same decode with the tiny profile: Qwen2 body layers q4 (block 32, f16 scales; held "
+                        f"in HBM as int8 codes n - 8 with the same blocks and scales), head and speech embedding "
+                        f"q8, KV {PREFILL}->{PREFILL + DECODE_TOKENS}; bytes_per_token counts the checkpoint's "
+                        f"packed q4 body",
             "decodes_timed": tiny["decodes"],
             "decode_step": "one kernel launch per token" if tiny["persistent"] else "five kernels per layer",
             "tok_s": round(tiny["tok_s"], 2), "ms_per_token": round(tiny["ms"] / DECODE_TOKENS, 5),

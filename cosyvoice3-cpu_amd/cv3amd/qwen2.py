@@ -88,10 +88,24 @@ def _host(a):
     return a.numpy() if isinstance(a, DeviceArray) else np.asarray(a)
 
 
-class _Stacked:
-    """Rows of several q8 or q4 QTensors (per layer, in order) stacked into one device array."""
+def widen_q4_codes(packed: np.ndarray) -> np.ndarray:
+    """q4 codes (quant.py:70-86: per 32-code block 16 bytes, byte j holding code j in its low
+    nibble and code j + 16 in its high nibble, each + 8) as int8 codes n - 8, K in order."""
+    b = np.ascontiguousarray(packed, dtype=np.uint8)
+    rows, half = b.shape
+    blocks = b.reshape(rows, half // 16, 16)
+    codes = np.concatenate([blocks & 0x0F, blocks >> 4], axis=2).astype(np.int16) - 8
+    return codes.reshape(rows, half * 2).astype(np.int8)
 
-    def __init__(self, per_layer: List[List[object]]):
+
+class _Stacked:
+    """Rows of several q8 or q4 QTensors (per layer, in order) stacked into one device array.
+
+    ``widen``: q4 rows are stored as int8 codes (n - 8) with their 32-code blocks and float16
+    scales, i.e. the same weights, dequantised to the same floats, twice the bytes.  The decode
+    step is latency-bound, and unpacking nibbles is VALU work on its critical path."""
+
+    def __init__(self, per_layer: List[List[object]], widen: bool = False):
         qs, ss = [], []
         first = per_layer[0][0]
         self.k = int(first.shape[1])
@@ -111,6 +125,11 @@ class _Stacked:
         q = np.concatenate(qs, axis=0)
         s = np.concatenate(ss, axis=0)
         self.kp = int(s.shape[1]) * self.block  # q4 rows hold kp / 2 bytes
+        self.source_nbytes = q.nbytes + s.nbytes   # the checkpoint's bytes (q4: packed nibbles)
+        self.widened = bool(widen and self.kind == "q4")
+        if self.widened:
+            q = widen_q4_codes(q)
+            self.kind = "q8"
         cpc = 32 if self.kind == "q4" else 16
         if self.kp % cpc or self.block % cpc:
             raise ValueError(f"padded K and block must be multiples of {cpc}")
@@ -135,13 +154,17 @@ class _Stacked:
 
     @property
     def nbytes(self):
+        """Bytes held in HBM (a widened q4 body: int8 codes)."""
         return self.q.nbytes + self.scales.nbytes
 
 
 class DeviceQwen2:
     """Qwen2 body + CosyVoice3 LM head resident on the device, decoding greedily."""
 
-    def __init__(self, weights, prefix: str = "llm.", cap: int = 1024):
+    def __init__(self, weights, prefix: str = "llm.", cap: int = 1024, widen_q4: bool = True):
+        """``widen_q4``: a q4 body (the tiny profile) is held in HBM as int8 codes with its own
+        blocks and scales (identical weights), which the decode kernels read faster than
+        packed nibbles; False keeps the packed nibbles (half the bytes)."""
         _lib.init()
         m = weights.meta["qwen2"]
         self.layers = int(m["num_hidden_layers"])
@@ -159,10 +182,10 @@ class DeviceQwen2:
         g = weights.get
         L = range(self.layers)
         lp = [f"{body}layers.{i}." for i in L]
-        self.qkv = _Stacked([[g(p + f"self_attn.{x}_proj.weight") for x in "qkv"] for p in lp])
-        self.o = _Stacked([[g(p + "self_attn.o_proj.weight")] for p in lp])
-        self.gate_up = _Stacked([[g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")] for p in lp])
-        self.down = _Stacked([[g(p + "mlp.down_proj.weight")] for p in lp])
+        self.qkv = _Stacked([[g(p + f"self_attn.{x}_proj.weight") for x in "qkv"] for p in lp], widen_q4)
+        self.o = _Stacked([[g(p + "self_attn.o_proj.weight")] for p in lp], widen_q4)
+        self.gate_up = _Stacked([[g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")] for p in lp], widen_q4)
+        self.down = _Stacked([[g(p + "mlp.down_proj.weight")] for p in lp], widen_q4)
         self.head = _Stacked([[g(prefix + "llm_decoder.weight")]])
         self.emb = _Stacked([[g(prefix + "speech_embedding")]])
         f32 = lambda a: np.asarray(_host(a), np.float32)  # noqa: E731
@@ -212,8 +235,9 @@ class DeviceQwen2:
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
-        """Algorithmic HBM bytes of one token at KV length ``length`` (keys read = length + 1)."""
-        body = self.qkv.nbytes + self.o.nbytes + self.gate_up.nbytes + self.down.nbytes
+        """Algorithmic HBM bytes of one token at KV length ``length`` (keys read = length + 1): the
+        checkpoint's weight bytes (a q4 body counts its packed nibbles even when held widened)."""
+        body = self.qkv.source_nbytes + self.o.source_nbytes + self.gate_up.source_nbytes + self.down.source_nbytes
         kv = 2 * self.layers * self.kv_heads * (length + 1) * self.head_dim * 4
         small = 4 * (self.qkv_bias.size + self.ln1.size + self.ln2.size + self.norm.size)
         return {"body": body, "kv": kv, "norms_biases": small, "head": self.head.nbytes}

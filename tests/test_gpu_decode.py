@@ -21,12 +21,14 @@ PREFILL = 512
 
 
 def _setup(layers, profile, seed=0):
+    """profile "tiny:packed" is the tiny profile held as packed nibbles on the device
+    (``DeviceQwen2(widen_q4=False)``); plain "tiny" widens its codes to int8."""
     import oracle.quant
     import cv3amd.quant
     from cv3amd import synth
     from cv3amd.weights import WeightStore
     t = synth.qwen2_tensors(layers=layers, seed=seed)
-    t = synth.quantize_store(t, profile, oracle.quant.quantize_q8, oracle.quant.quantize_q4)
+    t = synth.quantize_store(t, profile.split(":")[0], oracle.quant.quantize_q8, oracle.quant.quantize_q4)
     meta = synth.qwen2_meta(layers=layers)
     cpu = WeightStore(t, meta, oracle.quant.QTensor)
     dev = WeightStore(t, meta, cv3amd.quant.QTensor)
@@ -48,14 +50,14 @@ def _oracle_lm(cpu, k, v, steps):
     return lm, cache
 
 
-@pytest.mark.parametrize("profile", ["per_channel", "balanced", "tiny"])
+@pytest.mark.parametrize("profile", ["per_channel", "balanced", "tiny", "tiny:packed"])
 def test_decode_two_layers_logits_and_tokens(gpu, profile):
     from cv3amd.qwen2 import DeviceQwen2
     steps = 12
     cpu, dev, k, v = _setup(2, profile)
     print(f"[decode] 2 layers, profile={profile}, {steps} steps", flush=True)
     lm, cache = _oracle_lm(cpu, k, v, steps)
-    d = DeviceQwen2(dev, cap=1024)
+    d = DeviceQwen2(dev, cap=1024, widen_q4=not profile.endswith(":packed"))
     d.fill_cache(k, v)
     d.begin(lm.sos, PREFILL)
     x = lm.speech_emb([lm.sos])
@@ -75,7 +77,7 @@ def test_decode_two_layers_logits_and_tokens(gpu, profile):
         assert rel_err(kc[i][:, :PREFILL + steps], cache.k[i][:, :PREFILL + steps]) < 1e-5
 
 
-@pytest.mark.parametrize("profile", ["per_channel", "tiny"])
+@pytest.mark.parametrize("profile", ["per_channel", "tiny", "tiny:packed"])
 def test_decode_full_depth_graph_replay(gpu, profile):
     """24 layers, 8 greedy tokens replayed from one captured step graph."""
     from cv3amd.qwen2 import DeviceQwen2
@@ -84,7 +86,7 @@ def test_decode_full_depth_graph_replay(gpu, profile):
     print(f"[decode] 24 layers {profile}, {steps} steps, graph", flush=True)
     lm, cache = _oracle_lm(cpu, k, v, steps)
     want = lm.greedy(lm.speech_emb([lm.sos]), cache, steps)
-    d = DeviceQwen2(dev, cap=1024)
+    d = DeviceQwen2(dev, cap=1024, widen_q4=not profile.endswith(":packed"))
     d.fill_cache(k, v)
     got = d.generate(lm.sos, PREFILL, steps, graph=True)
     print(f"[decode] oracle {want}\n[decode] device {got}", flush=True)

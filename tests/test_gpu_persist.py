@@ -29,7 +29,7 @@ def _setup(layers, profile, n, seed=0):
     from cv3amd import synth
     from cv3amd.weights import WeightStore
     t = synth.qwen2_tensors(layers=layers, seed=seed)
-    t = synth.quantize_store(t, profile, oracle.quant.quantize_q8, oracle.quant.quantize_q4)
+    t = synth.quantize_store(t, profile.split(":")[0], oracle.quant.quantize_q8, oracle.quant.quantize_q4)
     meta = synth.qwen2_meta(layers=layers)
     cpu = WeightStore(t, meta, oracle.quant.QTensor)
     dev = WeightStore(t, meta, cv3amd.quant.QTensor)
@@ -56,14 +56,14 @@ def _oracle_lm(cpu, k, v, n, steps):
     ("balanced", 122, 10, False, "stream"), ("per_channel", 300, 6, True, "stream"),
     ("per_channel", 1000, 4, False, "stream"), ("balanced", 897, 4, False, "stream"),
     ("per_channel", 512, 6, False, "stacked"), ("balanced", 122, 6, False, "stacked"),
-    ("tiny", 300, 8, False, "stacked")])
+    ("tiny", 300, 8, False, "stacked"), ("tiny:packed", 300, 8, False, "stacked")])
 def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative, kernel):
     from cv3amd.qwen2 import DeviceQwen2
     cpu, dev, k, v = _setup(2, profile, n)
     print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps, cooperative={cooperative}, "
           f"{kernel} kernel", flush=True)
     lm, cache = _oracle_lm(cpu, k, v, n, steps)
-    d = DeviceQwen2(dev, cap=1024)
+    d = DeviceQwen2(dev, cap=1024, widen_q4=not profile.endswith(":packed"))
     d.cooperative = cooperative
     d.one_launch = kernel
     if n:
@@ -88,14 +88,15 @@ def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative, 
         assert rel_err(vc[i][:, :n + steps], cache.v[i][:, :n + steps]) < 1e-5
 
 
-@pytest.mark.parametrize("profile", ["balanced", "tiny"])
+@pytest.mark.parametrize("profile", ["balanced", "tiny", "tiny:packed"])
 def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
     """24 layers: the one-launch step and the five-kernel step give the same tokens."""
     from cv3amd.qwen2 import DeviceQwen2
     n, steps = 300, 16
     _, dev, k, v = _setup(24, profile, n)
     print(f"[persist] 24 layers, profile={profile}, {n} cached, {steps} steps", flush=True)
-    a = DeviceQwen2(dev, cap=1024)
+    widen = not profile.endswith(":packed")
+    a = DeviceQwen2(dev, cap=1024, widen_q4=widen)
     a.fill_cache(k, v)
     want = []
     a.begin(1, n)
@@ -103,7 +104,7 @@ def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
         a.step(graph=False)
         want.append(a.logits.numpy())
     want_tok = [int(t) for t in a.ints.numpy()[2 + n + 1: 2 + n + 1 + steps]]
-    b = DeviceQwen2(dev, cap=1024)
+    b = DeviceQwen2(dev, cap=1024, widen_q4=widen)
     b.fill_cache(k, v)
     b.begin(1, n)
     for s in range(steps):

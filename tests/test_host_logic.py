@@ -87,3 +87,22 @@ def test_synthetic_tensors_are_seeded_per_name():
     assert np.array_equal(a[k], b[k])
     assert a[k].dtype == np.float32 and abs(float(a[k].std()) - 0.02) < 1e-3
     assert not np.array_equal(tensor("x", (4,)), tensor("y", (4,)))
+
+
+def test_widened_q4_codes_dequantise_like_the_packed_ones():
+    """The decode harness may hold a q4 body as int8 codes n - 8 with the same 32-code
+    blocks and float16 scales: code x scale must equal the q4 dequantisation bit for bit
+    (quant.py:70-86), including padded K."""
+    import numpy as np
+    import oracle.quant as oq
+    from cv3amd.qwen2 import widen_q4_codes
+    rng = np.random.default_rng(11)
+    for rows, k in ((7, 896), (3, 100), (1, 4864)):
+        w = (rng.normal(size=(rows, k)) * 0.05).astype(np.float32)
+        q, s, kp = oq.quantize_q4(w)
+        codes = widen_q4_codes(q)
+        assert codes.dtype == np.int8 and codes.shape == (rows, kp)
+        assert codes.min() >= -8 and codes.max() <= 7
+        mine = codes.astype(np.float32) * np.repeat(s.astype(np.float32), 32, axis=1)
+        want = oq.QTensor("q4", q, s, (rows, k), 32).dequant()
+        assert np.array_equal(mine[:, :k], want)
