@@ -1075,27 +1075,17 @@ __device__ bool ll_get(const uint64_t* s0, int n0, const uint64_t* s1, int n1, c
       const int idx = b0 + (int)threadIdx.x + kPT * j;
       src[j] = idx < n0 ? s0 + idx : idx < n0 + n1 ? s1 + (idx - n0) : s2 + (idx - n0 - n1);
     }
-    // only the words still missing are polled again: hundreds of workgroups re-reading
-    // words that already arrived load the memory system the last ones travel through
     uint64_t w[NW];
-    bool have[NW];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      have[j] = b0 + (int)threadIdx.x + kPT * j >= n;
-      w[j] = 0;
-    }
     bool got = false;
     for (int spins = 0; spins < kPSpin; ++spins) {
 #pragma unroll
       for (int j = 0; j < NW; ++j) {
-        if (!have[j]) {
-          w[j] = __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          have[j] = (uint32_t)(w[j] >> 32) == e;
-        }
+        const int idx = b0 + (int)threadIdx.x + kPT * j;
+        w[j] = idx < n ? __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ((uint64_t)e << 32);
       }
       got = true;
 #pragma unroll
-      for (int j = 0; j < NW; ++j) got = got && have[j];
+      for (int j = 0; j < NW; ++j) got = got && (uint32_t)(w[j] >> 32) == e;
       if (got) break;
       if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
       // back off after a few misses: hundreds of workgroups polling the same words
