@@ -18,10 +18,12 @@
 
 Weights are synthetic (seeded N(0, 0.02), norms 1; cv3amd/synth.py); inputs are
 resident in HBM before the timed regions start.  Each workload reports its
-dominant kernel against the MI355X roofline (HBM 8 TB/s for the int8 GEMV, fp32
-matrix 157.3 TFLOP/s for the DiT GEMM), timed live with HIP events, next to the
-measured device copy rate and fp32 MFMA probe rate, and the oracle's NumPy
-restatement timed on the host cores on a bounded sample.
+dominant kernel against the MI355X roofline (HBM 8 TB/s for the int8 GEMV; for the
+DiT's float32 linears, held as three bfloat16 planes and run as six bfloat16 products
+each, the dense bfloat16 matrix peak over six, 416.7 TFLOP/s of float32 products; fp32
+matrix 157.3 TFLOP/s for what runs on the float32 matrix cores), timed live with HIP
+events, next to the measured device copy rate and fp32 MFMA probe rate, and the
+oracle's NumPy restatement timed on the host cores on a bounded sample.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -46,12 +48,14 @@ METRIC = "DiT flow RTF (10 s, CFG) + int8 LM decode tok/s, each as % of roofline
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
 # device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
-# the one-launch decode step (24 layers, per-channel int8, KV 512: 410.0 MB read + 12.4 MB written)
-# and the fused QKV GEMM of the 10 s solve (46.8 MB + 12.3 MB).  Counters cannot be read inside
-# this process, so these are the measured figures for exactly these kernels and shapes.
+# the one-launch decode step (24 layers, per-channel int8, KV 512: 410.0 MB read + 12.4 MB written).
+# Counters cannot be read inside this process, so this is the measured figure for exactly this
+# kernel and shape.
 TRAFFIC_DECODE_STEP = 422.4e6
-TRAFFIC_QKV_GEMM = 59.1e6
 FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
+# float32 products on the bfloat16 matrix cores: six bfloat16 plane products each (cv3_linear_x3),
+# so the dense bfloat16 peak (2.5 PFLOP/s) over six
+SPLIT_BF16_PEAK = 2.5e15 / 6
 PREFILL = 512             # KV cache positions pre-filled before each decode
 DECODE_TOKENS = 256       # tokens per decode: KV 512 -> 768
 AUDIO_SECONDS = 10.0       # 500 mel frames at 50 Hz
@@ -329,6 +333,7 @@ def bench_flow(args, tensors, meta):
         d.solve(x0, graph=args.graph)
     ms = tm.stop() / n
     flops = d.flops_per_solve()
+    on_planes, on_f32 = d.flops_by_unit()
     log(f"flow: {ms:.2f} ms/solve, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
 
     # Dominant kernel: the fused QKV projection GEMM, [1000, 1024] x [3072, 1024]^T, timed
@@ -347,8 +352,11 @@ def bench_flow(args, tensors, meta):
     kms = tm.stop() / (reps * d.depth)
     kflops = 2.0 * M * N * K
     log(f"flow: QKV GEMM {kms * 1e3:.1f} us/launch, {kflops / (kms / 1e3) / 1e12:.1f} TFLOP/s")
-    return {"ms": ms, "flops": flops, "T": T, "depth": d.depth,
-            "kernel": {"name": "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)", "flops_per_launch": kflops,
+    planes = d.qkv[0].planes is not None if d.depth else False
+    name = ("k_gemm_x3 (float32 GEMM as six bfloat16 plane products, fused QKV 1000x3072x1024)" if planes
+            else "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)")
+    return {"ms": ms, "flops": flops, "on_planes": on_planes, "on_f32": on_f32, "T": T, "depth": d.depth,
+            "kernel": {"name": name, "flops_per_launch": kflops, "peak": SPLIT_BF16_PEAK if planes else FP32_MFMA_PEAK,
                        "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
 
 
@@ -444,30 +452,35 @@ def bench_kernels(args):
     res_epi = _lib.epilogue(residual=d.h.ptr, ld_res=D, gate=g, gate_stride=0, rows_per_gate=1)
     k = d.conv_k
     mish = _lib.epilogue("mish")
+    # the block linears on bfloat16 planes (six products per float32 product) or fp32 MFMA
+    lin_peak, lin_unit = ((SPLIT_BF16_PEAK, "split-bf16") if d.qkv[0].planes is not None
+                          else (FP32_MFMA_PEAK, "fp32 MFMA"))
+    f32 = (FP32_MFMA_PEAK, "fp32 MFMA")
     launches = {
         "layer_norm + AdaLN [1000, 1024]": (
             lambda: _lib.call("layer_norm", d.h.ptr, d.n.ptr, BT, D, 1e-6, None, None, g, g + D * f4, 0, 0, None),
-            None),
+            None, None),
         f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T + rotary": (
-            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D, rope_epi), 2.0 * BT * 3 * D * D),
+            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D, rope_epi), 2.0 * BT * 3 * D * D, (lin_peak, lin_unit)),
         f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T, bias only": (
-            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D), 2.0 * BT * 3 * D * D),
+            lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D), 2.0 * BT * 3 * D * D, (lin_peak, lin_unit)),
         f"flash attention B={B} H={H} T={T} d={dh}": (
             lambda: _lib.call("attention", d.qkvb.ptr, d.qkvb.ptr + D * f4, d.qkvb.ptr + 2 * D * f4, d.att.ptr,
-                              B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None), 4.0 * B * H * T * T * dh),
+                              B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None), 4.0 * B * H * T * T * dh, f32),
         f"out GEMM [{BT}, {D}] x [{D}, {D}]^T + gated residual": (
-            lambda: d.out[0](d.att.ptr, BT, D, d.z1.ptr, D, res_epi), 2.0 * BT * D * D),
+            lambda: d.out[0](d.att.ptr, BT, D, d.z1.ptr, D, res_epi), 2.0 * BT * D * D, (lin_peak, lin_unit)),
         f"ff1 GEMM [{BT}, {D}] x [{F}, {D}]^T + GELU": (
-            lambda: d.ff1[0](d.n.ptr, BT, D, d.ffb.ptr, F, _lib.epilogue("gelu_tanh")), 2.0 * BT * F * D),
+            lambda: d.ff1[0](d.n.ptr, BT, D, d.ffb.ptr, F, _lib.epilogue("gelu_tanh")), 2.0 * BT * F * D,
+            (lin_peak, lin_unit)),
         f"ff2 GEMM [{BT}, {F}] x [{D}, {F}]^T + gated residual": (
-            lambda: d.ff2[0](d.ffb.ptr, BT, F, d.z1.ptr, D, res_epi), 2.0 * BT * D * F),
+            lambda: d.ff2[0](d.ffb.ptr, BT, F, d.z1.ptr, D, res_epi), 2.0 * BT * D * F, (lin_peak, lin_unit)),
         f"grouped causal conv k={k} groups={d.conv_groups} [{B}, {T}, {D}] + Mish": (
             lambda: _lib.call("conv1d_cl", d.h.ptr, B, T, D, D, d.conv_w[0].ptr, D, k, d.conv_groups, k - 1,
                               d.conv_b[0].ptr, d.z1.ptr, D, ctypes.byref(mish), None),
-            2.0 * BT * D * (D // d.conv_groups) * k),
+            2.0 * BT * D * (D // d.conv_groups) * k, f32),
     }
     reps = args.kernel_reps
-    for name, (fn, flops) in launches.items():
+    for name, (fn, flops, pk) in launches.items():
         run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
         run()
         synchronize()
@@ -476,8 +489,8 @@ def bench_kernels(args):
             run()
         us = tm.stop() / (5 * reps) * 1e3
         rate = flops / (us * 1e-6) / 1e12 if flops else None
-        log(f"kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / 157.3:.1%} of fp32 MFMA peak)"
-                                                   if rate else ""))
+        log(f"kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / (pk[0] / 1e12):.1%} of the "
+                                                   f"{pk[1]} peak)" if rate else ""))
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2) if rate else None}
     # the 30 s solve's q8 GEMMs (int8 B dequantised on its way into LDS), block-64 / f16 scales
     T3 = 1500
@@ -793,15 +806,20 @@ def main():
     if flow is not None:
         fk = flow["kernel"]
         rtf = flow["ms"] / 1e3 / AUDIO_SECONDS
+        # the solve's matrix-core floor: its linears' flops at the split-bfloat16 peak, attention,
+        # conv_pos and the AdaLN rows at the fp32 matrix peak
+        floor_ms = (flow["on_planes"] / SPLIT_BF16_PEAK + flow["on_f32"] / FP32_MFMA_PEAK) * 1e3
         line["flow"] = {
-            "workload": "DiT flow decoder, 10 s audio (500 frames), 22 blocks, 10 Euler steps, CFG, fp32",
+            "workload": "DiT flow decoder, 10 s audio (500 frames), 22 blocks, 10 Euler steps, CFG, fp32 "
+                        "(linears as six bfloat16 plane products, float32 accumulate)",
             "ms_per_solve": round(flow["ms"], 3), "rtf": round(rtf, 6),
             "tflops": round(flow["flops"] / (flow["ms"] / 1e3) / 1e12, 2),
-            "mfma_roofline_frac": round(flow["flops"] / (flow["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
-            "flops_per_solve": flow["flops"],
+            "roofline_ms": round(floor_ms, 3),
+            "mfma_roofline_frac": round(floor_ms / flow["ms"], 4),
+            "flops_per_solve": flow["flops"], "flops_on_bf16_planes": flow["on_planes"],
             "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
-                         "peak": FP32_MFMA_PEAK / 1e12, "unit": "TFLOP/s",
-                         "frac": round(fk["achieved_flops"] / FP32_MFMA_PEAK, 4), "traffic": TRAFFIC_QKV_GEMM,
+                         "peak": round(fk["peak"] / 1e12, 1), "unit": "TFLOP/s",
+                         "frac": round(fk["achieved_flops"] / fk["peak"], 4), "traffic": None,
                          "kernel": fk["name"], "us_per_launch": round(fk["us_per_launch"], 2)},
             "cpu_baseline": None if cpu_flow_s is None else {
                 "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",

@@ -11,6 +11,10 @@ int gemv(int wk, bool sf16, bool swiglu, const float* x, int64_t m, int64_t k, i
 int gemm(int bkind, const float* a, int64_t m, int64_t k, int64_t lda, const void* b, int64_t ldb,
          const void* scales, bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c,
          int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
+int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* planes, int64_t ldp, int64_t pstride,
+            int64_t n, const float* bias, float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
+int split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, int64_t pstride,
+             hipStream_t st);
 }  // namespace cv3
 
 using namespace cv3;
@@ -54,6 +58,22 @@ int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, co
   if (m <= kGemvRows)
     return gemv(2, true, false, x, m, k, ldx, q, kp / 2, scales, nb, block, n, bias, y, ldy, epi, nullptr, 0.f, st);
   return gemm(2, x, m, k, ldx, q, kp / 2, scales, true, nb, block, n, bias, y, ldy, epi, st);
+}
+
+// ops.linear with the weight held as three bfloat16 planes [3][n][ldp] (hi, mid, lo; the
+// float32 weight to all 24 bits): the same float32 GEMM, on the bfloat16 matrix cores.
+int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, cv3_stream_t s) {
+  CV3_REQUIRE(n >= 0 && k > 0 && ldw >= k && ldp >= k, CV3_EINVAL, "bad plane split shape n=%lld k=%lld",
+              (long long)n, (long long)k);
+  return split_x3(w, n, k, ldw, planes, ldp, n * ldp, stream_of(s));
+}
+
+int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* planes, int64_t ldp, int64_t n,
+                  const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_REQUIRE(m >= 0 && k > 0 && n >= 0 && ldp >= k && ldx >= k && ldy >= n, CV3_EINVAL,
+              "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
+  if (!m || !n) return CV3_OK;
+  return gemm_x3(x, m, k, ldx, planes, ldp, n * ldp, n, bias, y, ldy, epi, stream_of(s));
 }
 
 }  // extern "C"

@@ -56,10 +56,18 @@ def _host(a) -> np.ndarray:
 
 
 class DeviceLinear:
-    """One resident linear weight: float32 ``[N, K]`` or q8 codes + scales."""
+    """One resident linear weight: float32 ``[N, K]`` or q8 codes + scales.
 
-    def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]]):
+    ``planes=True`` holds a float32 weight (K % 64 == 0) as its three bfloat16 planes
+    instead (``cv3_split_x3``: W = hi + mid + lo to all 24 bits), and the product runs on
+    the bfloat16 matrix cores as six plane products with float32 accumulation
+    (``cv3_linear_x3``): the same float32 linear, with errors against float64 no larger
+    than the float32 matrix cores' own.
+    """
+
+    def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]], planes: bool = False):
         ws = list(weights)
+        self.planes = None
         if all(_is_q(w) for w in ws):
             kinds = {w.kind for w in ws}
             blocks = {int(w.block) for w in ws}
@@ -84,6 +92,10 @@ class DeviceLinear:
                                axis=0)
             self.n, self.k = w.shape
             self.w = to_device(np.ascontiguousarray(w))
+            if planes and self.k % 64 == 0:
+                self.planes = DeviceArray((3, self.n, self.k), np.uint16)
+                _lib.call("split_x3", self.w.ptr, self.n, self.k, self.k, self.planes.ptr, self.k, None)
+                self.w = None
         else:
             raise ValueError("cannot concatenate quantised and float weights")
         if any(b is not None for b in biases):
@@ -99,7 +111,7 @@ class DeviceLinear:
     def nbytes(self) -> int:
         if self.q8:
             return self.q.nbytes + self.scales.nbytes
-        return self.w.nbytes
+        return self.planes.nbytes if self.planes is not None else self.w.nbytes
 
     def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None):
         """y[m, n] = epi(x[m, :k] . W^T + bias) on the calling thread's stream."""
@@ -108,6 +120,8 @@ class DeviceLinear:
         if self.q8:
             _lib.call("linear_q", _lib.KIND_Q8, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
                       _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, None)
+        elif self.planes is not None:
+            _lib.call("linear_x3", x, m, self.k, ldx, self.planes.ptr, self.k, self.n, b, y, ldy, e, None)
         else:
             _lib.call("linear_f32", x, m, self.k, ldx, self.w.ptr, self.k, self.n, b, y, ldy, e, None)
 
@@ -157,7 +171,7 @@ class DeviceDiT:
     """
 
     def __init__(self, weights, prefix: str = "flow.decoder.estimator.", cfg_rate: float = 0.7,
-                 steps: int = 10):
+                 steps: int = 10, planes: bool = True):
         _lib.init()
         m = weights.meta.get("dit", {})
         self.dim = int(m.get("dim", 1024))
@@ -172,7 +186,9 @@ class DeviceDiT:
         D = self.dim
         self.time0 = DeviceLinear([g("time_embed.time_mlp.0.weight")], [g("time_embed.time_mlp.0.bias")])
         self.time2 = DeviceLinear([g("time_embed.time_mlp.2.weight")], [g("time_embed.time_mlp.2.bias")])
-        self.proj_in = DeviceLinear([g("input_embed.proj.weight")], [g("input_embed.proj.bias")])
+        # the linears over all B * T rows hold bfloat16 planes (DeviceLinear) unless planes=False
+        self.planes = bool(planes)
+        self.proj_in = DeviceLinear([g("input_embed.proj.weight")], [g("input_embed.proj.bias")], planes)
         self.mel = self.proj_in.k // 4
         self.conv_w, self.conv_b = [], []
         for c in ("conv1", "conv2"):
@@ -192,12 +208,12 @@ class DeviceDiT:
         for i in range(self.depth):
             b = f"transformer_blocks.{i}."
             self.qkv.append(DeviceLinear([g(b + f"attn.to_{p}.weight") for p in "qkv"],
-                                         [g(b + f"attn.to_{p}.bias") for p in "qkv"]))
-            self.out.append(DeviceLinear([g(b + "attn.to_out.0.weight")], [g(b + "attn.to_out.0.bias")]))
-            self.ff1.append(DeviceLinear([g(b + "ff.ff.0.0.weight")], [g(b + "ff.ff.0.0.bias")]))
-            self.ff2.append(DeviceLinear([g(b + "ff.ff.2.weight")], [g(b + "ff.ff.2.bias")]))
+                                         [g(b + f"attn.to_{p}.bias") for p in "qkv"], planes))
+            self.out.append(DeviceLinear([g(b + "attn.to_out.0.weight")], [g(b + "attn.to_out.0.bias")], planes))
+            self.ff1.append(DeviceLinear([g(b + "ff.ff.0.0.weight")], [g(b + "ff.ff.0.0.bias")], planes))
+            self.ff2.append(DeviceLinear([g(b + "ff.ff.2.weight")], [g(b + "ff.ff.2.bias")], planes))
         self.ff_dim = self.ff1[0].n if self.depth else 2 * D
-        self.proj_out = DeviceLinear([g("proj_out.weight")], [g("proj_out.bias")])
+        self.proj_out = DeviceLinear([g("proj_out.weight")], [g("proj_out.bias")], planes)
         self._T = None
         self._graph = None
 
@@ -320,6 +336,14 @@ class DeviceDiT:
         self._time_and_mod()
         self._step(s, 0.0, update=False)
         return self.outT.numpy()
+
+    def flops_by_unit(self):
+        """(flops of one solve on the bfloat16 planes, flops on the float32 matrix cores)."""
+        T, D, B = self._T, self.dim, 2
+        M = B * T
+        lins = [*self.qkv, *self.out, *self.ff1, *self.ff2, self.proj_in, self.proj_out]
+        planes = sum(2.0 * M * l.n * l.k for l in lins if l.planes is not None)
+        return self.steps * planes, self.flops_per_solve() - self.steps * planes
 
     def flops_per_solve(self) -> float:
         """Algorithmic flops of one solve (every contraction, 2 flops per MAC)."""

@@ -132,6 +132,13 @@ int cv3_embedding(int kind, const void* table, const void* scales, int scale_dty
 /* y[m, n] = epi(x[m, :k] . w[n, :k]).  fp32 weights [n, ldw].  Small m runs a GEMV, large m the MFMA GEMM. */
 int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t ldw, int64_t n,
                    const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
+/* The fp32 linear on the bfloat16 matrix cores (ops.linear, ops.py:121-123; no separate
+ * reference function): w is first split once into three bfloat16 planes [3][n][ldp] (uint16
+ * bit patterns, w = hi + mid + lo to all 24 bits), then each product runs as the six plane
+ * products that carry float32 precision.  K % 8 (split) and K % 64 (linear), 16-byte aligned rows. */
+int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, cv3_stream_t s);
+int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* planes, int64_t ldp, int64_t n,
+                  const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
 /* Quantised weights (q8: q [n, kp] int8; q4: q [n, kp/2]); scales [n, kp/block] (f16 or f32). */
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
                  int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,

@@ -51,15 +51,16 @@ def _oracle_forward(store, x0, mu, cond, spks, t):
                                                          np.array([t, t], np.float32), spk_in, cond_in)
 
 
-@pytest.mark.parametrize("step", [0, 7])
-def test_estimator_one_block_full_width(gpu, step):
-    """x [2, 500, 1024] through one AdaLN block plus the DiT's edges."""
+@pytest.mark.parametrize("step,planes", [(0, True), (7, True), (0, False)])
+def test_estimator_one_block_full_width(gpu, step, planes):
+    """x [2, 500, 1024] through one AdaLN block plus the DiT's edges, with the linears on
+    bfloat16 planes (the default) and on the float32 matrix cores."""
     from cv3amd.dit import DeviceDiT, euler_schedule
     cpu, dev = _stores(1)
     T = 500
     mu, cond, spks, x0 = _inputs(T)
-    print(f"[flow] one-block estimator T={T} step={step}", flush=True)
-    d = DeviceDiT(dev)
+    print(f"[flow] one-block estimator T={T} step={step} planes={planes}", flush=True)
+    d = DeviceDiT(dev, planes=planes)
     d.prepare(mu, spks, cond)
     got = d.estimate(x0, step)
     ts, _ = euler_schedule(10)

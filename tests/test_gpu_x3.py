@@ -1,0 +1,189 @@
+"""The float32 linear on the bfloat16 matrix cores (cv3_split_x3 / cv3_linear_x3).
+
+The weight is held as three bfloat16 planes (hi, mid, lo), each the round-to-nearest-even
+bfloat16 of what the planes before it leave, and each product runs as the six plane
+products of weight >= 2^-16.  No reference function corresponds to the planes; they are
+pinned here by what the arithmetic fixes:
+
+* the planes equal an independent NumPy restatement of the rounding (bit-exact), and
+  hi + mid + lo reproduces every float32 weight to 2^-24 of its magnitude;
+* the linear matches the oracle's float32 ``x @ W.T + b`` (ops.py:121-123) within the
+  same 1e-5 as every other linear, and its error against float64 is no larger than the
+  float32 matrix-core GEMM's (cv3_linear_f32) on the same inputs;
+* each epilogue (activation, gated residual, DiT rotary) gives what the float32 GEMM,
+  itself pinned to the oracle with these epilogues, gives.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+import oracle.ops as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def lib(gpu):
+    from cv3amd import _lib
+    from cv3amd.device import to_device, empty
+    return _lib, to_device, empty
+
+
+def bf16_rne(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (finite inputs)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = u + 0x7FFF + ((u >> 16) & 1)
+    return ((u >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def bf16_value(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def planes_numpy(w: np.ndarray):
+    w = np.asarray(w, np.float32)
+    hi = bf16_rne(w)
+    r1 = (w - bf16_value(hi)).astype(np.float32)
+    mid = bf16_rne(r1)
+    r2 = (r1 - bf16_value(mid)).astype(np.float32)
+    return hi, mid, bf16_rne(r2)
+
+
+def split(lib, w):
+    _lib, to_device, empty = lib
+    n, k = w.shape
+    dw = to_device(np.ascontiguousarray(w, np.float32))
+    planes = empty((3, n, k), np.uint16)
+    _lib.call("split_x3", dw.ptr, n, k, k, planes.ptr, k, None)
+    return planes
+
+
+def linear(lib, planes, x, n, bias=None, epi=None, out=None):
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = out if out is not None else empty((m, n))
+    _lib.call("linear_x3", dx.ptr, m, k, k, planes.ptr, k, n, db.ptr if db is not None else None, y.ptr, n,
+              ctypes.byref(epi) if epi is not None else None, None)
+    return y.numpy()
+
+
+def linear_f32(lib, w, x, bias=None, epi=None, out=None):
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    n = w.shape[0]
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    dw = to_device(np.ascontiguousarray(w, np.float32))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = out if out is not None else empty((m, n))
+    _lib.call("linear_f32", dx.ptr, m, k, k, dw.ptr, k, n, db.ptr if db is not None else None, y.ptr, n,
+              ctypes.byref(epi) if epi is not None else None, None)
+    return y.numpy()
+
+
+def test_planes_are_the_rounding_chain(lib):
+    rng = np.random.default_rng(1)
+    w = (rng.normal(size=(37, 1024)) * np.exp(rng.uniform(-30, 30, size=(37, 1))).astype(np.float32)).astype(np.float32)
+    w[0, :8] = [0.0, -0.0, 1.0, -1.0, 3.0e38, -1.17549435e-38, 1.0 + 2.0 ** -23, 65504.0]
+    w[1, :] = np.float32(1.0) + np.arange(1024, dtype=np.float32) * np.float32(2.0 ** -23)  # every low bit
+    got = split(lib, w).numpy()
+    hi, mid, lo = planes_numpy(w)
+    np.testing.assert_array_equal(got[0], hi)
+    np.testing.assert_array_equal(got[1], mid)
+    np.testing.assert_array_equal(got[2], lo)
+    total = bf16_value(got[0]).astype(np.float64) + bf16_value(got[1]) + bf16_value(got[2])
+    assert np.all(np.abs(total - w.astype(np.float64)) <= 2.0 ** -24 * np.abs(w.astype(np.float64)))
+
+
+SHAPES = [(1, 64, 64), (7, 128, 64), (65, 192, 130), (300, 1024, 1024), (1000, 1024, 3072),
+          (1000, 2048, 1024), (3000, 1024, 1024)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_linear_x3_matches_oracle(lib, m, k, n):
+    rng = np.random.default_rng(m * 7 + k + n)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    b = rng.normal(size=n).astype(np.float32)
+    print(f"[x3] m={m} k={k} n={n}", flush=True)
+    got = linear(lib, split(lib, w), x, n, b)
+    want = ref.linear(x, w, b)
+    assert rel_err(got, want) < TOL
+    # error against float64: no larger than the float32 matrix cores' own
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + b
+    e_x3 = np.abs(got - exact).max()
+    e_f32 = np.abs(linear_f32(lib, w, x, b) - exact).max()
+    print(f"[x3]   max err vs float64: split-bf16 {e_x3:.3e}, float32 MFMA {e_f32:.3e}", flush=True)
+    assert e_x3 <= e_f32 * 1.25 + 1e-30
+
+
+def test_linear_x3_wide_range(lib):
+    """Activations and weights spanning 2^-30 .. 2^30: the planes keep float32's range."""
+    rng = np.random.default_rng(5)
+    m, k, n = 128, 256, 128
+    x = (rng.normal(size=(m, k)) * np.exp2(rng.integers(-30, 30, size=(m, 1)))).astype(np.float32)
+    w = (rng.normal(size=(n, k)) * np.exp2(rng.integers(-30, 30, size=(n, 1)))).astype(np.float32)
+    got = linear(lib, split(lib, w), x, n)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+    assert np.all(np.abs(got - exact) <= 1e-6 * scale)
+
+
+def test_linear_x3_epilogues(lib):
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(3)
+    m, k, n = 1000, 1024, 3072
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) / 32).astype(np.float32)
+    b = rng.normal(size=n).astype(np.float32)
+    planes = split(lib, w)
+    # activation
+    for act in ("gelu_tanh", "silu", "mish"):
+        e = _lib.epilogue(act)
+        assert rel_err(linear(lib, planes, x, n, b, e), linear_f32(lib, w, x, b, e)) < TOL
+    # gated residual, one gate row per 500 output rows (the DiT's per-batch AdaLN gate)
+    res = rng.normal(size=(m, n)).astype(np.float32)
+    gate = rng.normal(size=(2, n)).astype(np.float32)
+    dres, dgate = to_device(res), to_device(gate)
+    e = _lib.epilogue(residual=dres.ptr, ld_res=n, gate=dgate.ptr, gate_stride=n, rows_per_gate=500)
+    assert rel_err(linear(lib, planes, x, n, b, e), linear_f32(lib, w, x, b, e)) < TOL
+    # DiT partial rotary on q and k (64 channels per head, period 1024, limit 2048), T = 500
+    from cv3amd.dit import dit_rope_tables
+    c, s = dit_rope_tables(500, 64)
+    dc, ds = to_device(c), to_device(s)
+    e = _lib.epilogue(rope=(dc.ptr, ds.ptr, 500, 1024, 64, 2048))
+    assert rel_err(linear(lib, planes, x, n, b, e), linear_f32(lib, w, x, b, e)) < TOL
+
+
+def test_linear_x3_in_place_residual(lib):
+    """y = y + gate * (x . W^T): C is the residual itself, as in the DiT's out / ff2 linears."""
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(4)
+    m, k, n = 1000, 2048, 1024
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) / 45).astype(np.float32)
+    h0 = rng.normal(size=(m, n)).astype(np.float32)
+    gate = rng.normal(size=(1, n)).astype(np.float32)
+    dgate = to_device(gate)
+    outs = []
+    for fn in (lambda e, y: linear(lib, split(lib, w), x, n, None, e, out=y),
+               lambda e, y: linear_f32(lib, w, x, None, e, out=y)):
+        y = to_device(h0)
+        e = _lib.epilogue(residual=y.ptr, ld_res=n, gate=dgate.ptr, gate_stride=0, rows_per_gate=1)
+        outs.append(fn(e, y))
+    assert rel_err(outs[0], outs[1]) < TOL
+    assert rel_err(outs[0], h0 + gate * (x @ w.T)) < TOL
+
+
+def test_linear_x3_rejects_ragged_k(lib):
+    _lib, to_device, empty = lib
+    w = np.ones((64, 96), np.float32)
+    planes = split(lib, w)
+    with pytest.raises(NotImplementedError):
+        linear(lib, planes, np.ones((64, 96), np.float32), 64)
