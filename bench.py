@@ -816,6 +816,8 @@ def main():
             "tflops": round(flow["flops"] / (flow["ms"] / 1e3) / 1e12, 2),
             "roofline_ms": round(floor_ms, 3),
             "mfma_roofline_frac": round(floor_ms / flow["ms"], 4),
+            # against the floor of running every flop on the fp32 matrix cores (26.9 ms)
+            "fp32_mfma_frac": round(flow["flops"] / (flow["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
             "flops_per_solve": flow["flops"], "flops_on_bf16_planes": flow["on_planes"],
             "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
                          "peak": round(fk["peak"] / 1e12, 1), "unit": "TFLOP/s",

@@ -789,7 +789,7 @@ int gemm(int bkind, const float* a, int64_t m, int64_t k, int64_t lda, const voi
 }
 
 // C = epi(A . B^T) on the bfloat16 matrix cores, B as three bfloat16 planes
-// planes[p][n][ldp] (pstride elements apart).
+// planes[p][n][ldp] (pstride elements apart).  K % 64 == 0.
 int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* planes, int64_t ldp, int64_t pstride,
             int64_t n, const float* bias, float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st) {
   CV3_REQUIRE(k % (2 * XBK) == 0, CV3_EUNSUPPORTED, "split-bfloat16 GEMM needs K %% 64 == 0 (K = %lld)",
