@@ -49,9 +49,12 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
 # device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
 # the one-launch decode step (24 layers, per-channel int8, KV 512: 410.0 MB read + 12.4 MB written).
-# Counters cannot be read inside this process, so this is the measured figure for exactly this
-# kernel and shape.
+# Counters cannot be read inside this process, so these are the measured figures for exactly
+# these kernels and shapes.
 TRAFFIC_DECODE_STEP = 422.4e6
+# the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes (k_gemm_x3,
+# [1000, 1024] x [3072, 1024]^T): 53.2 MB read + 12.3 MB written
+TRAFFIC_QKV_GEMM_X3 = 65.5e6
 FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
 # float32 products on the bfloat16 matrix cores: six bfloat16 plane products each (cv3_linear_x3),
 # so the dense bfloat16 peak (2.5 PFLOP/s) over six
@@ -357,6 +360,7 @@ def bench_flow(args, tensors, meta):
             else "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)")
     return {"ms": ms, "flops": flops, "on_planes": on_planes, "on_f32": on_f32, "T": T, "depth": d.depth,
             "kernel": {"name": name, "flops_per_launch": kflops, "peak": SPLIT_BF16_PEAK if planes else FP32_MFMA_PEAK,
+                       "traffic": TRAFFIC_QKV_GEMM_X3 if planes else None,
                        "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
 
 
@@ -821,7 +825,7 @@ def main():
             "flops_per_solve": flow["flops"], "flops_on_bf16_planes": flow["on_planes"],
             "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
                          "peak": round(fk["peak"] / 1e12, 1), "unit": "TFLOP/s",
-                         "frac": round(fk["achieved_flops"] / fk["peak"], 4), "traffic": None,
+                         "frac": round(fk["achieved_flops"] / fk["peak"], 4), "traffic": fk["traffic"],
                          "kernel": fk["name"], "us_per_launch": round(fk["us_per_launch"], 2)},
             "cpu_baseline": None if cpu_flow_s is None else {
                 "value": round(cpu_flow_s * 10 / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
