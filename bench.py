@@ -59,6 +59,14 @@ FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
 # float32 products on the bfloat16 matrix cores: six bfloat16 plane products each (cv3_linear_x3),
 # so the dense bfloat16 peak (2.5 PFLOP/s) over six
 SPLIT_BF16_PEAK = 2.5e15 / 6
+# q8 weights on the same cores: three products per code (cv3_linear_q8_x3)
+SPLIT_Q8_PEAK = 2.5e15 / 3
+
+
+def matrix_floor_ms(by_unit) -> float:
+    """The solve's matrix-core floor: each part of its flops at the peak of the unit it runs on."""
+    six, three, f32 = by_unit
+    return (six / SPLIT_BF16_PEAK + three / SPLIT_Q8_PEAK + f32 / FP32_MFMA_PEAK) * 1e3
 PREFILL = 512             # KV cache positions pre-filled before each decode
 DECODE_TOKENS = 256       # tokens per decode: KV 512 -> 768
 AUDIO_SECONDS = 10.0       # 500 mel frames at 50 Hz
@@ -336,7 +344,7 @@ def bench_flow(args, tensors, meta):
         d.solve(x0, graph=args.graph)
     ms = tm.stop() / n
     flops = d.flops_per_solve()
-    on_planes, on_f32 = d.flops_by_unit()
+    by_unit = d.flops_by_unit()
     log(f"flow: {ms:.2f} ms/solve, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}, {flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
 
     # Dominant kernel: the fused QKV projection GEMM, [1000, 1024] x [3072, 1024]^T, timed
@@ -358,7 +366,7 @@ def bench_flow(args, tensors, meta):
     planes = d.qkv[0].planes is not None if d.depth else False
     name = ("k_gemm_x3 (float32 GEMM as six bfloat16 plane products, fused QKV 1000x3072x1024)" if planes
             else "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)")
-    return {"ms": ms, "flops": flops, "on_planes": on_planes, "on_f32": on_f32, "T": T, "depth": d.depth,
+    return {"ms": ms, "flops": flops, "by_unit": by_unit, "T": T, "depth": d.depth,
             "kernel": {"name": name, "flops_per_launch": kflops, "peak": SPLIT_BF16_PEAK if planes else FP32_MFMA_PEAK,
                        "traffic": TRAFFIC_QKV_GEMM_X3 if planes else None,
                        "us_per_launch": kms * 1e3, "achieved_flops": kflops / (kms / 1e3)}}
@@ -391,7 +399,7 @@ def bench_flow_q8(args, tensors, meta, profile: str):
     flops = d.flops_per_solve()
     log(f"flow q8 ({profile}) 30 s: {ms:.2f} ms/solve, RTF {ms / 1e3 / 30.0:.2e}, "
         f"{flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
-    return {"ms": ms, "flops": flops, "T": T}
+    return {"ms": ms, "flops": flops, "by_unit": d.flops_by_unit(), "T": T}
 
 
 def bench_kernels(args):
@@ -496,7 +504,7 @@ def bench_kernels(args):
         log(f"kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / (pk[0] / 1e12):.1%} of the "
                                                    f"{pk[1]} peak)" if rate else ""))
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2) if rate else None}
-    # the 30 s solve's q8 GEMMs (int8 B dequantised on its way into LDS), block-64 / f16 scales
+    # the 30 s solve's q8 GEMMs (the activation's bfloat16 planes times the codes), block-64 / f16 scales
     T3 = 1500
     BT3 = B * T3
     rng = np.random.default_rng(0)
@@ -506,7 +514,7 @@ def bench_kernels(args):
         w = to_device(rng.standard_normal((n, kk), dtype=np.float32) * np.float32(0.02))
         qd, sd, kp = quant.quantize_q8(w, 64, np.float16)   # device quantiser
         y = DeviceArray((BT3, n), np.float32)
-        fn = lambda: _lib.call("linear_q", _lib.KIND_Q8, a_d.ptr, BT3, kk, F, qd.ptr, sd.ptr, _lib.F16, kp, 64, n,
+        fn = lambda: _lib.call("linear_q8_x3", a_d.ptr, BT3, kk, F, qd.ptr, sd.ptr, _lib.F16, kp, 64, n,
                                None, y.ptr, n, None, None)
         run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
         run()
@@ -517,7 +525,8 @@ def bench_kernels(args):
         us = tm.stop() / (5 * reps) * 1e3
         rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
         name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T (block 64, f16 scales)"
-        log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / 157.3:.1%})")
+        log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (SPLIT_Q8_PEAK / 1e12):.1%} of the split "
+            f"q8 peak)")
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
     # one whole-utterance vocoder inference (F0 net, excitation, decode; its convs are k_conv_cl_dma)
     from cv3amd.hift import DeviceHiFT
@@ -812,7 +821,7 @@ def main():
         rtf = flow["ms"] / 1e3 / AUDIO_SECONDS
         # the solve's matrix-core floor: its linears' flops at the split-bfloat16 peak, attention,
         # conv_pos and the AdaLN rows at the fp32 matrix peak
-        floor_ms = (flow["on_planes"] / SPLIT_BF16_PEAK + flow["on_f32"] / FP32_MFMA_PEAK) * 1e3
+        floor_ms = matrix_floor_ms(flow["by_unit"])
         line["flow"] = {
             "workload": "DiT flow decoder, 10 s audio (500 frames), 22 blocks, 10 Euler steps, CFG, fp32 "
                         "(linears as six bfloat16 plane products, float32 accumulate)",
@@ -822,7 +831,7 @@ def main():
             "mfma_roofline_frac": round(floor_ms / flow["ms"], 4),
             # against the floor of running every flop on the fp32 matrix cores (26.9 ms)
             "fp32_mfma_frac": round(flow["flops"] / (flow["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
-            "flops_per_solve": flow["flops"], "flops_on_bf16_planes": flow["on_planes"],
+            "flops_per_solve": flow["flops"], "flops_on_bf16_planes": flow["by_unit"][0],
             "roofline": {"bound": "mfma", "achieved": round(fk["achieved_flops"] / 1e12, 2),
                          "peak": round(fk["peak"] / 1e12, 1), "unit": "TFLOP/s",
                          "frac": round(fk["achieved_flops"] / fk["peak"], 4), "traffic": fk["traffic"],
@@ -837,10 +846,13 @@ def main():
         for prof, fq in flow_q8.items():
             line["flow_q8_30s" if prof == "per_channel" else "flow_q8_30s_block64"] = {
                 "workload": f"DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
-                            f"({scales[prof]}) dequantised in the GEMM, fp32 accumulate",
+                            f"({scales[prof]}): the activation's three bfloat16 planes times the codes (exact in "
+                            f"bfloat16), the block scale on each block sum, fp32 accumulate",
                 "ms_per_solve": round(fq["ms"], 3), "rtf": round(fq["ms"] / 1e3 / 30.0, 6),
                 "tflops": round(fq["flops"] / (fq["ms"] / 1e3) / 1e12, 2),
-                "mfma_roofline_frac": round(fq["flops"] / (fq["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
+                "roofline_ms": round(matrix_floor_ms(fq["by_unit"]), 3),
+                "mfma_roofline_frac": round(matrix_floor_ms(fq["by_unit"]) / fq["ms"], 4),
+                "fp32_mfma_frac": round(fq["flops"] / (fq["ms"] / 1e3) / FP32_MFMA_PEAK, 4),
                 "flops_per_solve": fq["flops"],
             }
     if voc is not None:

@@ -699,6 +699,122 @@ __global__ __launch_bounds__(256) void k_gemm_x3(GemmParams p, const uint16_t* p
   store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
 }
 
+// q8 weights on the bfloat16 matrix cores.  An int8 code is exact in bfloat16, so x . q
+// needs only x's three planes: xh q, xm q and xl q, each exact in the float32 accumulate
+// (three MFMAs per 16-k step where a float32 weight needs six).  The scale multiplies each
+// block's sum: y = sum_b s_b (sum_{k in b} x_k q_k), where the reference sums x_k (q_k s_b)
+// (quant.py:70-86,165-190): the same products, the scale applied once per block sum.  Tiling,
+// A's split and the LDS layout are those of k_gemm_x3; B is one bfloat16 plane in LDS.
+struct XStageQ {
+  float4 a0, a1;  // A: row lr, k = 8 * lc .. + 7 of the stage
+  uint2 b;        // B: the same row's 8 codes
+};
+
+__device__ __forceinline__ uint4 codes_bf16(uint2 w) {
+  uint4 r;
+  uint32_t* o = &r.x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t word = j < 2 ? w.x : w.y;
+    const int sh = (j & 1) * 16;
+    const f32x2_t v = {(float)((int32_t)(word << (24 - sh)) >> 24), (float)((int32_t)(word << (16 - sh)) >> 24)};
+    o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  }
+  return r;
+}
+
+// K % 64 == 0, block % 64 == 0; A rows 16-byte aligned, code rows 8-byte aligned.
+__global__ __launch_bounds__(256) void k_gemm_x3q(GemmParams p, int tiles_m) {
+  __shared__ uint4 sA[2][3][BM * 4];
+  __shared__ uint4 sB[2][BN * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  const int lr = tid >> 2, lc = tid & 3;
+  const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
+  const int8_t* pbr = reinterpret_cast<const int8_t*>(p.b) + min(n0 + lr, p.n - 1) * p.ldb + lc * 8;
+  const int wslot = xslot(lr, lc);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32, br = wn + r32, asw = (ar >> 2) & 3, bsw = (br >> 2) & 3;
+  const int64_t S = p.k / XBK, spb = p.block / XBK;
+  // the lane's output column's scales
+  const int64_t srow = min(n0 + wn + r32, p.n - 1) * p.nb;
+  auto scale = [&](int64_t b) {
+    return p.sf16 ? __half2float(reinterpret_cast<const __half*>(p.scales)[srow + b])
+                  : reinterpret_cast<const float*>(p.scales)[srow + b];
+  };
+  f32x16 big = {0.f}, small = {0.f}, acc = {0.f};
+  float s_cur = scale(0);
+  int64_t blk = 0;
+  // acc += s_b * (this block's sum); the next block's scale is loaded here, a block ahead
+  auto fold = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i] = fmaf(s_cur, big[i] + small[i], acc[i]);
+      big[i] = 0.f;
+      small[i] = 0.f;
+    }
+    ++blk;
+    s_cur = scale(min(blk, p.nb - 1));
+  };
+
+  auto load = [&](XStageQ& x, int64_t k0) {
+    x.a0 = *reinterpret_cast<const float4*>(pa + k0);
+    x.a1 = *reinterpret_cast<const float4*>(pa + k0 + 4);
+    x.b = *reinterpret_cast<const uint2*>(pbr + k0);
+  };
+  auto store = [&](int buf, const XStageQ& x) {
+    uint4 hi, mid, lo;
+    split_x3(x.a0, x.a1, hi, mid, lo);
+    sA[buf][0][wslot] = hi;
+    sA[buf][1][wslot] = mid;
+    sA[buf][2][wslot] = lo;
+    sB[buf][wslot] = codes_bf16(x.b);
+  };
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < XBK / 16; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ asw), sb = br * 4 + (c ^ bsw);
+      const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, sA[buf][0][sa]);
+      const bf16x8_t am = __builtin_bit_cast(bf16x8_t, sA[buf][1][sa]);
+      const bf16x8_t al = __builtin_bit_cast(bf16x8_t, sA[buf][2][sa]);
+      const bf16x8_t bq = __builtin_bit_cast(bf16x8_t, sB[buf][sb]);
+      big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bq, big, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bq, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bq, small, 0, 0, 0);
+    }
+  };
+
+  // S even and >= 2; a block is an even number of stages, so blocks end between iterations
+  XStageQ x, y;
+  load(x, 0);
+  load(y, XBK);
+  store(0, x);
+  __syncthreads();
+  int64_t s = 0;
+  for (; s + 2 < S; s += 2) {
+    load(x, (s + 2) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    store(1, y);
+    __syncthreads();
+    load(y, (s + 3) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1);
+    store(0, x);
+    __syncthreads();
+    if ((s + 2) % spb == 0) fold();
+  }
+  mma(0);
+  store(1, y);
+  __syncthreads();
+  mma(1);
+  fold();  // the last block (or the part of it K covers)
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
+}
+
 // planes[p][row][0 .. k) = plane p of w[row][0 .. k); eight k per thread.
 __global__ __launch_bounds__(256) void k_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* pb,
                                                   int64_t ldp, int64_t pstride) {
@@ -815,6 +931,42 @@ int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* p
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
   hipLaunchKernelGGL(k_gemm_x3, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, planes, ldp, pstride,
                      (int)tiles_m);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// C = epi(A . dequant(q)^T) on the bfloat16 matrix cores: q8 codes [n, ldq], scales [n, nb].
+int gemm_x3q(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* q, int64_t ldq, const void* scales,
+             bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
+             const cv3_epilogue* epi, hipStream_t st) {
+  CV3_REQUIRE(k % (2 * XBK) == 0 && block % (2 * XBK) == 0 && nb * block >= k, CV3_EUNSUPPORTED,
+              "split-bfloat16 q8 GEMM needs K %% 64 == 0 and blocks of a multiple of 64 (K = %lld, block = %lld)",
+              (long long)k, (long long)block);
+  CV3_REQUIRE(((uintptr_t)a % 16 == 0) && lda % 4 == 0 && ((uintptr_t)q % 8 == 0) && ldq % 8 == 0 && ldq >= k,
+              CV3_EINVAL, "split-bfloat16 q8 GEMM operands must be aligned rows");
+  GemmParams p{};
+  p.a = a;
+  p.lda = lda;
+  p.b = q;
+  p.ldb = ldq;
+  p.scales = scales;
+  p.sf16 = sf16;
+  p.nb = nb;
+  p.block = block;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.bias = bias;
+  p.c = c;
+  p.ldc = ldc;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  CV3_REQUIRE(!p.epi.rope_cos || (p.epi.rope_rows > 0 && p.epi.rope_period > 0 && p.epi.rope_width > 0 &&
+                                  p.epi.rope_rows * p.epi.rope_width < (1ll << 31) && m + 64 < (1ll << 31) &&
+                                  n < (1ll << 31)),
+              CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  hipLaunchKernelGGL(k_gemm_x3q, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, (int)tiles_m);
   CV3_LAUNCHED();
   return CV3_OK;
 }

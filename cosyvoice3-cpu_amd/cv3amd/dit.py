@@ -62,7 +62,9 @@ class DeviceLinear:
     instead (``cv3_split_x3``: W = hi + mid + lo to all 24 bits), and the product runs on
     the bfloat16 matrix cores as six plane products with float32 accumulation
     (``cv3_linear_x3``): the same float32 linear, with errors against float64 no larger
-    than the float32 matrix cores' own.
+    than the float32 matrix cores' own.  A q8 weight (blocks of a multiple of 64) then runs
+    as the activation's three planes times its codes, exact in bfloat16, with the block
+    scale on each block's sum (``cv3_linear_q8_x3``).
     """
 
     def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]], planes: bool = False):
@@ -86,6 +88,8 @@ class DeviceLinear:
             self.sf16 = sdt.pop() == np.dtype(np.float16)
             self.q = to_device(np.ascontiguousarray(q))
             self.scales = to_device(np.ascontiguousarray(s))
+            # the activation's bfloat16 planes times the codes (cv3_linear_q8_x3)
+            self.q8_planes = bool(planes) and self.k % 64 == 0 and self.block % 64 == 0
         elif not any(_is_q(w) for w in ws):
             self.q8 = False
             w = np.concatenate([np.asarray(_host(w), dtype=np.float32).reshape(np.shape(w)[0], -1) for w in ws],
@@ -118,7 +122,9 @@ class DeviceLinear:
         b = self.bias.ptr if self.bias is not None else None
         e = ctypes.byref(epi) if epi is not None else None
         if self.q8:
-            _lib.call("linear_q", _lib.KIND_Q8, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
+            fn = "linear_q8_x3" if self.q8_planes else "linear_q"
+            kind = () if self.q8_planes else (_lib.KIND_Q8,)
+            _lib.call(fn, *kind, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
                       _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, None)
         elif self.planes is not None:
             _lib.call("linear_x3", x, m, self.k, ldx, self.planes.ptr, self.k, self.n, b, y, ldy, e, None)
@@ -338,12 +344,15 @@ class DeviceDiT:
         return self.outT.numpy()
 
     def flops_by_unit(self):
-        """(flops of one solve on the bfloat16 planes, flops on the float32 matrix cores)."""
+        """Flops of one solve by how they run: (float32 weights on bfloat16 planes, six
+        products each; q8 weights on bfloat16 planes, three products each; the rest on the
+        float32 matrix cores)."""
         T, D, B = self._T, self.dim, 2
         M = B * T
         lins = [*self.qkv, *self.out, *self.ff1, *self.ff2, self.proj_in, self.proj_out]
-        planes = sum(2.0 * M * l.n * l.k for l in lins if l.planes is not None)
-        return self.steps * planes, self.flops_per_solve() - self.steps * planes
+        six = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.planes is not None)
+        three = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.q8 and l.q8_planes)
+        return six, three, self.flops_per_solve() - six - three
 
     def flops_per_solve(self) -> float:
         """Algorithmic flops of one solve (every contraction, 2 flops per MAC)."""

@@ -139,6 +139,12 @@ int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const floa
 int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, cv3_stream_t s);
 int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* planes, int64_t ldp, int64_t n,
                   const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
+/* quant.qmatmul on q8 weights (quant.py:165-190) on the bfloat16 matrix cores: the activation as
+ * bfloat16 planes, each int8 code exact in bfloat16 (three products per code), the block scale
+ * applied to each block's sum.  K % 64 == 0, block % 64 == 0 (per-channel: block = kp). */
+int cv3_linear_q8_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* q, const void* scales,
+                     int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
+                     const cv3_epilogue* epi, cv3_stream_t s);
 /* Quantised weights (q8: q [n, kp] int8; q4: q [n, kp/2]); scales [n, kp/block] (f16 or f32). */
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
                  int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,

@@ -187,3 +187,88 @@ def test_linear_x3_rejects_ragged_k(lib):
     planes = split(lib, w)
     with pytest.raises(NotImplementedError):
         linear(lib, planes, np.ones((64, 96), np.float32), 64)
+
+
+# ---- q8 weights: the activation's planes times the codes, exact in bfloat16 ----
+
+import oracle.quant as refq
+
+
+def linear_q8_x3(lib, q, s, kp, block, x, n, bias=None, epi=None):
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    dq = to_device(np.ascontiguousarray(q))
+    ds = to_device(np.ascontiguousarray(s))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = empty((m, n))
+    _lib.call("linear_q8_x3", dx.ptr, m, k, k, dq.ptr, ds.ptr, _lib.F16 if s.dtype == np.float16 else _lib.F32,
+              kp, block, n, db.ptr if db is not None else None, y.ptr, n,
+              ctypes.byref(epi) if epi is not None else None, None)
+    return y.numpy()
+
+
+def linear_q8_f32(lib, q, s, kp, block, x, n, bias=None):
+    """The same q8 linear on the float32 matrix cores (codes dequantised into LDS)."""
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx, dq, ds = to_device(np.ascontiguousarray(x, np.float32)), to_device(q), to_device(s)
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = empty((m, n))
+    _lib.call("linear_q", _lib.KIND_Q8, dx.ptr, m, k, k, dq.ptr, ds.ptr,
+              _lib.F16 if s.dtype == np.float16 else _lib.F32, kp, block, n,
+              db.ptr if db is not None else None, y.ptr, n, None, None)
+    return y.numpy()
+
+
+Q8_CASES = [(1000, 1024, 3072, 64, np.float16), (1000, 1024, 1024, 1024, np.float32),
+            (3000, 2048, 1024, 64, np.float16), (3000, 2048, 1024, 2048, np.float32),
+            (65, 128, 130, 128, np.float32), (7, 64, 64, 64, np.float16)]
+
+
+@pytest.mark.parametrize("m,k,n,block,sdt", Q8_CASES)
+def test_linear_q8_x3_matches_oracle(lib, m, k, n, block, sdt):
+    """Block-64 float16 scales (the converter's balanced profile) and per-output-channel float32
+    scales (block = K), at the 10 s and 30 s DiT shapes."""
+    rng = np.random.default_rng(m + k + n + block)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, kp = refq.quantize_q8(w, block, sdt)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    print(f"[x3q] m={m} k={k} n={n} block={block} {np.dtype(sdt).name}", flush=True)
+    got = linear_q8_x3(lib, q, s, kp, block, x, n, b)
+    want = refq.qmatmul(x, refq.QTensor("q8", q, s, (n, k), block), b)
+    assert rel_err(got, want) < TOL
+    # against float64 over the dequantised weight: no larger than the float32 matrix cores' error
+    wd = refq.QTensor("q8", q, s, (n, k), block).dequant().astype(np.float64)
+    exact = x.astype(np.float64) @ wd.T + b
+    e_x3 = np.abs(got - exact).max()
+    e_f32 = np.abs(linear_q8_f32(lib, q, s, kp, block, x, n, b) - exact).max()
+    print(f"[x3q]   max err vs float64: split-bf16 {e_x3:.3e}, float32 MFMA {e_f32:.3e}", flush=True)
+    assert e_x3 <= e_f32 * 1.25 + 1e-30
+
+
+def test_linear_q8_x3_epilogue(lib):
+    """The gated in-place residual of the DiT's out / ff2 linears, against the float32 path."""
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(9)
+    m, k, n = 1000, 2048, 1024
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, kp = refq.quantize_q8(w, 64, np.float16)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    res = rng.normal(size=(m, n)).astype(np.float32)
+    gate = rng.normal(size=(2, n)).astype(np.float32)
+    dres, dgate = to_device(res), to_device(gate)
+    e = _lib.epilogue("gelu_tanh", residual=dres.ptr, ld_res=n, gate=dgate.ptr, gate_stride=n, rows_per_gate=500)
+    got = linear_q8_x3(lib, q, s, kp, 64, x, n, None, e)
+    want = ref.gelu_tanh(refq.qmatmul(x, refq.QTensor("q8", q, s, (n, k), 64)))
+    want = res + np.repeat(gate, 500, axis=0) * want
+    assert rel_err(got, want) < TOL
+
+
+def test_linear_q8_x3_rejects_small_blocks(lib):
+    _lib, to_device, empty = lib
+    w = np.ones((64, 128), np.float32)
+    q, s, kp = refq.quantize_q8(w, 32, np.float16)
+    with pytest.raises(NotImplementedError):
+        linear_q8_x3(lib, q, s, kp, 32, np.ones((64, 128), np.float32), 64)
