@@ -477,8 +477,9 @@ def bench_kernels(args):
         f"QKV GEMM [{BT}, {D}] x [{3 * D}, {D}]^T, bias only": (
             lambda: d.qkv[0](d.n.ptr, BT, D, d.qkvb.ptr, 3 * D), 2.0 * BT * 3 * D * D, (lin_peak, lin_unit)),
         f"flash attention B={B} H={H} T={T} d={dh}": (
-            lambda: _lib.call("attention", d.qkvb.ptr, d.qkvb.ptr + D * f4, d.qkvb.ptr + 2 * D * f4, d.att.ptr,
-                              B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None), 4.0 * B * H * T * T * dh, f32),
+            lambda: _lib.call("attention_x3" if d.planes else "attention", d.qkvb.ptr, d.qkvb.ptr + D * f4,
+                              d.qkvb.ptr + 2 * D * f4, d.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0,
+                              None), 4.0 * B * H * T * T * dh, (lin_peak, lin_unit)),
         f"out GEMM [{BT}, {D}] x [{D}, {D}]^T + gated residual": (
             lambda: d.out[0](d.att.ptr, BT, D, d.z1.ptr, D, res_epi), 2.0 * BT * D * D, (lin_peak, lin_unit)),
         f"ff1 GEMM [{BT}, {D}] x [{F}, {D}]^T + GELU": (

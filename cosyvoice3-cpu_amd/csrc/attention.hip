@@ -10,6 +10,7 @@
 // v_mfma_f32_16x16x4_f32.  It computes S^T = K . Q^T so that each lane's
 // accumulator registers already hold P^T in the B-operand layout of the next
 // MFMA, O^T += V^T . P^T: no LDS round trip for the probabilities.
+#include "bf16x3.hpp"
 #include "common.hpp"
 
 using namespace cv3;
@@ -273,6 +274,251 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p, int nq) {
     for (int i = 0; i < 4; ++i) orow[db * 16 + 4 * g + i] = oacc[db][i] / l_tot;
 }
 
+// The same flash attention on the bfloat16 matrix cores (v_mfma_f32_16x16x32_bf16): q, k, v
+// and the probabilities split into three bfloat16 planes each (bf16x3.hpp), every product
+// as the six plane products of weight >= 2^-16, hh into one accumulator and the other five
+// into a second, added where the float32 kernel reads its accumulator.  Two key groups of
+// four waves (one 64-key tile each per stage), 16 queries per wave, as k_flash64<2>.
+//
+// LDS holds each tile's planes as 64 rows of 128 bytes (8 chunks of 8 bf16, chunk c of row r
+// in slot r * 8 + (c ^ (r / 2) % 8)): K as [key][dim] with key 4c + s in row 16 s + c, V^T as
+// [dim][key].  Score sub-tile s (MFMA rows r = LDS rows 16 s + r) then holds keys 4 r + s, so
+// lane (c16, g) ends with keys 16 g + 4 i + s (i, s < 4): the 16 consecutive keys 16 g .. + 15
+// of its query column.  P V step j takes keys 16 g + 8 j + t (t < 8) from lane group g, which
+// are the lane's own values sc[t % 4][2 j + t / 4] as the B operand (k index 8 g + t), and
+// V^T row d, chunk 2 g + j as the A operand: no data moves between the two products.
+__device__ __forceinline__ int xkv(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+
+__device__ __forceinline__ void mfma6(const bf16x8_t& ah, const bf16x8_t& am, const bf16x8_t& al,
+                                      const bf16x8_t& bh, const bf16x8_t& bm, const bf16x8_t& bl, f32x4& big,
+                                      f32x4& small) {
+  big = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, big, 0, 0, 0);
+  small = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, small, 0, 0, 0);
+  small = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, small, 0, 0, 0);
+  small = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, small, 0, 0, 0);
+  small = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, small, 0, 0, 0);
+  small = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, small, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
+  constexpr int NKG = 2;
+  __shared__ uint4 Ks[NKG][3][KT * 8];
+  __shared__ uint4 Vs[NKG][3][KT * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qw = wave & 3, kg = wave >> 2;
+  const int ntiles = (int)gridDim.x;
+  const int wg = (int)blockIdx.x;
+  const int tile = (ntiles & 7) == 0 ? (wg & 7) * (ntiles >> 3) + (wg >> 3) : wg;
+  const int qt = tile % nq, bh = tile / nq;
+  const int b = bh / p.h, hq = bh % p.h;
+  const int hkv = hq / (p.h / p.hk);
+  const int64_t q0 = (int64_t)qt * QT + qw * QW;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int64_t qi = q0 + c16;
+  const bool qvalid = qi < p.n;
+  int64_t klo64, khi64;
+  visible_keys(p, qi, klo64, khi64);
+  const int klo = (int)klo64, khi = (int)khi64;  // the host bounds m below 2^31 - 64
+
+  // Q^T fragments: query c16, dims 32 ks + 8 g .. + 7, pre-scaled like the reference's
+  // (q * scale) (ops.py:292), in base-2 units, as planes
+  bf16x8_t qh[2], qm[2], ql[2];
+  const float* qrow = p.q + b * p.q_sb + hq * p.q_sh + (qvalid ? qi : 0) * p.q_sn;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    float4 t0 = qvalid ? *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * g) : make_float4(0, 0, 0, 0);
+    float4 t1 = qvalid ? *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * g + 4) : make_float4(0, 0, 0, 0);
+    t0 = make_float4((t0.x * p.scale) * kLog2E, (t0.y * p.scale) * kLog2E, (t0.z * p.scale) * kLog2E,
+                     (t0.w * p.scale) * kLog2E);
+    t1 = make_float4((t1.x * p.scale) * kLog2E, (t1.y * p.scale) * kLog2E, (t1.z * p.scale) * kLog2E,
+                     (t1.w * p.scale) * kLog2E);
+    uint4 h4, m4, l4;
+    split_x3(t0, t1, h4, m4, l4);
+    qh[ks] = __builtin_bit_cast(bf16x8_t, h4);
+    qm[ks] = __builtin_bit_cast(bf16x8_t, m4);
+    ql[ks] = __builtin_bit_cast(bf16x8_t, l4);
+  }
+
+  f32x4 ob[4], os[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) ob[db] = os[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const float* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
+  const int64_t nstages = ceil_div(p.m, NKG * KT);
+  // Staging (next stage's rows in registers while this one is computed; rows past m clamp
+  // to m - 1 and are masked to -inf below):
+  // K: thread -> tile tid/256, key (tid%256)/4, dims 16 (tid%4) .. + 15 (two chunks);
+  // V: thread -> tile tid/256, keys 2 kp, 2 kp + 1 (kp = tid % 32), dims 8 dg .. + 7
+  //    (dg = (tid%256)/32): each dim's two keys are one 32-bit word of a V^T row.
+  const int ltile = tid >> 8, lkey = (tid & 255) >> 2, ld16 = (tid & 3) * 16;
+  const int lrow = (lkey & 3) * 16 + (lkey >> 2);
+  const int kp = tid & 31, dg = (tid & 255) >> 5;
+  float4 kr[4], va[2], vb[2];
+#define CV3_KVX_LOAD(KOFF)                                                                 \
+  {                                                                                        \
+    const int64_t jk = min((KOFF) + ltile * KT + lkey, p.m - 1);                           \
+    const float* kr_ = kbase + jk * p.k_sm + ld16;                                         \
+    kr[0] = *reinterpret_cast<const float4*>(kr_);                                         \
+    kr[1] = *reinterpret_cast<const float4*>(kr_ + 4);                                     \
+    kr[2] = *reinterpret_cast<const float4*>(kr_ + 8);                                     \
+    kr[3] = *reinterpret_cast<const float4*>(kr_ + 12);                                    \
+    const int64_t j0 = min((KOFF) + ltile * KT + 2 * kp, p.m - 1);                         \
+    const int64_t j1 = min((KOFF) + ltile * KT + 2 * kp + 1, p.m - 1);                     \
+    va[0] = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + 8 * dg);                \
+    va[1] = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + 8 * dg + 4);            \
+    vb[0] = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + 8 * dg);                \
+    vb[1] = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + 8 * dg + 4);            \
+  }
+  CV3_KVX_LOAD((int64_t)0)
+  for (int64_t st = 0; st < nstages; ++st) {
+    const int k0i = (int)(st * NKG * KT + kg * KT);  // first key of this wave's tile
+    __syncthreads();
+    {
+      uint4 h4, m4, l4;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        split_x3(kr[2 * half], kr[2 * half + 1], h4, m4, l4);
+        const int slot = xkv(lrow, (ld16 >> 3) + half);
+        Ks[ltile][0][slot] = h4;
+        Ks[ltile][1][slot] = m4;
+        Ks[ltile][2][slot] = l4;
+      }
+      const float a8[8] = {va[0].x, va[0].y, va[0].z, va[0].w, va[1].x, va[1].y, va[1].z, va[1].w};
+      const float b8[8] = {vb[0].x, vb[0].y, vb[0].z, vb[0].w, vb[1].x, vb[1].y, vb[1].z, vb[1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t hh, mm, ll;
+        split_x3(a8[e], b8[e], hh, mm, ll);
+        const int d = 8 * dg + e;
+        // keys 2 kp, 2 kp + 1: chunk kp / 4 of row d, 32-bit word kp % 4
+        uint32_t* w0 = reinterpret_cast<uint32_t*>(&Vs[ltile][0][xkv(d, kp >> 2)]) + (kp & 3);
+        uint32_t* w1 = reinterpret_cast<uint32_t*>(&Vs[ltile][1][xkv(d, kp >> 2)]) + (kp & 3);
+        uint32_t* w2 = reinterpret_cast<uint32_t*>(&Vs[ltile][2][xkv(d, kp >> 2)]) + (kp & 3);
+        *w0 = hh;
+        *w1 = mm;
+        *w2 = ll;
+      }
+    }
+    __syncthreads();
+    if (st + 1 < nstages) CV3_KVX_LOAD((st + 1) * NKG * KT)
+    __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this stage's math
+
+    // S^T sub-tiles: sub-tile s holds keys 4 r + s in MFMA row r; k = dims
+    f32x4 sb[4], ss[4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) sb[sub] = ss[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int slot = xkv(sub * 16 + c16, 4 * ks + g);
+        const bf16x8_t kh = __builtin_bit_cast(bf16x8_t, Ks[kg][0][slot]);
+        const bf16x8_t km = __builtin_bit_cast(bf16x8_t, Ks[kg][1][slot]);
+        const bf16x8_t kl = __builtin_bit_cast(bf16x8_t, Ks[kg][2][slot]);
+        mfma6(kh, km, kl, qh[ks], qm[ks], ql[ks], sb[sub], ss[sub]);
+      }
+    }
+    // lane (c16, g): sc[s][i] = score of key k0i + 16 g + 4 i + s for query c16
+    float sc[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kj = k0i + 16 * g + 4 * i + sub;
+        const bool ok = kj >= klo && kj < khi;
+        sc[sub][i] = ok ? sb[sub][i] + ss[sub][i] : -INFINITY;
+        mx = fmaxf(mx, sc[sub][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const bool none = m_new == -INFINITY;
+    const float m_use = none ? 0.f : m_new;
+    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[sub][i] = __builtin_amdgcn_exp2f(sc[sub][i] - m_use);
+        psum += sc[sub][i];
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      ob[db] *= alpha;
+      os[db] *= alpha;
+    }
+    // O^T += V^T P^T over keys 16 g + 8 j + t: P^T's B operand is the lane's own values
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float4 p0 = make_float4(sc[0][2 * j], sc[1][2 * j], sc[2][2 * j], sc[3][2 * j]);
+      const float4 p1 = make_float4(sc[0][2 * j + 1], sc[1][2 * j + 1], sc[2][2 * j + 1], sc[3][2 * j + 1]);
+      uint4 h4, m4, l4;
+      split_x3(p0, p1, h4, m4, l4);
+      const bf16x8_t ph = __builtin_bit_cast(bf16x8_t, h4);
+      const bf16x8_t pm = __builtin_bit_cast(bf16x8_t, m4);
+      const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, l4);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int slot = xkv(db * 16 + c16, 2 * g + j);
+        const bf16x8_t vh = __builtin_bit_cast(bf16x8_t, Vs[kg][0][slot]);
+        const bf16x8_t vm = __builtin_bit_cast(bf16x8_t, Vs[kg][1][slot]);
+        const bf16x8_t vl = __builtin_bit_cast(bf16x8_t, Vs[kg][2][slot]);
+        mfma6(vh, vm, vl, ph, pm, pl, ob[db], os[db]);
+      }
+    }
+  }
+#undef CV3_KVX_LOAD
+  f32x4 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = ob[db] + os[db];
+  // merge the key groups through LDS, as k_flash64
+  __syncthreads();
+  float* mb = reinterpret_cast<float*>(&Ks[0][0][0]);
+  static_assert((NKG - 1) * 4 * 64 * 18 * 4 <= (int)sizeof(Ks), "merge slots fit the K tiles");
+  if (kg > 0) {
+    float* slot = mb + (((kg - 1) * 4 + qw) * 64 + lane) * 18;
+    slot[0] = m_run;
+    slot[1] = l_run;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) slot[2 + db * 4 + i] = oacc[db][i];
+  }
+  __syncthreads();
+  if (kg > 0) return;
+  float M = m_run;
+#pragma unroll
+  for (int g2 = 1; g2 < NKG; ++g2) M = fmaxf(M, mb[(((g2 - 1) * 4 + qw) * 64 + lane) * 18]);
+  const float a0 = M == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - M);
+  l_run = l_run * a0;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] *= a0;
+#pragma unroll
+  for (int g2 = 1; g2 < NKG; ++g2) {
+    const float* slot = mb + (((g2 - 1) * 4 + qw) * 64 + lane) * 18;
+    const float ag = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(slot[0] - M);
+    l_run += slot[1] * ag;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[db][i] += slot[2 + db * 4 + i] * ag;
+  }
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (!qvalid) return;
+  float* orow = p.o + b * p.o_sb + hq * p.o_sh + qi * p.o_sn;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) orow[db * 16 + 4 * g + i] = oacc[db][i] / l_tot;
+}
+
 // Generic path for any head dim <= 256: one wave per query row, 64 keys per step.
 __global__ __launch_bounds__(256) void k_attn_generic(AttnParams p) {
   extern __shared__ float qs_all[];
@@ -331,10 +577,10 @@ __global__ __launch_bounds__(256) void k_attn_generic(AttnParams p) {
 
 }  // namespace
 
-extern "C" int cv3_attention(const float* q, const float* k, const float* v, float* out, int64_t batch, int h,
-                             int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
-                             const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
-                             float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+static int attention(bool x3, const float* q, const float* k, const float* v, float* out, int64_t batch, int h,
+                     int hk, int64_t n, int64_t m, int d, const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides, float scale, int mask_kind, int64_t mask_a,
+                     int64_t mask_b, cv3_stream_t s) {
   CV3_REQUIRE(h > 0 && hk > 0, CV3_EINVAL, "head counts must be positive");
   CV3_REQUIRE(h % hk == 0, CV3_EINVAL, "%d query heads is not a multiple of %d kv heads", h, hk);
   CV3_REQUIRE(d > 0 && d <= 256, CV3_EUNSUPPORTED, "head dim %d not supported (max 256)", d);
@@ -370,7 +616,9 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
     const int64_t nq = ceil_div(n, QT);
     CV3_REQUIRE(nq * h * batch < (int64_t)1 << 31, CV3_EUNSUPPORTED, "attention grid too large");
     const dim3 grid((unsigned)(nq * h * batch));
-    if (m >= 16 * KT)  // 1024 keys and up: 8 % faster at 1500 keys, no gain at 500
+    if (x3)
+      hipLaunchKernelGGL(k_flash64x, grid, dim3(512), 0, st, p, (int)nq);
+    else if (m >= 16 * KT)  // 1024 keys and up: 8 % faster at 1500 keys, no gain at 500
       hipLaunchKernelGGL(k_flash64<4>, grid, dim3(1024), 0, st, p, (int)nq);
     else
       hipLaunchKernelGGL(k_flash64<2>, grid, dim3(512), 0, st, p, (int)nq);
@@ -380,4 +628,20 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
   }
   CV3_LAUNCHED();
   return CV3_OK;
+}
+
+extern "C" int cv3_attention(const float* q, const float* k, const float* v, float* out, int64_t batch, int h,
+                             int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
+                             const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                             float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+  return attention(false, q, k, v, out, batch, h, hk, n, m, d, q_strides, k_strides, v_strides, o_strides, scale,
+                   mask_kind, mask_a, mask_b, s);
+}
+
+extern "C" int cv3_attention_x3(const float* q, const float* k, const float* v, float* out, int64_t batch, int h,
+                                int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
+                                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                                float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+  return attention(true, q, k, v, out, batch, h, hk, n, m, d, q_strides, k_strides, v_strides, o_strides, scale,
+                   mask_kind, mask_a, mask_b, s);
 }

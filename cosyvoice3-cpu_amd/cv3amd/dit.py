@@ -192,7 +192,8 @@ class DeviceDiT:
         D = self.dim
         self.time0 = DeviceLinear([g("time_embed.time_mlp.0.weight")], [g("time_embed.time_mlp.0.bias")])
         self.time2 = DeviceLinear([g("time_embed.time_mlp.2.weight")], [g("time_embed.time_mlp.2.bias")])
-        # the linears over all B * T rows hold bfloat16 planes (DeviceLinear) unless planes=False
+        # the linears over all B * T rows hold bfloat16 planes (DeviceLinear), and attention runs
+        # on planes (cv3_attention_x3), unless planes=False
         self.planes = bool(planes)
         self.proj_in = DeviceLinear([g("input_embed.proj.weight")], [g("input_embed.proj.bias")], planes)
         self.mel = self.proj_in.k // 4
@@ -296,8 +297,9 @@ class DeviceDiT:
             _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_a, sc_a, 0, 0, None)
             # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120), in the GEMM epilogue
             self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D, rope_epi)
-            _lib.call("attention", self.qkvb.ptr, self.qkvb.ptr + D * f4, self.qkvb.ptr + 2 * D * f4,
-                      self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, None)
+            _lib.call("attention_x3" if self.planes else "attention", self.qkvb.ptr, self.qkvb.ptr + D * f4,
+                      self.qkvb.ptr + 2 * D * f4, self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0,
+                      None)
             self.out[i](self.att.ptr, BT, D, self.h.ptr, D,
                         _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_a, gate_stride=0, rows_per_gate=1))
             _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_m, sc_m, 0, 0, None)
@@ -351,6 +353,8 @@ class DeviceDiT:
         M = B * T
         lins = [*self.qkv, *self.out, *self.ff1, *self.ff2, self.proj_in, self.proj_out]
         six = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.planes is not None)
+        if self.planes and self.dim_head == 64:   # attention on planes too (cv3_attention_x3)
+            six += self.steps * self.depth * 4.0 * B * self.heads * T * T * self.dim_head
         three = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.q8 and l.q8_planes)
         return six, three, self.flops_per_solve() - six - three
 

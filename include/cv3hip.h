@@ -200,6 +200,13 @@ int cv3_attention(const float* q, const float* k, const float* v, float* out, in
                   int64_t n, int64_t m, int d, const int64_t* q_strides, const int64_t* k_strides,
                   const int64_t* v_strides, const int64_t* o_strides, float scale, int mask_kind, int64_t mask_a,
                   int64_t mask_b, cv3_stream_t s);
+/* The same sdpa with head dim 64 on the bfloat16 matrix cores: q, k, v and the probabilities as three
+ * bfloat16 planes each, every product as the six plane products that carry float32 precision.
+ * Other head dims run the generic float32 kernel. */
+int cv3_attention_x3(const float* q, const float* k, const float* v, float* out, int64_t batch, int h, int hk,
+                     int64_t n, int64_t m, int d, const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides, float scale, int mask_kind,
+                     int64_t mask_a, int64_t mask_b, cv3_stream_t s);
 
 /* ---------------- convolution (ops.conv1d ops.py:165-219, ops.depthwise_conv1d ops.py:222-237) ---------------- */
 /* x (cin, t_in) with strides (x_cs, x_ts), optionally nearest-upsampled by `up` before padding;

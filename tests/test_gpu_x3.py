@@ -272,3 +272,57 @@ def test_linear_q8_x3_rejects_small_blocks(lib):
     q, s, kp = refq.quantize_q8(w, 32, np.float16)
     with pytest.raises(NotImplementedError):
         linear_q8_x3(lib, q, s, kp, 32, np.ones((64, 128), np.float32), 64)
+
+
+# ---- attention with head dim 64 on the bfloat16 matrix cores ----
+
+def attention(lib, name, q, k, v, mask=None):
+    """(H, N, 64) queries over (Hk, M, 64) keys/values through cv3_attention[_x3]."""
+    _lib, to_device, empty = lib
+    from cv3amd.ops import _mask_args
+    mk, ma, mb = _mask_args(mask)
+    h, n, d = q.shape
+    hk, m, _ = k.shape
+    dq, dk, dv = to_device(q), to_device(k), to_device(v)
+    out = empty((h, n, d))
+    S = ctypes.c_int64 * 3
+    _lib.call(name, dq.ptr, dk.ptr, dv.ptr, out.ptr, 1, h, hk, n, m, d, S(0, n * d, d), S(0, m * d, d),
+              S(0, m * d, d), S(0, n * d, d), float(np.float32(1.0 / np.sqrt(d))), mk, ma, mb, None)
+    return out.numpy()
+
+
+def sdpa64(q, k, v, mask=None):
+    """float64 attention, the same masks (oracle's mask semantics, in float64)."""
+    h, n, d = q.shape
+    hk, m, _ = k.shape
+    rep = h // hk
+    kk = np.repeat(k.astype(np.float64), rep, axis=0)
+    vv = np.repeat(v.astype(np.float64), rep, axis=0)
+    s = (q.astype(np.float64) * np.float64(np.float32(1.0 / np.sqrt(d)))) @ kk.transpose(0, 2, 1)
+    add = ref.additive_mask(0, n, m, mask)
+    if add is not None:
+        s = s + add.astype(np.float64)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    return (p / p.sum(axis=-1, keepdims=True)) @ vv
+
+
+ATT_CASES = [(16, 16, 500, 500, None), (16, 16, 1500, 1500, None), (14, 2, 200, 200, ("causal", 0)),
+             (8, 8, 130, 390, ("causal", 260)), (4, 4, 300, 300, ("chunk", 25, 1)), (2, 1, 1, 77, None),
+             (3, 3, 65, 64, None)]
+
+
+@pytest.mark.parametrize("h,hk,n,m,mask", ATT_CASES)
+def test_attention_x3_matches_oracle(lib, h, hk, n, m, mask):
+    rng = np.random.default_rng(h * 131 + n + m)
+    q = rng.normal(size=(h, n, 64)).astype(np.float32)
+    k = rng.normal(size=(hk, m, 64)).astype(np.float32)
+    v = rng.normal(size=(hk, m, 64)).astype(np.float32)
+    print(f"[att] h={h} hk={hk} n={n} m={m} mask={mask}", flush=True)
+    got = attention(lib, "attention_x3", q, k, v, mask)
+    assert rel_err(got, ref.sdpa(q, k, v, mask)) < TOL
+    exact = sdpa64(q, k, v, mask)
+    e_x3 = np.abs(got - exact).max()
+    e_f32 = np.abs(attention(lib, "attention", q, k, v, mask) - exact).max()
+    print(f"[att]   max err vs float64: split-bf16 {e_x3:.3e}, float32 MFMA {e_f32:.3e}", flush=True)
+    assert e_x3 <= e_f32 * 1.25 + 1e-30
