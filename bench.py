@@ -655,6 +655,8 @@ def bench_hift(args, tensors, meta):
         out[label] = ms
         log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
     out["flops_whole"] = d.flops(T)
+    planes, f32 = d.flops_by_unit(T)
+    out["by_unit_whole"] = (planes, 0.0, f32)
     return out
 
 
@@ -902,7 +904,10 @@ def main():
             "rtf_inference_whole": round(voc["inference_whole"] / 1e3 / AUDIO_SECONDS, 6),
             "ms_inference_chunked_1s": round(voc["inference_chunked_1s"], 3),
             "conv_tflops_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / 1e12, 2),
-            "mfma_roofline_frac_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / FP32_MFMA_PEAK, 4),
+            "roofline_ms_whole": round(matrix_floor_ms(voc["by_unit_whole"]), 3),
+            "flops_on_bf16_planes_whole": round(voc["by_unit_whole"][0] / voc["flops_whole"], 4),
+            "mfma_roofline_frac_whole": round(matrix_floor_ms(voc["by_unit_whole"]) / voc["whole"], 4),
+            "fp32_mfma_frac_whole": round(voc["flops_whole"] / (voc["whole"] / 1e3) / FP32_MFMA_PEAK, 4),
             "cpu_baseline": None if cpu_hift_s is None else {
                 "value": round(cpu_hift_s / AUDIO_SECONDS, 3), "unit": "RTF", "cores": cores, "kind": "port",
                 "sample": "one whole-utterance inference (F0 net, excitation, decode) of the same mel by the "

@@ -16,6 +16,7 @@
 //
 // Epilogue: y = residual + act(acc + bias), or y = snake(acc + bias) with a
 // per-output-channel alpha (the resblock's second Snake, hift.py:124).
+#include "bf16x3.hpp"
 #include "common.hpp"
 #include "epilogue.hpp"
 
@@ -394,6 +395,47 @@ __device__ __forceinline__ void cl_mma(const float* as, const float* bs, int aro
   }
 }
 
+// Epilogue of the channels-last conv's 32 x 32 accumulator (reg i -> time row
+// m0 + wm + (i/4)*8 + h*4 + i%4, output channel n0 + wn + lane%32): split-K partials, or
+// bias, Snake / activation and residual.
+__device__ __forceinline__ void cl_epilogue(const ConvCL& p, const f32x16& acc, int m0, int n0, int wm, int wn,
+                                            int r32, int h) {
+  const int co = n0 + wn + r32;
+  if (co >= p.cout) return;
+  if (p.ksplit > 1) {
+    float* dst = p.part + (int64_t)blockIdx.z * p.t_out * p.cout + co;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+      if (tr < p.t_out) dst[(int64_t)tr * p.cout] = acc[i];
+    }
+    return;
+  }
+  const float bias = p.bias ? p.bias[co] : 0.f;
+  const float alpha = p.snake_alpha ? p.snake_alpha[co] : 0.f;
+  float res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tr = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), p.t_out - 1);
+    res[i] = p.res ? p.res[(int64_t)tr * p.r_ts + co * p.r_cs] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (tr < p.t_out) {
+      float v = acc[i] + bias;
+      if (p.snake_alpha) {
+        const float sn = sinf(alpha * v);
+        v = v + (1.0f / (alpha + p.snake_eps)) * (sn * sn);
+      } else {
+        v = apply_act(p.act, v, p.act_param);
+      }
+      if (p.res) v = res[i] + v;
+      p.y[(int64_t)tr * p.y_ts + co * p.y_cs] = v;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_conv_cl_dma(ConvCL p, int tiles_m) {
   __shared__ float A0[2048], A1[2048], A2[2048];
   __shared__ float B0[2048], B1[2048], B2[2048];
@@ -439,41 +481,107 @@ __global__ __launch_bounds__(256) void k_conv_cl_dma(ConvCL p, int tiles_m) {
 #undef CV3_CL_STEP
   // no DMA may still be writing this workgroup's LDS when it ends
   __builtin_amdgcn_s_waitcnt(CV3_VMCNT(0));
-  // accumulator: reg i -> time row m0 + wm + (i/4)*8 + h*4 + i%4, output channel n0 + wn + lane%32
-  const int co = n0 + wn + r32;
-  if (co >= p.cout) return;
-  if (p.ksplit > 1) {
-    float* dst = p.part + (int64_t)blockIdx.z * p.t_out * p.cout + co;
+  cl_epilogue(p, acc, m0, n0, wm, wn, r32, h);
+}
+
+// The channels-last conv of k_conv_cl_dma on the bfloat16 matrix cores: x split into its
+// three bfloat16 planes on its way into LDS (bf16x3.hpp), the packed weight held as planes
+// [3][cout][k * cin], six 32x32x16 bf16 products per product (hh into one accumulator, the rest
+// into a second).  A stage is 32 channels of one tap, as there; the rows of 64 bytes per plane
+// sit at slot r * 4 + (c ^ (r / 4) % 4) (16-byte chunk c), conflict-free for a 16-lane read.
+// Loads run two stages ahead in ping-pong registers; a slice's stage count must be even.
+struct ClStageX {
+  float4 a0, a1;     // x: this thread's time row, channels 8 lc .. + 7 of the stage
+  uint4 b0, b1, b2;  // weight planes: this thread's output channel, the same 8 k
+};
+
+__device__ __forceinline__ int cl_xslot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
+
+__global__ __launch_bounds__(256) void k_conv_cl_x3(ConvCL p, const uint16_t* wp, int64_t wps, int tiles_m) {
+  __shared__ uint4 sA[2][3][64 * 4];
+  __shared__ uint4 sB[2][3][64 * 4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int m0 = (t % tiles_m) * 64, n0 = (t / tiles_m) * 64;
+  const int K = p.k * p.cin, cpt = p.cin / 32, tin_up = p.t_in * p.up;
+  const int lr = tid >> 2, lc = tid & 3, tr = m0 + lr;
+  const int wslot = cl_xslot(lr, lc);
+  const uint16_t* pbr = wp + (int64_t)min(n0 + lr, p.cout - 1) * K + lc * 8;
+  const int wm = (w >> 1) * 32, wn = (w & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32, br = wn + r32, asw = (ar >> 2) & 3, bsw = (br >> 2) & 3;
+  const int S = K / 32 / p.ksplit, sb = blockIdx.z * S;
+  f32x16 big = {0.f}, small = {0.f};
+
+  auto load = [&](ClStageX& x, int sg) {
+    const int j = sg / cpt, c0 = (sg - j * cpt) * 32;
+    const int u = tr + j * p.dil - p.pad_l;
+    const bool ok = tr < p.t_out && u >= 0 && u < tin_up;
+    const int q = ok ? (p.up == 1 ? u : (int)((unsigned)u / (unsigned)p.up)) : 0;
+    const float* a = ok ? p.x + (int64_t)q * p.ldx + c0 + lc * 8 : g_conv_zero_row + lc * 8;
+    x.a0 = *reinterpret_cast<const float4*>(a);
+    x.a1 = *reinterpret_cast<const float4*>(a + 4);
+    const uint16_t* b = pbr + (int64_t)sg * 32;
+    x.b0 = *reinterpret_cast<const uint4*>(b);
+    x.b1 = *reinterpret_cast<const uint4*>(b + wps);
+    x.b2 = *reinterpret_cast<const uint4*>(b + 2 * wps);
+  };
+  auto store = [&](int buf, const ClStageX& x) {
+    uint4 hi, mid, lo;
+    split_x3(x.a0, x.a1, hi, mid, lo);
+    sA[buf][0][wslot] = hi;
+    sA[buf][1][wslot] = mid;
+    sA[buf][2][wslot] = lo;
+    sB[buf][0][wslot] = x.b0;
+    sB[buf][1][wslot] = x.b1;
+    sB[buf][2][wslot] = x.b2;
+  };
+  auto mma = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
-      if (tr < p.t_out) dst[(int64_t)tr * p.cout] = acc[i];
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ asw), sbb = br * 4 + (c ^ bsw);
+      const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, sA[buf][0][sa]);
+      const bf16x8_t am = __builtin_bit_cast(bf16x8_t, sA[buf][1][sa]);
+      const bf16x8_t al = __builtin_bit_cast(bf16x8_t, sA[buf][2][sa]);
+      const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, sB[buf][0][sbb]);
+      const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, sB[buf][1][sbb]);
+      const bf16x8_t bl = __builtin_bit_cast(bf16x8_t, sB[buf][2][sbb]);
+      big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, big, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, small, 0, 0, 0);
     }
-    return;
+  };
+
+  // S even and >= 2
+  ClStageX x, y;
+  load(x, sb);
+  load(y, sb + 1);
+  store(0, x);
+  __syncthreads();
+  for (int s = 0; s + 2 < S; s += 2) {
+    load(x, sb + s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    store(1, y);
+    __syncthreads();
+    load(y, sb + s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1);
+    store(0, x);
+    __syncthreads();
   }
-  const float bias = p.bias ? p.bias[co] : 0.f;
-  const float alpha = p.snake_alpha ? p.snake_alpha[co] : 0.f;
-  float res[16];
+  mma(0);
+  store(1, y);
+  __syncthreads();
+  mma(1);
+  f32x16 acc;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int tr = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), p.t_out - 1);
-    res[i] = p.res ? p.res[(int64_t)tr * p.r_ts + co * p.r_cs] : 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int tr = m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3);
-    if (tr < p.t_out) {
-      float v = acc[i] + bias;
-      if (p.snake_alpha) {
-        const float sn = sinf(alpha * v);
-        v = v + (1.0f / (alpha + p.snake_eps)) * (sn * sn);
-      } else {
-        v = apply_act(p.act, v, p.act_param);
-      }
-      if (p.res) v = res[i] + v;
-      p.y[(int64_t)tr * p.y_ts + co * p.y_cs] = v;
-    }
-  }
+  for (int i = 0; i < 16; ++i) acc[i] = big[i] + small[i];
+  cl_epilogue(p, acc, m0, n0, wm, wn, r32, h);
 }
 
 // Split-K epilogue of k_conv_cl_dma: slices added in order z = 0, 1, ...
@@ -641,20 +749,27 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
   return CV3_OK;
 }
 
-int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
-                         int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r,
-                         int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
-                         const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
-                         int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s) {
+// The channels-last packed conv: float32 weights (k_conv_cl_dma) or, with `planes`, their three
+// bfloat16 planes [3][cout][k * cin] (k_conv_cl_x3).
+static int conv_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
+                          const uint16_t* planes, int64_t cout, int64_t k, const float* bias, int64_t dilation,
+                          int64_t pad_l, int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act,
+                          float act_param, const float* snake_alpha, float snake_eps, const float* residual,
+                          int64_t r_ts, int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
+                          cv3_stream_t s) {
   CV3_REQUIRE(dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0 && cin > 0 && cout > 0, CV3_EINVAL,
               "bad conv geometry");
   CV3_REQUIRE(cin % 32 == 0, CV3_EUNSUPPORTED, "channels-last packed conv needs cin %% 32 == 0 (cin %lld)",
               (long long)cin);
-  CV3_REQUIRE(((uintptr_t)x % 16) == 0 && ldx % 4 == 0 && ldx >= cin && ((uintptr_t)w_packed % 16) == 0, CV3_EINVAL,
+  const uintptr_t wa = planes ? (uintptr_t)planes : (uintptr_t)w_packed;
+  CV3_REQUIRE(((uintptr_t)x % 16) == 0 && ldx % 4 == 0 && ldx >= cin && wa % 16 == 0, CV3_EINVAL,
               "channels-last packed conv needs 16-byte aligned rows");
   const int64_t stages = k * cin / 32;
   CV3_REQUIRE(ksplit >= 1 && ksplit <= 16 && stages % ksplit == 0, CV3_EINVAL,
               "ksplit %lld must divide the %lld K stages", (long long)ksplit, (long long)stages);
+  CV3_REQUIRE(!planes || (stages / ksplit) % 2 == 0, CV3_EUNSUPPORTED,
+              "the bfloat16-plane conv needs an even number of 32-channel stages per K slice (%lld / %lld)",
+              (long long)stages, (long long)ksplit);
   const int64_t tp = t_in * up + pad_l + pad_r;
   const int64_t span = dilation * (k - 1) + 1;
   const int64_t t_out = tp >= span ? tp - span + 1 : 0;
@@ -690,8 +805,12 @@ int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx,
   p.ksplit = (int)ksplit;
   const int64_t tiles_m = ceil_div(t_out, 64), tiles_n = ceil_div(cout, 64);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "conv too large");
-  hipLaunchKernelGGL(k_conv_cl_dma, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
-                     stream_of(s), p, (int)tiles_m);
+  if (planes)
+    hipLaunchKernelGGL(k_conv_cl_x3, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
+                       stream_of(s), p, planes, cout * k * cin, (int)tiles_m);
+  else
+    hipLaunchKernelGGL(k_conv_cl_dma, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
+                       stream_of(s), p, (int)tiles_m);
   CV3_LAUNCHED();
   if (ksplit > 1) {
     const int64_t n = cout * t_out;
@@ -700,6 +819,28 @@ int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx,
     CV3_LAUNCHED();
   }
   return CV3_OK;
+}
+
+int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
+                         int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l, int64_t pad_r,
+                         int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
+                         const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
+                         int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s) {
+  return conv_cl_packed(x, t_in, cin, ldx, w_packed, nullptr, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts, y_cs,
+                        act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
+                        workspace_floats, s);
+}
+
+int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const uint16_t* w_planes,
+                            int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l,
+                            int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
+                            const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts,
+                            int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
+                            cv3_stream_t s) {
+  CV3_REQUIRE(w_planes, CV3_EINVAL, "null weight planes");
+  return conv_cl_packed(x, t_in, cin, ldx, nullptr, w_planes, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts,
+                        y_cs, act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
+                        workspace_floats, s);
 }
 
 int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,

@@ -44,15 +44,17 @@ def causal_pad(kernel_size: int, dilation: int = 1) -> int:
     return int((kernel_size * dilation - dilation) / 2) * 2 + (kernel_size + 1) % 2
 
 
-def split_k(t_out: int, cout: int, stages: int) -> int:
+def split_k(t_out: int, cout: int, stages: int, even: bool = False) -> int:
     """K slices for the packed conv: grids under 160 tiles of 64 x 64 (a 1 s chunk's
     256-channel stage has 60) are split until they cover about two tiles per CU; the
-    slices divide the k*cin/32 stages evenly."""
+    slices divide the k*cin/32 stages evenly (``even``: into an even count per slice, as the
+    bfloat16-plane conv needs)."""
     tiles = -(-t_out // 64) * -(-cout // 64)
     if tiles >= 160:
         return 1
+    step = 2 if even else 1
     for ks in (8, 6, 4, 3, 2):
-        if tiles * ks <= 512 and stages % ks == 0:
+        if tiles * ks <= 512 and stages % (ks * step) == 0:
             return ks
     return 1
 
@@ -66,7 +68,11 @@ def hann_window(n: int) -> np.ndarray:
 class DeviceHiFT:
     """HiFTNet weights resident in HBM; ``weights`` has ``get(name)`` and ``meta``."""
 
-    def __init__(self, weights, prefix: str = "hift."):
+    def __init__(self, weights, prefix: str = "hift.", planes: bool = True):
+        """``planes``: the channels-last convs run on the bfloat16 matrix cores with their
+        weights held as three bfloat16 planes (cv3_conv1d_cl_packed_x3: the same float32
+        conv, errors against float64 below the float32 matrix cores'); False keeps them on
+        the float32 matrix cores."""
         _lib.init()
         m = weights.meta.get("hift", {})
         self.rates = list(m.get("upsample_rates", [8, 5, 3]))
@@ -88,6 +94,7 @@ class DeviceHiFT:
         self.up_total = int(np.prod(self.rates))
         self.w = {}
         self.wp = {}   # conv weights repacked (out, k, in) for the channels-last implicit GEMM
+        self.wpx = {}  # ... and as three bfloat16 planes [3][out][k * in] (planes=True)
         self.shape = {}
         for name in weights.keys():
             if not name.startswith(prefix) or "f0_predictor.classifier" in name or "m_source" in name:
@@ -98,6 +105,11 @@ class DeviceHiFT:
             self.shape[key] = arr.shape
             if arr.ndim == 3 and arr.shape[1] % 32 == 0:
                 self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
+                cout, kin = arr.shape[0], arr.shape[1] * arr.shape[2]
+                if planes and (kin // 32) % 2 == 0:
+                    pl = DeviceArray((3, cout, kin), np.uint16)
+                    _lib.call("split_x3", self.wp[key].ptr, cout, kin, kin, pl.ptr, kin, None)
+                    self.wpx[key] = pl
         # the F0 predictor's condnet convs sit with the stack's weights above; its
         # classifier and the source merge (hift.py:56-72,108-110) are float32 vectors
         self.f0_depth = 0
@@ -160,7 +172,14 @@ class DeviceHiFT:
         res = residual.ptr if residual is not None else None
         r_ts = residual.shape[1] if residual is not None else 0
         wkey = key + ".weight"
-        if wkey in self.wp:   # cin % 32 == 0: the DMA implicit GEMM
+        if wkey in self.wpx:  # the bfloat16-plane implicit GEMM
+            ks = split_k(n, cout, k * cin // 32, even=True)
+            ws = self._new((ks * cout * n,)) if ks > 1 else None
+            _lib.call("conv1d_cl_packed_x3", x.ptr, t_in, cin, cin, self.wpx[wkey].ptr, cout, k,
+                      self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_ts,
+                      y_cs, ACT[act], float(act_param), alpha, 1e-9, res, r_ts, 1, ks, ws.ptr if ws else None,
+                      ws.size if ws else 0, None)
+        elif wkey in self.wp:   # cin % 32 == 0: the DMA implicit GEMM
             ks = split_k(n, cout, k * cin // 32)
             ws = self._new((ks * cout * n,)) if ks > 1 else None
             _lib.call("conv1d_cl_packed", x.ptr, t_in, cin, cin, self.wp[wkey].ptr, cout, k,
@@ -468,20 +487,29 @@ class DeviceHiFT:
 
     def flops(self, t: int) -> float:
         """Algorithmic conv flops of a whole-utterance decode of t mel frames."""
-        total = 0.0
+        return sum(self.flops_by_unit(t))
+
+    def flops_by_unit(self, t: int) -> tuple:
+        """(flops on the bfloat16 planes, flops on the float32 units) of a whole-utterance
+        decode of t mel frames: a conv runs on the planes when its weights were split."""
+        on = [0.0, 0.0]
+
+        def add(key, f):
+            on[0 if key + ".weight" in self.wpx else 1] += f
+
         cur_t = t
         kpre = self.shape["conv_pre.weight"]
-        total += 2.0 * kpre[0] * kpre[1] * kpre[2] * cur_t
+        add("conv_pre", 2.0 * kpre[0] * kpre[1] * kpre[2] * cur_t)
         for i, r in enumerate(self.rates):
             cur_t *= r
             co, ci, k = self.shape[f"ups.{i}.weight"]
-            total += 2.0 * co * ci * k * cur_t
+            add(f"ups.{i}", 2.0 * co * ci * k * cur_t)
             co, ci, k = self.shape[f"source_downs.{i}.weight"]
-            total += 2.0 * co * ci * k * cur_t
+            add(f"source_downs.{i}", 2.0 * co * ci * k * cur_t)
             for g, idx, kk in [("source_resblocks", i, self.src_k[i])] + \
                     [("resblocks", i * self.nk + j, self.rb_k[j]) for j in range(self.nk)]:
                 c = self.shape[f"{g}.{idx}.convs1.0.weight"][0]
-                total += 2 * 3 * 2.0 * c * c * kk * cur_t
+                add(f"{g}.{idx}.convs1.0", 2 * 3 * 2.0 * c * c * kk * cur_t)
         co, ci, k = self.shape["conv_post.weight"]
-        total += 2.0 * co * ci * k * cur_t
-        return total
+        add("conv_post", 2.0 * co * ci * k * cur_t)
+        return tuple(on)

@@ -238,6 +238,16 @@ int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx,
                          int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
                          const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
                          int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s);
+/* cv3_conv1d_cl_packed on the bfloat16 matrix cores: x split into three bfloat16 planes in the
+ * kernel, the packed weight given as its planes [3][cout][k * cin] (cv3_split_x3 over the packed
+ * (cout, k * cin) rows), six plane products per product with float32 accumulation.  Needs an even
+ * number of 32-channel stages per K slice (k * cin / 32 / ksplit). */
+int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const uint16_t* w_planes,
+                            int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l,
+                            int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
+                            const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts,
+                            int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
+                            cv3_stream_t s);
 /* The DiT's grouped causal conv_pos (dit.py:99-112, ops.conv1d with groups) on channels-last activations:
  * x [batch, t, ldx] (cin channels), y [batch, t, ldy] (cout channels),
  * y[b, s, co] = epi(bias[co] + sum_{j<k, c<cin/groups} W[co, c, j] x[b, s + j - pad_l, g*cin/groups + c]),

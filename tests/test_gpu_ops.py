@@ -417,12 +417,17 @@ CL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("x3", [False, True])
 @pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi,ks,cf", CL_CASES)
-def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf):
-    """Channels-last stride-1 conv through the DMA implicit GEMM, against the oracle's
-    upsample + conv1d + epilogue on (channel, time) data."""
+def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf, x3):
+    """Channels-last stride-1 conv through the DMA implicit GEMM (and, ``x3``, its
+    bfloat16-plane form, cv3_conv1d_cl_packed_x3, where a K slice has an even number of
+    32-channel stages), against the oracle's upsample + conv1d + epilogue on (channel, time)
+    data."""
     from cv3amd import _lib
     from cv3amd.device import DeviceArray, to_device
+    if x3 and (k * cin // 32 // ks) % 2:
+        pytest.skip("the bfloat16-plane conv needs an even number of stages per K slice")
     x = rng.normal(size=(cin, T)).astype(np.float32)
     w = (rng.normal(size=(cout, cin, k)) * 0.05).astype(np.float32)
     b = (rng.normal(size=cout) * 0.05).astype(np.float32)
@@ -442,10 +447,15 @@ def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf):
     else:
         yd, y_ts, y_cs = (to_device(res_cl) if epi == "residual" else DeviceArray((t_out, cout))), cout, 1
     ws = DeviceArray((ks * cout * t_out,)) if ks > 1 else None
+    wptr, fn = wd.ptr, "conv1d_cl_packed"
+    if x3:
+        planes = DeviceArray((3, cout, k * cin), np.uint16)
+        _lib.call("split_x3", wd.ptr, cout, k * cin, k * cin, planes.ptr, k * cin, None)
+        wptr, fn = planes.ptr, "conv1d_cl_packed_x3"
     for _ in range(2):  # the second call sees the first call's partials in the workspace
         if epi == "residual":
             _lib.call("copy_h2d", yd.ptr, res_cl.ctypes.data, res_cl.nbytes, None)
-        _lib.call("conv1d_cl_packed", xd.ptr, T, cin, cin, wd.ptr, cout, k, bd.ptr, dil, pad[0], pad[1], up,
+        _lib.call(fn, xd.ptr, T, cin, cin, wptr, cout, k, bd.ptr, dil, pad[0], pad[1], up,
                   yd.ptr, y_ts, y_cs, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
                   ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, cout, 1,
                   ks, ws.ptr if ws else None, ws.size if ws else 0, None)
