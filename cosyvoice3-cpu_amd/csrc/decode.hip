@@ -1215,7 +1215,22 @@ __device__ __forceinline__ uint64_t idle_wait(uint64_t t0, uint64_t prev) {
 
 // Q4: the body's matrices are q4 (32 codes per 16-byte chunk); the head and the
 // speech embedding stay q8, as the reference's converter stores them.
-template <bool SF16, bool Q4>
+// MX: phase D's [gate; up] rows (q8, one scale per row) run on the matrix cores.  x_mid * w
+// is split into four base-128 digit planes against a shared power of two,
+// X = rint(v 2^(27 - E)) with every |v| < 2^E, X = d0 + 128 d1 + 128^2 d2 + 128^3 d3,
+// d0..d2 the 7-bit fields of X's two's complement (0..127) and d3 = X >> 21 (-64..63),
+// all int8; v_mfma_i32_16x16x64_i8 of the planes (A rows 0..3) with 16 weight
+// rows (B: lane l holds row l % 16, codes 16 (l / 16) .. +16 of each 64) gives each
+// row's four plane sums exactly in int32, combined in float64 into sum_k q_k X_k, then
+// times 2^(E - 27), the row's scale and the RMSNorm factor.  The dot product is that
+// of the int8 row with v rounded 27 bits below its largest element, and the rows cost
+// no per-code VALU work (the VALU path spends two instructions per code).  The rows go
+// global -> LDS by DMA (global_load_lds_dwordx4) in the MFMA operand order, so they hold
+// no registers while the workgroup waits for x_mid.
+constexpr int kMxSteps = 16;  // 64-code steps of a row: hidden <= 1024
+// One 16-byte global -> LDS DMA per lane (lane l lands at lds + 16 l).
+__device__ __forceinline__ void dma16(const void* g, void* lds) { __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0); }
+template <bool SF16, bool Q4, bool MX = false>
 __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   constexpr int CPC = kCodes<Q4>;       // codes per chunk of the body rows
   constexpr int kStage = 64 * CPC;      // staged width of a one-chunk-per-lane body row
@@ -1229,6 +1244,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   __shared__ float hb_val[8];
   __shared__ int hb_i[8];
   __shared__ uint64_t hb_key[8];
+  __shared__ __align__(16) int8_t dpl[MX ? 4 * 64 * kMxSteps + 64 : 16];  // MX: digit planes, then 64 zero bytes
+  __shared__ __align__(16) int8_t dmw[MX ? 3 * kMxSteps * 1024 : 16];     // MX: phase D's rows, [block][step][lane][16]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps per-wave indices scalar
   const int G = gridDim.x, w = blockIdx.x;
@@ -1262,7 +1279,11 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   // while it polls.  (Loads complete in issue order, so a poll also waits for
   // every load issued before it; issuing the next phase's weights any earlier
   // holds up this phase's wait or its compute.)
-  RowDot<64, 1, SF16, Q4> dA0, dA1, dC0, dC1, dg[3], du[3];
+  RowDot<64, 1, SF16, Q4> dA0, dA1, dC0, dC1, dg[MX ? 1 : 3], du[MX ? 1 : 3];
+  // MX: wave b < ceil(perD / 8) loads and multiplies pairs 8b .. 8b + 7 of phase D: lane l the
+  // gate (l % 16 < 8) or up row of pair 8b + l % 8, codes 16 (l / 16) .. +16 of each 64-code step
+  float mxs = 0.f;
+  const int nsteps = (D + 63) / 64, nblk = (perD + 7) / 8;
   RowDot<64, kDownCPL, SF16, Q4> dd;
   NormStage ns1, ns2;
   float bA0, bA1;
@@ -1278,12 +1299,27 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     dC1.load(a.o, (int64_t)l * D + (lbC ? rbC : 0), lane, lbC);
   };
   auto load_D = [&](int l) {
+    if constexpr (MX) {
+      if (wave < nblk) {  // uniform per wave
+        const int r16 = lane & 15, pr = wave * 8 + (r16 & 7);
+        const int64_t row = (int64_t)l * 2 * I + (r16 < 8 ? 0 : I) + jbeg + (pr < perD ? pr : 0);
+        const int8_t* base = a.gu.q + row * a.gu.kp;
+        const int nch = (int)(a.gu.kp / 16);
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
-      const bool live = wave + 8 * t < perD;
-      const int64_t jr = live ? jbeg + wave + 8 * t : jbeg;
-      dg[t].load(a.gu, (int64_t)l * 2 * I + jr, lane, live);
-      du[t].load(a.gu, (int64_t)l * 2 * I + I + jr, lane, live);
+        for (int s = 0; s < kMxSteps; ++s)
+          if (s < nsteps)
+            dma16(base + 16 * min(4 * s + (lane >> 4), nch - 1), dmw + (wave * kMxSteps + s) * 1024);
+        mxs = SF16 ? __half2float(reinterpret_cast<const __half*>(a.gu.scales)[row])
+                   : reinterpret_cast<const float*>(a.gu.scales)[row];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const bool live = wave + 8 * t < perD;
+        const int64_t jr = live ? jbeg + wave + 8 * t : jbeg;
+        dg[t].load(a.gu, (int64_t)l * 2 * I + jr, lane, live);
+        du[t].load(a.gu, (int64_t)l * 2 * I + I + jr, lane, live);
+      }
     }
     ns2.prefetch(a.ln2 + (int64_t)l * D, D);
   };
@@ -1291,6 +1327,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
 
   // the dot products read xs up to 64 chunks per lane row: the tail past what a phase stages stays zero
   for (int i = tid; i < kXs; i += kPT) xs[i] = 0.f;
+  if constexpr (MX)
+    if (tid < 16) reinterpret_cast<uint32_t*>(dpl + 4 * 64 * kMxSteps)[tid] = 0u;
   load_A(0);
   __syncthreads();
   uint64_t waitA = 0, waitD = 0;  // the idle workgroups' previous waits (wall-clock ticks)
@@ -1422,22 +1460,45 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       if (!ll_get<16>(a.pb + (par * kRP + w % kRP) * a.sp, nact * H * kPPart, E + 1u, part, a.err)) return;
       // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den;
       // the chunk weights e^{m_c - M} / den, one thread per (chunk, head) = part index,
-      // into xmid (free until D)
+      // into xmid (free until D).  Every loop runs over all kPChunks slots with its LDS
+      // reads clamped to the last live chunk, so the reads issue together instead of one
+      // LDS round trip per chunk; the sums still add the live chunks in order.
       if (tid < nact * H) {
         const int hh = tid % H;
+        float m[kPChunks], lc[kPChunks];
+#pragma unroll
+        for (int cc = 0; cc < kPChunks; ++cc) {
+          const int c2 = min(cc, nact - 1);
+          m[cc] = part[(c2 * H + hh) * kPPart];
+          lc[cc] = part[(c2 * H + hh) * kPPart + 1];
+        }
         float M = -INFINITY;
-        for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, part[(cc * H + hh) * kPPart]);
+#pragma unroll
+        for (int cc = 0; cc < kPChunks; ++cc) M = fmaxf(M, m[cc]);  // clamped slots repeat a live m
         float den = 0.f;
-        for (int cc = 0; cc < nact; ++cc)
-          den = fmaf(part[(cc * H + hh) * kPPart + 1], __builtin_amdgcn_exp2f(part[(cc * H + hh) * kPPart] - M), den);
+#pragma unroll
+        for (int cc = 0; cc < kPChunks; ++cc)
+          if (cc < nact) den = fmaf(lc[cc], __builtin_amdgcn_exp2f(m[cc] - M), den);
         xmid[tid] = __builtin_amdgcn_exp2f(part[tid * kPPart] - M) / den;
       }
       __syncthreads();
-      for (int i = tid; i < kStage; i += kPT) {
+      static_assert(kStage % kPT == 0, "the staged width is a multiple of the workgroup");
+#pragma unroll 1
+      for (int it = 0; it < kStage / kPT; ++it) {
+        const int i = tid + it * kPT;
         float att = 0.f;  // the o_proj dot reads the staged vector up to kStage: zero past H dh
-        if (i < H * dh) {
-          const int hh = i / dh, d = i % dh;
-          for (int cc = 0; cc < nact; ++cc) att = fmaf(part[(cc * H + hh) * kPPart + 2 + d], xmid[cc * H + hh], att);
+        if (i < H * 64) {  // head dim 64
+          const int hh = i >> 6, d = i & 63;
+          float o[kPChunks], f[kPChunks];
+#pragma unroll
+          for (int cc = 0; cc < kPChunks; ++cc) {
+            const int c2 = min(cc, nact - 1);
+            o[cc] = part[(c2 * H + hh) * kPPart + 2 + d];
+            f[cc] = xmid[c2 * H + hh];
+          }
+#pragma unroll
+          for (int cc = 0; cc < kPChunks; ++cc)
+            if (cc < nact) att = fmaf(o[cc], f[cc], att);
         }
         xs[i] = att;
       }
@@ -1457,6 +1518,87 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       const uint64_t t0 = isC ? 0 : idle_wait(wall_clock64(), waitD);
       if (!ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)) return;
       if (!isC) waitD = wall_clock64() - t0;
+      if constexpr (MX) {
+        // RMSNorm statistic and max |x_mid * w| in one reduction, then the digit planes
+        const int t = tid;
+        const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(xmid)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float ss = 0.f;
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+        const float vw[4] = {v.x * ns2.w.x, v.y * ns2.w.y, v.z * ns2.w.z, v.w * ns2.w.w};
+        float mx = fmaxf(fmaxf(fabsf(vw[0]), fabsf(vw[1])), fmaxf(fabsf(vw[2]), fabsf(vw[3])));
+        ss = wave_sum_swap(ss);
+        mx = wave_max_dpp(mx);
+        if (lane == 0) {
+          red[wave] = ss;
+          red[8 + wave] = mx;
+        }
+        __syncthreads();
+        float tot = 0.f, m = 0.f;
+#pragma unroll
+        for (int i = 0; i < kPT / 64; ++i) {
+          tot += red[i];
+          m = fmaxf(m, red[8 + i]);
+        }
+        const float inv = 1.0f / sqrtf(tot / (float)D + a.eps);
+        int Ex = 0;
+        if (m > 0.f) (void)frexpf(m, &Ex);  // m = f 2^Ex, f in [0.5, 1): every |v| < 2^Ex
+        Ex = max(Ex, -96);                  // 2^(27 - Ex) stays finite; tiny vectors lose low bits only
+        if (t < 16 * kMxSteps) {            // planes to 64 kMxSteps bytes, zero past D
+          const float up = ldexpf(1.0f, 27 - Ex);
+          int X[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) X[i] = __float2int_rn(vw[i] * up);  // |X| < 2^27
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            uint32_t pk = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              pk |= (p < 3 ? ((uint32_t)X[i] >> (7 * p)) & 127u : (uint32_t)(X[i] >> 21) & 0xFFu) << (8 * i);
+            reinterpret_cast<uint32_t*>(dpl + p * 64 * kMxSteps)[t] = pk;
+          }
+        }
+        __syncthreads();
+        if (wave < nblk) {  // uniform per wave
+          const int i = lane & 15;
+          // lanes of MFMA rows 0..3 read plane i, rows 4..15 the zero bytes
+          const int8_t* ab = i < 4 ? dpl + i * 64 * kMxSteps + (lane >> 4) * 16 : dpl + 4 * 64 * kMxSteps;
+          const int ast = i < 4 ? 64 : 0;
+          const int8_t* wb = dmw + wave * kMxSteps * 1024 + lane * 16;
+          __builtin_amdgcn_s_waitcnt(CV3_VMCNT(0));  // this wave's row DMAs (they precede its polls anyway)
+          // two register sets of two steps each: one set's fragments are read from LDS while
+          // the other's multiply (reads past the last step repeat it and go unused)
+          auto fa = [&](int s) { return *reinterpret_cast<const i32x4*>(ab + min(s, nsteps - 1) * ast); };
+          auto fb = [&](int s) { return *reinterpret_cast<const i32x4*>(wb + min(s, nsteps - 1) * 1024); };
+          i32x4 c = {0, 0, 0, 0};
+          i32x4 pa0 = fa(0), pb0 = fb(0), pa1 = fa(1), pb1 = fb(1);
+          for (int s = 0; s < nsteps; s += 4) {
+            const i32x4 qa0 = fa(s + 2), qb0 = fb(s + 2), qa1 = fa(s + 3), qb1 = fb(s + 3);
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa0, pb0, c, 0, 0, 0);
+            if (s + 1 < nsteps) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa1, pb1, c, 0, 0, 0);
+            if (s + 2 >= nsteps) break;
+            pa0 = fa(s + 4);
+            pb0 = fb(s + 4);
+            pa1 = fa(s + 5);
+            pb1 = fb(s + 5);
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0, qb0, c, 0, 0, 0);
+            if (s + 3 < nsteps) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1, qb1, c, 0, 0, 0);
+          }
+          // lanes 0..15: the four plane sums of weight row i
+          const double T = (double)c[0] + 128.0 * (double)c[1] + 16384.0 * (double)c[2] + 2097152.0 * (double)c[3];
+          const float val = (float)(T * (double)ldexpf(1.0f, Ex - 27) * (double)mxs) * inv;
+          const float upv = __shfl_xor(val, 8, 64);  // lanes 0..7: the up row of the same pair
+          const int pr = wave * 8 + i;
+          if (lane < 8 && pr < perD) {
+            const float hv = (val / (1.0f + expf(-val))) * upv;
+#pragma unroll
+            for (int rr = 0; rr < kRH; ++rr) ll_put(a.hb + (par * kRH + rr) * a.sh + jbeg + pr, hv, E + 3u);
+          }
+        }
+        __syncthreads();
+      } else {
       const float inv = ns2.stage(xmid, D, a.eps, xs, red, kStage);
       XSlice<CPC> xv;
       xv.load(xs, lane);
@@ -1469,6 +1611,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         }
       }
       __syncthreads();  // xs is restaged below
+      }
     }
     // ---- E: down rows + residual -> x of the next layer ----
     if (isE) {
@@ -1843,7 +1986,10 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   CV3_HIP(hipGetDevice(&dev));
   CV3_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   const bool sf16 = m->qkv.scale_dtype == CV3_F16;
+  // phase D on the matrix cores: q8 [gate; up] rows with one scale per row (per-channel)
+  const bool mx = !q4 && m->gate_up.kp <= m->gate_up.block && D <= 64 * kMxSteps;
   const void* fn = q4     ? (const void*)k_dec_persist<true, true>
+                   : mx   ? (sf16 ? (const void*)k_dec_persist<true, false, true> : (const void*)k_dec_persist<false, false, true>)
                    : sf16 ? (const void*)k_dec_persist<true, false>
                           : (const void*)k_dec_persist<false, false>;
   int per_cu = 0;
@@ -1911,6 +2057,10 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   } else {
     if (q4)
       hipLaunchKernelGGL((k_dec_persist<true, true>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    else if (mx && sf16)
+      hipLaunchKernelGGL((k_dec_persist<true, false, true>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
+    else if (mx)
+      hipLaunchKernelGGL((k_dec_persist<false, false, true>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
     else if (sf16)
       hipLaunchKernelGGL((k_dec_persist<true, false>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
     else

@@ -14,6 +14,9 @@ constexpr int kPSpin = 1 << 18;          // polls (each with a short sleep) befo
 constexpr int kPPart = 66;               // words per attention partial: m, l, o[64]
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+// s_waitcnt immediate that waits for all but n vector-memory operations (gfx9 field layout)
+#define CV3_VMCNT(n) (((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
 struct QW {            // one stacked weight: layer l, row r at q + (l * rows + r) * row_bytes
   const int8_t* q;     // row_bytes = kp (q8) or kp / 2 (q4)

@@ -46,10 +46,6 @@ using namespace cv3;
 
 namespace {
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// s_waitcnt with only vmcnt limited (expcnt, lgkmcnt at their maxima)
-#define CV3_VMCNT(n) (((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
 constexpr int kST = 576;                 // threads: 8 compute waves + the loader wave
 constexpr int kSC = 8;                   // compute waves
