@@ -406,7 +406,28 @@ def vendor_gemm_calibration():
     """The vendor library's GEMMs (torch.matmul: hipBLASLt / rocBLAS) on the DiT QKV shape: plain
     fp32 [1000, 1024] x [1024, 3072], and bfloat16 with K = 6 x 1024, the bfloat16 work the split
     GEMM does for the same product (six plane products).  Contiguous 2-D operands only; the
-    calibration for the split GEMM's times, not a path of this library."""
+    calibration for the split GEMM's times, not a path of this library.
+
+    Measured in a child process: torch carries its own HIP and HSA runtime libraries, and
+    bringing them up in a process whose GPU this library's runtime already holds crashed under
+    rocprofv3's kernel trace (a null dereference in torch's first device call)."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-gemm"], capture_output=True,
+                           text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        log("kernels: vendor GEMM child timed out")
+        return None
+    sys.stderr.write(r.stderr)
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if r.returncode != 0 or not lines:
+        log(f"kernels: vendor GEMM child exited with status {r.returncode}")
+        return None
+    return json.loads(lines[-1])
+
+
+def vendor_gemm_measure():
+    """The child side of vendor_gemm_calibration: torch only, this library never loaded."""
     try:
         import torch
     except ImportError:
@@ -707,7 +728,12 @@ def main():
                     help="--kernels without the closing 22-block 10 s solve")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time the vendor library's GEMMs and print them as JSON (the --kernels child)")
     args = ap.parse_args()
+    if args.vendor_gemm:
+        print(json.dumps(vendor_gemm_measure()), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is "
               "described in DESIGN.md and is not measured", file=sys.stderr)

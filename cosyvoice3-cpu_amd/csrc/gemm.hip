@@ -617,14 +617,26 @@ struct XStage {
 __device__ __forceinline__ int xslot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
 
 // K % 64 == 0; A rows 16-byte aligned (lda % 4 == 0); plane rows 16-byte aligned.
+// Tile of workgroup L: the remap hands each XCD (workgroup L runs on XCD L % 8) a contiguous
+// range of tiles, walked in groups of gm row tiles across all column tiles.  gm = tiles_m walks
+// column by column (B streamed once, A re-read from L2: the DiT's plane GEMMs, whose weights are
+// the larger operand); a small gm keeps a few row tiles of A in L2 while the columns stream past
+// (the 30 s q8 GEMMs, whose float32 activations outweigh the int8 codes).
+__device__ __forceinline__ void tile_xcd(int L, int T, int tiles_m, int tiles_n, int gm, int64_t& m0, int64_t& n0) {
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int per = gm * tiles_n, g = t / per, r = t - g * per;
+  const int first = g * gm, gh = min(gm, tiles_m - first);
+  m0 = (int64_t)(first + r % gh) * BM;
+  n0 = (int64_t)(r / gh) * BN;
+}
+
 __global__ __launch_bounds__(256) void k_gemm_x3(GemmParams p, const uint16_t* pb, int64_t ldp, int64_t pstride,
-                                                 int tiles_m) {
+                                                 int tiles_m, int tiles_n, int gm) {
   __shared__ uint4 sA[2][3][BM * 4];
   __shared__ uint4 sB[2][3][BN * 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = gridDim.x, L = blockIdx.x;
-  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
-  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  int64_t m0, n0;
+  tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
   const int lr = tid >> 2, lc = tid & 3;
   const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
   const uint16_t* pbr = pb + min(n0 + lr, p.n - 1) * ldp + lc * 8;
@@ -724,13 +736,12 @@ __device__ __forceinline__ uint4 codes_bf16(uint2 w) {
 }
 
 // K % 64 == 0, block % 64 == 0; A rows 16-byte aligned, code rows 8-byte aligned.
-__global__ __launch_bounds__(256) void k_gemm_x3q(GemmParams p, int tiles_m) {
+__global__ __launch_bounds__(256) void k_gemm_x3q(GemmParams p, int tiles_m, int tiles_n, int gm) {
   __shared__ uint4 sA[2][3][BM * 4];
   __shared__ uint4 sB[2][BN * 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = gridDim.x, L = blockIdx.x;
-  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
-  const int64_t m0 = (int64_t)(t % tiles_m) * BM, n0 = (int64_t)(t / tiles_m) * BN;
+  int64_t m0, n0;
+  tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
   const int lr = tid >> 2, lc = tid & 3;
   const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
   const int8_t* pbr = reinterpret_cast<const int8_t*>(p.b) + min(n0 + lr, p.n - 1) * p.ldb + lc * 8;
@@ -904,6 +915,14 @@ int gemm(int bkind, const float* a, int64_t m, int64_t k, int64_t lda, const voi
   return CV3_OK;
 }
 
+// Group height for tile_xcd: column by column while A is the smaller operand; otherwise one
+// XCD's share of the tiles covers a few row tiles across all columns, so A streams from HBM once.
+static int tile_group(int64_t tiles_m, int64_t tiles_n, double a_bytes, double b_bytes) {
+  if (a_bytes <= b_bytes) return (int)tiles_m;
+  const int64_t per_xcd = ceil_div(tiles_m * tiles_n, 8);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(tiles_m, ceil_div(per_xcd, tiles_n)));
+}
+
 // C = epi(A . B^T) on the bfloat16 matrix cores, B as three bfloat16 planes
 // planes[p][n][ldp] (pstride elements apart).  K % 64 == 0.
 int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* planes, int64_t ldp, int64_t pstride,
@@ -929,8 +948,9 @@ int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* p
               CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
   const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, 6.0 * (double)n * k);
   hipLaunchKernelGGL(k_gemm_x3, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, planes, ldp, pstride,
-                     (int)tiles_m);
+                     (int)tiles_m, (int)tiles_n, gm);
   CV3_LAUNCHED();
   return CV3_OK;
 }
@@ -966,7 +986,9 @@ int gemm_x3q(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* q,
               CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
   const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
-  hipLaunchKernelGGL(k_gemm_x3q, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, (int)tiles_m);
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, (double)n * k);
+  hipLaunchKernelGGL(k_gemm_x3q, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, (int)tiles_m,
+                     (int)tiles_n, gm);
   CV3_LAUNCHED();
   return CV3_OK;
 }
