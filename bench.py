@@ -257,13 +257,16 @@ def bench_decode(args, tensors, meta, label: str = "decode", decodes: int = None
     log(f"{label}: sampled (top_p 0.8, top_k 25, repetition window 10) {sms:.2f} ms for {len(sampled)} tokens "
         f"= {sampled_tok_s:.1f} tok/s")
     sf16 = lm.gate_up.sf16
+    gs = lm.gate_up.struct()
+    mx = lm.gate_up.kind != "q4" and gs.kp <= gs.block   # phase D on the int8 matrix cores
     return {
         "sampled_tok_s": sampled_tok_s, "persistent": persistent,
         "tok_s": tok_s, "ms": ms, "tokens": tokens, "bytes_per_token": per_token, "bytes_parts": b,
         "five_kernel_tok_s": DECODE_TOKENS / (ms_k / 1e3), "decodes": decodes,
         # the one-launch step is a single kernel per token: its bytes are the token's
         "step_kernel": {"name": f"k_dec_persist<{'true' if sf16 else 'false'}, "
-                                f"{'true' if lm.gate_up.kind == 'q4' else 'false'}> (the whole decode step)",
+                                f"{'true' if lm.gate_up.kind == 'q4' else 'false'}, {'true' if mx else 'false'}> "
+                                "(the whole decode step)",
                         "bytes_per_launch": per_token, "us_per_launch": ms / DECODE_TOKENS * 1e3,
                         "achieved_Bps": per_token / (ms / DECODE_TOKENS / 1e3)},
         "kernel": {"name": "k_dec_gemv<8,4,2,q4> (RMSNorm + [gate;up] q4 GEMV + SwiGLU)" if lm.gate_up.kind == "q4"
