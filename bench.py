@@ -48,10 +48,10 @@ METRIC = "DiT flow RTF (10 s, CFG) + int8 LM decode tok/s, each as % of roofline
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
 # device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
-# the one-launch decode step (24 layers, per-channel int8, KV 512: 410.0 MB read + 12.4 MB written).
-# Counters cannot be read inside this process, so these are the measured figures for exactly
-# these kernels and shapes.
-TRAFFIC_DECODE_STEP = 422.4e6
+# the one-launch decode step (24 layers, per-channel int8 with phase D on the int8 matrix cores,
+# KV 512: 408.8 MB read + 7.6 MB written).  Counters cannot be read inside this process, so these
+# are the measured figures for exactly these kernels and shapes.
+TRAFFIC_DECODE_STEP = 416.4e6
 # the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes (k_gemm_x3,
 # [1000, 1024] x [3072, 1024]^T): 53.2 MB read + 12.3 MB written
 TRAFFIC_QKV_GEMM_X3 = 65.5e6
