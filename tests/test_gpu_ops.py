@@ -414,6 +414,12 @@ CL_CASES = [
     (64, 18, 7, 1, 1, 200, (6, 0), "none", 1, True),         # conv_post, written (channel, time)
     (96, 100, 5, 2, 2, 33, (3, 4), "residual", 5, False),    # ragged tiles, both pads, odd split
     (32, 40, 1, 1, 1, 17, (0, 0), "none", 1, False),         # one stage
+    # 32, 64 and 128 channels in at the resblocks' spans (split K, a right pad, spans of 64 and 80)
+    (128, 128, 11, 5, 1, 257, (50, 0), "snake", 2, False),
+    (128, 64, 3, 3, 1, 130, (6, 0), "residual", 1, False),
+    (32, 64, 6, 3, 1, 95, (15, 3), "leaky", 1, False),
+    (64, 64, 3, 32, 1, 200, (64, 0), "none", 1, False),
+    (64, 64, 3, 40, 1, 200, (80, 0), "none", 1, False),
 ]
 
 
