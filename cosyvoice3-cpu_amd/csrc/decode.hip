@@ -1228,7 +1228,9 @@ __device__ __forceinline__ uint64_t idle_wait(uint64_t t0, uint64_t prev) {
 // global -> LDS by DMA (global_load_lds_dwordx4) in the MFMA operand order, so they hold
 // no registers while the workgroup waits for x_mid.
 constexpr int kMxSteps = 16;  // 64-code steps of a row: hidden <= 1024
-// One 16-byte global -> LDS DMA per lane (lane l lands at lds + 16 l).
+// One 16-byte global -> LDS DMA per lane (lane l lands at lds + 16 l).  A function of its own:
+// the builtin called directly inside the kernel template's lambda made clang drop that
+// instantiation's host stub without a diagnostic (an undefined symbol at load time).
 __device__ __forceinline__ void dma16(const void* g, void* lds) { __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0); }
 template <bool SF16, bool Q4, bool MX = false>
 __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
