@@ -102,7 +102,9 @@ def test_planes_are_the_rounding_chain(lib):
 
 
 SHAPES = [(1, 64, 64), (7, 128, 64), (65, 192, 130), (300, 1024, 1024), (1000, 1024, 3072),
-          (1000, 2048, 1024), (3000, 1024, 1024)]
+          (1000, 2048, 1024), (3000, 1024, 1024),
+          # wide outputs: a ragged last column tile, one row, n a multiple of 128
+          (65, 128, 2100), (1, 64, 4096), (130, 256, 2048)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
