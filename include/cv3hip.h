@@ -382,7 +382,9 @@ int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_stat
  * of cv3_qwen2_decode_step; select 0: logits only (then cv3_qwen2_select).  The workgroups must all be resident
  * at once: cooperative 1 launches with hipLaunchCooperativeKernel, which guarantees that or fails; cooperative 0
  * launches ordinarily (about 20 us less per token), for a device with nothing else running: a workgroup that
- * cannot start shows up as *err, not as a hang.  One such launch at a time per device. */
+ * cannot start shows up as *err, not as a hang.  One such launch at a time per device.  With one scale
+ * per [gate; up] row (the per-channel profile) the MLP's [gate; up] dot products run as exact int8 MFMAs on
+ * base-128 digit planes of the normed activation; results stay within the same 1e-5 of the oracle. */
 typedef struct {
   uint64_t* words;
   int64_t words_len;
