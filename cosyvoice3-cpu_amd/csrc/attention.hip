@@ -288,6 +288,15 @@ __global__ __launch_bounds__(256 * NKG) void k_flash64(AttnParams p, int nq) {
 // are the lane's own values sc[t % 4][2 j + t / 4] as the B operand (k index 8 g + t), and
 // V^T row d, chunk 2 g + j as the A operand: no data moves between the two products.
 __device__ __forceinline__ int xkv(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+// V^T rows (64 dims of 8 16-byte key chunks) of k_flash64x: chunk c of row d at slot
+// (d / 2) 16 + ((8 (d % 2) + c) ^ f(d)), f(d) = 8 b5 + ((d / 2) % 8 ^ b4) with b4, b5 bits 4 and 5 of d.
+// A row pair fills 16 slots (256 bytes, one bank window).  The P.V reads (16 consecutive rows, one
+// chunk) and the staging writes (rows 4 q + e for q = 0..15, one chunk, 8 bytes each) both land on
+// 16 distinct slots of a window.
+__device__ __forceinline__ int vslot(int d, int c) {
+  const int f = (((d >> 5) & 1) << 3) | (((d >> 1) & 7) ^ ((d >> 4) & 1));
+  return (d >> 1) * 16 + (((d & 1) * 8 + c) ^ f);
+}
 
 __device__ __forceinline__ void mfma6(const bf16x8_t& ah, const bf16x8_t& am, const bf16x8_t& al,
                                       const bf16x8_t& bh, const bf16x8_t& bm, const bf16x8_t& bl, f32x4& big,
@@ -350,12 +359,12 @@ __global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
   // Staging (next stage's rows in registers while this one is computed; rows past m clamp
   // to m - 1 and are masked to -inf below):
   // K: thread -> tile tid/256, key (tid%256)/4, dims 16 (tid%4) .. + 15 (two chunks);
-  // V: thread -> tile tid/256, keys 2 kp, 2 kp + 1 (kp = tid % 32), dims 8 dg .. + 7
-  //    (dg = (tid%256)/32): each dim's two keys are one 32-bit word of a V^T row.
+  // V: thread -> tile tid/256, keys 4 kq .. + 3 (kq = (tid%256)/16), dims 4 dq .. + 3 (dq = tid%16):
+  //    each dim's four keys are one 8-byte half-chunk of a V^T row.
   const int ltile = tid >> 8, lkey = (tid & 255) >> 2, ld16 = (tid & 3) * 16;
   const int lrow = (lkey & 3) * 16 + (lkey >> 2);
-  const int kp = tid & 31, dg = (tid & 255) >> 5;
-  float4 kr[4], va[2], vb[2];
+  const int dq = tid & 15, kq = (tid & 255) >> 4;
+  float4 kr[4], vv[4];
 #define CV3_KVX_LOAD(KOFF)                                                                 \
   {                                                                                        \
     const int64_t jk = min((KOFF) + ltile * KT + lkey, p.m - 1);                           \
@@ -364,12 +373,10 @@ __global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
     kr[1] = *reinterpret_cast<const float4*>(kr_ + 4);                                     \
     kr[2] = *reinterpret_cast<const float4*>(kr_ + 8);                                     \
     kr[3] = *reinterpret_cast<const float4*>(kr_ + 12);                                    \
-    const int64_t j0 = min((KOFF) + ltile * KT + 2 * kp, p.m - 1);                         \
-    const int64_t j1 = min((KOFF) + ltile * KT + 2 * kp + 1, p.m - 1);                     \
-    va[0] = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + 8 * dg);                \
-    va[1] = *reinterpret_cast<const float4*>(vbase + j0 * p.v_sm + 8 * dg + 4);            \
-    vb[0] = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + 8 * dg);                \
-    vb[1] = *reinterpret_cast<const float4*>(vbase + j1 * p.v_sm + 8 * dg + 4);            \
+    _Pragma("unroll") for (int r_ = 0; r_ < 4; ++r_) {                                     \
+      const int64_t jv = min((KOFF) + ltile * KT + 4 * kq + r_, p.m - 1);                  \
+      vv[r_] = *reinterpret_cast<const float4*>(vbase + jv * p.v_sm + 4 * dq);             \
+    }                                                                                      \
   }
   CV3_KVX_LOAD((int64_t)0)
   for (int64_t st = 0; st < nstages; ++st) {
@@ -385,20 +392,17 @@ __global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
         Ks[ltile][1][slot] = m4;
         Ks[ltile][2][slot] = l4;
       }
-      const float a8[8] = {va[0].x, va[0].y, va[0].z, va[0].w, va[1].x, va[1].y, va[1].z, va[1].w};
-      const float b8[8] = {vb[0].x, vb[0].y, vb[0].z, vb[0].w, vb[1].x, vb[1].y, vb[1].z, vb[1].w};
+      const float vr[4][4] = {{vv[0].x, vv[0].y, vv[0].z, vv[0].w}, {vv[1].x, vv[1].y, vv[1].z, vv[1].w},
+                              {vv[2].x, vv[2].y, vv[2].z, vv[2].w}, {vv[3].x, vv[3].y, vv[3].z, vv[3].w}};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint32_t hh, mm, ll;
-        split_x3(a8[e], b8[e], hh, mm, ll);
-        const int d = 8 * dg + e;
-        // keys 2 kp, 2 kp + 1: chunk kp / 4 of row d, 32-bit word kp % 4
-        uint32_t* w0 = reinterpret_cast<uint32_t*>(&Vs[ltile][0][xkv(d, kp >> 2)]) + (kp & 3);
-        uint32_t* w1 = reinterpret_cast<uint32_t*>(&Vs[ltile][1][xkv(d, kp >> 2)]) + (kp & 3);
-        uint32_t* w2 = reinterpret_cast<uint32_t*>(&Vs[ltile][2][xkv(d, kp >> 2)]) + (kp & 3);
-        *w0 = hh;
-        *w1 = mm;
-        *w2 = ll;
+      for (int e = 0; e < 4; ++e) {
+        uint2 hh, mm, ll;
+        split_x3(vr[0][e], vr[1][e], hh.x, mm.x, ll.x);  // keys 4 kq, 4 kq + 1
+        split_x3(vr[2][e], vr[3][e], hh.y, mm.y, ll.y);  // keys 4 kq + 2, 4 kq + 3
+        const int sl = vslot(4 * dq + e, kq >> 1);
+        reinterpret_cast<uint2*>(&Vs[ltile][0][sl])[kq & 1] = hh;
+        reinterpret_cast<uint2*>(&Vs[ltile][1][sl])[kq & 1] = mm;
+        reinterpret_cast<uint2*>(&Vs[ltile][2][sl])[kq & 1] = ll;
       }
     }
     __syncthreads();
@@ -465,7 +469,7 @@ __global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
       const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, l4);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int slot = xkv(db * 16 + c16, 2 * g + j);
+        const int slot = vslot(db * 16 + c16, 2 * g + j);
         const bf16x8_t vh = __builtin_bit_cast(bf16x8_t, Vs[kg][0][slot]);
         const bf16x8_t vm = __builtin_bit_cast(bf16x8_t, Vs[kg][1][slot]);
         const bf16x8_t vl = __builtin_bit_cast(bf16x8_t, Vs[kg][2][slot]);
