@@ -169,7 +169,8 @@ def choose_kind(name: str, arr: np.ndarray, profile: str) -> str:
 
     ``f32``: everything float32.  ``balanced``: q8 block 64 / float16 scales for
     large matrices, float16 for time_embed / proj_out.  ``per_channel``: like
-    balanced, with one float32 scale per output row.  ``tiny``: like balanced, with
+    balanced, with one float32 scale per output row (``per_channel_f16``: one float16
+    scale per row, the reference's scale dtype at block = K).  ``tiny``: like balanced, with
     q4 for the matrices of ``llm.model.layers.*`` (convert.py:26-27,262-263).
     """
     if profile == "f32" or arr.ndim == 1 or _KEEP_F32.search(name) or arr.size < (1 << 16):
@@ -199,8 +200,8 @@ def quantize_store(tensors: Dict[str, np.ndarray], profile: str, quantize_q8, qu
                          "block": 32, "orig_shape": None}
         elif kind == "q8":
             k = arr.shape[1]
-            if profile == "per_channel":
-                q, s, kp = quantize_q8(arr, k, np.float32)
+            if profile in ("per_channel", "per_channel_f16"):
+                q, s, kp = quantize_q8(arr, k, np.float32 if profile == "per_channel" else np.float16)
                 block = k
             else:
                 q, s, kp = quantize_q8(arr, 64, np.float16)

@@ -1,7 +1,8 @@
 """The one-launch decode step (cv3_qwen2_decode_step_persistent) against the oracle.
 
 Same seeded synthetic Qwen2-0.5B weights as test_gpu_decode.py, q8 under the
-per-channel (float32 scales) and balanced (block 64, float16 scales) profiles, and
+per-channel (float32 scales, and float16 scales for the matrix-core phase D's
+float16 variant) and balanced (block 64, float16 scales) profiles, and
 the tiny profile's q4 body (head and embedding q8).
 Bars: per-step logits within 1e-5 (max abs error over max |logit|) of the
 oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
@@ -56,7 +57,8 @@ def _oracle_lm(cpu, k, v, n, steps):
     ("balanced", 122, 10, False, "stream"), ("per_channel", 300, 6, True, "stream"),
     ("per_channel", 1000, 4, False, "stream"), ("balanced", 897, 4, False, "stream"),
     ("per_channel", 512, 6, False, "stacked"), ("balanced", 122, 6, False, "stacked"),
-    ("tiny", 300, 8, False, "stacked"), ("tiny:packed", 300, 8, False, "stacked")])
+    ("tiny", 300, 8, False, "stacked"), ("tiny:packed", 300, 8, False, "stacked"),
+    ("per_channel_f16", 300, 6, False, "stacked")])
 def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative, kernel):
     from cv3amd.qwen2 import DeviceQwen2
     cpu, dev, k, v = _setup(2, profile, n)
@@ -88,7 +90,7 @@ def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative, 
         assert rel_err(vc[i][:, :n + steps], cache.v[i][:, :n + steps]) < 1e-5
 
 
-@pytest.mark.parametrize("profile", ["balanced", "tiny", "tiny:packed"])
+@pytest.mark.parametrize("profile", ["balanced", "tiny", "tiny:packed", "per_channel_f16"])
 def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
     """24 layers: the one-launch step and the five-kernel step give the same tokens."""
     from cv3amd.qwen2 import DeviceQwen2
