@@ -177,13 +177,14 @@ def test_persistent_sampled_generation(gpu, strict):
     assert cfg.rng.bit_generator.state == ref.rng.bit_generator.state
 
 
-def test_persistent_sampled_long_run_matches_five_kernel_step(gpu):
+@pytest.mark.parametrize("profile", ["balanced", "per_channel"])
+def test_persistent_sampled_long_run_matches_five_kernel_step(gpu, profile):
     """40 draws with SamplingConfig's defaults over 24 layers: the same tokens and
-    Generator state as the five-kernel sampled step."""
+    Generator state as the five-kernel sampled step (per-channel: phase D on the matrix cores)."""
     from cv3amd.qwen2 import DeviceQwen2
     from oracle.llm import Sampling
     n, max_len = 200, 40
-    _, dev, k, v = _setup(24, "balanced", n)
+    _, dev, k, v = _setup(24, profile, n)
     out = []
     for persistent in (False, True):
         d = DeviceQwen2(dev, cap=1024)
