@@ -405,60 +405,6 @@ def bench_flow_q8(args, tensors, meta, profile: str):
     return {"ms": ms, "flops": flops, "by_unit": d.flops_by_unit(), "T": T}
 
 
-def vendor_gemm_calibration():
-    """The vendor library's GEMMs (torch.matmul: hipBLASLt / rocBLAS) on the DiT QKV shape: plain
-    fp32 [1000, 1024] x [1024, 3072], and bfloat16 with K = 6 x 1024, the bfloat16 work the split
-    GEMM does for the same product (six plane products).  Contiguous 2-D operands only; the
-    calibration for the split GEMM's times, not a path of this library.
-
-    Measured in a child process: torch carries its own HIP and HSA runtime libraries, and
-    bringing them up in a process whose GPU this library's runtime already holds crashed under
-    rocprofv3's kernel trace (a null dereference in torch's first device call)."""
-    import subprocess
-    try:
-        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-gemm"], capture_output=True,
-                           text=True, timeout=300)
-    except subprocess.TimeoutExpired:
-        log("kernels: vendor GEMM child timed out")
-        return None
-    sys.stderr.write(r.stderr)
-    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
-    if r.returncode != 0 or not lines:
-        log(f"kernels: vendor GEMM child exited with status {r.returncode}")
-        return None
-    return json.loads(lines[-1])
-
-
-def vendor_gemm_measure():
-    """The child side of vendor_gemm_calibration: torch only, this library never loaded."""
-    try:
-        import torch
-    except ImportError:
-        return None
-    if not torch.cuda.is_available():
-        return None
-    dev = torch.device("cuda:0")
-    res = {}
-    for name, (m, k, n, dt) in {"fp32 [1000,1024]x[1024,3072]": (1000, 1024, 3072, torch.float32),
-                                "bf16 [1000,6144]x[6144,3072]": (1000, 6144, 3072, torch.bfloat16)}.items():
-        a = torch.randn(m, k, device=dev, dtype=dt)
-        b = torch.randn(k, n, device=dev, dtype=dt).contiguous()
-        for _ in range(5):
-            a @ b
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(20):
-            a @ b
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / 20 * 1e3
-        rate = 2.0 * m * k * n / (us * 1e-6) / 1e12
-        log(f"kernels: vendor {name}: {us:.1f} us, {rate:.0f} TFLOP/s")
-        res[name] = {"us": round(us, 2), "tflops": round(rate, 1)}
-    return res
-
-
 def bench_kernels(args):
     """The roofline kernels one by one, for per-kernel tables and rocprofv3 counter passes:
     16 tokens of the one-launch decode step (24 layers, per-channel int8, KV 512), each launch of
@@ -598,7 +544,6 @@ def bench_kernels(args):
     log(f"kernels: vocoder inference, 10 s whole: {ms:.2f} ms")
     out["vocoder_inference_ms"] = round(ms, 3)
     del h
-    out["vendor_gemm"] = vendor_gemm_calibration()
     if args.kernel_solve:
         # the whole 10 s solve (22 blocks, 10 steps, CFG) for the end-to-end figure
         del d
@@ -731,12 +676,7 @@ def main():
                     help="--kernels without the closing 22-block 10 s solve")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="issue every launch directly instead of replaying captured HIP graphs")
-    ap.add_argument("--vendor-gemm", action="store_true",
-                    help="only time the vendor library's GEMMs and print them as JSON (the --kernels child)")
     args = ap.parse_args()
-    if args.vendor_gemm:
-        print(json.dumps(vendor_gemm_measure()), flush=True)
-        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is "
               "described in DESIGN.md and is not measured", file=sys.stderr)

@@ -638,6 +638,7 @@ extern "C" int cv3_attention(const float* q, const float* k, const float* v, flo
                              int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
                              const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                              float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+  CV3_ALIVE();
   return attention(false, q, k, v, out, batch, h, hk, n, m, d, q_strides, k_strides, v_strides, o_strides, scale,
                    mask_kind, mask_a, mask_b, s);
 }
@@ -646,6 +647,7 @@ extern "C" int cv3_attention_x3(const float* q, const float* k, const float* v, 
                                 int hk, int64_t n, int64_t m, int d, const int64_t* q_strides,
                                 const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                                 float scale, int mask_kind, int64_t mask_a, int64_t mask_b, cv3_stream_t s) {
+  CV3_ALIVE();
   return attention(true, q, k, v, out, batch, h, hk, n, m, d, q_strides, k_strides, v_strides, o_strides, scale,
                    mask_kind, mask_a, mask_b, s);
 }

@@ -17,6 +17,9 @@ int fail(int code, const char* fmt, ...);
 // The stream a call runs on: `s` if non-null, else the calling thread's own
 // non-blocking stream (created on first use).
 hipStream_t stream_of(cv3_stream_t s);
+// True once cv3_shutdown has run: every block is freed and every stream destroyed, so
+// no entry point may enqueue work any more.
+bool shut_down();
 
 constexpr int kWave = 64;
 
@@ -84,3 +87,6 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
   do {                                                                             \
     if (!(cond)) return cv3::fail((code), __VA_ARGS__);                            \
   } while (0)
+
+// First statement of every entry point that enqueues device work.
+#define CV3_ALIVE() CV3_REQUIRE(!cv3::shut_down(), CV3_EINVAL, "the library has been shut down")

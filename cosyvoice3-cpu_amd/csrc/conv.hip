@@ -636,6 +636,7 @@ extern "C" {
 int cv3_conv1d_cl(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t ldx, const float* w_packed,
                   int64_t cout, int64_t k, int64_t groups, int64_t pad_l, const float* bias, float* y, int64_t ldy,
                   const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(groups >= 1 && cin % groups == 0 && cout % groups == 0, CV3_EASSERT,
               "channels %lld/%lld not divisible by groups %lld", (long long)cin, (long long)cout, (long long)groups);
   CV3_REQUIRE(cout / groups == 64, CV3_EUNSUPPORTED, "channels-last conv takes 64 output channels per group");
@@ -650,6 +651,7 @@ int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t 
                int64_t pad_r, int64_t up, float* y, int64_t y_cs, int64_t y_ts, int64_t* t_out_ptr, int act,
                float act_param, const float* snake_alpha, float snake_eps, const float* residual, int64_t r_cs,
                int64_t r_ts, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(groups >= 1 && cin % groups == 0 && cout % groups == 0, CV3_EASSERT,
               "channels %lld/%lld not divisible by groups %lld", (long long)cin, (long long)cout, (long long)groups);
   CV3_REQUIRE(stride >= 1 && dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0, CV3_EINVAL,
@@ -696,6 +698,7 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
                       float* y, int64_t y_cs, int64_t y_ts, int act, float act_param, const float* snake_alpha,
                       float snake_eps, const float* residual, int64_t r_cs, int64_t r_ts, int64_t ksplit,
                       float* workspace, int64_t workspace_floats, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(dilation >= 1 && up >= 1 && k >= 1 && pad_l >= 0 && pad_r >= 0 && cin > 0 && cout > 0, CV3_EINVAL,
               "bad conv geometry");
   CV3_REQUIRE(ksplit >= 1 && ksplit <= 16 && (k * cin / FBK) % (2 * ksplit) == 0, CV3_EINVAL,
@@ -826,6 +829,7 @@ int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx,
                          int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act, float act_param,
                          const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
                          int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s) {
+  CV3_ALIVE();
   return conv_cl_packed(x, t_in, cin, ldx, w_packed, nullptr, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts, y_cs,
                         act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
                         workspace_floats, s);
@@ -837,6 +841,7 @@ int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t l
                             const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts,
                             int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
                             cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(w_planes, CV3_EINVAL, "null weight planes");
   return conv_cl_packed(x, t_in, cin, ldx, nullptr, w_planes, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts,
                         y_cs, act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
@@ -846,6 +851,7 @@ int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t l
 int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,
                          int64_t dilation, int64_t pad_l, int64_t pad_r, float* y, int64_t* t_out_ptr,
                          cv3_stream_t s) {
+  CV3_ALIVE();
   const int64_t t_out = t_in + pad_l + pad_r - dilation * (k - 1);
   if (t_out_ptr) *t_out_ptr = t_out;
   if (t_out <= 0 || !y) return CV3_OK;

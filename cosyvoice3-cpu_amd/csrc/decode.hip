@@ -1858,11 +1858,13 @@ static int decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const
 }
 
 int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_ALIVE();
   return decode_step(m, s, nullptr, stream);
 }
 
 int cv3_qwen2_decode_step_sampled(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
                                   cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(smp, CV3_EINVAL, "null sampler");
   return decode_step(m, s, smp, stream);
 }
@@ -1919,6 +1921,7 @@ int decode_scratch_setup() { return scratch_of_current_device() ? CV3_OK : CV3_E
 extern "C" {
 
 int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
   const int64_t H = m->heads, I = m->inter;
   CV3_REQUIRE(H > 0 && H <= 16 && I > 0 && I <= kScratchInterMax, CV3_EINVAL,
@@ -1944,6 +1947,7 @@ static int64_t persist_words(const cv3_qwen2_model* m, int workgroups) {
 }
 
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && words && workgroups > 0, CV3_EINVAL, "null model or output, or no workgroups");
   *words = persist_words(m, workgroups);
   return CV3_OK;
@@ -1951,6 +1955,7 @@ int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* w
 
 int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,
                                      int select, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && s && p, CV3_EINVAL, "null model, state or exchange block");
   const int64_t H = m->heads, Hk = m->kv_heads, dh = m->head_dim, D = m->hidden, I = m->inter;
   CV3_REQUIRE(H > 0 && Hk > 0 && H % Hk == 0 && H / Hk <= 8 && dh == 64 && H * dh == D, CV3_EUNSUPPORTED,
@@ -2074,6 +2079,7 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
 
 int cv3_qwen2_select(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_sampler* smp,
                      cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
   int rc;
   if ((rc = check_qw(m->head, "llm_decoder", m->hidden))) return rc;
@@ -2100,6 +2106,7 @@ int cv3_qwen2_select(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const c
 }
 
 int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(pcg && n >= 0 && (n == 0 || out), CV3_EINVAL, "pcg64: null state or output");
   if (n == 0) return CV3_OK;
   hipLaunchKernelGGL(k_pcg64_random, dim3(1), dim3(1), 0, stream_of(stream), reinterpret_cast<uint64_t*>(pcg), n,
@@ -2111,6 +2118,7 @@ int cv3_pcg64_random(int64_t* pcg, int64_t n, double* out, cv3_stream_t stream) 
 
 int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float* rms_w, float eps, const float* bias,
                 float* y, int mode, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(w && x && y, CV3_EINVAL, "null argument");
   CV3_REQUIRE(mode >= 0 && mode <= 2, CV3_EINVAL, "gemv mode %d", mode);
   CV3_REQUIRE(layer >= 0, CV3_EINVAL, "negative layer");
@@ -2122,6 +2130,7 @@ int cv3_gemv_q8(const cv3_qweight* w, int64_t layer, const float* x, const float
 }
 
 int cv3_qwen2_embed_token(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && s, CV3_EINVAL, "null model or state");
   int rc;
   if ((rc = check_qw(m->embedding, "speech_embedding", m->hidden))) return rc;

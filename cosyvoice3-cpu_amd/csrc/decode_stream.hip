@@ -1090,6 +1090,7 @@ extern "C" {
 
 int cv3_qwen2_stream_size(const cv3_qwen2_model* m, int workgroups, int64_t* data_bytes, int64_t* plan_words,
                           int64_t* exchange_words) {
+  CV3_ALIVE();
   SGeo g;
   int rc = make_geo(m, default_workgroups(workgroups), &g);
   if (rc) return rc;
@@ -1104,6 +1105,7 @@ int cv3_qwen2_stream_size(const cv3_qwen2_model* m, int workgroups, int64_t* dat
 
 int cv3_qwen2_stream_pack(const cv3_qwen2_model* m, int workgroups, void* data, int64_t data_bytes, int64_t* plan,
                           int64_t plan_words, cv3_stream_t stream) {
+  CV3_ALIVE();
   SGeo g;
   int rc = make_geo(m, default_workgroups(workgroups), &g);
   if (rc) return rc;
@@ -1137,6 +1139,7 @@ int cv3_qwen2_stream_pack(const cv3_qwen2_model* m, int workgroups, void* data, 
 
 int cv3_qwen2_decode_step_stream(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_qwen2_stream* ws,
                                  const cv3_persist* p, int select, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(m && s && ws && p, CV3_EINVAL, "null model, state, weight stream or exchange block");
   SGeo g;
   int rc = make_geo(m, default_workgroups(ws->workgroups), &g);

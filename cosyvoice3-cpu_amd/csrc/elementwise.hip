@@ -414,6 +414,7 @@ __global__ void k_copy3(const float* __restrict__ x, float* __restrict__ y, int6
 extern "C" {
 
 int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_stream_t s) {
+  CV3_ALIVE();
   if (n <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_act, dim3(grid_for(n)), dim3(256), 0, stream_of(s), act, param, x, y, n);
   CV3_LAUNCHED();
@@ -421,6 +422,7 @@ int cv3_act(int act, float param, const float* x, float* y, int64_t n, cv3_strea
 }
 
 int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, float alpha, float beta, cv3_stream_t s) {
+  CV3_ALIVE();
   if (n <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_binary, dim3(grid_for(n)), dim3(256), 0, stream_of(s), op, a, b, y, n, alpha, beta);
   CV3_LAUNCHED();
@@ -428,6 +430,7 @@ int cv3_binary(int op, const float* a, const float* b, float* y, int64_t n, floa
 }
 
 int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t, float eps, cv3_stream_t s) {
+  CV3_ALIVE();
   if (c * t <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_snake, dim3(grid_for(c * t)), dim3(256), 0, stream_of(s), x, alpha, y, c, t, eps);
   CV3_LAUNCHED();
@@ -435,6 +438,7 @@ int cv3_snake(const float* x, const float* alpha, float* y, int64_t c, int64_t t
 }
 
 int cv3_snake_cl(const float* x, const float* alpha, float* y, int64_t t, int64_t c, float eps, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(t >= 0 && c > 0 && t * c < (1ll << 32), CV3_EINVAL, "snake: bad shape");
   if (t == 0) return CV3_OK;
   hipLaunchKernelGGL(k_snake_cl, dim3(grid_for(t * c)), dim3(256), 0, stream_of(s), x, alpha, y, (uint32_t)(t * c),
@@ -444,6 +448,7 @@ int cv3_snake_cl(const float* x, const float* alpha, float* y, int64_t t, int64_
 }
 
 int cv3_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, int log_softmax, cv3_stream_t s) {
+  CV3_ALIVE();
   if (rows <= 0 || cols <= 0) return CV3_OK;
   CV3_REQUIRE(rows < (1ll << 31), CV3_EINVAL, "too many rows");
   hipLaunchKernelGGL(k_softmax_rows, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, y, cols, log_softmax);
@@ -452,6 +457,7 @@ int cv3_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, int l
 }
 
 int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t cols, float eps, cv3_stream_t s) {
+  CV3_ALIVE();
   if (rows <= 0 || cols <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)rows), dim3(256), 0, stream_of(s), x, w, y, cols, eps);
   CV3_LAUNCHED();
@@ -461,6 +467,7 @@ int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t
 int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
                    const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
                    cv3_stream_t s) {
+  CV3_ALIVE();
   if (rows <= 0 || cols <= 0) return CV3_OK;
   auto a16 = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
   const bool vec = cols % 4 == 0 && cols <= 4096 && a16(x) && a16(y) && a16(w) && a16(b) && a16(shift) &&
@@ -491,6 +498,7 @@ int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float e
 
 int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* cos_out, float* sin_out,
                    cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(kind == 0 || kind == 1, CV3_EINVAL, "rope table kind must be 0 (dit) or 1 (qwen)");
   CV3_REQUIRE(dim > 0 && dim % 2 == 0, CV3_EINVAL, "rope dim must be even");
   if (n <= 0) return CV3_OK;
@@ -502,6 +510,7 @@ int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, flo
 
 int cv3_rope_pairs(float* x, int64_t ld, int64_t rows, int64_t rows_per_batch, int rot, const float* cos_tab,
                    const float* sin_tab, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(rot % 2 == 0 && rot <= ld, CV3_EINVAL, "rotary width must be even and <= row width");
   if (rows <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_rope_pairs, dim3(grid_for(rows * rot / 2)), dim3(256), 0, stream_of(s), x, ld, rows,
@@ -512,6 +521,7 @@ int cv3_rope_pairs(float* x, int64_t ld, int64_t rows, int64_t rows_per_batch, i
 
 int cv3_rope_half(float* x, int64_t nvec, int64_t per_pos, int64_t ld_pos, int d, const float* cos_tab,
                   const float* sin_tab, int64_t pos0, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(d % 2 == 0, CV3_EINVAL, "head dim must be even");
   if (nvec <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_rope_half, dim3(grid_for(nvec * d / 2)), dim3(256), 0, stream_of(s), x, nvec, per_pos, ld_pos,
@@ -522,6 +532,7 @@ int cv3_rope_half(float* x, int64_t nvec, int64_t per_pos, int64_t ld_pos, int d
 
 int cv3_cfg_euler(float* x, const float* d_cond, const float* d_uncond, int64_t n, float dt, float w,
                   cv3_stream_t s) {
+  CV3_ALIVE();
   if (n <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_cfg_euler, dim3(grid_for(n)), dim3(256), 0, stream_of(s), x, d_cond, d_uncond, n, dt, w);
   CV3_LAUNCHED();
@@ -529,6 +540,7 @@ int cv3_cfg_euler(float* x, const float* d_cond, const float* d_uncond, int64_t 
 }
 
 int cv3_interp_nearest(const float* x, float* y, int64_t c, int64_t t, int r, cv3_stream_t s) {
+  CV3_ALIVE();
   if (c * t * r <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_interp_nearest, dim3(grid_for(c * t * r)), dim3(256), 0, stream_of(s), x, y, c, t, r);
   CV3_LAUNCHED();
@@ -537,6 +549,7 @@ int cv3_interp_nearest(const float* x, float* y, int64_t c, int64_t t, int r, cv
 
 int cv3_interp_linear(const float* x, float* y, int64_t c, int64_t t, int64_t size, int align_corners,
                       cv3_stream_t s) {
+  CV3_ALIVE();
   if (c * size <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_interp_linear, dim3(grid_for(c * size)), dim3(256), 0, stream_of(s), x, y, c, t, size,
                      align_corners);
@@ -545,6 +558,7 @@ int cv3_interp_linear(const float* x, float* y, int64_t c, int64_t t, int64_t si
 }
 
 int cv3_hann_window(int n, int periodic, float* out, cv3_stream_t s) {
+  CV3_ALIVE();
   if (n <= 0) return CV3_OK;
   hipLaunchKernelGGL(k_hann, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream_of(s), n, periodic, out);
   CV3_LAUNCHED();
@@ -552,6 +566,7 @@ int cv3_hann_window(int n, int periodic, float* out, cv3_stream_t s) {
 }
 
 int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t cols, cv3_stream_t s) {
+  CV3_ALIVE();
   if (batch * rows * cols <= 0) return CV3_OK;
   const dim3 grid((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32), (unsigned)batch);
   hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, stream_of(s), x, y, rows, cols);
@@ -561,6 +576,7 @@ int cv3_transpose(const float* x, float* y, int64_t batch, int64_t rows, int64_t
 
 int cv3_copy_strided(const float* x, float* y, int64_t d0, int64_t d1, int64_t d2, const int64_t* x_strides,
                      const int64_t* y_strides, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(d0 >= 0 && d1 >= 0 && d2 >= 0, CV3_EINVAL, "negative copy extent");
   if (d0 * d1 * d2 == 0) return CV3_OK;
   hipLaunchKernelGGL(k_copy3, dim3(grid_for(d0 * d1 * d2)), dim3(256), 0, stream_of(s), x, y, d0, d1, d2,

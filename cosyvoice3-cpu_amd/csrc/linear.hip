@@ -28,6 +28,7 @@ extern "C" {
 
 int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t ldw, int64_t n,
                    const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(m >= 0 && k > 0 && n >= 0 && ldw >= k && ldx >= k && ldy >= n, CV3_EINVAL,
               "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
   if (!m || !n) return CV3_OK;
@@ -41,6 +42,7 @@ int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const floa
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
                  int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
                  const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(kind == CV3_KIND_Q8 || kind == CV3_KIND_Q4, CV3_EINVAL, "unknown quant kind %d", kind);
   CV3_REQUIRE(m >= 0 && k > 0 && kp >= k && block > 0 && kp % block == 0 && ldx >= k && ldy >= n, CV3_EINVAL,
               "bad quantised linear shape m=%lld k=%lld kp=%lld block=%lld", (long long)m, (long long)k,
@@ -66,6 +68,7 @@ int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, co
 // ops.linear with the weight held as three bfloat16 planes [3][n][ldp] (hi, mid, lo; the
 // float32 weight to all 24 bits): the same float32 GEMM, on the bfloat16 matrix cores.
 int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(n >= 0 && k > 0 && ldw >= k && ldp >= k, CV3_EINVAL, "bad plane split shape n=%lld k=%lld",
               (long long)n, (long long)k);
   return split_x3(w, n, k, ldw, planes, ldp, n * ldp, stream_of(s));
@@ -73,6 +76,7 @@ int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* pl
 
 int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* planes, int64_t ldp, int64_t n,
                   const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(m >= 0 && k > 0 && n >= 0 && ldp >= k && ldx >= k && ldy >= n, CV3_EINVAL,
               "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
   if (!m || !n) return CV3_OK;
@@ -84,6 +88,7 @@ int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint1
 int cv3_linear_q8_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* q, const void* scales,
                      int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
                      const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(m >= 0 && k > 0 && kp >= k && block > 0 && kp % block == 0 && ldx >= k && ldy >= n, CV3_EINVAL,
               "bad quantised linear shape m=%lld k=%lld kp=%lld block=%lld", (long long)m, (long long)k,
               (long long)kp, (long long)block);

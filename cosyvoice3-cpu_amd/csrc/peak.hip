@@ -30,6 +30,7 @@ __global__ __launch_bounds__(512) void k_mfma_peak(int64_t iters, float* __restr
 
 extern "C" int cv3_mfma_peak_f32(int64_t iters, int64_t workgroups, float* out, double* flops,
                                  cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(iters > 0 && workgroups > 0 && workgroups <= (1 << 20) && out, CV3_EINVAL,
               "bad MFMA probe arguments iters=%lld workgroups=%lld", (long long)iters, (long long)workgroups);
   hipLaunchKernelGGL(k_mfma_peak, dim3((unsigned)workgroups), dim3(512), 0, cv3::stream_of(s), iters, out);

@@ -132,6 +132,7 @@ extern "C" {
 
 int cv3_quantize_q8(const float* w, int64_t n, int64_t k, int64_t block, int scale_dtype, int8_t* q,
                     void* scales, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(n >= 0 && k > 0 && block > 0, CV3_EINVAL, "bad quantize_q8 shape n=%lld k=%lld block=%lld",
               (long long)n, (long long)k, (long long)block);
   CV3_REQUIRE(scale_dtype == CV3_F16 || scale_dtype == CV3_F32, CV3_EINVAL, "scale dtype must be f16 or f32");
@@ -149,6 +150,7 @@ int cv3_quantize_q8(const float* w, int64_t n, int64_t k, int64_t block, int sca
 
 int cv3_quantize_q4(const float* w, int64_t n, int64_t k, int64_t block, uint8_t* q, void* scales_f16,
                     cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(n >= 0 && k > 0 && block > 0 && block <= 64 && block % 2 == 0, CV3_EINVAL,
               "q4 block must be even and <= 64 (got %lld)", (long long)block);
   if (n == 0) return CV3_OK;
@@ -162,6 +164,7 @@ int cv3_quantize_q4(const float* w, int64_t n, int64_t k, int64_t block, uint8_t
 
 int cv3_dequant_rows(int kind, const void* q, const void* scales, int scale_dtype, int64_t kp, int64_t block,
                      int64_t k, int64_t r0, int64_t r1, float* out, int64_t ld_out, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(kind == CV3_KIND_Q8 || kind == CV3_KIND_Q4, CV3_EINVAL, "unknown quant kind %d", kind);
   CV3_REQUIRE(r1 >= r0 && k <= kp && kp % block == 0, CV3_EINVAL, "bad dequant_rows range/shape");
   const int64_t rows = r1 - r0;
@@ -177,6 +180,7 @@ int cv3_dequant_rows(int kind, const void* q, const void* scales, int scale_dtyp
 // bounds check runs on the device and is reported as CV3_EINDEX.
 int cv3_embedding(int kind, const void* table, const void* scales, int scale_dtype, int64_t rows, int64_t cols,
                   int64_t kp, int64_t block, const int64_t* ids, int64_t n, float* out, cv3_stream_t s) {
+  CV3_ALIVE();
   if (n == 0) return CV3_OK;
   hipStream_t st = stream_of(s);
   int* bad = nullptr;

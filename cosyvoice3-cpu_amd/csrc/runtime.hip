@@ -32,13 +32,28 @@ int fail(int code, const char* fmt, ...) {
 // host language releases during its own teardown never touch a torn-down runtime.
 static std::atomic<bool> g_shut{false};
 
-static std::mutex g_mu;                          // allocator, stream and graph registries
+static std::mutex g_mu;                          // allocator, stream, event and graph registries
+// A thread's own stream is tagged with the shutdown generation it was made in: after
+// cv3_shutdown destroys it, a thread that still holds the handle (a daemon thread
+// running past interpreter exit) must not launch onto it.
 static thread_local hipStream_t g_tls_stream = nullptr;
 static std::vector<hipStream_t> g_thread_streams;  // every per-thread stream, for cv3_shutdown
+// Every stream and event handed out by cv3_stream_create / cv3_event_create: cv3_shutdown
+// destroys whatever the host language has not released yet, so no HIP object of this
+// library outlives it into the runtime's own exit handlers.
+static std::unordered_map<hipStream_t, bool> g_user_streams;
+static std::unordered_map<hipEvent_t, bool> g_user_events;
 
 int decode_scratch_setup();   // decode.hip: looks up its fixed scratch on the current device
 
+bool shut_down() { return g_shut.load(); }
+
 hipStream_t stream_of(cv3_stream_t s) {
+  // After cv3_shutdown nothing may be enqueued: every block is freed, every stream destroyed.
+  if (g_shut.load()) {
+    fail(CV3_EINVAL, "the library has been shut down");
+    return nullptr;
+  }
   if (s) return reinterpret_cast<hipStream_t>(s);
   if (!g_tls_stream) {
     // Default priority only: streams of different priorities are avoided.
@@ -107,21 +122,31 @@ static size_t size_class(size_t b) {
 }
 
 // Records the block's pending events on `streams` and parks it in the free list.
-// Caller holds g_mu.
+// Caller holds g_mu.  The block always ends up parked: if an event cannot be created or
+// recorded, the device is synchronised instead (so no stream can still touch the block),
+// its pending list is emptied, and the HIP error is returned.
 static int release_locked(void* ptr, Block& b, const std::vector<hipStream_t>& streams) {
   b.pending.clear();
-  for (size_t i = 0; i < streams.size(); ++i) {
+  hipError_t err = hipSuccess;
+  for (size_t i = 0; i < streams.size() && err == hipSuccess; ++i) {
     if (i == b.events.size()) {
       hipEvent_t ev;
-      CV3_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+      err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (err != hipSuccess) break;
       b.events.push_back(ev);
     }
-    CV3_HIP(hipEventRecord(b.events[i], streams[i]));
-    b.pending.emplace_back(streams[i], b.events[i]);
+    err = hipEventRecord(b.events[i], streams[i]);
+    if (err == hipSuccess) b.pending.emplace_back(streams[i], b.events[i]);
   }
+  if (err != hipSuccess) {
+    (void)hipDeviceSynchronize();
+    b.pending.clear();
+  }
+  b.users.clear();
   g_free.emplace(b.size, ptr);
   g_in_use -= b.size;
   g_cached += b.size;
+  if (err != hipSuccess) return fail(CV3_EHIP, "recording a freed block's stream events failed: %s", hipGetErrorString(err));
   return CV3_OK;
 }
 
@@ -263,6 +288,7 @@ int cv3_mem_stats(size_t* in_use, size_t* cached) {
 }
 
 int cv3_copy_h2d(void* dst, const void* src, size_t bytes, cv3_stream_t s) {
+  CV3_ALIVE();
   if (!bytes) return CV3_OK;
   hipStream_t st = stream_of(s);
   CV3_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st));
@@ -271,6 +297,7 @@ int cv3_copy_h2d(void* dst, const void* src, size_t bytes, cv3_stream_t s) {
 }
 
 int cv3_copy_d2h(void* dst, const void* src, size_t bytes, cv3_stream_t s) {
+  CV3_ALIVE();
   if (!bytes) return CV3_OK;
   hipStream_t st = stream_of(s);
   CV3_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st));
@@ -279,69 +306,112 @@ int cv3_copy_d2h(void* dst, const void* src, size_t bytes, cv3_stream_t s) {
 }
 
 int cv3_copy_d2d(void* dst, const void* src, size_t bytes, cv3_stream_t s) {
+  CV3_ALIVE();
   if (!bytes) return CV3_OK;
   CV3_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream_of(s)));
   return CV3_OK;
 }
 
 int cv3_stream_create(cv3_stream_t* s) {
+  CV3_REQUIRE(s, CV3_EINVAL, "null output pointer");
+  CV3_REQUIRE(!g_shut.load(), CV3_EINVAL, "the library has been shut down");
   hipStream_t h;
   CV3_HIP(hipStreamCreateWithFlags(&h, hipStreamNonBlocking));
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_user_streams[h] = true;
   *s = reinterpret_cast<cv3_stream_t>(h);
   return CV3_OK;
 }
 
+// The stream is drained first, then forgotten by every block that recorded it (as a
+// user or in the events of its last free, which are complete once the stream is
+// drained), so a block freed after its stream is gone never records onto it.
 int cv3_stream_destroy(cv3_stream_t s) {
-  if (s && !g_shut.load()) CV3_HIP(hipStreamDestroy(reinterpret_cast<hipStream_t>(s)));
+  if (!s || g_shut.load()) return CV3_OK;
+  hipStream_t h = reinterpret_cast<hipStream_t>(s);
+  std::lock_guard<std::mutex> lk(g_mu);
+  CV3_REQUIRE(g_user_streams.erase(h), CV3_EINVAL, "cv3_stream_destroy of a stream not from cv3_stream_create");
+  const hipError_t se = hipStreamSynchronize(h);
+  for (auto& kv : g_blocks) {
+    Block& b = kv.second;
+    for (size_t i = 0; i < b.users.size();)
+      if (b.users[i] == h) b.users.erase(b.users.begin() + i); else ++i;
+    for (size_t i = 0; i < b.pending.size();)
+      if (b.pending[i].first == h) b.pending.erase(b.pending.begin() + i); else ++i;
+  }
+  for (auto& kv : g_graphs)
+    if (kv.first->last == h) kv.first->last = nullptr;  // its launches are done
+  const hipError_t de = hipStreamDestroy(h);
+  if (se != hipSuccess) return fail(CV3_EHIP, "hipStreamSynchronize failed: %s", hipGetErrorString(se));
+  if (de != hipSuccess) return fail(CV3_EHIP, "hipStreamDestroy failed: %s", hipGetErrorString(de));
   return CV3_OK;
 }
 
 int cv3_stream_sync(cv3_stream_t s) {
-  CV3_HIP(hipStreamSynchronize(stream_of(s)));
+  hipStream_t st = stream_of(s);
+  CV3_REQUIRE(st, CV3_EINVAL, "%s", cv3_last_error());
+  CV3_HIP(hipStreamSynchronize(st));
   return CV3_OK;
 }
 
 int cv3_device_sync(void) {
+  CV3_ALIVE();
   CV3_HIP(hipDeviceSynchronize());
   return CV3_OK;
 }
 
 int cv3_event_create(void** ev) {
+  CV3_REQUIRE(ev, CV3_EINVAL, "null output pointer");
+  CV3_REQUIRE(!g_shut.load(), CV3_EINVAL, "the library has been shut down");
   hipEvent_t e;
   CV3_HIP(hipEventCreate(&e));
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_user_events[e] = true;
   *ev = e;
   return CV3_OK;
 }
 
 int cv3_event_destroy(void* ev) {
-  if (ev && !g_shut.load()) CV3_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  if (!ev || g_shut.load()) return CV3_OK;
+  hipEvent_t e = reinterpret_cast<hipEvent_t>(ev);
+  std::lock_guard<std::mutex> lk(g_mu);
+  CV3_REQUIRE(g_user_events.erase(e), CV3_EINVAL, "cv3_event_destroy of an event not from cv3_event_create");
+  CV3_HIP(hipEventDestroy(e));
   return CV3_OK;
 }
 
 int cv3_event_record(void* ev, cv3_stream_t s) {
-  CV3_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), stream_of(s)));
+  CV3_REQUIRE(ev, CV3_EINVAL, "null event");
+  hipStream_t st = stream_of(s);
+  CV3_REQUIRE(st, CV3_EINVAL, "%s", cv3_last_error());
+  CV3_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), st));
   return CV3_OK;
 }
 
 int cv3_stream_wait_event(cv3_stream_t s, void* ev) {
   CV3_REQUIRE(ev, CV3_EINVAL, "null event");
-  CV3_HIP(hipStreamWaitEvent(stream_of(s), reinterpret_cast<hipEvent_t>(ev), 0));
+  hipStream_t st = stream_of(s);
+  CV3_REQUIRE(st, CV3_EINVAL, "%s", cv3_last_error());
+  CV3_HIP(hipStreamWaitEvent(st, reinterpret_cast<hipEvent_t>(ev), 0));
   return CV3_OK;
 }
 
 int cv3_event_elapsed_ms(void* ev0, void* ev1, float* ms) {
+  CV3_REQUIRE(!g_shut.load(), CV3_EINVAL, "the library has been shut down");
   CV3_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev1)));
   CV3_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(ev0), reinterpret_cast<hipEvent_t>(ev1)));
   return CV3_OK;
 }
 
 int cv3_graph_begin(cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(g_tls_deferred.empty(), CV3_EINVAL, "a capture is already in progress on this thread");
   CV3_HIP(hipStreamBeginCapture(stream_of(s), hipStreamCaptureModeThreadLocal));
   return CV3_OK;
 }
 
 int cv3_graph_end(cv3_stream_t s, void** exec) {
+  CV3_ALIVE();
   hipGraph_t g = nullptr;
   hipStream_t st = stream_of(s);
   std::vector<void*> owned;
@@ -369,6 +439,7 @@ int cv3_graph_end(cv3_stream_t s, void** exec) {
 }
 
 int cv3_graph_launch(void* exec, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(exec, CV3_EINVAL, "null graph");
   GraphExec* w = reinterpret_cast<GraphExec*>(exec);
   hipStream_t st = stream_of(s);
@@ -382,12 +453,12 @@ int cv3_graph_destroy(void* exec) {
   GraphExec* w = reinterpret_cast<GraphExec*>(exec);
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_graphs.erase(w)) return fail(CV3_EINVAL, "cv3_graph_destroy of an unknown graph");
-  for (void* p : w->owned) {   // behind the graph's last launch
+  for (void* p : w->owned) {   // behind the graph's last launch (none if its stream was destroyed)
     auto it = g_blocks.find(p);
     if (it != g_blocks.end()) {
       std::vector<hipStream_t> streams{it->second.home};
       for (hipStream_t u : it->second.users) add_stream(streams, u);
-      add_stream(streams, w->last);
+      if (w->last) add_stream(streams, w->last);
       release_locked(p, it->second, streams);
     }
   }
@@ -418,6 +489,23 @@ int cv3_shutdown(void) {
   for (hipStream_t st : g_thread_streams) hipStreamDestroy(st);
   g_thread_streams.clear();
   g_tls_stream = nullptr;
+  for (auto& kv : g_user_streams) hipStreamDestroy(kv.first);
+  g_user_streams.clear();
+  for (auto& kv : g_user_events) hipEventDestroy(kv.first);
+  g_user_events.clear();
+  return CV3_OK;
+}
+
+int cv3_live_handles(int64_t* streams, int64_t* events, int64_t* graphs, int64_t* blocks) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (streams) *streams = (int64_t)(g_thread_streams.size() + g_user_streams.size());
+  if (events) {
+    size_t n = g_user_events.size();
+    for (auto& kv : g_blocks) n += kv.second.events.size();
+    *events = (int64_t)n;
+  }
+  if (graphs) *graphs = (int64_t)g_graphs.size();
+  if (blocks) *blocks = (int64_t)g_blocks.size();
   return CV3_OK;
 }
 
@@ -438,6 +526,7 @@ __global__ void k_fill_zero_bytes(uint8_t* __restrict__ p, int64_t n) {
 }
 
 extern "C" int cv3_fill_zero(void* dst, size_t bytes, cv3_stream_t s) {
+  CV3_ALIVE();
   if (!bytes) return CV3_OK;
   hipStream_t st = stream_of(s);
   const int64_t words = (int64_t)(bytes / 4);

@@ -96,6 +96,7 @@ extern "C" {
 
 int cv3_f0_classify(const float* x, int64_t c, int64_t t, int64_t x_cs, int64_t x_ts, const float* w, const float* b,
                     float* f0, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(c > 0 && t >= 0, CV3_EINVAL, "f0 classifier: %lld channels, %lld frames", (long long)c, (long long)t);
   if (t == 0) return CV3_OK;
   CV3_REQUIRE(x && w && b && f0, CV3_EINVAL, "f0 classifier: null argument");
@@ -108,6 +109,7 @@ int cv3_f0_classify(const float* x, int64_t c, int64_t t, int64_t x_cs, int64_t 
 int cv3_nsf_source(const float* f0, int64_t t, int up, int harmonics, double sampling_rate, double alpha, double sigma,
                    double voiced_threshold, const float* noise, const float* l_w, const float* l_b, double* phase,
                    float* out, cv3_stream_t stream) {
+  CV3_ALIVE();
   CV3_REQUIRE(t >= 0 && up > 0, CV3_EINVAL, "nsf source: %lld frames, upsampling %d", (long long)t, up);
   CV3_REQUIRE(harmonics > 0 && harmonics <= kMaxHarmonics, CV3_EUNSUPPORTED, "nsf source: %d harmonics (at most %d)",
               harmonics, kMaxHarmonics);

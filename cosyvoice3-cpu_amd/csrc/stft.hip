@@ -106,6 +106,7 @@ extern "C" {
 
 int cv3_stft(const float* x, int64_t n, int n_fft, int hop, const float* win, int center, float* re, float* im,
              int64_t* frames_ptr, cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(n_fft > 0 && hop > 0, CV3_EINVAL, "bad stft geometry");
   CV3_REQUIRE(!center || n > n_fft / 2, CV3_EINVAL, "reflect padding needs more than n_fft/2 samples");
   const int64_t padded = n + (center ? 2 * (n_fft / 2) : 0);
@@ -127,6 +128,7 @@ int cv3_stft(const float* x, int64_t n, int n_fft, int hop, const float* win, in
 int cv3_istft(int mode, const float* a, const float* b, int64_t frames, int n_fft, int hop, const float* win,
               int center, int64_t length, float limit, float* frame_buf, float* y, int64_t* out_len_ptr,
               cv3_stream_t s) {
+  CV3_ALIVE();
   CV3_REQUIRE(n_fft > 0 && n_fft % 2 == 0 && hop > 0, CV3_EINVAL, "istft needs an even n_fft");
   CV3_REQUIRE(frames > 0, CV3_EINVAL, "istft of zero frames");
   const int64_t total = (frames - 1) * hop + n_fft;

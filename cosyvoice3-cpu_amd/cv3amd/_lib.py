@@ -72,6 +72,7 @@ def parse_header(path: str = HEADER):
 _lock = threading.RLock()
 _lib = None
 _inited = False
+_shut = False
 
 
 def lib():
@@ -110,7 +111,11 @@ def _raise(rc: int, what: str):
 
 
 def call(name: str, *args):
-    """Call ``cv3_<name>`` and raise on a non-zero status."""
+    """Call ``cv3_<name>`` and raise on a non-zero status (RuntimeError after :func:`shutdown`:
+    the library's device objects are gone, and a thread still running past interpreter exit
+    must not enqueue work)."""
+    if _shut:
+        raise RuntimeError(f"cv3_{name}: the library has been shut down")
     fn = getattr(lib(), "cv3_" + name)
     rc = fn(*args)
     if rc:
@@ -131,12 +136,24 @@ def init(device: int = 0):
 
 
 def shutdown():
-    """Release every device object the library holds (graphs, blocks, per-thread streams)
-    after synchronising the device.  Runs from ``atexit``, i.e. before the interpreter
-    tears down the objects that own those handles and before the HIP runtime's own
-    exit handlers; device arrays, events and graphs released after it are no-ops."""
-    if _lib is not None and _inited:
+    """Release every device object the library holds (graphs, blocks, per-thread streams,
+    and the streams and events it handed out) after synchronising the device.  Runs from
+    ``atexit``, i.e. before the interpreter tears down the objects that own those handles
+    and before the HIP runtime's own exit handlers; device arrays, streams, events and
+    graphs released after it are no-ops, and every other call raises."""
+    global _shut
+    if _lib is not None and _inited and not _shut:
+        _shut = True
         _lib.cv3_shutdown()
+
+
+def live_handles():
+    """{streams, events, graphs, blocks} the library still holds (all 0 after :func:`shutdown`)."""
+    vals = [ctypes.c_int64() for _ in range(4)]
+    rc = lib().cv3_live_handles(*[ctypes.addressof(v) for v in vals])
+    if rc:
+        _raise(rc, "cv3_live_handles")
+    return dict(zip(("streams", "events", "graphs", "blocks"), (v.value for v in vals)))
 
 
 def device_info():

@@ -97,10 +97,15 @@ int cv3_graph_begin(cv3_stream_t s);
 int cv3_graph_end(cv3_stream_t s, void** exec);
 int cv3_graph_launch(void* exec, cv3_stream_t s);
 int cv3_graph_destroy(void* exec);
-/* Synchronises the device and releases every graph, cached or live block and per-thread stream; afterwards
- * frees and destroys are no-ops (no counterpart in the reference: called once at process exit, before the
+/* Synchronises the device and releases every graph, cached or live block, per-thread stream, and every
+ * stream and event from cv3_stream_create / cv3_event_create; afterwards frees and destroys are no-ops and
+ * every other entry point returns CV3_EINVAL (no counterpart in the reference: called once at process exit, before the
  * HIP runtime's own teardown). */
 int cv3_shutdown(void);
+/* Counts of the HIP objects the library holds: streams (per-thread and created), events (created and the
+ * allocator's), captured graphs and allocator blocks; all 0 after cv3_shutdown (no counterpart in the
+ * reference: lets a caller check that nothing outlives the shutdown into the runtime's exit handlers). */
+int cv3_live_handles(int64_t* streams, int64_t* events, int64_t* graphs, int64_t* blocks);
 /* fp32 matrix-core rate probe: workgroups x 512 threads, each wave `iters` rounds of four independent
  * v_mfma_f32_32x32x2f32 on registers; *flops = the flops issued; out holds workgroups*512 floats (no
  * counterpart in the reference: the measured ceiling beside the published 157.3 TFLOP/s). */
