@@ -49,14 +49,6 @@ class Persist(ctypes.Structure):
                 ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int)]
 
 
-class WeightStream(ctypes.Structure):
-    """``cv3_qwen2_stream``: per-workgroup weight streams packed by cv3_qwen2_stream_pack."""
-    _fields_ = [("data", c_vp), ("plan", c_vp), ("workgroups", ctypes.c_int)]
-
-
-PLAN_WORDS = 24   # int64 per workgroup in the stream plan
-
-
 class Sampler(ctypes.Structure):
     _fields_ = [("top_p", ctypes.c_double), ("rep_threshold", ctypes.c_double), ("top_k", c_i64),
                 ("win_size", c_i64), ("speech_token_size", c_i64), ("min_len", c_i64),
@@ -224,14 +216,6 @@ class DeviceQwen2:
         # the one-launch step's launch: ordinary (the device runs nothing else meanwhile) or
         # hipLaunchCooperativeKernel, which guarantees co-residency at ~20 us more per token
         self.cooperative = False
-        # which one-launch step: "stacked" (cv3_qwen2_decode_step_persistent: the stacked weights,
-        # int8 or q4 bodies; the faster one) or "stream" (cv3_qwen2_decode_step_stream: int8 bodies
-        # only, each workgroup's weights streamed into LDS ahead of use and multiplied on the
-        # matrix cores; 40 us per layer against 18 for "stacked" at KV 512, its phases being
-        # latency-bound rather than fetch-bound)
-        self.one_launch = "stacked"
-        self._wstream: Optional[WeightStream] = None
-        self._wstream_words = 0
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
@@ -448,12 +432,9 @@ class DeviceQwen2:
         for the sampler (``step_sampled(persistent=True)``)."""
         if self._pos_host + 1 >= self.cap:
             raise ValueError("the KV cache is full")
-        stream = self.one_launch == "stream"
-        if stream and self._wstream is None:
-            self.pack_stream()
         need = ctypes.c_int64()
         _lib.call("qwen2_persist_words", ctypes.byref(self.model), 256, _lib.ptr(need))
-        need = max(need.value, self._wstream_words if stream else 0)
+        need = need.value
         if self._persist is None or self._persist.words_len < need:
             # fresh words are zero, the cleared state no epoch matches
             self._pwords = DeviceArray((need,), np.int64).zero_()
@@ -467,32 +448,9 @@ class DeviceQwen2:
             self._pwords.zero_()
             base = 256
         p.epoch_base = base
-        if stream:
-            _lib.call("qwen2_decode_step_stream", ctypes.byref(self.model), ctypes.byref(self.state),
-                      ctypes.byref(self._wstream), ctypes.byref(p), 1 if select else 0, None)
-        else:
-            _lib.call("qwen2_decode_step_persistent", ctypes.byref(self.model), ctypes.byref(self.state),
-                      ctypes.byref(p), 1 if select else 0, None)
+        _lib.call("qwen2_decode_step_persistent", ctypes.byref(self.model), ctypes.byref(self.state),
+                  ctypes.byref(p), 1 if select else 0, None)
         self._pos_host += 1 if select else 0
-
-    def pack_stream(self, workgroups: int = 0):
-        """Lay the int8 weights out as per-workgroup streams for the streamed one-launch step
-        (cv3_qwen2_stream_pack): ``workgroups`` 0 is one per CU, at most 256."""
-        nb, npw, nw = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
-        _lib.call("qwen2_stream_size", ctypes.byref(self.model), workgroups, _lib.ptr(nb), _lib.ptr(npw),
-                  _lib.ptr(nw))
-        self._sdata = DeviceArray((nb.value,), np.uint8)
-        self._splan = DeviceArray((npw.value,), np.int64)
-        _lib.call("qwen2_stream_pack", ctypes.byref(self.model), workgroups, self._sdata.ptr, nb.value,
-                  self._splan.ptr, npw.value, None)
-        self._wstream = WeightStream(self._sdata.ptr, self._splan.ptr, npw.value // PLAN_WORDS)
-        self._wstream_words = nw.value
-
-    def stream_plan(self) -> np.ndarray:
-        """The streamed step's plan table, [workgroups, PLAN_WORDS] int64."""
-        if self._wstream is None:
-            self.pack_stream()
-        return self._splan.numpy().reshape(-1, PLAN_WORDS)
 
     def persistent_error(self) -> bool:
         """True if a launch of the one-launch step gave up waiting (its results are invalid)."""

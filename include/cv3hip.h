@@ -399,28 +399,6 @@ typedef struct {
   int cooperative; /* 1: hipLaunchCooperativeKernel; 0: ordinary launch */
 } cv3_persist;
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words);
-/* The decode step of cv3_qwen2_decode_step (qwen2.py:139-179, llm.py:74-77,121,138) as one launch over
- * per-workgroup weight streams, for int8 bodies scaled per row (block = K, per-channel profile) or by block-64
- * float16 scales (balanced profile); cv3_qwen2_decode_step_persistent serves the q4 body.  Each workgroup's
- * share of every layer (16-row units of [q; k; v] in rotary pairs, o_proj, [gate; up] pairs, down in four K
- * quarters, and the head) is one contiguous stream of 1 KB MFMA-operand tiles that a loader wave DMAs into LDS
- * ahead of use; the dot products run as exact int8 MFMAs on the activation split into four base-128 digit
- * planes.  cv3_qwen2_stream_size gives the packed bytes, the plan words (int64) and the exchange words
- * (uint64, for cv3_persist) for `workgroups` (0: one per CU, at most 256); cv3_qwen2_stream_pack builds the
- * plan and the streams from the stacked weights of m into caller device memory (data 256-byte aligned).
- * The step's launch rules (epoch_base, cooperative, one launch at a time per device, the error flag) are those of
- * cv3_qwen2_decode_step_persistent. */
-typedef struct {
-  const void* data;     /* packed streams (cv3_qwen2_stream_pack) */
-  const int64_t* plan;  /* its plan table, device memory */
-  int workgroups;       /* as packed (0 is resolved to the device's count) */
-} cv3_qwen2_stream;
-int cv3_qwen2_stream_size(const cv3_qwen2_model* m, int workgroups, int64_t* data_bytes, int64_t* plan_words,
-                          int64_t* exchange_words);
-int cv3_qwen2_stream_pack(const cv3_qwen2_model* m, int workgroups, void* data, int64_t data_bytes, int64_t* plan,
-                          int64_t plan_words, cv3_stream_t stream);
-int cv3_qwen2_decode_step_stream(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_qwen2_stream* ws,
-                                 const cv3_persist* p, int select, cv3_stream_t stream);
 int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,
                                      int select, cv3_stream_t stream);
 /* The token selection of a decode step alone, on the logits already in s->logits: greedy (smp == NULL) or the

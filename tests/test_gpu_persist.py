@@ -9,9 +9,7 @@ oracle, identical greedy tokens, the appended cache rows within 1e-5; at 24
 layers the tokens equal the five-kernel step's and the logits agree within 1e-5.
 Positions cover an empty cache (one attention chunk), a start just below the
 128-key chunk boundary, 512 cached positions (five chunks) and the last chunks of a
-1024-position cache; ordinary and cooperative launches.  The int8 profiles run the
-streamed kernel (cv3_qwen2_decode_step_stream) and the stacked one
-(cv3_qwen2_decode_step_persistent), the q4 body the stacked one.  Failure handling is forced from the host: a preset error
+1024-position cache; ordinary and cooperative launches.  Failure handling is forced from the host: a preset error
 flag (every wait gives up within its bounded polls, the host raises) and the
 launch counter's wrap.
 """
@@ -52,22 +50,19 @@ def _oracle_lm(cpu, k, v, n, steps):
     return lm, cache
 
 
-@pytest.mark.parametrize("profile,n,steps,cooperative,kernel", [
-    ("per_channel", 512, 10, False, "stream"), ("balanced", 0, 6, False, "stream"),
-    ("balanced", 122, 10, False, "stream"), ("per_channel", 300, 6, True, "stream"),
-    ("per_channel", 1000, 4, False, "stream"), ("balanced", 897, 4, False, "stream"),
-    ("per_channel", 512, 6, False, "stacked"), ("balanced", 122, 6, False, "stacked"),
-    ("tiny", 300, 8, False, "stacked"), ("tiny:packed", 300, 8, False, "stacked"),
-    ("per_channel_f16", 300, 6, False, "stacked")])
-def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative, kernel):
+@pytest.mark.parametrize("profile,n,steps,cooperative", [
+    ("per_channel", 512, 10, False), ("balanced", 0, 6, False), ("per_channel", 0, 6, False),
+    ("balanced", 122, 10, False), ("per_channel", 122, 10, False), ("per_channel", 300, 6, True),
+    ("per_channel", 1000, 4, False), ("balanced", 897, 4, False), ("per_channel", 895, 4, False),
+    ("tiny", 300, 8, False), ("tiny:packed", 300, 8, False), ("per_channel_f16", 300, 6, False)])
+def test_persistent_step_logits_and_tokens(gpu, profile, n, steps, cooperative):
     from cv3amd.qwen2 import DeviceQwen2
     cpu, dev, k, v = _setup(2, profile, n)
-    print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps, cooperative={cooperative}, "
-          f"{kernel} kernel", flush=True)
+    print(f"[persist] 2 layers, profile={profile}, {n} cached, {steps} steps, cooperative={cooperative}",
+          flush=True)
     lm, cache = _oracle_lm(cpu, k, v, n, steps)
     d = DeviceQwen2(dev, cap=1024, widen_q4=not profile.endswith(":packed"))
     d.cooperative = cooperative
-    d.one_launch = kernel
     if n:
         d.fill_cache(k, v)
     d.begin(lm.sos, n)
@@ -124,20 +119,16 @@ def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
 
 
 def test_persistent_step_rejects_too_few_workgroups(gpu):
-    """The host checks the launch before it is made: 64 workgroups cannot hold phase E's
-    128 down-row workgroups (stacked kernel), nor 72 qkv + 56 o_proj units beside 112
-    attention items (streamed kernel, refused when packing)."""
+    """The host checks the launch before it is made: 64 workgroups cannot hold the
+    step's phases (128 o_proj / reduce workgroups, 112 attention items at this cache)."""
     from cv3amd.qwen2 import DeviceQwen2
     _, dev, _, _ = _setup(2, "per_channel", 0)
     d = DeviceQwen2(dev, cap=1024)
-    d.one_launch = "stacked"
     d.begin(1, 0)
     d.step_persistent()
     d._persist.workgroups = 64
     with pytest.raises(NotImplementedError):
         d.step_persistent()
-    with pytest.raises(NotImplementedError):
-        d.pack_stream(64)
 
 
 @pytest.mark.parametrize("strict", [False, True])
