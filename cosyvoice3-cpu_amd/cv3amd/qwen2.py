@@ -46,7 +46,7 @@ class Model(ctypes.Structure):
 
 class Persist(ctypes.Structure):
     _fields_ = [("words", c_vp), ("words_len", c_i64), ("err", c_vp), ("epoch_base", ctypes.c_uint32),
-                ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int)]
+                ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int), ("kernel", ctypes.c_int)]
 
 
 class Sampler(ctypes.Structure):
@@ -216,6 +216,9 @@ class DeviceQwen2:
         # the one-launch step's launch: ordinary (the device runs nothing else meanwhile) or
         # hipLaunchCooperativeKernel, which guarantees co-residency at ~20 us more per token
         self.cooperative = False
+        # the one-launch step's kernel: True lets the attention items make their own query head and
+        # o_proj share where the weights allow it (one scale per row); False keeps five exchanges per layer
+        self.fused = True
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
@@ -443,6 +446,7 @@ class DeviceQwen2:
             self._persist = Persist(self._pwords.ptr, need, self._perr.ptr, base, 0, 0)
         p = self._persist
         p.cooperative = 1 if self.cooperative else 0
+        p.kernel = 0 if self.fused else 1
         base = (p.epoch_base + 256) & 0xFFFFFFFF
         if base == 0:   # the launch counter wrapped: clear the words so no old epoch can match
             self._pwords.zero_()
