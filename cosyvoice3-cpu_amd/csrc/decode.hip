@@ -1052,8 +1052,6 @@ struct PersistArgs {
   int64_t* err;                              // set when a wait gives up
   uint32_t epoch_base;                       // launch counter * 256, from the host
   int select;                                // 1: greedy argmax + next input here
-  uint64_t* kvb;                             // k_dec_fused: k, v of the new position, two sets
-  int64_t srec;                              // k_dec_fused: words per item record
 };
 
 
@@ -1711,674 +1709,6 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
 }
 
 
-// ---------------------------------------------------------------------------
-// The whole decode step as one launch with the attention items computing their own
-// query head and their share of o_proj (q8 with one scale per weight row: the
-// per-channel profile, float32 or float16 scales).
-//
-// k_dec_persist pays five grid-wide exchanges per layer: x -> [q; k; v] -> attention
-// partials -> o_proj -> [gate; up] -> down.  Here the attention item of (head h,
-// 128-key chunk c) starts from x itself: it normalises x, multiplies its head's 64
-// query rows on the int8 matrix cores, applies the rotary, scores its chunk of the
-// cache, and multiplies its unnormalised partial output by the head's 64 columns of
-// o_proj (all 896 rows, again on the matrix cores).  It publishes (m, l, W_o[:, h] .
-// o) and the o_proj phase becomes a reduce: x_mid[r] = x[r] + sum over items of
-// e^{m - M_h} / sum_c e^{m_c - M_h} l_c times the item's row r, reading 9 words per
-// item (m, l and its 7 rows) instead of every partial output vector.
-// The k and v rows of the new position are made by 16 other workgroups and read by
-// the one item per head whose chunk holds the position, after it has scored its
-// older keys (the new key is folded in last, flash style).  Per layer:
-//   P1  items: x -> q (matrix cores) -> rotary -> chunk attention -> o_proj partial
-//       kv workgroups: x -> k, v rows -> rotary on k -> cache row and exchange words
-//   P2  128 workgroups: reduce the partials of 7 rows + residual -> x_mid
-//   P3  all workgroups: RMSNorm(x_mid) -> [gate; up] (matrix cores) -> h
-//   P4  the same 128 workgroups: down rows + residual -> x of the next layer
-// then the head as in k_dec_persist.  Items sit in the top half of the grid, every
-// chunk of a head on one XCD (workgroup w runs on XCD w % 8), so a head's query rows
-// and o_proj columns are fetched into one L2.  An item fetches its next layer's rows
-// (LDS DMA) and cache chunk (registers) right after its P3, while P4 runs without it.
-//
-// Reuse of the exchange words (two sets by layer parity, a word of layer l rewritten
-// in layer l + 2): x(l) is read by the items, the kv workgroups and the reduce, all of
-// which finish before any x_mid(l) exists, hence before x(l + 2) is written; the k, v
-// words of layer l are read by items of layer l, each of which runs before the same
-// workgroup's item of layer l + 1, and all of those before the reduce of layer l + 1;
-// the partials of layer l are read by the reduce of layer l, before x_mid(l), before
-// every later item; x_mid(l) and h(l) as in k_dec_persist.  Epochs: layer l's words
-// carry base + 8 l + phase (k, v: 0; partials: 1; x_mid: 2; h: 3; x of layer l + 1: 4).
-// ---------------------------------------------------------------------------
-constexpr int kFRec = 64;    // words of an item's record before its o_proj partial sums: m, l, padding
-constexpr int kFKV = 16;     // workgroups making the new position's k and v rows
-constexpr int kFTiles = 64;  // 1 KB MFMA operand tiles per LDS region: 4 x 16 query steps, or D / 16 o_proj blocks
-
-// Item index (head * nact + chunk) of workgroup w, or -1.  Item (h, c): XCD x = h % 8,
-// slot = (h / 8) nact + c, workgroup x + 8 (G / 8 - 1 - slot).
-__device__ __forceinline__ int fused_item(int w, int G, int H, int nact) {
-  const int slot = G / 8 - 1 - (w >> 3), hh = (w & 7) + 8 * (slot / nact);
-  return slot >= 0 && slot / nact < 2 && hh < H ? hh * nact + slot % nact : -1;
-}
-
-// Bounded poll of n words, word i at src(i) carrying epoch ep(i), into dst[i] (LDS):
-// NW words per thread per round; false (and the error flag set) if one never arrives.
-template <int NW, class Src>
-__device__ bool ll_gather(int n, Src src, float* dst, int64_t* err) {
-  bool ok = true;
-  for (int b0 = 0; b0 < n && ok; b0 += kPT * NW) {
-    const uint64_t* p[NW];
-    uint32_t ep[NW];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const int idx = b0 + (int)threadIdx.x + kPT * j;
-      p[j] = nullptr;
-      ep[j] = 0;
-      if (idx < n) src(idx, p[j], ep[j]);
-    }
-    uint64_t v[NW];
-    bool got = false;
-    for (int spins = 0; spins < kPSpin; ++spins) {
-#pragma unroll
-      for (int j = 0; j < NW; ++j)
-        v[j] = p[j] ? __hip_atomic_load(p[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ((uint64_t)ep[j] << 32);
-      got = true;
-#pragma unroll
-      for (int j = 0; j < NW; ++j) got = got && (uint32_t)(v[j] >> 32) == ep[j];
-      if (got) break;
-      if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-      if (spins < 8)
-        __builtin_amdgcn_s_sleep(1);
-      else
-        __builtin_amdgcn_s_sleep(8);
-    }
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const int idx = b0 + (int)threadIdx.x + kPT * j;
-      if (idx < n) dst[idx] = __uint_as_float((uint32_t)v[j]);
-    }
-    ok = !__syncthreads_or(!got);
-  }
-  if (!ok && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(err), 1ull);
-  return ok;
-}
-
-// Four base-128 digit planes of v (< 2^Ex in magnitude) against 2^(27 - Ex): byte p of the
-// result is digit p of X = rint(v 2^(27 - Ex)) (digits 0..2: 7-bit fields, 0..127; digit 3:
-// X >> 21, -64..63), so X = d0 + 128 d1 + 16384 d2 + 2097152 d3 exactly.
-__device__ __forceinline__ void digit_planes(const float* v, int n, float up, uint32_t* pk) {
-  int X[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) X[i] = i < n ? __float2int_rn(v[i] * up) : 0;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    uint32_t k = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      k |= (p < 3 ? ((uint32_t)X[i] >> (7 * p)) & 127u : (uint32_t)(X[i] >> 21) & 0xFFu) << (8 * i);
-    pk[p] = k;
-  }
-}
-// Exponent of a planes split: every |v| <= m is below 2^Ex (floored at -96 so 2^(27 - Ex) stays finite).
-__device__ __forceinline__ int plane_exp(float m) {
-  int Ex = 0;
-  if (m > 0.f) (void)frexpf(m, &Ex);
-  return max(Ex, -96);
-}
-// sum_k q_k X_k from the four plane sums c[0..3] of an i32 MFMA, times 2^(Ex - 27) and the row scale.
-__device__ __forceinline__ float plane_dot(const i32x4 c, int Ex, float scale) {
-  const double T = (double)c[0] + 128.0 * (double)c[1] + 16384.0 * (double)c[2] + 2097152.0 * (double)c[3];
-  return (float)(T * (double)ldexpf(1.0f, Ex - 27) * (double)scale);
-}
-
-template <bool SF16>
-__global__ __launch_bounds__(kPT) void k_dec_fused(PersistArgs a) {
-  constexpr int kDownCPL = 5;  // chunks per lane of a down row: inter <= 5120
-  __shared__ __align__(16) int8_t regA[kFTiles * 1024];  // items: query tiles; all: P3 rows; P4: staged h; head: staged x
-  __shared__ __align__(16) int8_t regB[kFTiles * 1024];  // items: o_proj column tiles; P2: gathered words; kv: staged x
-  __shared__ __align__(16) float xin[1024];               // x of the layer (items, kv)
-  __shared__ __align__(16) float xmid[1024];              // x_mid (P3, then P4's residual)
-  __shared__ __align__(16) int8_t dpl[4 * 64 * kMxSteps + 64];  // digit planes of the normed vector, then 64 zero bytes
-  __shared__ __align__(16) int8_t dplo[4 * 64 + 64];            // digit planes of an item's partial output, then zeros
-  __shared__ __align__(16) float att[8 * 64 + 16];        // per-wave outputs of an item, then m, l per wave
-  __shared__ __align__(16) float qs[64];                  // the item's rotated query, times scale log2(e)
-  __shared__ __align__(16) int8_t osc_l[4096];            // the item's o_proj row scales (float or half)
-  __shared__ float red[24];
-  __shared__ float fj[8 * kPChunks * 2];                  // P2: weight of each item
-  __shared__ float hb_val[8];
-  __shared__ int hb_i[8];
-  __shared__ uint64_t hb_key[8];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = gridDim.x, w = blockIdx.x;
-  const int D = a.D, H = a.H, Hk = a.Hk, I = a.I;
-  const int R = (H + 2 * Hk) * 64;  // [q; k; v] rows per layer (head dim 64)
-  const int GQ = H / Hk;
-  const uint32_t base = a.epoch_base;
-  const int64_t pos = *a.pos;
-  const int ipos = (int)pos, last = ipos > 0 ? ipos - 1 : 0;  // cache rows before pos come from earlier launches
-  const int nact = (int)((pos + kPKeys) / kPKeys);             // chunks holding keys 0..pos
-  const int nitems = H * nact;
-  const int nsteps = D / 64;          // 64-code steps of a hidden-wide row
-  const int nblo = D / 16;            // 16-row blocks of o_proj
-  const int nbw = (nblo + 7) / 8;     // o_proj blocks per wave of an item
-  const int item = fused_item(w, G, H, nact);
-  const bool isItem = item >= 0;
-  const int ih = isItem ? item / nact : 0, ic = isItem ? item % nact : 0, ig = ih / GQ;
-  const bool posChunk = isItem && ic == ipos / kPKeys;
-  int kvi = -1;  // rank among the non-item workgroups of the top half: the first kFKV make k and v
-  if (w >= kPOproj && !isItem) {
-    int r = 0;
-    for (int u = kPOproj; u < w; ++u) r += fused_item(u, G, H, nact) < 0;
-    kvi = r < kFKV ? r : -1;
-  }
-  const bool isKV = kvi >= 0;
-  const bool isC = w < kPOproj;  // P2 reduce rows and P4 down rows
-  const int rowsC = (D + kPOproj - 1) / kPOproj;
-  const int jbeg = (int)((int64_t)w * I / G), perD = (int)((int64_t)(w + 1) * I / G) - jbeg;
-  const int nblk = (perD + 7) / 8;
-  const int rE = w * rowsC + wave;
-  const bool liveE = isC && wave < rowsC && rE < D;
-  float* const xsA = reinterpret_cast<float*>(regA);
-  float* const xsB = reinterpret_cast<float*>(regB);
-  uint64_t* const recs = a.pb;  // item records, [2 sets][H * kPChunks][a.srec]
-
-  // ---- what an item fetches ahead: query tiles, o_proj column tiles (LDS DMA), its cache chunk ----
-  // Query tiles: wave v < 4 owns the 16 rows v*8 + j and v*8 + 32 + j (j < 8) of head ih as the 16
-  // columns of its tiles, so MFMA columns j and j + 8 are a rotary pair; tile v * nsteps + s holds
-  // codes 64 s .. 64 s + 63 of those rows in operand order (lane l: column l % 16, codes 16 (l / 16) ..).
-  const int qj = lane & 15, qd = wave * 8 + (qj < 8 ? qj : 24 + qj);  // the query dim of MFMA column qj
-  float q_sc = 0.f, q_b = 0.f, r_c = 0.f, r_s = 0.f;
-  float4 kr[4];
-  float vr[16];
-  NormStage nsI;
-  const int kw = ic * kPKeys + 16 * wave, key = kw + (lane >> 2), kq = (lane & 3) * 16;
-  auto item_prefetch = [&](int l) {
-    for (int t = wave; t < 4 * nsteps; t += 8) {  // uniform
-      const int v = t / nsteps, s = t % nsteps, jj = lane & 15;
-      const int row = ih * 64 + v * 8 + (jj < 8 ? jj : 24 + jj);
-      dma16(a.qkv.q + ((int64_t)l * R + row) * a.qkv.kp + 64 * s + 16 * (lane >> 4), regA + t * 1024);
-    }
-    for (int t = 0; t < nbw; ++t) {
-      const int b = wave * nbw + t;
-      if (b < nblo)  // uniform
-        dma16(a.o.q + ((int64_t)l * D + b * 16 + (lane & 15)) * a.o.kp + ih * 64 + 16 * (lane >> 4), regB + b * 1024);
-    }
-    const float* kb = a.k_cache + ((int64_t)l * Hk + ig) * a.cap * 64;
-    const float* vb = a.v_cache + ((int64_t)l * Hk + ig) * a.cap * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4*>(kb + (int64_t)min(key, last) * 64 + kq)[i];
-#pragma unroll
-    for (int t = 0; t < 16; ++t) vr[t] = vb[(int64_t)min(kw + t, last) * 64 + lane];
-    nsI.prefetch(a.ln1 + (int64_t)l * D, D);
-    if (wave < 4) {
-      const int64_t qrow = (int64_t)l * R + ih * 64 + qd;
-      q_sc = SF16 ? __half2float(reinterpret_cast<const __half*>(a.qkv.scales)[qrow])
-                  : reinterpret_cast<const float*>(a.qkv.scales)[qrow];
-      q_b = a.qkv_bias[qrow];
-    }
-    // the o_proj rows' scales (one per row, D contiguous values of the layer) into LDS
-    {
-      const int sb = SF16 ? 2 : 4, nb16 = (D * sb + 1023) / 1024;
-      for (int t = wave; t < nb16; t += 8)  // uniform
-        if (t * 1024 + lane * 16 < D * sb)
-          dma16(reinterpret_cast<const int8_t*>(a.o.scales) + (int64_t)l * D * sb + t * 1024 + lane * 16,
-                osc_l + t * 1024);
-    }
-  };
-  if (isItem && wave < 4) {
-    r_c = a.rope_cos[pos * 64 + qd];
-    r_s = a.rope_sin[pos * 64 + qd];
-  }
-  // ---- the kv workgroups' rows: pair p = kvi * 8 + wave, rows j and j + 32 of k (p < Hk * 32) or v ----
-  const int pKV = kvi * 8 + wave;
-  const bool liveKV = isKV && pKV < Hk * 64;
-  const bool kvK = pKV < Hk * 32;
-  const int kvh = (pKV % (Hk * 32)) / 32, kvj = pKV % 32;  // kv head, dim j of the pair
-  const int kvr0 = (kvK ? H : H + Hk) * 64 + kvh * 64 + kvj, kvr1 = kvr0 + 32;
-  RowDot<64, 1, SF16, false> dK0, dK1;
-  float bK0 = 0.f, bK1 = 0.f, kc0 = 0.f, ks0 = 0.f, kc1 = 0.f, ks1 = 0.f;
-  NormStage nsK;
-  auto kv_prefetch = [&](int l) {
-    dK0.load(a.qkv, (int64_t)l * R + (liveKV ? kvr0 : 0), lane, liveKV);
-    dK1.load(a.qkv, (int64_t)l * R + (liveKV ? kvr1 : 0), lane, liveKV);
-    bK0 = a.qkv_bias[(int64_t)l * R + kvr0];
-    bK1 = a.qkv_bias[(int64_t)l * R + kvr1];
-    nsK.prefetch(a.ln1 + (int64_t)l * D, D);
-  };
-  if (isKV) {
-    kc0 = a.rope_cos[pos * 64 + kvj];
-    ks0 = a.rope_sin[pos * 64 + kvj];
-    kc1 = a.rope_cos[pos * 64 + kvj + 32];
-    ks1 = a.rope_sin[pos * 64 + kvj + 32];
-  }
-  // ---- P3 and P4 weights ----
-  float mxs = 0.f;
-  NormStage ns2;
-  RowDot<64, kDownCPL, SF16, false> dd;
-  auto load_D = [&](int l) {
-    if (wave < nblk) {  // uniform: wave b multiplies pairs 8b .. 8b + 7 (lane l: gate (l % 16 < 8) or up row)
-      const int r16 = lane & 15, pr = wave * 8 + (r16 & 7);
-      const int64_t row = (int64_t)l * 2 * I + (r16 < 8 ? 0 : I) + jbeg + (pr < perD ? pr : 0);
-      const int8_t* rb = a.gu.q + row * a.gu.kp;
-#pragma unroll
-      for (int s = 0; s < kMxSteps; ++s)
-        if (s < nsteps) dma16(rb + 64 * s + 16 * (lane >> 4), regA + (wave * kMxSteps + s) * 1024);
-      mxs = SF16 ? __half2float(reinterpret_cast<const __half*>(a.gu.scales)[row])
-                 : reinterpret_cast<const float*>(a.gu.scales)[row];
-    }
-    ns2.prefetch(a.ln2 + (int64_t)l * D, D);
-  };
-  auto load_E = [&](int l) { dd.load(a.dn, (int64_t)l * D + (liveE ? rE : 0), lane, liveE); };
-
-  if (tid < 16) {
-    reinterpret_cast<uint32_t*>(dpl + 4 * 64 * kMxSteps)[tid] = 0u;
-    reinterpret_cast<uint32_t*>(dplo + 4 * 64)[tid] = 0u;
-  }
-  if (isItem) item_prefetch(0);
-  __syncthreads();
-  uint64_t waitX = 0, waitC = 0, waitD = 0;  // idle workgroups' previous waits (wall-clock ticks)
-
-  for (int l = 0; l < a.layers; ++l) {
-    const int par = l & 1;
-    const uint32_t E = base + (uint32_t)l * 8u;
-    const uint64_t* xw = a.xb + ((par ^ 1) * kRX + w % kRX) * a.sx;  // x of this layer (phase 4 of layer l - 1)
-    // ---- P1: kv rows of the new position ----
-    if (isKV) {
-      kv_prefetch(l);
-      if (l == 0) {
-        for (int i = tid; i < D; i += kPT) xin[i] = a.x[i];
-        __syncthreads();
-      } else {
-        const uint64_t t0 = idle_wait(wall_clock64(), waitX);
-        if (!ll_get<2>(xw, D, E - 4u, xin, a.err)) return;
-        waitX = wall_clock64() - t0;
-      }
-      const float inv = nsK.stage(xin, D, a.eps, xsB, red, 64 * 16);
-      XSlice<16> xv;
-      xv.load(xsB, lane);
-      float v0 = wdot(dK0, xv) * inv + bK0;
-      float v1 = wdot(dK1, xv) * inv + bK1;
-      if (liveKV && lane == 0) {
-        if (kvK) {  // rotary on k: x cos + rotate_half(x) sin
-          const float o0 = v0 * kc0 + (-v1) * ks0, o1 = v1 * kc1 + v0 * ks1;
-          v0 = o0;
-          v1 = o1;
-        }
-        uint64_t* kvw = a.kvb + par * (2 * Hk * 64) + (kvK ? 0 : Hk * 64) + kvh * 64 + kvj;
-        ll_put(kvw, v0, E);
-        ll_put(kvw + 32, v1, E);
-        float* row = (kvK ? a.k_cache : a.v_cache) + (((int64_t)l * Hk + kvh) * a.cap + pos) * 64;
-        row[kvj] = v0;
-        row[kvj + 32] = v1;
-      }
-      __syncthreads();
-    }
-    // ---- P1: attention item (head ih, chunk ic) ----
-    if (isItem) {
-      if (l == 0) {
-        for (int i = tid; i < D; i += kPT) xin[i] = a.x[i];
-        __syncthreads();
-      } else {
-        const uint64_t t0 = idle_wait(wall_clock64(), waitX);
-        if (!ll_get<2>(xw, D, E - 4u, xin, a.err)) return;
-        waitX = wall_clock64() - t0;
-      }
-      // RMSNorm statistic and max |x * g| in one reduction, then the planes of x * g
-      {
-        const int t = tid;
-        const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(xin)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
-        float ss = 0.f;
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
-        const float vw[4] = {v.x * nsI.w.x, v.y * nsI.w.y, v.z * nsI.w.z, v.w * nsI.w.w};
-        float mx = fmaxf(fmaxf(fabsf(vw[0]), fabsf(vw[1])), fmaxf(fabsf(vw[2]), fabsf(vw[3])));
-        ss = wave_sum_swap(ss);
-        mx = wave_max_dpp(mx);
-        if (lane == 0) {
-          red[wave] = ss;
-          red[8 + wave] = mx;
-        }
-        __syncthreads();
-        float tot = 0.f, m = 0.f;
-#pragma unroll
-        for (int i = 0; i < kPT / 64; ++i) {
-          tot += red[i];
-          m = fmaxf(m, red[8 + i]);
-        }
-        const float inv = 1.0f / sqrtf(tot / (float)D + a.eps);
-        const int Ex = plane_exp(m);
-        if (t < 16 * kMxSteps) {
-          uint32_t pk[4];
-          digit_planes(vw, 4, ldexpf(1.0f, 27 - Ex), pk);
-#pragma unroll
-          for (int p = 0; p < 4; ++p) reinterpret_cast<uint32_t*>(dpl + p * 64 * kMxSteps)[t] = pk[p];
-        }
-        __syncthreads();
-        // the query head on the matrix cores: waves 0..3, two accumulators over the steps
-        if (wave < 4) {
-          const int i = lane & 15;
-          const int8_t* ab = i < 4 ? dpl + i * 64 * kMxSteps + (lane >> 4) * 16 : dpl + 4 * 64 * kMxSteps;
-          const int ast = i < 4 ? 64 : 0;
-          const int8_t* wb = regA + wave * nsteps * 1024 + lane * 16;
-          i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-          for (int s = 0; s < nsteps; s += 2) {
-            const i32x4 a0 = *reinterpret_cast<const i32x4*>(ab + s * ast);
-            const i32x4 b0 = *reinterpret_cast<const i32x4*>(wb + s * 1024);
-            const int s1 = min(s + 1, nsteps - 1);
-            const i32x4 a1 = *reinterpret_cast<const i32x4*>(ab + s1 * ast);
-            const i32x4 b1 = *reinterpret_cast<const i32x4*>(wb + s1 * 1024);
-            c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c0, 0, 0, 0);
-            if (s + 1 < nsteps) c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c1, 0, 0, 0);
-          }
-          const i32x4 c = c0 + c1;
-          const float val = plane_dot(c, Ex, q_sc) * inv + q_b;   // lanes 0..15: query dim qd
-          const float partner = __shfl_xor(val, 8, 64);           // the other row of the rotary pair
-          // rotary (qwen2.py:64-71): dim d < 32: q_d cos - q_{d+32} sin; d >= 32: q_d cos + q_{d-32} sin;
-          // then (q * scale) * log2(e): the scores come out in base-2 units
-          const float o = qj < 8 ? val * r_c + (-partner) * r_s : val * r_c + partner * r_s;
-          if (lane < 16) qs[qd] = (o * a.scale) * kLog2E;
-        }
-        __syncthreads();
-      }
-      // scores of the chunk's older keys (key < pos): wave `wave` has keys kw + lane / 4, 16 dims per lane
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 q4 = reinterpret_cast<const float4*>(qs + kq)[i];
-        s = fmaf(q4.x, kr[i].x, s);
-        s = fmaf(q4.y, kr[i].y, s);
-        s = fmaf(q4.z, kr[i].z, s);
-        s = fmaf(q4.w, kr[i].w, s);
-      }
-      s += __uint_as_float(dpp32<kDppXor1>(__float_as_uint(s)));
-      s += __uint_as_float(dpp32<kDppXor2>(__float_as_uint(s)));
-      s = key < ipos ? s : -INFINITY;
-      const float mw = wave_max_dpp(s);
-      const float p = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mw);
-      const float lw = wave_sum_swap((lane & 3) == 0 ? p : 0.f);
-      float o = 0.f;  // dim = lane
-#pragma unroll
-      for (int t = 0; t < 16; ++t) o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 4 * t)), vr[t], o);
-      att[wave * 64 + lane] = o;
-      if (lane == 0) {
-        att[512 + wave] = mw;
-        att[520 + wave] = lw;
-      }
-      __syncthreads();
-      uint64_t* rec = recs + ((int64_t)par * H * kPChunks + item) * a.srec;
-      if (wave == 0) {
-        if (lane == 0) red[16] = 0.f;  // set below if the new key never arrives
-        float M = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) M = fmaxf(M, att[512 + i]);
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float mi = att[512 + i];
-          const float f = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
-          L = fmaf(att[520 + i], f, L);
-          O = fmaf(att[i * 64 + lane], f, O);
-        }
-        if (posChunk) {  // the new key: k and v from the kv workgroups, folded in last
-          const uint64_t* kvw = a.kvb + par * (2 * Hk * 64) + ig * 64 + lane;
-          uint64_t kk = 0, vv = 0;
-          bool got = false;
-          for (int spins = 0; spins < kPSpin; ++spins) {
-            kk = __hip_atomic_load(kvw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            vv = __hip_atomic_load(kvw + Hk * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            got = __all((uint32_t)(kk >> 32) == E && (uint32_t)(vv >> 32) == E);
-            if (got) break;
-            if ((spins & 255) == 255 && __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-            if (spins < 8)
-        __builtin_amdgcn_s_sleep(1);
-      else
-        __builtin_amdgcn_s_sleep(8);
-          }
-          if (!got && lane == 0) {
-            atomicOr(reinterpret_cast<unsigned long long*>(a.err), 1ull);
-            red[16] = 1.f;  // the workgroup stops after the barrier below
-          }
-          const float sn = wave_sum_swap(qs[lane] * __uint_as_float((uint32_t)kk));
-          const float M2 = fmaxf(M, sn);
-          const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - M2);
-          const float e = __builtin_amdgcn_exp2f(sn - M2);
-          L = fmaf(L, f, e);
-          O = fmaf(O, f, e * __uint_as_float((uint32_t)vv));
-          M = M2;
-        }
-        // digit planes of the partial output for the o_proj columns
-        const int Eo = plane_exp(wave_max_dpp(fabsf(O)));
-        int X = __float2int_rn(O * ldexpf(1.0f, 27 - Eo));
-        dplo[lane] = (int8_t)((uint32_t)X & 127u);
-        dplo[64 + lane] = (int8_t)(((uint32_t)X >> 7) & 127u);
-        dplo[128 + lane] = (int8_t)(((uint32_t)X >> 14) & 127u);
-        dplo[192 + lane] = (int8_t)(X >> 21);
-        if (lane == 0) {
-          red[17] = __int_as_float(Eo);
-          ll_put(rec, M, E + 1u);
-          ll_put(rec + 1, L, E + 1u);
-        }
-      }
-      __syncthreads();
-      if (red[16] != 0.f) return;
-      // o_proj partial: rows b*16 + i of block b = wave * nbw + t, one MFMA step of the head's 64 columns
-      {
-        const int Eo = __float_as_int(red[17]);
-        const int i = lane & 15;
-        const i32x4 af = *reinterpret_cast<const i32x4*>(i < 4 ? dplo + i * 64 + (lane >> 4) * 16 : dplo + 4 * 64);
-        for (int t = 0; t < nbw; ++t) {
-          const int b = wave * nbw + t;
-          if (b < nblo) {  // uniform
-            const i32x4 bf = *reinterpret_cast<const i32x4*>(regB + b * 1024 + lane * 16);
-            const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, i32x4{0, 0, 0, 0}, 0, 0, 0);
-            const int r = b * 16 + i;
-            const float sc = SF16 ? __half2float(reinterpret_cast<const __half*>(osc_l)[r])
-                                  : reinterpret_cast<const float*>(osc_l)[r];
-            if (lane < 16) ll_put(rec + kFRec + r, plane_dot(c, Eo, sc), E + 1u);
-          }
-        }
-      }
-      __syncthreads();  // LDS is reused below
-    }
-    // ---- P2: reduce the items' o_proj partials of 7 rows + residual -> x_mid ----
-    if (isC) {
-      const uint64_t t0 = idle_wait(wall_clock64(), waitC);
-      const int r0 = w * rowsC;
-      const int nw = 9 * nitems;  // per item: m, l, its rowsC (<= 7) rows
-      float* gw = xsB;            // [nitems][9], then x rows
-      auto src = [&](int i, const uint64_t*& p, uint32_t& ep) {
-        if (i < nw) {
-          const int j = i / 9, k = i % 9;
-          const uint64_t* rec = recs + ((int64_t)par * H * kPChunks + j) * a.srec;
-          p = k < 2 ? rec + k : (k - 2 < rowsC && r0 + k - 2 < D ? rec + kFRec + r0 + k - 2 : nullptr);
-          ep = E + 1u;
-        } else if (l > 0) {
-          p = r0 + (i - nw) < D ? xw + r0 + (i - nw) : nullptr;
-          ep = E - 4u;
-        }
-      };
-      if (!ll_gather<2>(nw + (l > 0 ? rowsC : 0), src, gw, a.err)) return;
-      waitC = wall_clock64() - t0;
-      if (l == 0 && tid < rowsC && r0 + tid < D) gw[nw + tid] = a.x[r0 + tid];
-      // weight of item j = (h, c): e^{m_j - M_h} / sum_c e^{m_c - M_h} l_c (m in base-2 units)
-      if (tid < nitems) {
-        const int hh = tid / nact;
-        float M = -INFINITY;
-        for (int c = 0; c < nact; ++c) M = fmaxf(M, gw[(hh * nact + c) * 9]);
-        float den = 0.f;
-        for (int c = 0; c < nact; ++c) {
-          const float mc = gw[(hh * nact + c) * 9];
-          den = fmaf(gw[(hh * nact + c) * 9 + 1], mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - M), den);
-        }
-        const float mj = gw[tid * 9];
-        fj[tid] = (mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - M)) / den;
-      }
-      __syncthreads();
-      const int r = r0 + wave;
-      if (wave < rowsC && r < D) {  // uniform
-        float acc = 0.f;
-        for (int j = lane; j < nitems; j += 64) acc = fmaf(fj[j], gw[j * 9 + 2 + wave], acc);
-        acc = wave_sum_swap(acc);
-        if (lane < kRM) ll_put(a.mb + (par * kRM + lane) * a.sm + r, gw[nw + wave] + acc, E + 2u);
-      }
-      __syncthreads();
-    }
-    // ---- P3: [gate; up] pairs -> h (all workgroups) ----
-    {
-      load_D(l);
-      const uint64_t t0 = isC ? 0 : idle_wait(wall_clock64(), waitD);
-      if (!ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)) return;
-      if (!isC) waitD = wall_clock64() - t0;
-      const int t = tid;
-      const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(xmid)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
-      float ss = 0.f;
-      ss = fmaf(v.x, v.x, ss);
-      ss = fmaf(v.y, v.y, ss);
-      ss = fmaf(v.z, v.z, ss);
-      ss = fmaf(v.w, v.w, ss);
-      const float vw[4] = {v.x * ns2.w.x, v.y * ns2.w.y, v.z * ns2.w.z, v.w * ns2.w.w};
-      float mx = fmaxf(fmaxf(fabsf(vw[0]), fabsf(vw[1])), fmaxf(fabsf(vw[2]), fabsf(vw[3])));
-      ss = wave_sum_swap(ss);
-      mx = wave_max_dpp(mx);
-      if (lane == 0) {
-        red[wave] = ss;
-        red[8 + wave] = mx;
-      }
-      __syncthreads();
-      float tot = 0.f, m = 0.f;
-#pragma unroll
-      for (int i = 0; i < kPT / 64; ++i) {
-        tot += red[i];
-        m = fmaxf(m, red[8 + i]);
-      }
-      const float inv = 1.0f / sqrtf(tot / (float)D + a.eps);
-      const int Ex = plane_exp(m);
-      if (t < 16 * kMxSteps) {
-        uint32_t pk[4];
-        digit_planes(vw, 4, ldexpf(1.0f, 27 - Ex), pk);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) reinterpret_cast<uint32_t*>(dpl + p * 64 * kMxSteps)[t] = pk[p];
-      }
-      __syncthreads();
-      if (wave < nblk) {  // uniform
-        const int i = lane & 15;
-        const int8_t* ab = i < 4 ? dpl + i * 64 * kMxSteps + (lane >> 4) * 16 : dpl + 4 * 64 * kMxSteps;
-        const int ast = i < 4 ? 64 : 0;
-        const int8_t* wb = regA + wave * kMxSteps * 1024 + lane * 16;
-        __builtin_amdgcn_s_waitcnt(CV3_VMCNT(0));
-        i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-        for (int s = 0; s < nsteps; s += 2) {
-          const i32x4 a0 = *reinterpret_cast<const i32x4*>(ab + s * ast);
-          const i32x4 b0 = *reinterpret_cast<const i32x4*>(wb + s * 1024);
-          const int s1 = min(s + 1, nsteps - 1);
-          const i32x4 a1 = *reinterpret_cast<const i32x4*>(ab + s1 * ast);
-          const i32x4 b1 = *reinterpret_cast<const i32x4*>(wb + s1 * 1024);
-          c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c0, 0, 0, 0);
-          if (s + 1 < nsteps) c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c1, 0, 0, 0);
-        }
-        const float val = plane_dot(c0 + c1, Ex, mxs) * inv;
-        const float upv = __shfl_xor(val, 8, 64);  // lanes 0..7: the up row of the same pair
-        const int pr = wave * 8 + i;
-        if (lane < 8 && pr < perD) {
-          const float hv = (val / (1.0f + expf(-val))) * upv;
-#pragma unroll
-          for (int rr = 0; rr < kRH; ++rr) ll_put(a.hb + (par * kRH + rr) * a.sh + jbeg + pr, hv, E + 3u);
-        }
-      }
-      __syncthreads();  // regA is refilled below
-    }
-    if (l + 1 < a.layers && isItem) item_prefetch(l + 1);  // the next layer's item fetches overlap P4
-    // ---- P4: down rows + residual -> x of the next layer ----
-    if (isC) {
-      load_E(l);
-      const ChunkT<16, 64 * kDownCPL> tmap;
-      for (int k = I + tid; k < 64 * kDownCPL * 16; k += kPT) xsA[tmap(k)] = 0.f;
-      if (!ll_get<10>(a.hb + (par * kRH + w % kRH) * a.sh, I, E + 3u, xsA, a.err, tmap)) return;
-      const float v = wdot_t(dd, xsA, lane);
-      if (liveE && lane < kRX) ll_put(a.xb + (par * kRX + lane) * a.sx + rE, xmid[rE] + v, E + 4u);
-      __syncthreads();
-    }
-  }
-  // ---- head rows, then the greedy pick (as k_dec_persist) ----
-  const uint32_t EH = base + (uint32_t)a.layers * 8u;
-  {
-    const int V = (int)a.head.rows, per = (V + G - 1) / G, rbeg = w * per;
-    RowDot<64, 1, SF16, false> dh4[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rr = rbeg + wave + 8 * t;
-      const bool live = wave + 8 * t < per && rr < V;
-      dh4[t].load(a.head, live ? rr : 0, lane, live);
-    }
-    NormStage ns;
-    ns.prefetch(a.norm, D);
-    float hbias[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rr = rbeg + wave + 8 * t;
-      hbias[t] = a.head_bias && rr < V ? a.head_bias[rr] : 0.f;
-    }
-    const int lp = (a.layers - 1) & 1;
-    if (!ll_get<2>(a.xb + (lp * kRX + w % kRX) * a.sx, D, EH - 8u + 4u, xin, a.err)) return;
-    const float inv = ns.stage(xin, D, a.eps, xsA, red, 64 * 16);
-    XSlice<16> xv;
-    xv.load(xsA, lane);
-    float best = -INFINITY;
-    int bidx = 0x7fffffff;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rr = rbeg + wave + 8 * t;
-      if (wave + 8 * t < per && rr < V) {  // uniform per wave
-        const float v = wdot(dh4[t], xv) * inv + hbias[t];
-        if (lane == 0) a.logits[rr] = v;
-        if (v > best) {
-          best = v;
-          bidx = rr;
-        }
-      }
-    }
-    if (lane == 0) {
-      hb_val[wave] = best;
-      hb_i[wave] = bidx;
-    }
-    __syncthreads();
-    if (!a.select) return;
-    if (tid == 0) {
-      float b = hb_val[0];
-      int bi = hb_i[0];
-      for (int k = 1; k < kPT / 64; ++k)
-        if (hb_val[k] > b || (hb_val[k] == b && hb_i[k] < bi)) {
-          b = hb_val[k];
-          bi = hb_i[k];
-        }
-      ll_put(a.arg + 2 * w, b, EH);
-      ll_put(a.arg + 2 * w + 1, __int_as_float(bi), EH);
-    }
-    if (w != 0) return;
-    float* cand = xsB;
-    if (!ll_get<1>(a.arg, 2 * G, EH, cand, a.err)) return;
-    uint64_t k = 0;
-    if (tid < G) k = ((uint64_t)ord_bits(cand[2 * tid]) << 32) | (0xffffffffu - (uint32_t)__float_as_int(cand[2 * tid + 1]));
-    k = wave_max_u64(k);
-    if (lane == 0) hb_key[wave] = k;
-    __syncthreads();
-    uint64_t kb = hb_key[0];
-#pragma unroll
-    for (int i = 1; i < kPT / 64; ++i) kb = max(kb, hb_key[i]);
-    int bi = (int)(0xffffffffu - (uint32_t)kb);
-    if (bi < 0 || bi >= V) bi = 0;
-    const int64_t id = bi;
-    for (int64_t cc = tid; cc < a.emb.k; cc += kPT)
-      a.x[cc] = (float)a.emb.q[id * a.emb.kp + cc] * sc_at(a.emb, id, cc);
-    if (tid == 0) {
-      a.history[pos + 1] = id;
-      *a.token = id;
-      *a.pos = pos + 1;
-    }
-  }
-}
-
-
 template <int LPR, int CPL, bool Q4>
 void launch_gemv(const GemvArgs& a, hipStream_t st) {
   const int64_t rows_per_block = 4 * (64 / LPR) / (a.mode == 2 ? 2 : 1);
@@ -2610,15 +1940,10 @@ int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_stat
 // so the copies start in different channels.
 static int64_t replica_stride(int64_t n) { return (n + 511) / 512 * 512 + 64; }
 
-// Words of one item record of k_dec_fused: m, l, padding, then the hidden-wide partial sums.
-static int64_t fused_record(int64_t D) { return kFRec + (D + 63) / 64 * 64; }
-
 static int64_t persist_words(const cv3_qwen2_model* m, int workgroups) {
   const int64_t D = m->hidden, R = (m->heads + 2 * m->kv_heads) * m->head_dim;
   return 2 * kRX * replica_stride(D) + 2 * R + 2 * kRP * replica_stride((int64_t)kPChunks * m->heads * kPPart) +
-         2 * kRM * replica_stride(D) + 2 * kRH * replica_stride(m->inter) + 2 * (int64_t)workgroups +
-         // k_dec_fused: k, v of the new position and the item records, two sets each
-         2 * 2 * m->kv_heads * m->head_dim + 2 * m->heads * kPChunks * fused_record(D);
+         2 * kRM * replica_stride(D) + 2 * kRH * replica_stride(m->inter) + 2 * (int64_t)workgroups;
 }
 
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words) {
@@ -2670,22 +1995,13 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   const bool sf16 = m->qkv.scale_dtype == CV3_F16;
   // phase D on the matrix cores: q8 [gate; up] rows with one scale per row (per-channel)
   const bool mx = !q4 && m->gate_up.kp <= m->gate_up.block && D <= 64 * kMxSteps;
-  const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
-  // k_dec_fused: query rows, o_proj and [gate; up] rows with one scale per row, the hidden size a whole
-  // number of 64-code steps; 128 reduce workgroups below the items (at most two heads per XCD, every
-  // chunk of a full cache) and kFKV kv workgroups beside them
-  const int64_t nact_max = (s->cap + kPKeys - 1) / kPKeys;
-  const bool fused = p->kernel == 0 && mx && m->qkv.kp <= m->qkv.block && m->o.kp <= m->o.block && D % 64 == 0 &&
-                     D <= 64 * kMxSteps && H <= 16 && Hk * dh <= 8 * kFKV && I <= 5120 && G % 8 == 0 &&
-                     G >= 2 * kPOproj && (H > 8 ? 2 : 1) * nact_max <= (G - kPOproj) / 8 &&
-                     H * nact_max + kFKV <= G - kPOproj;
-  const void* fn = fused  ? (sf16 ? (const void*)k_dec_fused<true> : (const void*)k_dec_fused<false>)
-                   : q4   ? (const void*)k_dec_persist<true, true>
+  const void* fn = q4     ? (const void*)k_dec_persist<true, true>
                    : mx   ? (sf16 ? (const void*)k_dec_persist<true, false, true> : (const void*)k_dec_persist<false, false, true>)
                    : sf16 ? (const void*)k_dec_persist<true, false>
                           : (const void*)k_dec_persist<false, false>;
   int per_cu = 0;
   CV3_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPT, 0));
+  const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
   // phase C needs kPOproj workgroups; phase E at most 8 rows (one per wave) on min(kPDown, G)
   CV3_REQUIRE(G >= kPOproj && G <= per_cu * cus && G <= I && (D + std::min(kPDown, G) - 1) / std::min(kPDown, G) <= 8,
               CV3_EUNSUPPORTED, "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G,
@@ -2742,22 +2058,6 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   a.err = p->err;
   a.epoch_base = p->epoch_base;
   a.select = select ? 1 : 0;
-  a.kvb = a.arg + 2 * (int64_t)G;
-  a.srec = fused_record(D);
-  a.pb = fused ? a.kvb + 2 * 2 * Hk * dh : a.pb;  // k_dec_fused's item records
-  if (fused) {
-    if (p->cooperative) {
-      void* args[] = {&a};
-      CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));
-    } else {
-      if (sf16)
-        hipLaunchKernelGGL((k_dec_fused<true>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
-      else
-        hipLaunchKernelGGL((k_dec_fused<false>), dim3((unsigned)G), dim3(kPT), 0, stream_of(stream), a);
-      CV3_LAUNCHED();
-    }
-    return CV3_OK;
-  }
   if (p->cooperative) {
     void* args[] = {&a};
     CV3_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)G), dim3(kPT), args, 0, stream_of(stream)));

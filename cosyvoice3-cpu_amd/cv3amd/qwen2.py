@@ -46,7 +46,7 @@ class Model(ctypes.Structure):
 
 class Persist(ctypes.Structure):
     _fields_ = [("words", c_vp), ("words_len", c_i64), ("err", c_vp), ("epoch_base", ctypes.c_uint32),
-                ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int), ("kernel", ctypes.c_int)]
+                ("workgroups", ctypes.c_int), ("cooperative", ctypes.c_int)]
 
 
 class Sampler(ctypes.Structure):
@@ -216,18 +216,18 @@ class DeviceQwen2:
         # the one-launch step's launch: ordinary (the device runs nothing else meanwhile) or
         # hipLaunchCooperativeKernel, which guarantees co-residency at ~20 us more per token
         self.cooperative = False
-        # the one-launch step's kernel: True lets the attention items make their own query head and
-        # o_proj share where the weights allow it (one scale per row); False keeps five exchanges per layer
-        self.fused = True
 
     # -- weights streamed per token (the HBM roofline numerator) -----------
     def bytes_per_token(self, length: int) -> dict:
         """Algorithmic HBM bytes of one token at KV length ``length`` (keys read = length + 1): the
-        checkpoint's weight bytes (a q4 body counts its packed nibbles even when held widened)."""
+        checkpoint's weight bytes (a q4 body counts its packed nibbles even when held widened).
+        ``body_held`` is what the kernels actually stream for the body: the widened int8 codes
+        and their scales when a q4 body is held widened, else the same as ``body``."""
         body = self.qkv.source_nbytes + self.o.source_nbytes + self.gate_up.source_nbytes + self.down.source_nbytes
+        held = self.qkv.nbytes + self.o.nbytes + self.gate_up.nbytes + self.down.nbytes
         kv = 2 * self.layers * self.kv_heads * (length + 1) * self.head_dim * 4
         small = 4 * (self.qkv_bias.size + self.ln1.size + self.ln2.size + self.norm.size)
-        return {"body": body, "kv": kv, "norms_biases": small, "head": self.head.nbytes}
+        return {"body": body, "kv": kv, "norms_biases": small, "head": self.head.nbytes, "body_held": held}
 
     # -- state ------------------------------------------------------------
     def fill_cache(self, k: np.ndarray, v: np.ndarray):
@@ -446,7 +446,6 @@ class DeviceQwen2:
             self._persist = Persist(self._pwords.ptr, need, self._perr.ptr, base, 0, 0)
         p = self._persist
         p.cooperative = 1 if self.cooperative else 0
-        p.kernel = 0 if self.fused else 1
         base = (p.epoch_base + 256) & 0xFFFFFFFF
         if base == 0:   # the launch counter wrapped: clear the words so no old epoch can match
             self._pwords.zero_()

@@ -397,8 +397,6 @@ typedef struct {
   uint32_t epoch_base;
   int workgroups;  /* 0: one per CU, at most 256 */
   int cooperative; /* 1: hipLaunchCooperativeKernel; 0: ordinary launch */
-  int kernel;      /* 0: the attention items make their own query head and o_proj share where the weights
-                      allow it (per-row scales), else the five-exchange step; 1: always the five-exchange step */
 } cv3_persist;
 int cv3_qwen2_persist_words(const cv3_qwen2_model* m, int workgroups, int64_t* words);
 int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_state* s, const cv3_persist* p,
