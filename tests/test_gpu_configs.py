@@ -143,7 +143,7 @@ def test_flow_10s_22_blocks_10_steps(gpu, dit22):
 
 
 @pytest.mark.timeout(300)
-@pytest.mark.parametrize("profile,steps", [("per_channel", 10), ("balanced", 3)])
+@pytest.mark.parametrize("profile,steps", [("per_channel", 10), ("balanced", 10)])
 def test_flow_30s_q8_22_blocks(gpu, dit22, profile, steps):
     import oracle.quant
     from cv3amd import synth
