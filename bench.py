@@ -539,6 +539,25 @@ def bench_kernels(args):
         log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (SPLIT_Q8_PEAK / 1e12):.1%} of the split "
             f"q8 peak)")
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
+    # the 30 s solve's attention: 1500 x 1500 per head, the CFG pair x 16 heads, on bfloat16 planes
+    qkv3 = to_device(rng.standard_normal((BT3, 3 * D), dtype=np.float32))
+    att3 = DeviceArray((BT3, D), np.float32)
+    qs3, os3 = S3(T3 * 3 * D, dh, 3 * D), S3(T3 * D, dh, D)
+    fn = lambda: _lib.call("attention_x3" if d.planes else "attention", qkv3.ptr, qkv3.ptr + D * f4,
+                           qkv3.ptr + 2 * D * f4, att3.ptr, B, H, H, T3, T3, dh, qs3, qs3, qs3, os3, scale, 0, 0, 0,
+                           None)
+    run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
+    run()
+    synchronize()
+    tm.start()
+    for _ in range(5):
+        run()
+    us = tm.stop() / (5 * reps) * 1e3
+    rate = 4.0 * B * H * T3 * T3 * dh / (us * 1e-6) / 1e12
+    name = f"flash attention B={B} H={H} T={T3} d={dh}"
+    log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (lin_peak / 1e12):.1%} of the {lin_unit} peak)")
+    out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
+    del qkv3, att3
     # one whole-utterance vocoder inference (F0 net, excitation, decode; its convs are k_conv_cl_dma)
     from cv3amd.hift import DeviceHiFT
     h = DeviceHiFT(WeightStore(synth.hift_tensors(base=512), synth.hift_meta()))
