@@ -374,7 +374,8 @@ def bench_flow(args, tensors, meta):
     kflops = 2.0 * M * N * K
     log(f"flow: QKV GEMM {kms * 1e3:.1f} us/launch, {kflops / (kms / 1e3) / 1e12:.1f} TFLOP/s")
     planes = d.qkv[0].planes is not None if d.depth else False
-    name = ("k_gemm_x3 (float32 GEMM as six bfloat16 plane products, fused QKV 1000x3072x1024)" if planes
+    name = ("k_gemm_x3f (float32 GEMM as six bfloat16 plane products, weight fragments straight to registers, "
+            "fused QKV 1000x3072x1024)" if planes
             else "k_gemm<0> (fp32 MFMA GEMM, fused QKV 1000x3072x1024)")
     return {"ms": ms, "flops": flops, "by_unit": by_unit, "T": T, "depth": d.depth,
             "kernel": {"name": name, "flops_per_launch": kflops, "peak": SPLIT_BF16_PEAK if planes else FP32_MFMA_PEAK,

@@ -711,6 +711,126 @@ __global__ __launch_bounds__(256) void k_gemm_x3(GemmParams p, const uint16_t* p
   store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
 }
 
+// The same GEMM with B's planes packed once in MFMA fragment order (k_split_x3_frag):
+// frag[p][nb][t][l] is the 16-byte B operand of lane l for the 16-k step t of the 32-row block
+// nb (row 32 nb + l % 32, k = 16 t + 8 (l / 32) .. + 7), so each wave loads its B fragments
+// straight into registers, one contiguous kilobyte per plane and step, a stage ahead; only A
+// goes through LDS (half the LDS traffic of k_gemm_x3).  Every MFMA sees the operands
+// k_gemm_x3 gives it, in the same order: the results are the same bits.
+__global__ __launch_bounds__(256) void k_gemm_x3f(GemmParams p, const uint4* frag, int64_t per_plane, int tiles_m,
+                                                  int tiles_n, int gm) {
+  __shared__ uint4 sA[2][3][BM * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int64_t m0, n0;
+  tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
+  const int lr = tid >> 2, lc = tid & 3;
+  const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
+  const int wslot = xslot(lr, lc);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32, asw = (ar >> 2) & 3;
+  const int64_t S = p.k / XBK, T16 = p.k / 16;
+  const uint4* fb = frag + ((n0 + wn) >> 5) * T16 * 64 + lane;  // this wave's 32-column block
+  f32x16 big = {0.f}, small = {0.f};
+  struct XA {
+    float4 a0, a1;
+  };
+  struct BF {
+    uint4 v[2][3];  // [16-k step of the stage][plane]
+  };
+  auto load = [&](XA& x, int64_t k0) {
+    x.a0 = *reinterpret_cast<const float4*>(pa + k0);
+    x.a1 = *reinterpret_cast<const float4*>(pa + k0 + 4);
+  };
+  auto loadb = [&](BF& b, int64_t st) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl) b.v[ks][pl] = fb[pl * per_plane + (2 * st + ks) * 64];
+  };
+  auto store = [&](int buf, const XA& x) {
+    uint4 hi, mid, lo;
+    split_x3(x.a0, x.a1, hi, mid, lo);
+    sA[buf][0][wslot] = hi;
+    sA[buf][1][wslot] = mid;
+    sA[buf][2][wslot] = lo;
+  };
+  auto mma = [&](int buf, const BF& b) {
+#pragma unroll
+    for (int ks = 0; ks < XBK / 16; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ asw);
+      const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, sA[buf][0][sa]);
+      const bf16x8_t am = __builtin_bit_cast(bf16x8_t, sA[buf][1][sa]);
+      const bf16x8_t al = __builtin_bit_cast(bf16x8_t, sA[buf][2][sa]);
+      const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, b.v[ks][0]);
+      const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, b.v[ks][1]);
+      const bf16x8_t bl = __builtin_bit_cast(bf16x8_t, b.v[ks][2]);
+      big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, big, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, small, 0, 0, 0);
+    }
+  };
+
+  // S even and >= 2: A ping-pongs through registers x / y and LDS buffers 0 / 1 as in k_gemm_x3;
+  // the B fragments of the even and odd stages in b0 / b1, each refilled right after its use
+  XA x, y;
+  BF b0, b1;
+  load(x, 0);
+  load(y, XBK);
+  loadb(b0, 0);
+  loadb(b1, 1);
+  store(0, x);
+  __syncthreads();
+  for (int64_t s = 0; s + 2 < S; s += 2) {
+    load(x, (s + 2) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0, b0);
+    loadb(b0, s + 2);
+    store(1, y);
+    __syncthreads();
+    load(y, (s + 3) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, b1);
+    loadb(b1, s + 3);
+    store(0, x);
+    __syncthreads();
+  }
+  mma(0, b0);
+  store(1, y);
+  __syncthreads();
+  mma(1, b1);
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = big[i] + small[i];
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
+}
+
+// frag[p][nb][t][l] = plane p of w[32 nb + l % 32][16 t + 8 (l / 32) .. + 7] (rows past n zero), the
+// planes k_split_x3 makes, in k_gemm_x3f's fragment order.
+__global__ __launch_bounds__(256) void k_split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint4* frag,
+                                                       int64_t per_plane) {
+  const int64_t T = k / 16;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per_plane;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t t = (i >> 6) % T, nb = (i >> 6) / T;
+    const int64_t row = nb * 32 + (l & 31), k0 = 16 * t + 8 * (l >> 5);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (row < n) {
+      a = *reinterpret_cast<const float4*>(w + row * ldw + k0);
+      b = *reinterpret_cast<const float4*>(w + row * ldw + k0 + 4);
+    }
+    uint4 hi, mid, lo;
+    split_x3(a, b, hi, mid, lo);
+    frag[i] = hi;
+    frag[per_plane + i] = mid;
+    frag[2 * per_plane + i] = lo;
+  }
+}
+
 // q8 weights on the bfloat16 matrix cores.  An int8 code is exact in bfloat16, so x . q
 // needs only x's three planes: xh q, xm q and xl q, each exact in the float32 accumulate
 // (three MFMAs per 16-k step where a float32 weight needs six).  The scale multiplies each
@@ -824,6 +944,125 @@ __global__ __launch_bounds__(256) void k_gemm_x3q(GemmParams p, int tiles_m, int
   mma(1);
   fold();  // the last block (or the part of it K covers)
   store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
+}
+
+// The same q8 GEMM with the codes packed once in MFMA fragment order (k_pack_q8_frag):
+// qfrag[nb][t][l] holds the 8 codes of lane l for the 16-k step t of the 32-row block nb (row
+// 32 nb + l % 32, k = 16 t + 8 (l / 32) .. + 7), so each wave loads its B fragments (8 bytes per
+// lane, 512 contiguous bytes) straight into registers a stage ahead and widens them to bfloat16
+// there; only A goes through LDS.  The same products in the same order as k_gemm_x3q.
+__global__ __launch_bounds__(256) void k_gemm_x3qf(GemmParams p, const uint2* qfrag, int tiles_m, int tiles_n,
+                                                   int gm) {
+  __shared__ uint4 sA[2][3][BM * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int64_t m0, n0;
+  tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
+  const int lr = tid >> 2, lc = tid & 3;
+  const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
+  const int wslot = xslot(lr, lc);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32, asw = (ar >> 2) & 3;
+  const int64_t S = p.k / XBK, spb = p.block / XBK, T16 = p.k / 16;
+  const uint2* fb = qfrag + ((n0 + wn) >> 5) * T16 * 64 + lane;  // this wave's 32-column block
+  // the lane's output column's scales
+  const int64_t srow = min(n0 + wn + r32, p.n - 1) * p.nb;
+  auto scale = [&](int64_t b) {
+    return p.sf16 ? __half2float(reinterpret_cast<const __half*>(p.scales)[srow + b])
+                  : reinterpret_cast<const float*>(p.scales)[srow + b];
+  };
+  f32x16 big = {0.f}, small = {0.f}, acc = {0.f};
+  float s_cur = scale(0);
+  int64_t blk = 0;
+  auto fold = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i] = fmaf(s_cur, big[i] + small[i], acc[i]);
+      big[i] = 0.f;
+      small[i] = 0.f;
+    }
+    ++blk;
+    s_cur = scale(min(blk, p.nb - 1));
+  };
+  struct XA {
+    float4 a0, a1;
+  };
+  struct BQ {
+    uint2 v[2];  // the stage's two 16-k steps
+  };
+  auto load = [&](XA& x, int64_t k0) {
+    x.a0 = *reinterpret_cast<const float4*>(pa + k0);
+    x.a1 = *reinterpret_cast<const float4*>(pa + k0 + 4);
+  };
+  auto loadb = [&](BQ& b, int64_t st) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) b.v[ks] = fb[(2 * st + ks) * 64];
+  };
+  auto store = [&](int buf, const XA& x) {
+    uint4 hi, mid, lo;
+    split_x3(x.a0, x.a1, hi, mid, lo);
+    sA[buf][0][wslot] = hi;
+    sA[buf][1][wslot] = mid;
+    sA[buf][2][wslot] = lo;
+  };
+  auto mma = [&](int buf, const BQ& b) {
+#pragma unroll
+    for (int ks = 0; ks < XBK / 16; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ asw);
+      const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, sA[buf][0][sa]);
+      const bf16x8_t am = __builtin_bit_cast(bf16x8_t, sA[buf][1][sa]);
+      const bf16x8_t al = __builtin_bit_cast(bf16x8_t, sA[buf][2][sa]);
+      const bf16x8_t bq = __builtin_bit_cast(bf16x8_t, codes_bf16(b.v[ks]));
+      big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bq, big, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bq, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bq, small, 0, 0, 0);
+    }
+  };
+
+  // as k_gemm_x3f: A through registers x / y and LDS buffers 0 / 1, B fragments in b0 / b1
+  XA x, y;
+  BQ b0, b1;
+  load(x, 0);
+  load(y, XBK);
+  loadb(b0, 0);
+  loadb(b1, 1);
+  store(0, x);
+  __syncthreads();
+  int64_t s = 0;
+  for (; s + 2 < S; s += 2) {
+    load(x, (s + 2) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0, b0);
+    loadb(b0, s + 2);
+    store(1, y);
+    __syncthreads();
+    load(y, (s + 3) * XBK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, b1);
+    loadb(b1, s + 3);
+    store(0, x);
+    __syncthreads();
+    if ((s + 2) % spb == 0) fold();
+  }
+  mma(0, b0);
+  store(1, y);
+  __syncthreads();
+  mma(1, b1);
+  fold();  // the last block (or the part of it K covers)
+  store_tile(p, acc, m0 + wm, h, n0 + wn + r32);
+}
+
+// qfrag[nb][t][l] = the 8 codes q[32 nb + l % 32][16 t + 8 (l / 32) .. + 7] (rows past n zero): the
+// q8 codes in k_gemm_x3qf's fragment order.
+__global__ __launch_bounds__(256) void k_pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, uint2* frag,
+                                                      int64_t total) {
+  const int64_t T = k / 16;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t t = (i >> 6) % T, nb = (i >> 6) / T;
+    const int64_t row = nb * 32 + (l & 31), k0 = 16 * t + 8 * (l >> 5);
+    frag[i] = row < n ? *reinterpret_cast<const uint2*>(q + row * ldq + k0) : make_uint2(0u, 0u);
+  }
 }
 
 // planes[p][row][0 .. k) = plane p of w[row][0 .. k); eight k per thread.
@@ -951,6 +1190,99 @@ int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* p
   const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, 6.0 * (double)n * k);
   hipLaunchKernelGGL(k_gemm_x3, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p, planes, ldp, pstride,
                      (int)tiles_m, (int)tiles_n, gm);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+int pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, hipStream_t st) {
+  CV3_REQUIRE(k % 64 == 0 && ((uintptr_t)q % 8 == 0) && ldq % 8 == 0 && ldq >= k && ((uintptr_t)frag % 8 == 0),
+              CV3_EINVAL, "fragment-ordered codes need K %% 64 == 0 and 8-byte aligned rows");
+  const int64_t total = ceil_div(n, 32) * 32 * k / 8;  // 8-byte fragments
+  if (total == 0) return CV3_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipLaunchKernelGGL(k_pack_q8_frag, dim3((unsigned)blocks), dim3(256), 0, st, q, n, k, ldq,
+                     reinterpret_cast<uint2*>(frag), total);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// C = epi(A . dequant(q)^T) with the codes in fragment order (pack_q8_frag), scales [n, nb].
+int gemm_x3qf(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* qfrag, const void* scales, bool sf16,
+              int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
+              const cv3_epilogue* epi, hipStream_t st) {
+  CV3_REQUIRE(k % (2 * XBK) == 0 && block % (2 * XBK) == 0 && nb * block >= k, CV3_EUNSUPPORTED,
+              "split-bfloat16 q8 GEMM needs K %% 64 == 0 and blocks of a multiple of 64 (K = %lld, block = %lld)",
+              (long long)k, (long long)block);
+  CV3_REQUIRE(((uintptr_t)a % 16 == 0) && lda % 4 == 0 && ((uintptr_t)qfrag % 8 == 0), CV3_EINVAL,
+              "split-bfloat16 q8 GEMM operands must be aligned rows");
+  GemmParams p{};
+  p.a = a;
+  p.lda = lda;
+  p.scales = scales;
+  p.sf16 = sf16;
+  p.nb = nb;
+  p.block = block;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.bias = bias;
+  p.c = c;
+  p.ldc = ldc;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  CV3_REQUIRE(!p.epi.rope_cos || (p.epi.rope_rows > 0 && p.epi.rope_period > 0 && p.epi.rope_width > 0 &&
+                                  p.epi.rope_rows * p.epi.rope_width < (1ll << 31) && m + 64 < (1ll << 31) &&
+                                  n < (1ll << 31)),
+              CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, (double)n * k);
+  hipLaunchKernelGGL(k_gemm_x3qf, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
+                     reinterpret_cast<const uint2*>(qfrag), (int)tiles_m, (int)tiles_n, gm);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// Elements of one plane of the fragment-ordered weight: 32-row blocks x K.
+int64_t x3_frag_plane(int64_t n, int64_t k) { return ceil_div(n, 32) * 32 * k; }
+
+int split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* frag, hipStream_t st) {
+  CV3_REQUIRE(k % 64 == 0 && ((uintptr_t)w % 16 == 0) && ldw % 4 == 0 && ldw >= k && ((uintptr_t)frag % 16 == 0),
+              CV3_EINVAL, "fragment-ordered planes need K %% 64 == 0 and 16-byte aligned rows");
+  const int64_t per_plane = x3_frag_plane(n, k) / 8;  // 16-byte fragments
+  if (per_plane == 0) return CV3_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(per_plane, 256), 65536);
+  hipLaunchKernelGGL(k_split_x3_frag, dim3((unsigned)blocks), dim3(256), 0, st, w, n, k, ldw,
+                     reinterpret_cast<uint4*>(frag), per_plane);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// C = epi(A . B^T) with B as fragment-ordered planes (split_x3_frag).  K % 64 == 0.
+int gemm_x3f(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* frag, int64_t n, const float* bias,
+             float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st) {
+  CV3_REQUIRE(k % (2 * XBK) == 0, CV3_EUNSUPPORTED, "split-bfloat16 GEMM needs K %% 64 == 0 (K = %lld)",
+              (long long)k);
+  CV3_REQUIRE(((uintptr_t)a % 16 == 0) && lda % 4 == 0 && ((uintptr_t)frag % 16 == 0), CV3_EINVAL,
+              "split-bfloat16 GEMM operands must be 16-byte aligned rows");
+  GemmParams p{};
+  p.a = a;
+  p.lda = lda;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.bias = bias;
+  p.c = c;
+  p.ldc = ldc;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  CV3_REQUIRE(!p.epi.rope_cos || (p.epi.rope_rows > 0 && p.epi.rope_period > 0 && p.epi.rope_width > 0 &&
+                                  p.epi.rope_rows * p.epi.rope_width < (1ll << 31) && m + 64 < (1ll << 31) &&
+                                  n < (1ll << 31)),
+              CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, 6.0 * (double)n * k);
+  hipLaunchKernelGGL(k_gemm_x3f, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
+                     reinterpret_cast<const uint4*>(frag), x3_frag_plane(n, k) / 8, (int)tiles_m, (int)tiles_n, gm);
   CV3_LAUNCHED();
   return CV3_OK;
 }

@@ -15,6 +15,14 @@ int gemm_x3(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* p
             int64_t n, const float* bias, float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
 int split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, int64_t pstride,
              hipStream_t st);
+int64_t x3_frag_plane(int64_t n, int64_t k);
+int split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* frag, hipStream_t st);
+int gemm_x3f(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* frag, int64_t n, const float* bias,
+             float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
+int pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, hipStream_t st);
+int gemm_x3qf(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* qfrag, const void* scales, bool sf16,
+              int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
+              const cv3_epilogue* epi, hipStream_t st);
 int gemm_x3q(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* q, int64_t ldq, const void* scales,
              bool sf16, int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
              const cv3_epilogue* epi, hipStream_t st);
@@ -81,6 +89,47 @@ int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint1
               "bad linear shape m=%lld k=%lld n=%lld", (long long)m, (long long)k, (long long)n);
   if (!m || !n) return CV3_OK;
   return gemm_x3(x, m, k, ldx, planes, ldp, n * ldp, n, bias, y, ldy, epi, stream_of(s));
+}
+
+int cv3_split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* frag, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(n >= 0 && k > 0 && ldw >= k, CV3_EINVAL, "bad plane split shape n=%lld k=%lld", (long long)n,
+              (long long)k);
+  return split_x3_frag(w, n, k, ldw, frag, stream_of(s));
+}
+
+int cv3_x3_frag_elems(int64_t n, int64_t k, int64_t* elems) {
+  CV3_REQUIRE(n >= 0 && k > 0 && elems, CV3_EINVAL, "bad shape or null output");
+  *elems = 3 * x3_frag_plane(n, k);
+  return CV3_OK;
+}
+
+int cv3_linear_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* frag, int64_t n,
+                       const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(m >= 0 && k > 0 && n >= 0 && ldx >= k && ldy >= n, CV3_EINVAL, "bad linear shape m=%lld k=%lld n=%lld",
+              (long long)m, (long long)k, (long long)n);
+  if (!m || !n) return CV3_OK;
+  return gemm_x3f(x, m, k, ldx, frag, n, bias, y, ldy, epi, stream_of(s));
+}
+
+int cv3_pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(n >= 0 && k > 0 && ldq >= k, CV3_EINVAL, "bad code pack shape n=%lld k=%lld", (long long)n,
+              (long long)k);
+  return pack_q8_frag(q, n, k, ldq, frag, stream_of(s));
+}
+
+int cv3_linear_q8_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qfrag, const void* scales,
+                          int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y,
+                          int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(m >= 0 && k > 0 && kp >= k && block > 0 && kp % block == 0 && ldx >= k && ldy >= n, CV3_EINVAL,
+              "bad quantised linear shape m=%lld k=%lld kp=%lld block=%lld", (long long)m, (long long)k,
+              (long long)kp, (long long)block);
+  if (!m || !n) return CV3_OK;
+  return gemm_x3qf(x, m, k, ldx, qfrag, scales, scale_dtype == CV3_F16, kp / block, block, n, bias, y, ldy, epi,
+                   stream_of(s));
 }
 
 // quant.qmatmul on q8 weights (quant.py:165-190) with the activation as bfloat16 planes and

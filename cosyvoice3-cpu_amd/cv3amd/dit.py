@@ -59,10 +59,11 @@ class DeviceLinear:
     """One resident linear weight: float32 ``[N, K]`` or q8 codes + scales.
 
     ``planes=True`` holds a float32 weight (K % 64 == 0) as its three bfloat16 planes
-    instead (``cv3_split_x3``: W = hi + mid + lo to all 24 bits), and the product runs on
-    the bfloat16 matrix cores as six plane products with float32 accumulation
-    (``cv3_linear_x3``): the same float32 linear, with errors against float64 no larger
-    than the float32 matrix cores' own.  A q8 weight (blocks of a multiple of 64) then runs
+    instead (W = hi + mid + lo to all 24 bits), packed in the matrix cores' fragment order
+    (``cv3_split_x3_frag``), and the product runs on the bfloat16 matrix cores as six plane
+    products with float32 accumulation, each wave loading its weight fragments straight into
+    registers (``cv3_linear_x3_frag``): the same float32 linear, with errors against float64
+    no larger than the float32 matrix cores' own.  A q8 weight (blocks of a multiple of 64) then runs
     as the activation's three planes times its codes, exact in bfloat16, with the block
     scale on each block's sum (``cv3_linear_q8_x3``).
     """
@@ -88,8 +89,13 @@ class DeviceLinear:
             self.sf16 = sdt.pop() == np.dtype(np.float16)
             self.q = to_device(np.ascontiguousarray(q))
             self.scales = to_device(np.ascontiguousarray(s))
-            # the activation's bfloat16 planes times the codes (cv3_linear_q8_x3)
+            # the activation's bfloat16 planes times the codes, held in the matrix cores' fragment
+            # order (cv3_pack_q8_frag, cv3_linear_q8_x3_frag)
             self.q8_planes = bool(planes) and self.k % 64 == 0 and self.block % 64 == 0
+            if self.q8_planes:
+                qf = DeviceArray((-(-self.n // 32) * 32 * self.k,), np.int8)
+                _lib.call("pack_q8_frag", self.q.ptr, self.n, self.k, self.kp, qf.ptr, None)
+                self.q = qf
         elif not any(_is_q(w) for w in ws):
             self.q8 = False
             w = np.concatenate([np.asarray(_host(w), dtype=np.float32).reshape(np.shape(w)[0], -1) for w in ws],
@@ -97,8 +103,10 @@ class DeviceLinear:
             self.n, self.k = w.shape
             self.w = to_device(np.ascontiguousarray(w))
             if planes and self.k % 64 == 0:
-                self.planes = DeviceArray((3, self.n, self.k), np.uint16)
-                _lib.call("split_x3", self.w.ptr, self.n, self.k, self.k, self.planes.ptr, self.k, None)
+                ne = ctypes.c_int64()
+                _lib.call("x3_frag_elems", self.n, self.k, ctypes.byref(ne))
+                self.planes = DeviceArray((ne.value,), np.uint16)
+                _lib.call("split_x3_frag", self.w.ptr, self.n, self.k, self.k, self.planes.ptr, None)
                 self.w = None
         else:
             raise ValueError("cannot concatenate quantised and float weights")
@@ -122,12 +130,12 @@ class DeviceLinear:
         b = self.bias.ptr if self.bias is not None else None
         e = ctypes.byref(epi) if epi is not None else None
         if self.q8:
-            fn = "linear_q8_x3" if self.q8_planes else "linear_q"
+            fn = "linear_q8_x3_frag" if self.q8_planes else "linear_q"
             kind = () if self.q8_planes else (_lib.KIND_Q8,)
             _lib.call(fn, *kind, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
                       _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, None)
         elif self.planes is not None:
-            _lib.call("linear_x3", x, m, self.k, ldx, self.planes.ptr, self.k, self.n, b, y, ldy, e, None)
+            _lib.call("linear_x3_frag", x, m, self.k, ldx, self.planes.ptr, self.n, b, y, ldy, e, None)
         else:
             _lib.call("linear_f32", x, m, self.k, ldx, self.w.ptr, self.k, self.n, b, y, ldy, e, None)
 

@@ -144,12 +144,29 @@ int cv3_linear_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const floa
 int cv3_split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes, int64_t ldp, cv3_stream_t s);
 int cv3_linear_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* planes, int64_t ldp, int64_t n,
                   const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
+/* The same linear with the weight's planes packed once in the matrix cores' fragment order:
+ * frag[p][nb][t][l] (8 bfloat16) = plane p of w[32 nb + l % 32][16 t + 8 (l / 32) .. + 7], rows past n zero,
+ * cv3_x3_frag_elems(n, k) uint16 in all (3 planes of ceil(n / 32) * 32 * k).  The product then loads each
+ * wave's weight fragments straight into registers and stages only the activation in LDS; it returns the
+ * same bits as cv3_linear_x3 on the same weight.  K % 64 == 0, 16-byte aligned rows. */
+int cv3_split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* frag, cv3_stream_t s);
+int cv3_x3_frag_elems(int64_t n, int64_t k, int64_t* elems);
+int cv3_linear_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* frag, int64_t n,
+                       const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
 /* quant.qmatmul on q8 weights (quant.py:165-190) on the bfloat16 matrix cores: the activation as
  * bfloat16 planes, each int8 code exact in bfloat16 (three products per code), the block scale
  * applied to each block's sum.  K % 64 == 0, block % 64 == 0 (per-channel: block = kp). */
 int cv3_linear_q8_x3(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* q, const void* scales,
                      int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
                      const cv3_epilogue* epi, cv3_stream_t s);
+/* The same q8 linear with the codes packed once in fragment order: frag[nb][t][l] = the 8 codes
+ * q[32 nb + l % 32][16 t + 8 (l / 32) .. + 7], rows past n zero (ceil(n / 32) * 32 * k bytes); the scales
+ * stay [n, kp / block].  Each wave loads its codes straight into registers; the same bits as
+ * cv3_linear_q8_x3.  K % 64 == 0 (the packed k), block % 64 == 0. */
+int cv3_pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, cv3_stream_t s);
+int cv3_linear_q8_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qfrag, const void* scales,
+                          int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y,
+                          int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
 /* Quantised weights (q8: q [n, kp] int8; q4: q [n, kp/2]); scales [n, kp/block] (f16 or f32). */
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
                  int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,

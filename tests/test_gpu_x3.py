@@ -328,3 +328,118 @@ def test_attention_x3_matches_oracle(lib, h, hk, n, m, mask):
     e_f32 = np.abs(attention(lib, "attention", q, k, v, mask) - exact).max()
     print(f"[att]   max err vs float64: split-bf16 {e_x3:.3e}, float32 MFMA {e_f32:.3e}", flush=True)
     assert e_x3 <= e_f32 * 1.25 + 1e-30
+
+
+# ---- the weight planes in fragment order (cv3_split_x3_frag / cv3_linear_x3_frag) ----
+
+def split_frag(lib, w):
+    _lib, to_device, empty = lib
+    n, k = w.shape
+    dw = to_device(np.ascontiguousarray(w, np.float32))
+    ne = ctypes.c_int64()
+    _lib.call("x3_frag_elems", n, k, ctypes.byref(ne))
+    frag = empty((ne.value,), np.uint16)
+    _lib.call("split_x3_frag", dw.ptr, n, k, k, frag.ptr, None)
+    return frag
+
+
+def linear_frag(lib, frag, x, n, bias=None, epi=None, out=None):
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = out if out is not None else empty((m, n))
+    _lib.call("linear_x3_frag", dx.ptr, m, k, k, frag.ptr, n, db.ptr if db is not None else None, y.ptr, n,
+              ctypes.byref(epi) if epi is not None else None, None)
+    return y.numpy()
+
+
+@pytest.mark.parametrize("n,k", [(130, 128), (3072, 1024), (32, 64), (1, 64)])
+def test_frag_planes_are_the_planes_in_fragment_order(lib, n, k):
+    """frag[p][nb][t][l] = plane p of w[32 nb + l % 32][16 t + 8 (l / 32) .. + 7], rows past n zero:
+    the NumPy rounding chain's planes, reordered."""
+    rng = np.random.default_rng(n + k)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    got = split_frag(lib, w).numpy()
+    nb = -(-n // 32)
+    planes = np.zeros((3, nb * 32, k), np.uint16)
+    planes[:, :n] = np.stack(planes_numpy(w))
+    # [p][nb][32 rows][T][2 halves][8] -> [p][nb][T][2 halves][32 rows][8] = [p][nb][T][lane][8]
+    want = planes.reshape(3, nb, 32, k // 16, 2, 8).transpose(0, 1, 3, 4, 2, 5).reshape(-1)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_linear_x3_frag_is_linear_x3(lib, m, k, n):
+    """The same MFMA operands in the same order: bit-identical to the LDS-staged kernel, at the DiT's
+    shapes and ragged ones (rows and columns past a tile)."""
+    if k % 64:
+        pytest.skip("the split GEMMs take K % 64 == 0")
+    rng = np.random.default_rng(m + 3 * k + n)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    got = linear_frag(lib, split_frag(lib, w), x, n, b)
+    np.testing.assert_array_equal(got, linear(lib, split(lib, w), x, n, b))
+    assert rel_err(got, ref.linear(x, w, b)) < TOL
+
+
+def test_linear_x3_frag_epilogues(lib):
+    """GELU, the DiT's partial rotary and the gated in-place residual, bit-identical to cv3_linear_x3."""
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(31)
+    m, k, n = 1000, 1024, 3072
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    fr, pl = split_frag(lib, w), split(lib, w)
+    np.testing.assert_array_equal(linear_frag(lib, fr, x, n, b, _lib.epilogue("gelu_tanh")),
+                                  linear(lib, pl, x, n, b, _lib.epilogue("gelu_tanh")))
+    T = 500
+    ang = np.arange(T, dtype=np.float64)[:, None] * (1.0 / 10000 ** (np.arange(0, 64, 2) / 64))[None, :]
+    ang = np.repeat(ang, 2, axis=1).astype(np.float32)
+    cos, sin = to_device(np.cos(ang)), to_device(np.sin(ang))
+    rope = _lib.epilogue(rope=(cos.ptr, sin.ptr, T, 1024, 64, 2048))
+    np.testing.assert_array_equal(linear_frag(lib, fr, x, n, b, rope), linear(lib, pl, x, n, b, rope))
+    h0 = rng.normal(size=(m, n)).astype(np.float32)
+    gate = to_device(rng.normal(size=n).astype(np.float32))
+    outs = []
+    for fn, wts in ((linear_frag, fr), (linear, pl)):
+        y = to_device(h0)
+        e = _lib.epilogue(residual=y.ptr, ld_res=n, gate=gate.ptr, gate_stride=0, rows_per_gate=1)
+        outs.append(fn(lib, wts, x, n, b, e, out=y))
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def linear_q8_frag(lib, q, s, kp, block, x, n, bias=None, epi=None):
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    dq = to_device(np.ascontiguousarray(q))
+    qf = empty((-(-n // 32) * 32 * k,), np.int8)
+    _lib.call("pack_q8_frag", dq.ptr, n, k, kp, qf.ptr, None)
+    ds = to_device(np.ascontiguousarray(s))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = empty((m, n))
+    _lib.call("linear_q8_x3_frag", dx.ptr, m, k, k, qf.ptr, ds.ptr, _lib.F16 if s.dtype == np.float16 else _lib.F32,
+              kp, block, n, db.ptr if db is not None else None, y.ptr, n,
+              ctypes.byref(epi) if epi is not None else None, None)
+    return y.numpy(), qf.numpy()
+
+
+@pytest.mark.parametrize("m,k,n,block,sdt", Q8_CASES)
+def test_linear_q8_x3_frag_is_linear_q8_x3(lib, m, k, n, block, sdt):
+    """Codes in fragment order (rows past n zero) and the q8 product from them: bit-identical to the
+    LDS-staged kernel, block-64 float16 and per-channel float32 scales, ragged shapes."""
+    rng = np.random.default_rng(3 * m + k + n + block)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, kp = refq.quantize_q8(w, block, sdt)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    got, qf = linear_q8_frag(lib, q, s, kp, block, x, n, b)
+    nb = -(-n // 32)
+    qp = np.zeros((nb * 32, k), np.int8)
+    qp[:n] = q[:, :k]
+    want_qf = qp.reshape(nb, 32, k // 16, 2, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+    np.testing.assert_array_equal(qf, want_qf)
+    np.testing.assert_array_equal(got, linear_q8_x3(lib, q, s, kp, block, x, n, b))
