@@ -584,6 +584,111 @@ __global__ __launch_bounds__(256) void k_conv_cl_x3(ConvCL p, const uint16_t* wp
   cl_epilogue(p, acc, m0, n0, wm, wn, r32, h);
 }
 
+// k_conv_cl_x3 with the weight planes packed once in MFMA fragment order (cv3_split_x3_frag over
+// the packed (cout, k * cin) rows): frag[p][nb][t][l] is plane p of w[32 nb + l % 32][16 t + 8 (l / 32)
+// .. + 7], the B operand of lane l for 16-k step t of output-channel block nb, so each wave loads
+// its B fragments straight into registers two stages ahead and only x goes through LDS.  Every
+// MFMA sees the operands k_conv_cl_x3 gives it, in the same order: the results are the same bits.
+__global__ __launch_bounds__(256) void k_conv_cl_x3f(ConvCL p, const uint4* frag, int64_t per_plane, int tiles_m) {
+  __shared__ uint4 sA[2][3][64 * 4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = gridDim.x, L = blockIdx.x;
+  const int t = (T % 8 == 0) ? (L % 8) * (T / 8) + L / 8 : L;
+  const int m0 = (t % tiles_m) * 64, n0 = (t / tiles_m) * 64;
+  const int K = p.k * p.cin, cpt = p.cin / 32, tin_up = p.t_in * p.up;
+  const int lr = tid >> 2, lc = tid & 3, tr = m0 + lr;
+  const int wslot = cl_xslot(lr, lc);
+  const int wm = (w >> 1) * 32, wn = (w & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32, asw = (ar >> 2) & 3;
+  const int S = K / 32 / p.ksplit, sb = blockIdx.z * S;
+  // this wave's 32-channel block; one past the last (cout % 64 in 1 .. 32) reads the last one
+  // instead, its channels are dropped by cl_epilogue
+  const int nblk = min((n0 + wn) >> 5, (p.cout - 1) >> 5);
+  const uint4* fb = frag + (int64_t)nblk * (K / 16) * 64 + lane;
+  f32x16 big = {0.f}, small = {0.f};
+  struct XA {
+    float4 a0, a1;  // this thread's time row, channels 8 lc .. + 7 of the stage
+  };
+  struct BF {
+    uint4 v[2][3];  // [16-k step of the stage][plane]
+  };
+
+  auto load = [&](XA& x, int sg) {
+    const int j = sg / cpt, c0 = (sg - j * cpt) * 32;
+    const int u = tr + j * p.dil - p.pad_l;
+    const bool ok = tr < p.t_out && u >= 0 && u < tin_up;
+    const int q = ok ? (p.up == 1 ? u : (int)((unsigned)u / (unsigned)p.up)) : 0;
+    const float* a = ok ? p.x + (int64_t)q * p.ldx + c0 + lc * 8 : g_conv_zero_row + lc * 8;
+    x.a0 = *reinterpret_cast<const float4*>(a);
+    x.a1 = *reinterpret_cast<const float4*>(a + 4);
+  };
+  auto loadb = [&](BF& b, int sg) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl) b.v[ks][pl] = fb[pl * per_plane + (int64_t)(2 * sg + ks) * 64];
+  };
+  auto store = [&](int buf, const XA& x) {
+    uint4 hi, mid, lo;
+    split_x3(x.a0, x.a1, hi, mid, lo);
+    sA[buf][0][wslot] = hi;
+    sA[buf][1][wslot] = mid;
+    sA[buf][2][wslot] = lo;
+  };
+  auto mma = [&](int buf, const BF& b) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ asw);
+      const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, sA[buf][0][sa]);
+      const bf16x8_t am = __builtin_bit_cast(bf16x8_t, sA[buf][1][sa]);
+      const bf16x8_t al = __builtin_bit_cast(bf16x8_t, sA[buf][2][sa]);
+      const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, b.v[ks][0]);
+      const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, b.v[ks][1]);
+      const bf16x8_t bl = __builtin_bit_cast(bf16x8_t, b.v[ks][2]);
+      big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, big, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, small, 0, 0, 0);
+      small = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, small, 0, 0, 0);
+    }
+  };
+
+  // S even and >= 2: x ping-pongs through registers x / y and LDS buffers 0 / 1, the B fragments
+  // of the even and odd stages through b0 / b1, each refilled right after its use
+  XA x, y;
+  BF b0, b1;
+  load(x, sb);
+  load(y, sb + 1);
+  loadb(b0, sb);
+  loadb(b1, sb + 1);
+  store(0, x);
+  __syncthreads();
+  for (int s = 0; s + 2 < S; s += 2) {
+    load(x, sb + s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0, b0);
+    loadb(b0, sb + s + 2);
+    store(1, y);
+    __syncthreads();
+    load(y, sb + s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, b1);
+    loadb(b1, sb + s + 3);
+    store(0, x);
+    __syncthreads();
+  }
+  mma(0, b0);
+  store(1, y);
+  __syncthreads();
+  mma(1, b1);
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = big[i] + small[i];
+  cl_epilogue(p, acc, m0, n0, wm, wn, r32, h);
+}
+
 // Split-K epilogue of k_conv_cl_dma: slices added in order z = 0, 1, ...
 __global__ void k_conv_cl_reduce(ConvCL p) {
   const int64_t n = (int64_t)p.t_out * p.cout;
@@ -629,6 +734,7 @@ namespace cv3 {
 int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* w, int64_t cout, int64_t k,
             int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
             hipStream_t st);
+int64_t x3_frag_plane(int64_t n, int64_t k);  // gemm.hip: one plane of a fragment-ordered weight
 }
 
 extern "C" {
@@ -755,7 +861,8 @@ int cv3_conv1d_packed(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, c
 // The channels-last packed conv: float32 weights (k_conv_cl_dma) or, with `planes`, their three
 // bfloat16 planes [3][cout][k * cin] (k_conv_cl_x3).
 static int conv_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const float* w_packed,
-                          const uint16_t* planes, int64_t cout, int64_t k, const float* bias, int64_t dilation,
+                          const uint16_t* planes, bool frag, int64_t cout, int64_t k, const float* bias,
+                          int64_t dilation,
                           int64_t pad_l, int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act,
                           float act_param, const float* snake_alpha, float snake_eps, const float* residual,
                           int64_t r_ts, int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
@@ -808,7 +915,11 @@ static int conv_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx
   p.ksplit = (int)ksplit;
   const int64_t tiles_m = ceil_div(t_out, 64), tiles_n = ceil_div(cout, 64);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "conv too large");
-  if (planes)
+  if (planes && frag)
+    hipLaunchKernelGGL(k_conv_cl_x3f, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
+                       stream_of(s), p, reinterpret_cast<const uint4*>(planes), x3_frag_plane(cout, k * cin) / 8,
+                       (int)tiles_m);
+  else if (planes)
     hipLaunchKernelGGL(k_conv_cl_x3, dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)ksplit), dim3(256), 0,
                        stream_of(s), p, planes, cout * k * cin, (int)tiles_m);
   else
@@ -830,7 +941,8 @@ int cv3_conv1d_cl_packed(const float* x, int64_t t_in, int64_t cin, int64_t ldx,
                          const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts, int64_t r_cs,
                          int64_t ksplit, float* workspace, int64_t workspace_floats, cv3_stream_t s) {
   CV3_ALIVE();
-  return conv_cl_packed(x, t_in, cin, ldx, w_packed, nullptr, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts, y_cs,
+  return conv_cl_packed(x, t_in, cin, ldx, w_packed, nullptr, false, cout, k, bias, dilation, pad_l, pad_r, up, y,
+                        y_ts, y_cs,
                         act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
                         workspace_floats, s);
 }
@@ -843,7 +955,20 @@ int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t l
                             cv3_stream_t s) {
   CV3_ALIVE();
   CV3_REQUIRE(w_planes, CV3_EINVAL, "null weight planes");
-  return conv_cl_packed(x, t_in, cin, ldx, nullptr, w_planes, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts,
+  return conv_cl_packed(x, t_in, cin, ldx, nullptr, w_planes, false, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts,
+                        y_cs, act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
+                        workspace_floats, s);
+}
+
+int cv3_conv1d_cl_packed_x3f(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const uint16_t* w_frag,
+                             int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l,
+                             int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act,
+                             float act_param, const float* snake_alpha, float snake_eps, const float* residual,
+                             int64_t r_ts, int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
+                             cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(w_frag, CV3_EINVAL, "null weight fragments");
+  return conv_cl_packed(x, t_in, cin, ldx, nullptr, w_frag, true, cout, k, bias, dilation, pad_l, pad_r, up, y, y_ts,
                         y_cs, act, act_param, snake_alpha, snake_eps, residual, r_ts, r_cs, ksplit, workspace,
                         workspace_floats, s);
 }

@@ -729,7 +729,10 @@ __global__ __launch_bounds__(256) void k_gemm_x3f(GemmParams p, const uint4* fra
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
   const int ar = wm + r32, asw = (ar >> 2) & 3;
   const int64_t S = p.k / XBK, T16 = p.k / 16;
-  const uint4* fb = frag + ((n0 + wn) >> 5) * T16 * 64 + lane;  // this wave's 32-column block
+  // this wave's 32-column block; a block past the last (n % 64 in 1 .. 32) reads the last one
+  // instead, its columns are dropped by store_tile
+  const int64_t nblk = min((n0 + wn) >> 5, (p.n - 1) >> 5);
+  const uint4* fb = frag + nblk * T16 * 64 + lane;
   f32x16 big = {0.f}, small = {0.f};
   struct XA {
     float4 a0, a1;
@@ -963,7 +966,8 @@ __global__ __launch_bounds__(256) void k_gemm_x3qf(GemmParams p, const uint2* qf
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
   const int ar = wm + r32, asw = (ar >> 2) & 3;
   const int64_t S = p.k / XBK, spb = p.block / XBK, T16 = p.k / 16;
-  const uint2* fb = qfrag + ((n0 + wn) >> 5) * T16 * 64 + lane;  // this wave's 32-column block
+  const int64_t nblk = min((n0 + wn) >> 5, (p.n - 1) >> 5);  // clamped as in k_gemm_x3f
+  const uint2* fb = qfrag + nblk * T16 * 64 + lane;
   // the lane's output column's scales
   const int64_t srow = min(n0 + wn + r32, p.n - 1) * p.nb;
   auto scale = [&](int64_t b) {

@@ -70,9 +70,9 @@ class DeviceHiFT:
 
     def __init__(self, weights, prefix: str = "hift.", planes: bool = True):
         """``planes``: the channels-last convs run on the bfloat16 matrix cores with their
-        weights held as three bfloat16 planes (cv3_conv1d_cl_packed_x3: the same float32
-        conv, errors against float64 below the float32 matrix cores'); False keeps them on
-        the float32 matrix cores."""
+        weights held as three bfloat16 planes in the matrix cores' fragment order
+        (cv3_conv1d_cl_packed_x3f: the same float32 conv, errors against float64 below the
+        float32 matrix cores'); False keeps them on the float32 matrix cores."""
         _lib.init()
         m = weights.meta.get("hift", {})
         self.rates = list(m.get("upsample_rates", [8, 5, 3]))
@@ -94,7 +94,7 @@ class DeviceHiFT:
         self.up_total = int(np.prod(self.rates))
         self.w = {}
         self.wp = {}   # conv weights repacked (out, k, in) for the channels-last implicit GEMM
-        self.wpx = {}  # ... and as three bfloat16 planes [3][out][k * in] (planes=True)
+        self.wpx = {}  # ... and as three bfloat16 planes in fragment order (planes=True)
         self.shape = {}
         for name in weights.keys():
             if not name.startswith(prefix) or "f0_predictor.classifier" in name or "m_source" in name:
@@ -107,8 +107,10 @@ class DeviceHiFT:
                 self.wp[key] = to_device(np.ascontiguousarray(arr.transpose(0, 2, 1)))
                 cout, kin = arr.shape[0], arr.shape[1] * arr.shape[2]
                 if planes and (kin // 32) % 2 == 0:
-                    pl = DeviceArray((3, cout, kin), np.uint16)
-                    _lib.call("split_x3", self.wp[key].ptr, cout, kin, kin, pl.ptr, kin, None)
+                    ne = ctypes.c_int64()
+                    _lib.call("x3_frag_elems", cout, kin, ctypes.byref(ne))
+                    pl = DeviceArray((ne.value,), np.uint16)
+                    _lib.call("split_x3_frag", self.wp[key].ptr, cout, kin, kin, pl.ptr, None)
                     self.wpx[key] = pl
         # the F0 predictor's condnet convs sit with the stack's weights above; its
         # classifier and the source merge (hift.py:56-72,108-110) are float32 vectors
@@ -172,10 +174,10 @@ class DeviceHiFT:
         res = residual.ptr if residual is not None else None
         r_ts = residual.shape[1] if residual is not None else 0
         wkey = key + ".weight"
-        if wkey in self.wpx:  # the bfloat16-plane implicit GEMM
+        if wkey in self.wpx:  # the bfloat16-plane implicit GEMM, weights in fragment order
             ks = split_k(n, cout, k * cin // 32, even=True)
             ws = self._new((ks * cout * n,)) if ks > 1 else None
-            _lib.call("conv1d_cl_packed_x3", x.ptr, t_in, cin, cin, self.wpx[wkey].ptr, cout, k,
+            _lib.call("conv1d_cl_packed_x3f", x.ptr, t_in, cin, cin, self.wpx[wkey].ptr, cout, k,
                       self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_ts,
                       y_cs, ACT[act], float(act_param), alpha, 1e-9, res, r_ts, 1, ks, ws.ptr if ws else None,
                       ws.size if ws else 0, None)

@@ -270,6 +270,16 @@ int cv3_conv1d_cl_packed_x3(const float* x, int64_t t_in, int64_t cin, int64_t l
                             const float* snake_alpha, float snake_eps, const float* residual, int64_t r_ts,
                             int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
                             cv3_stream_t s);
+/* cv3_conv1d_cl_packed_x3 with the weight planes in MFMA fragment order: w_frag is
+ * cv3_split_x3_frag over the packed (cout, k * cin) rows (cv3_x3_frag_elems(cout, k * cin) elements),
+ * so each wave loads its weight operands straight into registers; the same results, bit for bit.
+ * Same requirements, and k * cin % 64 == 0 for the packing. */
+int cv3_conv1d_cl_packed_x3f(const float* x, int64_t t_in, int64_t cin, int64_t ldx, const uint16_t* w_frag,
+                             int64_t cout, int64_t k, const float* bias, int64_t dilation, int64_t pad_l,
+                             int64_t pad_r, int64_t up, float* y, int64_t y_ts, int64_t y_cs, int act,
+                             float act_param, const float* snake_alpha, float snake_eps, const float* residual,
+                             int64_t r_ts, int64_t r_cs, int64_t ksplit, float* workspace, int64_t workspace_floats,
+                             cv3_stream_t s);
 /* The DiT's grouped causal conv_pos (dit.py:99-112, ops.conv1d with groups) on channels-last activations:
  * x [batch, t, ldx] (cin channels), y [batch, t, ldy] (cout channels),
  * y[b, s, co] = epi(bias[co] + sum_{j<k, c<cin/groups} W[co, c, j] x[b, s + j - pad_l, g*cin/groups + c]),

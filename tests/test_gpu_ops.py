@@ -4,6 +4,8 @@ Tolerances: int8 codes and scales bit-exact; fp32 outputs within 1e-5 of the
 oracle in the reference's max-norm relative error (rel_err).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -427,9 +429,10 @@ CL_CASES = [
 @pytest.mark.parametrize("cin,cout,k,dil,up,T,pad,epi,ks,cf", CL_CASES)
 def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf, x3):
     """Channels-last stride-1 conv through the DMA implicit GEMM (and, ``x3``, its
-    bfloat16-plane form, cv3_conv1d_cl_packed_x3, where a K slice has an even number of
-    32-channel stages), against the oracle's upsample + conv1d + epilogue on (channel, time)
-    data."""
+    bfloat16-plane forms, cv3_conv1d_cl_packed_x3 and, with the planes in fragment order,
+    cv3_conv1d_cl_packed_x3f, where a K slice has an even number of 32-channel stages),
+    against the oracle's upsample + conv1d + epilogue on (channel, time) data; the two plane
+    forms give the same bits."""
     from cv3amd import _lib
     from cv3amd.device import DeviceArray, to_device
     if x3 and (k * cin // 32 // ks) % 2:
@@ -453,20 +456,30 @@ def test_conv1d_cl_packed(dev, rng, cin, cout, k, dil, up, T, pad, epi, ks, cf, 
     else:
         yd, y_ts, y_cs = (to_device(res_cl) if epi == "residual" else DeviceArray((t_out, cout))), cout, 1
     ws = DeviceArray((ks * cout * t_out,)) if ks > 1 else None
-    wptr, fn = wd.ptr, "conv1d_cl_packed"
+    forms = [(wd.ptr, "conv1d_cl_packed")]
     if x3:
         planes = DeviceArray((3, cout, k * cin), np.uint16)
         _lib.call("split_x3", wd.ptr, cout, k * cin, k * cin, planes.ptr, k * cin, None)
-        wptr, fn = planes.ptr, "conv1d_cl_packed_x3"
-    for _ in range(2):  # the second call sees the first call's partials in the workspace
-        if epi == "residual":
-            _lib.call("copy_h2d", yd.ptr, res_cl.ctypes.data, res_cl.nbytes, None)
-        _lib.call(fn, xd.ptr, T, cin, cin, wptr, cout, k, bd.ptr, dil, pad[0], pad[1], up,
-                  yd.ptr, y_ts, y_cs, _lib.ACT["leaky" if epi == "leaky" else "none"], 0.1 if epi == "leaky" else 0.0,
-                  ad.ptr if epi == "snake" else None, 1e-9, yd.ptr if epi == "residual" else None, cout, 1,
-                  ks, ws.ptr if ws else None, ws.size if ws else 0, None)
-        got = yd.numpy() if cf else yd.numpy().T
-        assert rel_err(got, want) < TOL
+        ne = ctypes.c_int64()
+        _lib.call("x3_frag_elems", cout, k * cin, ctypes.byref(ne))
+        frag = DeviceArray((ne.value,), np.uint16)
+        _lib.call("split_x3_frag", wd.ptr, cout, k * cin, k * cin, frag.ptr, None)
+        forms = [(planes.ptr, "conv1d_cl_packed_x3"), (frag.ptr, "conv1d_cl_packed_x3f")]
+    outs = []
+    for wptr, fn in forms:
+        for _ in range(2):  # the second call sees the first call's partials in the workspace
+            if epi == "residual":
+                _lib.call("copy_h2d", yd.ptr, res_cl.ctypes.data, res_cl.nbytes, None)
+            _lib.call(fn, xd.ptr, T, cin, cin, wptr, cout, k, bd.ptr, dil, pad[0], pad[1], up,
+                      yd.ptr, y_ts, y_cs, _lib.ACT["leaky" if epi == "leaky" else "none"],
+                      0.1 if epi == "leaky" else 0.0, ad.ptr if epi == "snake" else None, 1e-9,
+                      yd.ptr if epi == "residual" else None, cout, 1, ks, ws.ptr if ws else None,
+                      ws.size if ws else 0, None)
+            got = yd.numpy() if cf else yd.numpy().T
+            assert rel_err(got, want) < TOL, fn
+        outs.append(got)
+    if x3:
+        assert np.array_equal(outs[0], outs[1])
 
 
 def test_empty_inputs_match_the_reference(dev, rng):
