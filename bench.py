@@ -629,7 +629,8 @@ def bench_hift(args, tensors, meta):
     mel, source = hift_inputs(T)
     mel_d, src_d = to_device(mel), to_device(source)
     out = {}
-    for label, chunk in (("whole", None), ("chunked_1s", 50)):
+    for label, chunk, trim in (("whole", None, True), ("chunked_1s", 50, True), ("chunked_1s_context64", 50, False)):
+        d.trim_context = trim   # False: every window carries all 64 frames of history
         d.decode(mel_d, src_d, chunk=chunk, graph=args.graph)
         synchronize()
         tm = Timer()
@@ -639,6 +640,8 @@ def bench_hift(args, tensors, meta):
         ms = tm.stop() / args.hift_runs
         out[label] = ms
         log(f"vocoder ({label}): {ms:.2f} ms per 10 s of audio, RTF {ms / 1e3 / AUDIO_SECONDS:.2e}")
+    d.trim_context = True
+    out["window_history"] = d.receptive
     # mel -> waveform with the F0 predictor and the excitation on the device as well
     for label, chunk in (("inference_whole", None), ("inference_chunked_1s", 50)):
         d.inference(mel_d, chunk=chunk, graph=args.graph)
@@ -896,10 +899,14 @@ def main():
         line["vocoder"] = {
             "workload": "causal HiFTNet, mel [1, 80, 500] (10 s), base 512, ups x8/x5/x3, iSTFT 16/4, fp32; "
                         "ms_whole / ms_chunked_1s decode a precomputed source, ms_inference_* run mel -> waveform "
-                        "(F0 net, NSF excitation and decode) on the device",
+                        "(F0 net, NSF excitation and decode) on the device; 1 s windows with 64 frames of context, "
+                        "each window computed from window_history_frames of it (the stack's receptive field: "
+                        "the same samples), ms_chunked_1s_context64 from all 64",
             "ms_whole": round(voc["whole"], 3), "rtf_whole": round(voc["whole"] / 1e3 / AUDIO_SECONDS, 6),
             "ms_chunked_1s": round(voc["chunked_1s"], 3),
             "rtf_chunked_1s": round(voc["chunked_1s"] / 1e3 / AUDIO_SECONDS, 6),
+            "window_history_frames": voc["window_history"],
+            "ms_chunked_1s_context64": round(voc["chunked_1s_context64"], 3),
             "ms_inference_whole": round(voc["inference_whole"], 3),
             "rtf_inference_whole": round(voc["inference_whole"] / 1e3 / AUDIO_SECONDS, 6),
             "ms_inference_chunked_1s": round(voc["inference_chunked_1s"], 3),

@@ -36,12 +36,44 @@ from .device import DeviceArray, Event, Graph, Stream, to_device, wait_event
 
 ACT = _lib.ACT
 F4 = 4
-WINDOW_STREAMS = 4   # vocoder windows replayed side by side (one stream each, default priority)
+WINDOW_STREAMS = 16  # vocoder windows replayed side by side (one stream each, default priority); a
+                     # 10 s decode in 1 s windows: 4 streams 10.1 ms, 10 or 16 streams 7.4 ms
 
 
 def causal_pad(kernel_size: int, dilation: int = 1) -> int:
     """int((k d - d) / 2) * 2 + (k + 1) % 2 (hift.py:14-16)."""
     return int((kernel_size * dilation - dilation) / 2) * 2 + (kernel_size + 1) % 2
+
+
+def receptive_frames(rates, up_k, rb_k, rb_d, src_k, src_d, src_kd, post_k) -> int:
+    """Mel frames of history that the spectral stack's output at a frame depends on: the first
+    output row of a frame far from the start is followed back through conv_post, the resblocks
+    (each step reads (k - 1) d + (k - 1) rows back), the upsampling convs (nearest upsample,
+    pad k - 1), the reflect-padded row of the last stage, and the strided source convs to the
+    first mel frame and the first source-STFT frame it reads (hift.py:131-168).  conv_pre and
+    the source STFT look only forward or at their own frame.  ``src_kd`` lists the source
+    convs' kernel sizes; ``up_k`` the upsampling convs'."""
+    up = int(np.prod(rates))
+    m0 = 1 << 20                          # far from the start: no row is clamped at zero
+    a = 1 + m0 * up - causal_pad(post_k)  # the frame's first output row, then conv_post's reach
+
+    def resblock(k, dils, a):
+        for d in reversed(dils):
+            a -= causal_pad(k, d) + causal_pad(k, 1)
+        return a
+
+    downs = [1] + list(rates[::-1][:-1])
+    down_cum = list(np.cumprod(downs))[::-1]
+    first_src = a
+    for i in reversed(range(len(rates))):
+        a_xs = min(resblock(k, d, a) for k, d in zip(rb_k, rb_d))
+        u = int(down_cum[i])
+        a_si = resblock(src_k[i], src_d[i], a_xs)
+        first_src = min(first_src, a_si * u - (causal_pad(src_kd[i]) if u == 1 else u - 1))
+        a_c = a_xs - 1 if i == len(rates) - 1 else a_xs  # the last stage's rows sit one down
+        a = (a_c - (up_k[i] - 1)) // rates[i]
+    frames = max(m0 - a, m0 - first_src // up)
+    return int(frames)
 
 
 def split_k(t_out: int, cout: int, stages: int, even: bool = False) -> int:
@@ -68,11 +100,14 @@ def hann_window(n: int) -> np.ndarray:
 class DeviceHiFT:
     """HiFTNet weights resident in HBM; ``weights`` has ``get(name)`` and ``meta``."""
 
-    def __init__(self, weights, prefix: str = "hift.", planes: bool = True):
+    def __init__(self, weights, prefix: str = "hift.", planes: bool = True, trim_context: bool = True):
         """``planes``: the channels-last convs run on the bfloat16 matrix cores with their
         weights held as three bfloat16 planes in the matrix cores' fragment order
         (cv3_conv1d_cl_packed_x3f: the same float32 conv, errors against float64 below the
-        float32 matrix cores'); False keeps them on the float32 matrix cores."""
+        float32 matrix cores'); False keeps them on the float32 matrix cores.
+        ``trim_context``: a window of the windowed decode carries min(context, receptive field)
+        frames of history rather than all ``context`` frames: the frames beyond the stack's
+        receptive field cannot reach a kept sample, so the output is the same."""
         _lib.init()
         m = weights.meta.get("hift", {})
         self.rates = list(m.get("upsample_rates", [8, 5, 3]))
@@ -92,6 +127,7 @@ class DeviceHiFT:
         self.noise_seed = int(m.get("noise_seed", 0))
         self.nk = len(self.rb_k)
         self.up_total = int(np.prod(self.rates))
+        self.trim_context = trim_context
         self.w = {}
         self.wp = {}   # conv weights repacked (out, k, in) for the channels-last implicit GEMM
         self.wpx = {}  # ... and as three bfloat16 planes in fragment order (planes=True)
@@ -112,6 +148,10 @@ class DeviceHiFT:
                     pl = DeviceArray((ne.value,), np.uint16)
                     _lib.call("split_x3_frag", self.wp[key].ptr, cout, kin, kin, pl.ptr, None)
                     self.wpx[key] = pl
+        self.receptive = receptive_frames(
+            self.rates, [self.shape[f"ups.{i}.weight"][2] for i in range(len(self.rates))], self.rb_k, self.rb_d,
+            self.src_k, self.src_d, [self.shape[f"source_downs.{i}.weight"][2] for i in range(len(self.rates))],
+            self.shape["conv_post.weight"][2])
         # the F0 predictor's condnet convs sit with the stack's weights above; its
         # classifier and the source merge (hift.py:56-72,108-110) are float32 vectors
         self.f0_depth = 0
@@ -336,7 +376,11 @@ class DeviceHiFT:
     def spectral_chunked(self, mel: DeviceArray, s_stft: DeviceArray, chunk: int, context: int,
                          graph: bool = True) -> DeviceArray:
         """Windows of ``chunk`` frames with ``context`` frames of history and conv_pre's
-        lookahead, cut back to the window's own samples (hift.py:170-194)."""
+        lookahead, cut back to the window's own samples (hift.py:170-194).  With
+        ``trim_context`` the history stops at the stack's receptive field (``receptive``
+        frames), which reproduces the full-utterance result as the whole context does."""
+        if self.trim_context:
+            context = min(context, self.receptive)
         up = self.up_total
         t = mel.shape[1]
         look = causal_pad(self.shape["conv_pre.weight"][2])

@@ -106,3 +106,67 @@ def test_widened_q4_codes_dequantise_like_the_packed_ones():
         mine = codes.astype(np.float32) * np.repeat(s.astype(np.float32), 32, axis=1)
         want = oq.QTensor("q4", q, s, (rows, k), 32).dequant()
         assert np.array_equal(mine[:, :k], want)
+
+
+def _vocoder_receptive_case():
+    import oracle.quant
+    from oracle.hift import HiFTGenerator
+    from cv3amd import synth
+    from cv3amd.hift import receptive_frames
+    from cv3amd.weights import WeightStore
+    m = synth.hift_meta()["hift"]
+    t = synth.hift_tensors(base=64, f0_ch=64)
+    h = HiFTGenerator(WeightStore(t, synth.hift_meta(), oracle.quant.QTensor), "hift.")
+    rates = m["upsample_rates"]
+    R = receptive_frames(rates, m["upsample_kernel_sizes"], m["resblock_kernel_sizes"], m["resblock_dilation_sizes"],
+                         m["source_resblock_kernel_sizes"], m["source_resblock_dilation_sizes"],
+                         [t[f"hift.source_downs.{i}.weight"].shape[2] for i in range(len(rates))],
+                         t["hift.conv_post.weight"].shape[2])
+    return h, R
+
+
+def test_vocoder_receptive_field_bounds_what_a_frame_reads():
+    """The windowed vocoder's history is cut to the stack's receptive field (receptive_frames):
+    on the oracle's stack, a large change to every mel frame and source-STFT frame before that
+    field leaves the samples of the frame after it unchanged, bit for bit; the field is not far
+    too large (the mel 19 frames back and the source STFT 28 frames back still reach the frame,
+    so a bound that dropped the source branch or a resblock fails)."""
+    h, R = _vocoder_receptive_case()
+    assert R == 29   # for this geometry: the source branch of the first stage reaches furthest
+    rng = np.random.default_rng(1)
+    T, m0, up = 80, 50, 120
+    mel = (rng.standard_normal((80, T), dtype=np.float32) * 2 - 5).astype(np.float32)
+    src = np.tanh(rng.standard_normal(480 * T, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    s = h.source_stft(src)
+    base = h.spectral(mel, s)
+    r0 = 1 + m0 * up               # the frame's first output row
+
+    def changed(mel2, s2):
+        return np.abs(h.spectral(mel2, s2)[:, r0:] - base[:, r0:]).max() > 0
+
+    m2 = mel.copy()
+    m2[:, :m0 - R] += 1e5
+    s2 = s.copy()
+    s2[:, :(m0 - R) * up] += 1e5
+    assert not changed(m2, s)
+    assert not changed(mel, s2)
+    m3 = mel.copy()
+    m3[:, m0 - 19] += 1e5
+    assert changed(m3, s)
+    s3 = s.copy()
+    s3[:, (m0 - 28) * up:(m0 - 27) * up] += 1e5
+    assert changed(mel, s3)
+
+
+def test_vocoder_windows_with_receptive_history_equal_the_full_context():
+    """The reference's windowed decode (hift.py:170-194) with the receptive field as its history
+    gives the samples it gives with 64 frames, and the full-utterance samples."""
+    h, R = _vocoder_receptive_case()
+    rng = np.random.default_rng(2)
+    T = 200
+    mel = (rng.standard_normal((80, T), dtype=np.float32) * 2 - 5).astype(np.float32)
+    src = np.tanh(rng.standard_normal(480 * T, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    s = h.source_stft(src)
+    full = h.spectral_chunked(mel, s, 50, 64)
+    assert np.array_equal(h.spectral_chunked(mel, s, 50, R), full)
+    assert np.array_equal(h.spectral(mel, s), full)
