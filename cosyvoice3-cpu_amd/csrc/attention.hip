@@ -424,18 +424,29 @@ __global__ __launch_bounds__(512) void k_flash64x(AttnParams p, int nq) {
         mfma6(kh, km, kl, qh[ks], qm[ks], ql[ks], sb[sub], ss[sub]);
       }
     }
-    // lane (c16, g): sc[s][i] = score of key k0i + 16 g + 4 i + s for query c16
+    // lane (c16, g): sc[s][i] = score of key k0i + 16 g + 4 i + s for query c16; a tile that every
+    // query of the wave sees whole skips the per-key selects
     float sc[4][4];
     float mx = -INFINITY;
+    if (__all(k0i >= klo && k0i + KT <= khi)) {
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
+      for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kj = k0i + 16 * g + 4 * i + sub;
-        const bool ok = kj >= klo && kj < khi;
-        sc[sub][i] = ok ? sb[sub][i] + ss[sub][i] : -INFINITY;
-        mx = fmaxf(mx, sc[sub][i]);
-      }
+        for (int i = 0; i < 4; ++i) {
+          sc[sub][i] = sb[sub][i] + ss[sub][i];
+          mx = fmaxf(mx, sc[sub][i]);
+        }
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kj = k0i + 16 * g + 4 * i + sub;
+          const bool ok = kj >= klo && kj < khi;
+          sc[sub][i] = ok ? sb[sub][i] + ss[sub][i] : -INFINITY;
+          mx = fmaxf(mx, sc[sub][i]);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
