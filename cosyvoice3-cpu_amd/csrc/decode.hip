@@ -1133,12 +1133,21 @@ __device__ __forceinline__ float wdot(const RowDot<64, CPL, SF16, Q4>& rd, const
 template <int CPC>
 struct XSlice {
   float v[CPC];
+  // the vector is staged chunk-transposed (xslot): float4 i of lane l's chunk at slot 64 i + l, so
+  // the 16 lanes of an LDS pass read 16 consecutive 16-byte slots (in lane order a 64- or 128-byte
+  // stride put them on 4 or 2 bank groups)
   __device__ __forceinline__ void load(const float* xs, int lane) {
 #pragma unroll
     for (int i = 0; i < CPC / 4; ++i)
-      reinterpret_cast<float4*>(v)[i] = reinterpret_cast<const float4*>(xs + lane * CPC)[i];
+      reinterpret_cast<float4*>(v)[i] = reinterpret_cast<const float4*>(xs)[64 * i + lane];
   }
 };
+// The float4 slot of elements 4 t .. 4 t + 3 in a one-chunk-per-lane vector of CPC-code chunks
+// staged for XSlice<CPC>.
+template <int CPC>
+__device__ __forceinline__ int xslot(int t) {
+  return (t % (CPC / 4)) * 64 + t / (CPC / 4);
+}
 template <bool SF16, bool Q4>
 __device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, Q4>& rd, const XSlice<kCodes<Q4>>& x) {
   const float acc = fmaf(Q4 ? dot32_q4(rd.wv[0], x.v) : dot16(rd.wv[0], x.v), rd.sc[0], 0.f);
@@ -1181,7 +1190,9 @@ struct NormStage {
     const int t = threadIdx.x;
     w = t < D / 4 ? reinterpret_cast<const float4*>(g)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red, int width) {
+  // stages the 64 CPC floats XSlice<CPC> reads (zero past D) in its chunk-transposed order
+  template <int CPC>
+  __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red) {
     const int t = threadIdx.x;
     const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
     float ss = 0.f;
@@ -1189,7 +1200,8 @@ struct NormStage {
     ss = fmaf(v.y, v.y, ss);
     ss = fmaf(v.z, v.z, ss);
     ss = fmaf(v.w, v.w, ss);
-    if (t < width / 4) reinterpret_cast<float4*>(xs)[t] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+    if (t < 16 * CPC)
+      reinterpret_cast<float4*>(xs)[xslot<CPC>(t)] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
     ss = wave_sum_swap(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
@@ -1349,7 +1361,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         if (!ll_get<2>(a.xb + ((par ^ 1) * kRX + w % kRX) * a.sx, D, E - 8u + 4u, xin, a.err)) return;
         if (!isE) waitA = wall_clock64() - t0;
       }
-      const float inv = ns1.stage(xin, D, a.eps, xs, red, kStage);
+      const float inv = ns1.stage<CPC>(xin, D, a.eps, xs, red);
       XSlice<CPC> xv;
       xv.load(xs, lane);
       float v0 = wdot(dA0, xv) * inv + bA0;
@@ -1502,7 +1514,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
           for (int cc = 0; cc < kPChunks; ++cc)
             if (cc < nact) att = fmaf(o[cc], f[cc], att);
         }
-        xs[i] = att;
+        xs[4 * xslot<CPC>(i >> 2) + (i & 3)] = att;
       }
       __syncthreads();
       XSlice<CPC> xv;
@@ -1601,7 +1613,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         }
         __syncthreads();
       } else {
-      const float inv = ns2.stage(xmid, D, a.eps, xs, red, kStage);
+      const float inv = ns2.stage<CPC>(xmid, D, a.eps, xs, red);
       XSlice<CPC> xv;
       xv.load(xs, lane);
 #pragma unroll
@@ -1649,7 +1661,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     }
     const int lp = (a.layers - 1) & 1;
     if (!ll_get<2>(a.xb + (lp * kRX + w % kRX) * a.sx, D, EH - 8u + 4u, xin, a.err)) return;
-    const float inv = ns.stage(xin, D, a.eps, xs, red, kStage);
+    const float inv = ns.stage<16>(xin, D, a.eps, xs, red);
     XSlice<16> xv;
     xv.load(xs, lane);
     float best = -INFINITY;
