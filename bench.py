@@ -219,7 +219,7 @@ def bench_decode(args, tensors, meta, label: str = "decode", decodes: int = None
     parts = [lm.bytes_per_token(PREFILL + s) for s in range(DECODE_TOKENS)]
     b = {key: sum(p[key] for p in parts) / DECODE_TOKENS for key in parts[0]}
     per_token = b["body"] + b["kv"] + b["norms_biases"] + b["head"]
-    held = per_token - b["body"] + b["body_held"]   # what the kernels stream (a widened q4 body: int8 codes)
+    held = per_token - b["body"] + b["body_held"]   # what the kernels stream (a q4 body held widened: int8 codes)
     if held != per_token:
         log(f"{label}: {tok_s:.1f} tok/s; checkpoint bytes {per_token / 1e6:.1f} MB/token -> "
             f"{per_token * tok_s / 1e9:.0f} GB/s algorithmic; held in HBM {held / 1e6:.1f} MB/token -> "
@@ -833,17 +833,16 @@ def main():
         tsk = tiny["step_kernel"] if tiny["persistent"] else tk
         line["decode_tiny"] = {
             "workload": f"the same decode with the tiny profile: Qwen2 body layers q4 (block 32, f16 scales; held "
-                        f"in HBM as int8 codes n - 8 with the same blocks and scales), head and speech embedding "
-                        f"q8, KV {PREFILL}->{PREFILL + DECODE_TOKENS}; bytes_per_token counts the checkpoint's "
-                        f"packed q4 body",
+                        f"in HBM as the checkpoint's packed nibbles), head and speech embedding q8, "
+                        f"KV {PREFILL}->{PREFILL + DECODE_TOKENS}",
             "decodes_timed": tiny["decodes"],
             "decode_step": "one kernel launch per token" if tiny["persistent"] else "five kernels per layer",
             "tok_s": round(tiny["tok_s"], 2), "ms_per_token": round(tiny["ms"] / DECODE_TOKENS, 5),
             "five_kernel_tok_s": round(tiny["five_kernel_tok_s"], 2),
             "bytes_per_token": tiny["bytes_per_token"],
             "hbm_roofline_frac": round(tiny["bytes_per_token"] * tiny["tok_s"] / HBM_PEAK, 4),
-            # what the kernels stream per token with the body held widened (int8 codes): the
-            # achieved-bandwidth figure, as opposed to the checkpoint-algorithmic one above
+            # what the kernels stream per token as the body is held (equal to bytes_per_token
+            # for packed nibbles; int8 codes with DeviceQwen2(widen_q4=True))
             "bytes_per_token_held": tiny["bytes_per_token_held"],
             "held_GBps": round(tiny["bytes_per_token_held"] * tiny["tok_s"] / 1e9, 1),
             "roofline": {"bound": "hbm", "achieved": round(tsk["achieved_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,

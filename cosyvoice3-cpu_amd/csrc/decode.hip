@@ -30,6 +30,7 @@
 // stored +8; quant.py:70-86,123-131), so the tiny profile's body layers stream
 // half the bytes through the same kernels.
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include "decode_common.hpp"
@@ -202,6 +203,51 @@ struct RowDot {
     return acc;
   }
 };
+
+// A q4 row of the one-launch step over 64 lanes, half a 32-code block per lane (16 codes, the
+// per-lane work of a q8 chunk): lane l holds bytes 8 (l % 2) .. + 7 of block l / 2, i.e. codes
+// 8 (l % 2) .. + 7 in their low nibbles and 16 + 8 (l % 2) .. + 7 in their high ones (each
+// stored + 8, quant.py:70-86,123-131), and its block's scale.  Halves past the row are clamped
+// to its last half and meet the zero padding of the staged vector.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <bool SF16>
+struct RowQ4H {
+  u32x2 wv;
+  float sc;
+  __device__ __forceinline__ void load(const QW& w, int64_t row, int lane, bool /*live*/) {
+    const int64_t row_bytes = w.kp / 2;
+    const u32x2* base = reinterpret_cast<const u32x2*>(w.q + row * row_bytes);
+    const int c = min(lane, (int)(row_bytes / 8) - 1);
+    wv = __builtin_nontemporal_load(base + c);
+    const int64_t si = row * (w.kp / w.block) + (int64_t)((unsigned)(c >> 1) / (unsigned)(w.block / 32));
+    if constexpr (SF16)
+      sc = __half2float(reinterpret_cast<const __half*>(w.scales)[si]);
+    else
+      sc = reinterpret_cast<const float*>(w.scales)[si];
+  }
+};
+// 16 x the dot of a half block with its 16 staged values: xs[0..7] meet the low nibbles,
+// xs[8..15] the high ones (widened as in dot32_q4).
+__device__ __forceinline__ float dot16_q4h(const u32x2 v, const float* __restrict__ xs) {
+  const uint32_t ws[2] = {v.x, v.y};
+  float a = 0.f;
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const float4 xl = *reinterpret_cast<const float4*>(xs + 4 * d);
+    const float4 xh = *reinterpret_cast<const float4*>(xs + 8 + 4 * d);
+    const uint32_t u = ws[d] ^ 0x88888888u;
+    const uint32_t lo = (u << 4) & 0xF0F0F0F0u, hi = u & 0xF0F0F0F0u;
+    a = fmaf(sext(lo, 0, 8), xl.x, a);
+    a = fmaf(sext(lo, 8, 8), xl.y, a);
+    a = fmaf(sext(lo, 16, 8), xl.z, a);
+    a = fmaf(sext(lo, 24, 8), xl.w, a);
+    a = fmaf(sext(hi, 0, 8), xh.x, a);
+    a = fmaf(sext(hi, 8, 8), xh.y, a);
+    a = fmaf(sext(hi, 16, 8), xh.z, a);
+    a = fmaf(sext(hi, 24, 8), xh.w, a);
+  }
+  return a;
+}
 
 // ---------------------------------------------------------------------------
 // Generic GEMV y = epi(W . vec): 256 threads, RPW = 64 / LPR rows per wave.
@@ -1148,6 +1194,20 @@ template <int CPC>
 __device__ __forceinline__ int xslot(int t) {
   return (t % (CPC / 4)) * 64 + t / (CPC / 4);
 }
+// The same for RowQ4H rows: float4 e (e < 8) of block b holds elements 4 e .. 4 e + 3 of the block,
+// which lane 2 b + (e / 2) % 2 reads as its float4 2 (e / 4) + e % 2.
+__device__ __forceinline__ int xslot_q4h(int t) {
+  const int b = t >> 3, e = t & 7;
+  return 64 * (2 * (e >> 2) + (e & 1)) + 2 * b + ((e >> 1) & 1);
+}
+template <bool Q4H>
+__device__ __forceinline__ int body_slot(int t) {
+  return Q4H ? xslot_q4h(t) : xslot<16>(t);
+}
+template <bool SF16>
+__device__ __forceinline__ float wdot(const RowQ4H<SF16>& rd, const XSlice<16>& x) {
+  return wave_sum_swap(fmaf(dot16_q4h(rd.wv, x.v), rd.sc, 0.f) * 0.0625f);
+}
 template <bool SF16, bool Q4>
 __device__ __forceinline__ float wdot(const RowDot<64, 1, SF16, Q4>& rd, const XSlice<kCodes<Q4>>& x) {
   const float acc = fmaf(Q4 ? dot32_q4(rd.wv[0], x.v) : dot16(rd.wv[0], x.v), rd.sc[0], 0.f);
@@ -1190,8 +1250,9 @@ struct NormStage {
     const int t = threadIdx.x;
     w = t < D / 4 ? reinterpret_cast<const float4*>(g)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  // stages the 64 CPC floats XSlice<CPC> reads (zero past D) in its chunk-transposed order
-  template <int CPC>
+  // stages the 1024 floats XSlice<16> reads (zero past D) in the order of its rows: xslot<16>
+  // (q8 chunks) or xslot_q4h (RowQ4H halves)
+  template <bool Q4H>
   __device__ __forceinline__ float stage(const float* x, int D, float eps, float* xs, float* red) {
     const int t = threadIdx.x;
     const float4 v = t < D / 4 ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1200,8 +1261,8 @@ struct NormStage {
     ss = fmaf(v.y, v.y, ss);
     ss = fmaf(v.z, v.z, ss);
     ss = fmaf(v.w, v.w, ss);
-    if (t < 16 * CPC)
-      reinterpret_cast<float4*>(xs)[xslot<CPC>(t)] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+    if (t < 256)
+      reinterpret_cast<float4*>(xs)[body_slot<Q4H>(t)] = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
     ss = wave_sum_swap(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
@@ -1247,7 +1308,7 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) { __builtin_amdg
 template <bool SF16, bool Q4, bool MX = false>
 __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   constexpr int CPC = kCodes<Q4>;       // codes per chunk of the body rows
-  constexpr int kStage = 64 * CPC;      // staged width of a one-chunk-per-lane body row
+  constexpr int kStage = 64 * 16;       // staged width of a body row: 16 codes per lane (q8 chunk, q4 half block)
   constexpr int kDownCPL = Q4 ? 3 : 5;  // chunks per lane of a down row
   constexpr int kXs = 64 * kDownCPL * CPC;
   __shared__ __align__(16) float xin[1024];   // x of the layer (raw), for A's norm and C's residual
@@ -1293,7 +1354,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   // while it polls.  (Loads complete in issue order, so a poll also waits for
   // every load issued before it; issuing the next phase's weights any earlier
   // holds up this phase's wait or its compute.)
-  RowDot<64, 1, SF16, Q4> dA0, dA1, dC0, dC1, dg[MX ? 1 : 3], du[MX ? 1 : 3];
+  using BodyRow = std::conditional_t<Q4, RowQ4H<SF16>, RowDot<64, 1, SF16, false>>;
+  BodyRow dA0, dA1, dC0, dC1, dg[MX ? 1 : 3], du[MX ? 1 : 3];
   // MX: wave b < ceil(perD / 8) loads and multiplies pairs 8b .. 8b + 7 of phase D: lane l the
   // gate (l % 16 < 8) or up row of pair 8b + l % 8, codes 16 (l / 16) .. +16 of each 64-code step
   float mxs = 0.f;
@@ -1361,8 +1423,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         if (!ll_get<2>(a.xb + ((par ^ 1) * kRX + w % kRX) * a.sx, D, E - 8u + 4u, xin, a.err)) return;
         if (!isE) waitA = wall_clock64() - t0;
       }
-      const float inv = ns1.stage<CPC>(xin, D, a.eps, xs, red);
-      XSlice<CPC> xv;
+      const float inv = ns1.stage<Q4>(xin, D, a.eps, xs, red);
+      XSlice<16> xv;
       xv.load(xs, lane);
       float v0 = wdot(dA0, xv) * inv + bA0;
       float v1 = wdot(dA1, xv) * inv + bA1;
@@ -1514,10 +1576,10 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
           for (int cc = 0; cc < kPChunks; ++cc)
             if (cc < nact) att = fmaf(o[cc], f[cc], att);
         }
-        xs[4 * xslot<CPC>(i >> 2) + (i & 3)] = att;
+        xs[4 * body_slot<Q4>(i >> 2) + (i & 3)] = att;
       }
       __syncthreads();
-      XSlice<CPC> xv;
+      XSlice<16> xv;
       xv.load(xs, lane);
       const float va = wdot(dC0, xv), vb2 = wdot(dC1, xv);
       if (lane < kRM) {  // lane i writes replica i
@@ -1613,8 +1675,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         }
         __syncthreads();
       } else {
-      const float inv = ns2.stage<CPC>(xmid, D, a.eps, xs, red);
-      XSlice<CPC> xv;
+      const float inv = ns2.stage<Q4>(xmid, D, a.eps, xs, red);
+      XSlice<16> xv;
       xv.load(xs, lane);
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
@@ -1661,7 +1723,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     }
     const int lp = (a.layers - 1) & 1;
     if (!ll_get<2>(a.xb + (lp * kRX + w % kRX) * a.sx, D, EH - 8u + 4u, xin, a.err)) return;
-    const float inv = ns.stage<16>(xin, D, a.eps, xs, red);
+    const float inv = ns.stage<false>(xin, D, a.eps, xs, red);
     XSlice<16> xv;
     xv.load(xs, lane);
     float best = -INFINITY;

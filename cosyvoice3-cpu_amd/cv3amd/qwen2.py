@@ -153,10 +153,11 @@ class _Stacked:
 class DeviceQwen2:
     """Qwen2 body + CosyVoice3 LM head resident on the device, decoding greedily."""
 
-    def __init__(self, weights, prefix: str = "llm.", cap: int = 1024, widen_q4: bool = True):
-        """``widen_q4``: a q4 body (the tiny profile) is held in HBM as int8 codes with its own
-        blocks and scales (identical weights), which the decode kernels read faster than
-        packed nibbles; False keeps the packed nibbles (half the bytes)."""
+    def __init__(self, weights, prefix: str = "llm.", cap: int = 1024, widen_q4: bool = False):
+        """A q4 body (the tiny profile) is held in HBM as the checkpoint's packed nibbles; the
+        one-launch step decodes it at the int8 body's rate.  ``widen_q4`` holds it as int8
+        codes with the same blocks and scales instead (identical weights, twice the bytes),
+        which the five-kernel step reads a little faster."""
         _lib.init()
         m = weights.meta["qwen2"]
         self.layers = int(m["num_hidden_layers"])
