@@ -52,9 +52,9 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # KV 512: 408.8 MB read + 7.6 MB written).  Counters cannot be read inside this process, so these
 # are the measured figures for exactly these kernels and shapes.
 TRAFFIC_DECODE_STEP = 416.4e6
-# the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes (k_gemm_x3,
-# [1000, 1024] x [3072, 1024]^T): 53.2 MB read + 12.3 MB written
-TRAFFIC_QKV_GEMM_X3 = 65.5e6
+# the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes in fragment order
+# (k_gemm_x3f, [1000, 1024] x [3072, 1024]^T): 53.4 MB read + 12.3 MB written
+TRAFFIC_QKV_GEMM_X3 = 65.7e6
 FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
 # float32 products on the bfloat16 matrix cores: six bfloat16 plane products each (cv3_linear_x3),
 # so the dense bfloat16 peak (2.5 PFLOP/s) over six
@@ -516,7 +516,8 @@ def bench_kernels(args):
         log(f"kernels: {name}: {us:.1f} us" + (f", {rate:.1f} TFLOP/s ({rate / (pk[0] / 1e12):.1%} of the "
                                                    f"{pk[1]} peak)" if rate else ""))
         out[name] = {"us": round(us, 2), "tflops": round(rate, 2) if rate else None}
-    # the 30 s solve's q8 GEMMs (the activation's bfloat16 planes times the codes), block-64 / f16 scales
+    # the 30 s solve's q8 GEMMs (the activation's bfloat16 planes times the codes, held in the matrix
+    # cores' fragment order as the solve holds them): per-output-channel f32 scales and block-64 / f16
     T3 = 1500
     BT3 = B * T3
     rng = np.random.default_rng(0)
@@ -524,22 +525,26 @@ def bench_kernels(args):
     a_d = to_device(a)
     for (n, kk, label) in ((3 * D, D, "QKV"), (F, D, "ff1"), (D, D, "out"), (D, F, "ff2")):
         w = to_device(rng.standard_normal((n, kk), dtype=np.float32) * np.float32(0.02))
-        qd, sd, kp = quant.quantize_q8(w, 64, np.float16)   # device quantiser
-        y = DeviceArray((BT3, n), np.float32)
-        fn = lambda: _lib.call("linear_q8_x3", a_d.ptr, BT3, kk, F, qd.ptr, sd.ptr, _lib.F16, kp, 64, n,
-                               None, y.ptr, n, None, None)
-        run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
-        run()
-        synchronize()
-        tm.start()
-        for _ in range(5):
+        for block, sdt, what in ((kk, np.float32, "per-channel f32 scales"), (64, np.float16, "block 64, f16 scales")):
+            qd, sd, kp = quant.quantize_q8(w, block, sdt)   # device quantiser
+            qf = DeviceArray((-(-n // 32) * 32 * kp,), np.int8)
+            _lib.call("pack_q8_frag", qd.ptr, n, kp, kp, qf.ptr, None)
+            y = DeviceArray((BT3, n), np.float32)
+            sdt_c = _lib.F16 if sdt == np.float16 else _lib.F32
+            fn = lambda: _lib.call("linear_q8_x3_frag", a_d.ptr, BT3, kk, F, qf.ptr, sd.ptr, sdt_c, kp, block, n,
+                                   None, y.ptr, n, None, None)
+            run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
             run()
-        us = tm.stop() / (5 * reps) * 1e3
-        rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
-        name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T (block 64, f16 scales)"
-        log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (SPLIT_Q8_PEAK / 1e12):.1%} of the split "
-            f"q8 peak)")
-        out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
+            synchronize()
+            tm.start()
+            for _ in range(5):
+                run()
+            us = tm.stop() / (5 * reps) * 1e3
+            rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
+            name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T ({what})"
+            log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (SPLIT_Q8_PEAK / 1e12):.1%} of the "
+                f"split q8 peak)")
+            out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
     # the 30 s solve's attention: 1500 x 1500 per head, the CFG pair x 16 heads, on bfloat16 planes
     qkv3 = to_device(rng.standard_normal((BT3, 3 * D), dtype=np.float32))
     att3 = DeviceArray((BT3, D), np.float32)
