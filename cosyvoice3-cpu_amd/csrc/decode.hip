@@ -1987,10 +1987,36 @@ float* scratch_of_current_device() {
 }
 }  // namespace
 
+// Calls of the no-workspace step on one device share its scratch.  The device's event marks
+// where the last call's step ended; a call from another stream waits for it first, so calls from
+// different streams or threads run one after another (under graph capture the graph's launches
+// order them instead).  Created once per device at init (a library event: cv3_shutdown releases it).
+struct ScratchOrder {
+  void* ev = nullptr;
+  hipStream_t last = nullptr;
+  bool recorded = false;
+};
+static ScratchOrder g_scratch_order[kScratchDevices];
+static std::mutex g_scratch_order_mu;
+}  // namespace
+
+extern "C" int cv3_event_create(void** ev);
+extern "C" int cv3_event_record(void* ev, cv3_stream_t s);
+extern "C" int cv3_stream_wait_event(cv3_stream_t s, void* ev);
+
 namespace cv3 {
 // Called by cv3_init with the selected device current.
-int decode_scratch_setup() { return scratch_of_current_device() ? CV3_OK : CV3_EHIP; }
+int decode_scratch_setup() {
+  if (!scratch_of_current_device()) return CV3_EHIP;
+  int dev = 0;
+  CV3_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_scratch_order_mu);
+  ScratchOrder& o = g_scratch_order[dev];
+  return o.ev ? CV3_OK : cv3_event_create(&o.ev);
+}
 }  // namespace cv3
+
+namespace {
 
 extern "C" {
 
@@ -2004,10 +2030,28 @@ int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_stat
               (long long)H, (long long)I, (long long)kScratchInterMax, (long long)kScratchFloats);
   float* ws = scratch_of_current_device();
   if (!ws) return CV3_EHIP;
+  int dev = 0;
+  CV3_HIP(hipGetDevice(&dev));
+  hipStream_t st = stream_of(stream);
+  CV3_REQUIRE(st, CV3_EINVAL, "%s", cv3_last_error());
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  CV3_HIP(hipStreamIsCapturing(st, &cs));
+  const bool order = cs == hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lk(g_scratch_order_mu);
+  ScratchOrder& o = g_scratch_order[dev];
+  CV3_REQUIRE(o.ev, CV3_EINVAL, "decode step without workspace: device %d was not set up by cv3_init", dev);
+  int rc;
+  if (order && o.recorded && o.last != st && (rc = cv3_stream_wait_event(stream, o.ev))) return rc;
   cv3_qwen2_state t = *s;
   t.workspace = ws;
   t.workspace_floats = kScratchFloats;
-  return decode_step(m, &t, nullptr, stream);
+  if ((rc = decode_step(m, &t, nullptr, stream))) return rc;
+  if (order) {
+    if ((rc = cv3_event_record(o.ev, stream))) return rc;
+    o.last = st;
+    o.recorded = true;
+  }
+  return CV3_OK;
 }
 
 // Words between replicas of an n-word vector: whole 4 KiB pages plus 512 bytes,

@@ -375,8 +375,10 @@ int cv3_qwen2_decode_step(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv
  * capture, serving loops that forbid hipMalloc): no counterpart in the reference.  s->workspace and
  * s->workspace_floats are ignored; the step's scratch is a fixed device array of the library (137.5 KB, held
  * on each device until the process ends), so it allocates nothing.  Geometries beyond that scratch (more than
- * 16 heads, or an intermediate size above 16384) are rejected.  Every call on one device shares the array:
- * calls that overlap on one device race. */
+ * 16 heads, or an intermediate size above 16384) are rejected.  Every call on one device shares the array, so
+ * the library orders them: a call from another stream than the previous call's waits for that call's end (an
+ * event created once per device by cv3_init).  Under graph capture nothing is recorded: the captured steps share
+ * the array, and replays of graphs holding them must not overlap on one device. */
 int cv3_qwen2_decode_step_noalloc(const cv3_qwen2_model* m, const cv3_qwen2_state* s, cv3_stream_t stream);
 /* The decode step's q8 / q4 GEMV on its own (quant.py:172-204 at m = 1, K1): layer `layer` of a stacked weight,
  * y = W . v with v = x, or v = rms_norm(x, rms_w, eps) when rms_w is given (ops.py:101-104).

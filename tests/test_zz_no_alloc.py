@@ -68,3 +68,27 @@ def test_noalloc_step_refuses_geometries_beyond_its_scratch(gpu):
     m.layers, m.hidden, m.heads, m.kv_heads, m.head_dim, m.inter = 1, 896, 14, 2, 64, 40000
     with pytest.raises(ValueError, match="scratch"):
         _lib.call("qwen2_decode_step_noalloc", ctypes.byref(m), ctypes.byref(State()), None)
+
+
+def test_noalloc_calls_from_two_streams_run_one_after_another(gpu):
+    """Calls on two streams share the device's scratch: the library orders them (each waits for the
+    previous call's end on the other stream), so two decoders stepped alternately on their own
+    streams, with no host synchronisation between calls, match the workspace step."""
+    from cv3amd import _lib
+    from cv3amd.device import Stream, synchronize
+    case = dict(layers=2, hidden=896, heads=14, kv_heads=2, inter=4864, n=300, seed=0)
+    ref, got = _pair(**case)
+    ref2, got2 = _pair(**case)
+    sa, sb = Stream(), Stream()
+    synchronize()                                 # the caches and states are filled on this thread's stream
+    for s in range(4):
+        for r in (ref, ref2):
+            _lib.call("qwen2_decode_step", ctypes.byref(r.model), ctypes.byref(r.state), None)
+        _lib.call("qwen2_decode_step_noalloc", ctypes.byref(got.model), ctypes.byref(got.state), sa.handle)
+        _lib.call("qwen2_decode_step_noalloc", ctypes.byref(got2.model), ctypes.byref(got2.state), sb.handle)
+    synchronize()
+    _lib.call("stream_sync", sa.handle)
+    _lib.call("stream_sync", sb.handle)
+    for r, g in ((ref, got), (ref2, got2)):
+        assert np.array_equal(g.logits.numpy(), r.logits.numpy())
+        assert np.array_equal(g.k_cache.numpy(), r.k_cache.numpy())
