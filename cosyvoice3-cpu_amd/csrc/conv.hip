@@ -735,6 +735,9 @@ int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* 
             int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
             hipStream_t st);
 int64_t x3_frag_plane(int64_t n, int64_t k);  // gemm.hip: one plane of a fragment-ordered weight
+int conv_cl_x3f(const float* x, int64_t batch, int64_t t, int64_t ldx, const uint16_t* frag, int64_t cout, int64_t k,
+                int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
+                hipStream_t st);
 }
 
 extern "C" {
@@ -751,6 +754,19 @@ int cv3_conv1d_cl(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t
   return conv_cl(x, batch, t, ldx, w_packed, cout, k, cin / groups, pad_l, bias, y, ldy, epi, stream_of(s));
 }
 
+
+int cv3_conv1d_cl_x3f(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t ldx, const uint16_t* w_frag,
+                      int64_t cout, int64_t k, int64_t groups, int64_t pad_l, const float* bias, float* y, int64_t ldy,
+                      const cv3_epilogue* epi, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(w_frag, CV3_EINVAL, "null weight fragments");
+  CV3_REQUIRE(groups >= 1 && cin % groups == 0 && cout % groups == 0, CV3_EASSERT,
+              "channels %lld/%lld not divisible by groups %lld", (long long)cin, (long long)cout, (long long)groups);
+  CV3_REQUIRE(cout / groups == 64, CV3_EUNSUPPORTED, "channels-last conv takes 64 output channels per group");
+  CV3_REQUIRE(ldx >= cin && ldy >= cout && k >= 1, CV3_EINVAL, "bad channels-last conv strides");
+  if (batch <= 0 || t <= 0) return CV3_OK;
+  return conv_cl_x3f(x, batch, t, ldx, w_frag, cout, k, cin / groups, pad_l, bias, y, ldy, epi, stream_of(s));
+}
 
 int cv3_conv1d(const float* x, int64_t cin, int64_t t_in, int64_t x_cs, int64_t x_ts, const float* w, int64_t cout,
                int64_t k, const float* bias, int64_t stride, int64_t dilation, int64_t groups, int64_t pad_l,

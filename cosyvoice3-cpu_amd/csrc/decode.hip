@@ -1985,7 +1985,6 @@ float* scratch_of_current_device() {
   }
   return g_scratch_ptr[dev];
 }
-}  // namespace
 
 // Calls of the no-workspace step on one device share its scratch.  The device's event marks
 // where the last call's step ended; a call from another stream waits for it first, so calls from
@@ -2015,8 +2014,6 @@ int decode_scratch_setup() {
   return o.ev ? CV3_OK : cv3_event_create(&o.ev);
 }
 }  // namespace cv3
-
-namespace {
 
 extern "C" {
 

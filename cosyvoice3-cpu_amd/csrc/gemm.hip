@@ -717,6 +717,10 @@ __global__ __launch_bounds__(256) void k_gemm_x3(GemmParams p, const uint16_t* p
 // straight into registers, one contiguous kilobyte per plane and step, a stage ahead; only A
 // goes through LDS (half the LDS traffic of k_gemm_x3).  Every MFMA sees the operands
 // k_gemm_x3 gives it, in the same order: the results are the same bits.
+// AMODE A_CONV reads A as the channels-last grouped causal conv's implicit im2col (load_a_fast): each
+// 64-column tile is one group of 64 output channels, whose rows of the fragment-ordered weight are its
+// own (cout, k * cin_g) rows, so B needs no group addressing.
+template <int AMODE>
 __global__ __launch_bounds__(256) void k_gemm_x3f(GemmParams p, const uint4* frag, int64_t per_plane, int tiles_m,
                                                   int tiles_n, int gm) {
   __shared__ uint4 sA[2][3][BM * 4];
@@ -724,7 +728,16 @@ __global__ __launch_bounds__(256) void k_gemm_x3f(GemmParams p, const uint4* fra
   int64_t m0, n0;
   tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
   const int lr = tid >> 2, lc = tid & 3;
-  const float* pa = p.a + min(m0 + lr, p.m - 1) * p.lda + lc * 8;
+  const int64_t arow = min(m0 + lr, p.m - 1);
+  int t_row = 0;
+  const float* pa;
+  if constexpr (AMODE == A_CONV) {
+    const int bi = (int)arow / p.conv_t;
+    t_row = (int)arow - bi * p.conv_t;
+    pa = p.a + (int64_t)bi * p.conv_t * p.lda + (n0 / BN) * p.conv_cg + lc * 8;
+  } else {
+    pa = p.a + arow * p.lda + lc * 8;
+  }
   const int wslot = xslot(lr, lc);
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
   const int ar = wm + r32, asw = (ar >> 2) & 3;
@@ -741,8 +754,8 @@ __global__ __launch_bounds__(256) void k_gemm_x3f(GemmParams p, const uint4* fra
     uint4 v[2][3];  // [16-k step of the stage][plane]
   };
   auto load = [&](XA& x, int64_t k0) {
-    x.a0 = *reinterpret_cast<const float4*>(pa + k0);
-    x.a1 = *reinterpret_cast<const float4*>(pa + k0 + 4);
+    x.a0 = load_a_fast<AMODE>(p, pa, t_row, k0);
+    x.a1 = load_a_fast<AMODE>(p, pa, t_row, k0 + 4);
   };
   auto loadb = [&](BF& b, int64_t st) {
 #pragma unroll
@@ -1285,7 +1298,7 @@ int gemm_x3f(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* 
   const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
   CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
   const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, 6.0 * (double)n * k);
-  hipLaunchKernelGGL(k_gemm_x3f, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
+  hipLaunchKernelGGL(k_gemm_x3f<A_ROWS>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
                      reinterpret_cast<const uint4*>(frag), x3_frag_plane(n, k) / 8, (int)tiles_m, (int)tiles_n, gm);
   CV3_LAUNCHED();
   return CV3_OK;
@@ -1346,6 +1359,39 @@ int split_x3(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* planes
 // g = co / 64: the DiT's grouped conv_pos (cv3cpu/models/dit.py:99-112) on
 // channels-last activations, as an implicit GEMM on the FAST kernel.  w is the
 // reference's (cout, cin_g, k) weight repacked as (cout, k, cin_g).
+// The same grouped conv with the packed weight as bfloat16 planes in fragment order
+// (split_x3_frag of the (cout, k * cin_g) rows): k_gemm_x3f in its conv mode.
+int conv_cl_x3f(const float* x, int64_t batch, int64_t t, int64_t ldx, const uint16_t* frag, int64_t cout, int64_t k,
+                int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
+                hipStream_t st) {
+  CV3_REQUIRE(cin_g % XBK == 0 && (k * cin_g) % (2 * XBK) == 0 && cout % BN == 0, CV3_EUNSUPPORTED,
+              "channels-last conv needs cin/groups %% 32 == 0, k*cin/groups %% 64 == 0, 64 outputs per group");
+  CV3_REQUIRE(((uintptr_t)x % 16 == 0) && ldx % 4 == 0 && ((uintptr_t)frag % 16 == 0), CV3_EINVAL,
+              "channels-last conv operands must be 16-byte aligned");
+  CV3_REQUIRE(batch * t < (1ll << 31) && pad_l >= 0 && pad_l < k, CV3_EINVAL, "bad conv geometry");
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.m = batch * t;
+  p.n = cout;
+  p.k = k * cin_g;
+  p.bias = bias;
+  p.c = y;
+  p.ldc = ldy;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  CV3_REQUIRE(!p.epi.rope_cos, CV3_EINVAL, "no rotary epilogue on a conv");
+  p.conv_t = (int)t;
+  p.conv_cg = (int)cin_g;
+  p.conv_pad = (int)pad_l;
+  const int64_t tiles_m = ceil_div(p.m, BM), tiles_n = cout / BN;
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)p.m * p.k, 6.0 * (double)cout * p.k);
+  hipLaunchKernelGGL(k_gemm_x3f<A_CONV>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
+                     reinterpret_cast<const uint4*>(frag), x3_frag_plane(cout, p.k) / 8, (int)tiles_m, (int)tiles_n,
+                     gm);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
 int conv_cl(const float* x, int64_t batch, int64_t t, int64_t ldx, const float* w, int64_t cout, int64_t k,
             int64_t cin_g, int64_t pad_l, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
             hipStream_t st) {

@@ -210,9 +210,19 @@ class DeviceDiT:
             w = g(f"input_embed.conv_pos_embed.{c}.0.weight")
             if _is_q(w):
                 raise ValueError("conv_pos weights are float on this path")
-            # (cout, cin/groups, k) -> (cout, k, cin/groups): K-contiguous rows for the implicit GEMM
-            self.conv_w.append(to_device(np.ascontiguousarray(np.asarray(w, np.float32).transpose(0, 2, 1))))
+            # (cout, cin/groups, k) -> (cout, k, cin/groups): K-contiguous rows for the implicit GEMM,
+            # with planes held as bfloat16 planes in fragment order (cv3_conv1d_cl_x3f)
+            wp = to_device(np.ascontiguousarray(np.asarray(w, np.float32).transpose(0, 2, 1)))
+            cout, kk = wp.shape[0], wp.shape[1] * wp.shape[2]
+            if self.planes and kk % 64 == 0:
+                ne = ctypes.c_int64()
+                _lib.call("x3_frag_elems", cout, kk, ctypes.byref(ne))
+                fr = DeviceArray((ne.value,), np.uint16)
+                _lib.call("split_x3_frag", wp.ptr, cout, kk, kk, fr.ptr, None)
+                wp = fr
+            self.conv_w.append(wp)
             self.conv_b.append(to_device(np.asarray(g(f"input_embed.conv_pos_embed.{c}.0.bias"), np.float32)))
+        self.conv_planes = self.planes and self.conv_w[0].dtype == np.uint16
         mods = [g(f"transformer_blocks.{i}.attn_norm.linear.weight") for i in range(self.depth)]
         mods.append(g("norm_out.linear.weight"))
         mbias = [g(f"transformer_blocks.{i}.attn_norm.linear.bias") for i in range(self.depth)]
@@ -289,9 +299,10 @@ class DeviceDiT:
         # conv_pos: two grouped causal convs with Mish on channels-last [B*T, D] activations,
         # the second adding the projection back in place (dit.py:99-112)
         k = self.conv_k
-        _lib.call("conv1d_cl", self.h.ptr, B, T, D, D, self.conv_w[0].ptr, D, k, self.conv_groups, k - 1,
+        conv = "conv1d_cl_x3f" if self.conv_planes else "conv1d_cl"
+        _lib.call(conv, self.h.ptr, B, T, D, D, self.conv_w[0].ptr, D, k, self.conv_groups, k - 1,
                   self.conv_b[0].ptr, self.z1.ptr, D, ctypes.byref(_lib.epilogue("mish")), None)
-        _lib.call("conv1d_cl", self.z1.ptr, B, T, D, D, self.conv_w[1].ptr, D, k, self.conv_groups, k - 1,
+        _lib.call(conv, self.z1.ptr, B, T, D, D, self.conv_w[1].ptr, D, k, self.conv_groups, k - 1,
                   self.conv_b[1].ptr, self.h.ptr, D,
                   ctypes.byref(_lib.epilogue("mish", residual=self.h.ptr, ld_res=D)), None)
         mrow = self.mods.ptr + s * self.ld_mod * f4
@@ -363,6 +374,8 @@ class DeviceDiT:
         six = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.planes is not None)
         if self.planes and self.dim_head == 64:   # attention on planes too (cv3_attention_x3)
             six += self.steps * self.depth * 4.0 * B * self.heads * T * T * self.dim_head
+        if self.conv_planes:                      # the conv_pos convs (cv3_conv1d_cl_x3f)
+            six += self.steps * 2 * 2.0 * M * D * (D // self.conv_groups) * self.conv_k
         three = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.q8 and l.q8_planes)
         return six, three, self.flops_per_solve() - six - three
 

@@ -289,6 +289,12 @@ int cv3_conv1d_cl_packed_x3f(const float* x, int64_t t_in, int64_t cin, int64_t 
 int cv3_conv1d_cl(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t ldx, const float* w_packed,
                   int64_t cout, int64_t k, int64_t groups, int64_t pad_l, const float* bias, float* y, int64_t ldy,
                   const cv3_epilogue* epi, cv3_stream_t s);
+/* cv3_conv1d_cl on the bfloat16 matrix cores: w_frag is the packed (cout, k, cin/groups) weight as bfloat16
+ * planes in fragment order (cv3_split_x3_frag with n = cout, k = k * cin/groups; cv3_x3_frag_elems elements), six
+ * plane products per product with float32 accumulation.  Same requirements, and k * cin/groups % 64 == 0. */
+int cv3_conv1d_cl_x3f(const float* x, int64_t batch, int64_t t, int64_t cin, int64_t ldx, const uint16_t* w_frag,
+                      int64_t cout, int64_t k, int64_t groups, int64_t pad_l, const float* bias, float* y, int64_t ldy,
+                      const cv3_epilogue* epi, cv3_stream_t s);
 int cv3_depthwise_conv1d(const float* x, int64_t c, int64_t t_in, const float* w, int64_t k, const float* bias,
                          int64_t dilation, int64_t pad_l, int64_t pad_r, float* y, int64_t* t_out_ptr,
                          cv3_stream_t s);

@@ -309,7 +309,8 @@ def test_interpolation(dev, rng):
     assert np.array_equal(ops.interpolate_nearest(x, 3), ref.interpolate_nearest(x, 3))
 
 
-@pytest.mark.parametrize("T,k,cin,groups", [(500, 31, 1024, 16), (37, 31, 1024, 16), (70, 5, 256, 4)])
+@pytest.mark.parametrize("T,k,cin,groups", [(500, 31, 1024, 16), (37, 31, 1024, 16), (70, 5, 256, 4),
+                                            (100, 4, 512, 8), (3, 2, 128, 2)])
 def test_conv1d_channels_last(dev, rng, T, k, cin, groups):
     """The DiT conv_pos path: grouped causal conv on [batch, time, channel] activations
     against the oracle's (channel, time) conv1d, per batch row, with the Mish + residual epilogue."""
@@ -331,6 +332,18 @@ def test_conv1d_channels_last(dev, rng, T, k, cin, groups):
     _lib.call("conv1d_cl", xd.ptr, B, T, cin, cin, wd.ptr, cout, k, groups, k - 1, bd.ptr, yd.ptr, cout,
               ctypes.byref(epi), None)
     assert rel_err(yd.numpy(), want) < TOL
+    # the same conv with the weight as bfloat16 planes in fragment order (cv3_conv1d_cl_x3f)
+    kk = k * (cin // groups)
+    if kk % 64 == 0:
+        ne = ctypes.c_int64()
+        _lib.call("x3_frag_elems", cout, kk, ctypes.byref(ne))
+        fr = DeviceArray((ne.value,), np.uint16)
+        _lib.call("split_x3_frag", wd.ptr, cout, kk, kk, fr.ptr, None)
+        y3 = to_device(res)
+        epi3 = _lib.epilogue("mish", residual=y3.ptr, ld_res=cout)
+        _lib.call("conv1d_cl_x3f", xd.ptr, B, T, cin, cin, fr.ptr, cout, k, groups, k - 1, bd.ptr, y3.ptr, cout,
+                  ctypes.byref(epi3), None)
+        assert rel_err(y3.numpy(), want) < TOL
 
 
 PACKED_CASES = [
