@@ -1055,8 +1055,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
 //   A  all workgroups: RMSNorm(x) -> [q; k; v] row pairs + bias + rotary; k, v
 //      also to the cache (read back by later tokens, after the kernel boundary)
 //   B  H x 8 workgroups: one query head over one 128-key chunk of the cache
-//      (flash-decoding partial: max, sum, unnormalised output)
-//   C  128 workgroups: merge the partials, o_proj rows + residual -> x_mid
+//      (flash-decoding partial: max, sum, unnormalised output); the item of the
+//      head's last live chunk merges the head's partials into its 64 outputs
+//   C  up to 256 workgroups (224 at hidden 896): o_proj rows + residual -> x_mid
 //   D  all workgroups: RMSNorm(x_mid) -> [gate; up] pairs -> h = silu(g) * u
 //   E  up to 256 workgroups (224 at hidden 896): down rows + residual -> x for the next layer
 // then the head rows, and (greedy) the argmax, speech_embedding row and
@@ -1076,13 +1077,14 @@ __global__ __launch_bounds__(kSampleThreads) void k_dec_sample(SampleArgs a) {
 // within 256 polls of seeing it.
 // ---------------------------------------------------------------------------
 constexpr int kPT = 512;                 // threads per workgroup
-constexpr int kPOproj = 128;             // workgroups of phase C (64: 4 % slower, 192 and 256: 2-3 %)
+constexpr int kPMinG = 128;              // workgroups the step needs at least
+constexpr int kPOproj = 256;             // workgroups of phase C, at most (64: 4 % slower, 96: 2 %, than 128; 256: 1.5 % faster)
 constexpr int kPDown = 256;              // workgroups of phase E, at most (128: 2 % slower)
 // Replicas of the exchanged vectors that many workgroups poll (x: all, x_mid: all,
 // h: 128): workgroup w reads replica w % n.  Measured with the throttled polling
 // below: one copy is 2 % slower, 4 and 8 copies no faster or slower (the producers'
 // extra stores sit on their critical path).
-constexpr int kRX = 2, kRM = 2, kRH = 2, kRP = 1;
+constexpr int kRX = 2, kRM = 2, kRH = 2, kRA = 2;
 
 struct PersistArgs {
   QW qkv, o, gu, dn, head, emb;
@@ -1093,8 +1095,8 @@ struct PersistArgs {
   int64_t cap;
   int64_t *pos, *token, *history;
   float *x, *logits;
-  uint64_t *xb, *qkvb, *pb, *mb, *hb, *arg;  // exchange words, two sets each (arg: one)
-  int64_t sx, sp, sm, sh;                    // words between replicas of x, partials, x_mid, h
+  uint64_t *xb, *qkvb, *pb, *ab, *mb, *hb, *arg;  // exchange words, two sets each (arg: one)
+  int64_t sx, sp, sa, sm, sh;                    // words between replicas of x, partials, attention, x_mid, h
   int64_t* err;                              // set when a wait gives up
   uint32_t epoch_base;                       // launch counter * 256, from the host
   int select;                                // 1: greedy argmax + next input here
@@ -1135,8 +1137,9 @@ __device__ bool ll_get(const uint64_t* s0, int n0, const uint64_t* s1, int n1, c
       if (got) break;
       if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
       // back off after a few misses: hundreds of workgroups polling the same words
-      // slow every exchange down
-      if (spins < 8)
+      // slow every exchange down (the narrow waits, up to two words per thread, keep
+      // the short sleep: 0.6 % faster decode)
+      if (spins < 8 || NW <= 2)
         __builtin_amdgcn_s_sleep(1);
       else
         __builtin_amdgcn_s_sleep(8);
@@ -1157,6 +1160,49 @@ __device__ __forceinline__ bool ll_get(const uint64_t* src, int n, uint32_t e, f
   return ll_get<NW, Map>(src, n, nullptr, 0, nullptr, 0, e, dst, err, map);
 }
 
+
+// The same for one range, polled by the last NPT threads only, so that the waves with weight
+// DMAs in flight (loads complete in issue order) do not hold up the poll: the matrix-core phase
+// D's wait for x_mid, polled by waves 3-7 while waves 0-2 fetch the [gate; up] rows (0.6 %
+// faster decode; the down rows' wait polled by waves 4-7 alone was 6 % slower: fewer waves
+// polling 4864 words take longer per round).
+template <int NW, int NPT, class Map = Ident>
+__device__ bool ll_get_tail(const uint64_t* src, int n, uint32_t e, float* dst, int64_t* err, Map map = Map()) {
+  const int pt = (int)threadIdx.x - (kPT - NPT);
+  const bool poller = pt >= 0;
+  bool ok = true;
+  for (int b0 = 0; b0 < n && ok; b0 += NPT * NW) {
+    uint64_t w[NW];
+    bool got = true;
+    if (poller) {
+      got = false;
+      for (int spins = 0; spins < kPSpin; ++spins) {
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+          const int idx = b0 + pt + NPT * j;
+          w[j] = idx < n ? __hip_atomic_load(src + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ((uint64_t)e << 32);
+        }
+        got = true;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) got = got && (uint32_t)(w[j] >> 32) == e;
+        if (got) break;
+        if ((spins & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+        if (spins < 8 || NW <= 3)
+          __builtin_amdgcn_s_sleep(1);
+        else
+          __builtin_amdgcn_s_sleep(8);
+      }
+#pragma unroll
+      for (int j = 0; j < NW; ++j) {
+        const int idx = b0 + pt + NPT * j;
+        if (idx < n) dst[map(idx)] = __uint_as_float((uint32_t)w[j]);
+      }
+    }
+    ok = !__syncthreads_or(!got);
+  }
+  if (!ok && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(err), 1ull);
+  return ok;
+}
 
 
 // Dot product of one weight row spread over the whole wave (64 lanes x CPL
@@ -1204,6 +1250,11 @@ template <bool Q4H>
 __device__ __forceinline__ int body_slot(int t) {
   return Q4H ? xslot_q4h(t) : xslot<16>(t);
 }
+// ll_get destination map: element i of a vector to its staged float in body_slot order
+template <bool Q4H>
+struct SlotMap {
+  __device__ __forceinline__ int operator()(int i) const { return 4 * body_slot<Q4H>(i >> 2) + (i & 3); }
+};
 template <bool SF16>
 __device__ __forceinline__ float wdot(const RowQ4H<SF16>& rd, const XSlice<16>& x) {
   return wave_sum_swap(fmaf(dot16_q4h(rd.wv, x.v), rd.sc, 0.f) * 0.0625f);
@@ -1332,9 +1383,13 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   const int nact = (int)((pos + kPKeys) / kPKeys);  // attention chunks in use
   const int half = dh / 2;
   const int nE = min(kPDown, G);  // phase E's workgroups
-  const int rowsC = (D + kPOproj - 1) / kPOproj, rowsE = (D + nE - 1) / nE;
+  const int nC = min(kPOproj, G);  // phase C's workgroups
+  const int rowsC = (D + nC - 1) / nC, rowsE = (D + nE - 1) / nE;
   const bool isB = w < H * kPChunks && (w % kPChunks) < nact;
-  const bool isC = w < kPOproj, isE = w < nE && w * rowsE < D;  // only workgroups that own rows wait in E
+  // every workgroup waits in C (those without rows then go straight to D's wait: 1.5 % faster
+  // than sleeping through most of it, as the idle ones do before A); only those that own rows
+  // wait in E
+  const bool isC = w < nC, isE = w < nE && w * rowsE < D;
   // phase A's pair of this wave and its rotary factors (the same in every layer)
   const int npairs = R / 2;
   const int pA = w + G * wave;
@@ -1505,11 +1560,14 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
         ow[8 * dh + 8 + wave] = lw;
       }
       __syncthreads();
+      // the item of the last live chunk merges its head: it waits for the other chunks'
+      // partials and publishes the head's 64 outputs, so phase C reads H dh words instead of
+      // every partial (nact H 66) and does no merge of its own
+      const bool merger = c == nact - 1;
+      float M = -INFINITY, L = 0.f, O = 0.f;
       if (wave == 0) {
-        float M = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 8; ++i) M = fmaxf(M, ow[8 * dh + i]);
-        float L = 0.f, O = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float mi = ow[8 * dh + i];
@@ -1517,9 +1575,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
           L = fmaf(ow[8 * dh + 8 + i], f, L);
           O = fmaf(ow[i * dh + lane], f, O);
         }
-#pragma unroll
-        for (int rr = 0; rr < kRP; ++rr) {
-          uint64_t* out = a.pb + (par * kRP + rr) * a.sp + ((int64_t)c * H + h) * kPPart;
+        if (!merger) {
+          uint64_t* out = a.pb + par * a.sp + ((int64_t)h * kPChunks + c) * kPPart;
           if (lane == 0) {
             ll_put(out, M, E + 1u);
             ll_put(out + 1, L, E + 1u);
@@ -1527,58 +1584,42 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
           ll_put(out + 2 + lane, O, E + 1u);
         }
       }
+      if (merger) {
+        float* pm = big + 1024;  // [nact - 1][66]: chunks 0 .. nact - 2 of head h
+        if (nact > 1 &&
+            !ll_get<1>(a.pb + par * a.sp + (int64_t)h * kPChunks * kPPart, (nact - 1) * kPPart, E + 1u, pm, a.err))
+          return;
+        if (wave == 0) {
+          // M = max m_c, den = sum l_c 2^{m_c - M}, out = sum o_c 2^{m_c - M} / den, chunks in order
+          float Mx = M;
+#pragma unroll
+          for (int cc = 0; cc < kPChunks - 1; ++cc)
+            if (cc < nact - 1) Mx = fmaxf(Mx, pm[cc * kPPart]);
+          float den = 0.f;
+#pragma unroll
+          for (int cc = 0; cc < kPChunks - 1; ++cc)
+            if (cc < nact - 1) den = fmaf(pm[cc * kPPart + 1], __builtin_amdgcn_exp2f(pm[cc * kPPart] - Mx), den);
+          den = fmaf(L, __builtin_amdgcn_exp2f(M - Mx), den);
+          float att = 0.f;
+#pragma unroll
+          for (int cc = 0; cc < kPChunks - 1; ++cc)
+            if (cc < nact - 1)
+              att = fmaf(pm[cc * kPPart + 2 + lane], __builtin_amdgcn_exp2f(pm[cc * kPPart] - Mx) / den, att);
+          att = fmaf(O, __builtin_amdgcn_exp2f(M - Mx) / den, att);
+#pragma unroll
+          for (int rr = 0; rr < kRA; ++rr) ll_put(a.ab + (par * kRA + rr) * a.sa + h * dh + lane, att, E + 5u);
+        }
+      }
       __syncthreads();  // big is reused below
     }
     // ---- C: merge + o_proj rows + residual -> x_mid ----
     if (isC) {
       load_C(l);
-      float* part = big;  // [nact][H][66]
-      if (!ll_get<16>(a.pb + (par * kRP + w % kRP) * a.sp, nact * H * kPPart, E + 1u, part, a.err)) return;
-      // per head: M = max m_c, den = sum l_c e^{m_c - M}, att = sum o_c e^{m_c - M} / den;
-      // the chunk weights e^{m_c - M} / den, one thread per (chunk, head) = part index,
-      // into xmid (free until D).  Every loop runs over all kPChunks slots with its LDS
-      // reads clamped to the last live chunk, so the reads issue together instead of one
-      // LDS round trip per chunk; the sums still add the live chunks in order.
-      if (tid < nact * H) {
-        const int hh = tid % H;
-        float m[kPChunks], lc[kPChunks];
-#pragma unroll
-        for (int cc = 0; cc < kPChunks; ++cc) {
-          const int c2 = min(cc, nact - 1);
-          m[cc] = part[(c2 * H + hh) * kPPart];
-          lc[cc] = part[(c2 * H + hh) * kPPart + 1];
-        }
-        float M = -INFINITY;
-#pragma unroll
-        for (int cc = 0; cc < kPChunks; ++cc) M = fmaxf(M, m[cc]);  // clamped slots repeat a live m
-        float den = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < kPChunks; ++cc)
-          if (cc < nact) den = fmaf(lc[cc], __builtin_amdgcn_exp2f(m[cc] - M), den);
-        xmid[tid] = __builtin_amdgcn_exp2f(part[tid * kPPart] - M) / den;
-      }
-      __syncthreads();
+      // the merged attention output (H dh words, from phase B's merging items) goes straight
+      // into the staged slots of the o_proj rows; the slots up to kStage stay zero
       static_assert(kStage % kPT == 0, "the staged width is a multiple of the workgroup");
-#pragma unroll 1
-      for (int it = 0; it < kStage / kPT; ++it) {
-        const int i = tid + it * kPT;
-        float att = 0.f;  // the o_proj dot reads the staged vector up to kStage: zero past H dh
-        if (i < H * 64) {  // head dim 64
-          const int hh = i >> 6, d = i & 63;
-          float o[kPChunks], f[kPChunks];
-#pragma unroll
-          for (int cc = 0; cc < kPChunks; ++cc) {
-            const int c2 = min(cc, nact - 1);
-            o[cc] = part[(c2 * H + hh) * kPPart + 2 + d];
-            f[cc] = xmid[c2 * H + hh];
-          }
-#pragma unroll
-          for (int cc = 0; cc < kPChunks; ++cc)
-            if (cc < nact) att = fmaf(o[cc], f[cc], att);
-        }
-        xs[4 * body_slot<Q4>(i >> 2) + (i & 3)] = att;
-      }
-      __syncthreads();
+      for (int i = H * dh + tid; i < kStage; i += kPT) xs[4 * body_slot<Q4>(i >> 2) + (i & 3)] = 0.f;
+      if (!ll_get<2>(a.ab + (par * kRA + w % kRA) * a.sa, H * dh, E + 5u, xs, a.err, SlotMap<Q4>())) return;
       XSlice<16> xv;
       xv.load(xs, lane);
       const float va = wdot(dC0, xv), vb2 = wdot(dC1, xv);
@@ -1592,7 +1633,9 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
     {
       load_D(l);
       const uint64_t t0 = isC ? 0 : idle_wait(wall_clock64(), waitD);
-      if (!ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)) return;
+      if (MX ? !ll_get_tail<3, kPT - 192>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err)
+             : !ll_get<2>(a.mb + (par * kRM + w % kRM) * a.sm, D, E + 2u, xmid, a.err))
+        return;
       if (!isC) waitD = wall_clock64() - t0;
       if constexpr (MX) {
         // RMSNorm statistic and max |x_mid * w| in one reduction, then the digit planes
@@ -2057,7 +2100,8 @@ static int64_t replica_stride(int64_t n) { return (n + 511) / 512 * 512 + 64; }
 
 static int64_t persist_words(const cv3_qwen2_model* m, int workgroups) {
   const int64_t D = m->hidden, R = (m->heads + 2 * m->kv_heads) * m->head_dim;
-  return 2 * kRX * replica_stride(D) + 2 * R + 2 * kRP * replica_stride((int64_t)kPChunks * m->heads * kPPart) +
+  return 2 * kRX * replica_stride(D) + 2 * R + 2 * replica_stride((int64_t)kPChunks * m->heads * kPPart) +
+         2 * kRA * replica_stride(D) +
          2 * kRM * replica_stride(D) + 2 * kRH * replica_stride(m->inter) + 2 * (int64_t)workgroups;
 }
 
@@ -2077,7 +2121,7 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
               "persistent step: heads %lld / kv heads %lld / head dim %lld", (long long)H, (long long)Hk,
               (long long)dh);
   const bool q4 = m->qkv.kind == CV3_KIND_Q4;
-  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= (q4 ? 6144 : 5120) && I >= kPOproj, CV3_EUNSUPPORTED,
+  CV3_REQUIRE(D <= 1024 && D % 4 == 0 && I <= (q4 ? 6144 : 5120) && I >= kPMinG, CV3_EUNSUPPORTED,
               "persistent step: hidden %lld / inter %lld", (long long)D, (long long)I);
   CV3_REQUIRE(m->layers > 0 && m->layers * 8 + 8 <= 256, CV3_EUNSUPPORTED, "persistent step: %lld layers (at most 31)",
               (long long)m->layers);
@@ -2117,10 +2161,10 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   int per_cu = 0;
   CV3_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPT, 0));
   const int G = p->workgroups > 0 ? p->workgroups : (int)std::min<int64_t>(std::min(cus, 256), I);
-  // phase C needs kPOproj workgroups; phase E at most 8 rows (one per wave) on min(kPDown, G)
-  CV3_REQUIRE(G >= kPOproj && G <= per_cu * cus && G <= I && (D + std::min(kPDown, G) - 1) / std::min(kPDown, G) <= 8,
+  // phases C and E at most 8 rows (one per wave) on min(kPOproj, G) and min(kPDown, G)
+  CV3_REQUIRE(G >= kPMinG && G <= per_cu * cus && G <= I && (D + std::min(kPDown, G) - 1) / std::min(kPDown, G) <= 8,
               CV3_EUNSUPPORTED, "persistent step: %d workgroups (needs %d..%d resident, at most inter %lld)", G,
-              kPOproj, per_cu * cus,
+              kPMinG, per_cu * cus,
               (long long)I);
   CV3_REQUIRE((H + 2 * Hk) * dh / 2 <= 8LL * G && I <= 24LL * G && m->head.rows <= 32LL * G &&
                   H * kPChunks <= G && H * kPChunks * kPPart <= 8192,
@@ -2167,7 +2211,9 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
   a.xb = wds;
   a.qkvb = a.xb + 2 * kRX * a.sx;
   a.pb = a.qkvb + 2 * R;
-  a.mb = a.pb + 2 * kRP * a.sp;
+  a.sa = replica_stride(D);
+  a.ab = a.pb + 2 * a.sp;
+  a.mb = a.ab + 2 * kRA * a.sa;
   a.hb = a.mb + 2 * kRM * a.sm;
   a.arg = a.hb + 2 * kRH * a.sh;
   a.err = p->err;
