@@ -49,9 +49,9 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
 # device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
 # the one-launch decode step (24 layers, per-channel int8 with phase D on the int8 matrix cores,
-# KV 512: 408.8 MB read + 7.6 MB written).  Counters cannot be read inside this process, so these
+# KV 512: 400.9 MB read + 7.8 MB written).  Counters cannot be read inside this process, so these
 # are the measured figures for exactly these kernels and shapes.
-TRAFFIC_DECODE_STEP = 416.4e6
+TRAFFIC_DECODE_STEP = 408.7e6
 # the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes in fragment order
 # (k_gemm_x3f, [1000, 1024] x [3072, 1024]^T): 53.4 MB read + 12.3 MB written
 TRAFFIC_QKV_GEMM_X3 = 65.7e6
@@ -499,9 +499,10 @@ def bench_kernels(args):
         f"ff2 GEMM [{BT}, {F}] x [{D}, {F}]^T + gated residual": (
             lambda: d.ff2[0](d.ffb.ptr, BT, F, d.z1.ptr, D, res_epi), 2.0 * BT * D * F, (lin_peak, lin_unit)),
         f"grouped causal conv k={k} groups={d.conv_groups} [{B}, {T}, {D}] + Mish": (
-            lambda: _lib.call("conv1d_cl", d.h.ptr, B, T, D, D, d.conv_w[0].ptr, D, k, d.conv_groups, k - 1,
-                              d.conv_b[0].ptr, d.z1.ptr, D, ctypes.byref(mish), None),
-            2.0 * BT * D * (D // d.conv_groups) * k, f32),
+            lambda: _lib.call("conv1d_cl_x3f" if d.conv_planes else "conv1d_cl", d.h.ptr, B, T, D, D,
+                              d.conv_w[0].ptr, D, k, d.conv_groups, k - 1, d.conv_b[0].ptr, d.z1.ptr, D,
+                              ctypes.byref(mish), None),
+            2.0 * BT * D * (D // d.conv_groups) * k, (lin_peak, lin_unit) if d.conv_planes else f32),
     }
     reps = args.kernel_reps
     for name, (fn, flops, pk) in launches.items():
