@@ -218,15 +218,17 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
   const float4* sc = reinterpret_cast<const float4*>(scale ? scale + g * mod_stride : x);
   const float4* w4 = reinterpret_cast<const float4*>(w ? w : x);
   const float4* b4 = reinterpret_cast<const float4*>(b ? b : x);
+  // the optional vectors are loaded only when given (uniform branches): the DiT's AdaLN has
+  // shift and scale but no affine weight or bias
   float4 v[NV], wv[NV], bv[NV], shv[NV], scv[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t j = min((int64_t)lane + 64 * i, c4 - 1);
     v[i] = xr[j];
-    wv[i] = w4[j];
-    bv[i] = b4[j];
-    shv[i] = sh[j];
-    scv[i] = sc[j];
+    if (w) wv[i] = w4[j];
+    if (b) bv[i] = b4[j];
+    if (shift) shv[i] = sh[j];
+    if (scale) scv[i] = sc[j];
   }
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
