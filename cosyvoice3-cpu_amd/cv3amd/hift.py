@@ -36,6 +36,12 @@ from .device import DeviceArray, Event, Graph, Stream, to_device, wait_event
 
 ACT = _lib.ACT
 F4 = 4
+# The whole-input spectral stack's independent branches (each stage's source branch beside its
+# upsampling conv, and its resblocks side by side) run on side streams forked off the thread's
+# stream when the stack is recorded and captured; in the graph the forks and joins are edges.
+# 10 s whole: 4.12 -> 3.37 ms.  The 1 s windows already run side by side on WINDOW_STREAMS
+# streams, and their stacks with branches took 12.0 ms against 7.76, so they keep none.
+BRANCHES = True
 WINDOW_STREAMS = 16  # vocoder windows replayed side by side (one stream each, default priority); a
                      # 10 s decode in 1 s windows: 4 streams 10.1 ms, 10 or 16 streams 7.4 ms
 
@@ -175,6 +181,9 @@ class DeviceHiFT:
         self._graphs = {}
         self._streams: List[Stream] = []
         self._recorded = set()   # (width, slot, stream) whose stack buffers are recorded on the stream
+        self._side: List[Stream] = []   # branch streams of the spectral stack (BRANCHES)
+        self._branch = False             # set while a whole-input stack is recorded and captured
+        self._ev: List[Event] = []
         self._arena = None       # while recording or capturing: every intermediate of the stack
         self._arena_i = -1       # >= 0 while capturing: the next arena entry to hand out
 
@@ -198,7 +207,7 @@ class DeviceHiFT:
     def _conv(self, x: DeviceArray, key: str, dilation: int = 1, pad=(0, 0), up: int = 1,
               act: str = "none", act_param: float = 0.0, snake: Optional[str] = None,
               residual: Optional[DeviceArray] = None, out: Optional[DeviceArray] = None, out_row0: int = 0,
-              channels_first_out: bool = False) -> DeviceArray:
+              channels_first_out: bool = False, st: Optional[int] = None) -> DeviceArray:
         """Stride-1 conv1d (ops.py:165-219) on channels-last x (T_in, C_in) -> (T_out, C_out),
         or (C_out, T_out) with ``channels_first_out``; nearest upsample, activation / Snake
         and residual (channels-last) fused."""
@@ -220,22 +229,22 @@ class DeviceHiFT:
             _lib.call("conv1d_cl_packed_x3f", x.ptr, t_in, cin, cin, self.wpx[wkey].ptr, cout, k,
                       self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_ts,
                       y_cs, ACT[act], float(act_param), alpha, 1e-9, res, r_ts, 1, ks, ws.ptr if ws else None,
-                      ws.size if ws else 0, None)
+                      ws.size if ws else 0, st)
         elif wkey in self.wp:   # cin % 32 == 0: the DMA implicit GEMM
             ks = split_k(n, cout, k * cin // 32)
             ws = self._new((ks * cout * n,)) if ks > 1 else None
             _lib.call("conv1d_cl_packed", x.ptr, t_in, cin, cin, self.wp[wkey].ptr, cout, k,
                       self.w[key + ".bias"].ptr, dilation, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_ts,
                       y_cs, ACT[act], float(act_param), alpha, 1e-9, res, r_ts, 1, ks, ws.ptr if ws else None,
-                      ws.size if ws else 0, None)
+                      ws.size if ws else 0, st)
         else:                 # narrow stacks: the generic kernel, addressed channels-last
             _lib.call("conv1d", x.ptr, cin, t_in, 1, cin, self.w[wkey].ptr, cout, k, self.w[key + ".bias"].ptr, 1,
                       dilation, 1, pad[0], pad[1], up, out.ptr + out_row0 * y_ts * F4, y_cs, y_ts, None,
-                      ACT[act], float(act_param), alpha, 1e-9, res, 1, r_ts, None)
+                      ACT[act], float(act_param), alpha, 1e-9, res, 1, r_ts, st)
         return out
 
     def _conv_in(self, x: DeviceArray, key: str, stride: int = 1, pad=(0, 0), act: str = "none",
-                 act_param: float = 0.0) -> DeviceArray:
+                 act_param: float = 0.0, st: Optional[int] = None) -> DeviceArray:
         """conv1d (ops.py:165-219) from channels-first x (C_in, T_in) to channels-last output,
         for the convs on the stack's inputs (conv_pre on the mel, the strided source_downs on
         the source STFT), through the generic strided kernel."""
@@ -247,12 +256,12 @@ class DeviceHiFT:
         out = self._new((n, cout))
         _lib.call("conv1d", x.ptr, cin, t_in, t_in, 1, self.w[key + ".weight"].ptr, cout, k,
                   self.w[key + ".bias"].ptr, stride, 1, 1, pad[0], pad[1], 1, out.ptr, 1, cout, None,
-                  ACT[act], float(act_param), None, 0.0, None, 0, 0, None)
+                  ACT[act], float(act_param), None, 0.0, None, 0, 0, st)
         return out
 
-    def _snake(self, x: DeviceArray, key: str) -> DeviceArray:
+    def _snake(self, x: DeviceArray, key: str, st: Optional[int] = None) -> DeviceArray:
         y = self._new(x.shape)
-        _lib.call("snake_cl", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, None)
+        _lib.call("snake_cl", x.ptr, self.w[key].ptr, y.ptr, x.shape[0], x.shape[1], 1e-9, st)
         return y
 
     def _act(self, x: DeviceArray, name: str, param: float) -> DeviceArray:
@@ -260,18 +269,29 @@ class DeviceHiFT:
         _lib.call("act", ACT[name], float(param), x.ptr, y.ptr, x.size, None)
         return y
 
-    def _resblock(self, group: str, idx: int, x: DeviceArray, kernel: int, dilations) -> DeviceArray:
-        """3 x [snake, dilated causal conv, snake, causal conv] + residual (hift.py:114-129).
-        ``x`` is left untouched; the result is a new buffer."""
+    def _resblock(self, group: str, idx: int, x: DeviceArray, kernel: int, dilations,
+                  st: Optional[int] = None) -> DeviceArray:
+        """3 x [snake, dilated causal conv, snake, causal conv] + residual (hift.py:114-129),
+        on stream handle ``st`` (None: the thread's).  ``x`` is left untouched; the result is a
+        new buffer."""
         base = f"{group}.{idx}."
         cur = x
         for j, d in enumerate(dilations):
-            y = self._snake(cur, base + f"activations1.{j}.alpha")
+            y = self._snake(cur, base + f"activations1.{j}.alpha", st)
             y = self._conv(y, base + f"convs1.{j}", dilation=d, pad=(causal_pad(kernel, d), 0),
-                           snake=base + f"activations2.{j}.alpha")
+                           snake=base + f"activations2.{j}.alpha", st=st)
             out = self._new(x.shape) if cur is x else cur   # in place after the first step
-            cur = self._conv(y, base + f"convs2.{j}", pad=(causal_pad(kernel, 1), 0), residual=cur, out=out)
+            cur = self._conv(y, base + f"convs2.{j}", pad=(causal_pad(kernel, 1), 0), residual=cur, out=out, st=st)
         return cur
+
+    def _branches(self, n: int):
+        """n side streams and n + 1 events for forking independent branches off the thread's
+        stream (inside a capture the forks and joins become graph edges)."""
+        while len(self._side) < n:
+            self._side.append(Stream())
+        while len(self._ev) < n + 1:
+            self._ev.append(Event())
+        return self._side[:n], self._ev[:n + 1]
 
     # -- the spectral stack -------------------------------------------------
     def spectral(self, mel: DeviceArray, s_stft: DeviceArray) -> DeviceArray:
@@ -280,7 +300,17 @@ class DeviceHiFT:
         x = self._conv_in(mel, "conv_pre", pad=(0, causal_pad(kpre)))
         downs = [1] + self.rates[::-1][:-1]
         down_cum = list(np.cumprod(downs))[::-1]
+        # branches only while a stack is recorded or captured: its arena keeps every
+        # intermediate alive, so no buffer a side stream uses is freed and reused meanwhile
+        branch = self._branch and self._arena is not None
         for i, r in enumerate(self.rates):
+            if branch:  # the source branch beside the leaky + upsampling conv
+                side, ev = self._branches(max(1, self.nk - 1))
+                sst = side[0].handle
+                ev[0].record(None)
+                side[0].wait(ev[0])
+            else:
+                sst = None
             xl = self._act(x, "leaky", self.slope)
             k = self.shape[f"ups.{i}.weight"][2]
             cout = self.shape[f"ups.{i}.weight"][0]
@@ -297,16 +327,30 @@ class DeviceHiFT:
             u = int(down_cum[i])
             ks = self.shape[f"source_downs.{i}.weight"][2]
             if u == 1:
-                si = self._conv_in(s_stft, f"source_downs.{i}", pad=(causal_pad(ks), 0))
+                si = self._conv_in(s_stft, f"source_downs.{i}", pad=(causal_pad(ks), 0), st=sst)
             else:
-                si = self._conv_in(s_stft, f"source_downs.{i}", stride=u, pad=(u - 1, 0))
-            si = self._resblock("source_resblocks", i, si, self.src_k[i], self.src_d[i])
+                si = self._conv_in(s_stft, f"source_downs.{i}", stride=u, pad=(u - 1, 0), st=sst)
+            si = self._resblock("source_resblocks", i, si, self.src_k[i], self.src_d[i], st=sst)
+            if branch:
+                ev[1].record(side[0])
+                wait_event(ev[1])
             if si.shape != xu.shape:
                 raise ValueError(f"stage {i}: source branch {si.shape} vs upsampled {xu.shape}")
             xs = self._new(xu.shape)
             _lib.call("binary", 0, xu.ptr, si.ptr, xs.ptr, xs.size, 0.0, 0.0, None)
-            rs = [self._resblock("resblocks", i * self.nk + j, xs, self.rb_k[j], self.rb_d[j])
+            # the resblocks read xs and write their own buffers: resblock j > 0 on side stream
+            # j - 1, joined before the sum
+            if branch:
+                ev[0].record(None)
+                for sd in side:
+                    sd.wait(ev[0])
+            rs = [self._resblock("resblocks", i * self.nk + j, xs, self.rb_k[j], self.rb_d[j],
+                                 st=side[j - 1].handle if branch and j > 0 else None)
                   for j in range(self.nk)]
+            if branch:
+                for j, sd in enumerate(side):
+                    ev[j + 1].record(sd)
+                    wait_event(ev[j + 1])
             acc = rs[0]
             for j in range(1, self.nk):
                 nxt = self._new(xs.shape)
@@ -320,18 +364,19 @@ class DeviceHiFT:
         kpost = self.shape["conv_post.weight"][2]
         return self._conv(x, "conv_post", pad=(causal_pad(kpost), 0), channels_first_out=True)
 
-    def _stack(self, w: int, slot: int = 0):
+    def _stack(self, w: int, slot: int = 0, branches: bool = False):
         """The spectral stack for a w-frame input, captured once per (w, slot): its staging
         inputs, its output and the graph (each slot owns its buffers, so windows on
         different streams run side by side).  Recorded eagerly first (on zeroed inputs),
         then captured with the recorded intermediates (see ``_new``)."""
-        g = self._graphs.get((w, slot))
+        g = self._graphs.get((w, slot, branches))
         if g is None:
             mel_w = DeviceArray((self.shape["conv_pre.weight"][1], w))
             st_w = DeviceArray((self.n_fft + 2, w * self.up_total + 1))
             _lib.call("fill_zero", mel_w.ptr, mel_w.nbytes, None)
             _lib.call("fill_zero", st_w.ptr, st_w.nbytes, None)
             self._arena, self._arena_i = [], -1
+            self._branch = branches and BRANCHES
             try:
                 out = self.spectral(mel_w, st_w)
                 self._arena_i = 0
@@ -343,18 +388,19 @@ class DeviceHiFT:
                 g = (graph, mel_w, st_w, out, self._arena)
             finally:
                 self._arena, self._arena_i = None, -1
-            self._graphs[(w, slot)] = g
+                self._branch = False
+            self._graphs[(w, slot, branches)] = g
         return g
 
     def spectral_graph(self, mel: DeviceArray, s_stft: DeviceArray, c0: int = 0, c1: Optional[int] = None,
-                       slot: int = 0, stream: Optional[Stream] = None):
+                       slot: int = 0, stream: Optional[Stream] = None, branches: bool = False):
         """spectral() of mel[:, c0:c1] and its source STFT columns by graph replay on ``stream``
         (None: the calling thread's); returns the stack's own output buffer, valid until the
         next replay of the same (length, slot)."""
         t = mel.shape[1]
         c1 = t if c1 is None else c1
         w = c1 - c0
-        graph, mel_w, st_w, out, arena = self._stack(w, slot)
+        graph, mel_w, st_w, out, arena = self._stack(w, slot, branches)
         S3 = ctypes.c_int64 * 3
         up = self.up_total
         sh = stream.handle if stream is not None else None
@@ -465,7 +511,7 @@ class DeviceHiFT:
         src_d = source if isinstance(source, DeviceArray) else to_device(np.ascontiguousarray(source, np.float32))
         s_stft = self.source_stft(src_d)
         if chunk is None or mel_d.shape[1] <= chunk:
-            x = self.spectral_graph(mel_d, s_stft) if graph else self.spectral(mel_d, s_stft)
+            x = self.spectral_graph(mel_d, s_stft, branches=True) if graph else self.spectral(mel_d, s_stft)
         else:
             x = self.spectral_chunked(mel_d, s_stft, chunk, context, graph=graph)
         return self.istft_head(x)
