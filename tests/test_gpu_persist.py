@@ -120,7 +120,7 @@ def test_persistent_full_depth_matches_five_kernel_step(gpu, profile):
 
 def test_persistent_step_rejects_too_few_workgroups(gpu):
     """The host checks the launch before it is made: 64 workgroups cannot hold the
-    step's phases (128 o_proj / reduce workgroups, 112 attention items at this cache)."""
+    step's phases (it needs at least 128 workgroups, and 112 attention items at this cache)."""
     from cv3amd.qwen2 import DeviceQwen2
     _, dev, _, _ = _setup(2, "per_channel", 0)
     d = DeviceQwen2(dev, cap=1024)
