@@ -1081,10 +1081,11 @@ constexpr int kPMinG = 128;              // workgroups the step needs at least
 constexpr int kPOproj = 256;             // workgroups of phase C, at most (64: 4 % slower, 96: 2 %, than 128; 256: 1.5 % faster)
 constexpr int kPDown = 256;              // workgroups of phase E, at most (128: 2 % slower)
 // Replicas of the exchanged vectors that many workgroups poll (x: all, x_mid: all,
-// h: 128): workgroup w reads replica w % n.  Measured with the throttled polling
-// below: one copy is 2 % slower, 4 and 8 copies no faster or slower (the producers'
-// extra stores sit on their critical path).
-constexpr int kRX = 2, kRM = 2, kRH = 2, kRA = 2;
+// h: 224, the merged attention output: all): workgroup w reads replica w % n.  Measured
+// with the throttled polling below: one copy is 2 % slower; 4 copies of x_mid are 0.5 %
+// faster than 2 (8: 0.3 % slower), and 1 or 4 copies of x, h or the attention output
+// change nothing (the producers' extra stores sit on their critical path).
+constexpr int kRX = 2, kRM = 4, kRH = 2, kRA = 2;
 
 struct PersistArgs {
   QW qkv, o, gu, dn, head, emb;
