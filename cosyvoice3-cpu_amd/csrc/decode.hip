@@ -1368,7 +1368,8 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
   __shared__ __align__(16) float xin[1024];   // x of the layer (raw), for A's norm and C's residual
   __shared__ __align__(16) float xmid[1024];  // x after o_proj (phase D keeps it for E)
   __shared__ __align__(16) float xs[kXs];     // staged (normed, zero-padded) vector of the dot products
-  __shared__ __align__(16) float big[8192];   // phase B: q, k, v, per-wave partials; C: partials
+  __shared__ __align__(16) float big[8192];   // phase B: q, k, v, per-wave partials, the merge's partials; the head's candidates
+  static_assert(1024 + (kPChunks - 1) * kPPart <= 8192, "the merging item's partials fit after B's per-wave partials");
   __shared__ float red[16];
   __shared__ float hb_val[8];
   __shared__ int hb_i[8];
@@ -1619,7 +1620,7 @@ __global__ __launch_bounds__(kPT) void k_dec_persist(PersistArgs a) {
       }
       __syncthreads();  // big is reused below
     }
-    // ---- C: merge + o_proj rows + residual -> x_mid ----
+    // ---- C: o_proj rows + residual -> x_mid ----
     if (isC) {
       load_C(l);
       // the merged attention output (H dh words, from phase B's merging items) goes straight
@@ -2174,7 +2175,7 @@ int cv3_qwen2_decode_step_persistent(const cv3_qwen2_model* m, const cv3_qwen2_s
               kPMinG, per_cu * cus,
               (long long)I);
   CV3_REQUIRE((H + 2 * Hk) * dh / 2 <= 8LL * G && I <= 24LL * G && m->head.rows <= 32LL * G &&
-                  H * kPChunks <= G && H * kPChunks * kPPart <= 8192,
+                  H * kPChunks <= G && 2LL * G <= 8192,
               CV3_EUNSUPPORTED, "persistent step: too few workgroups for the geometry");
   CV3_REQUIRE(p->words && p->err && p->words_len >= persist_words(m, G), CV3_EINVAL,
               "persistent step: exchange words missing or too few");
