@@ -49,9 +49,9 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 # HBM bytes per launch that rocprofv3 counted (FETCH_SIZE x2 + WRITE_SIZE x1, the factors a 256 MiB
 # device copy needs; `bench.py --kernels --no-graph` under `rocprofv3 --pmc`, one counter per run):
 # the one-launch decode step (24 layers, per-channel int8 with phase D on the int8 matrix cores,
-# KV 512: 400.9 MB read + 7.8 MB written).  Counters cannot be read inside this process, so these
+# KV 512: 400.9 MB read + 9.2 MB written).  Counters cannot be read inside this process, so these
 # are the measured figures for exactly these kernels and shapes.
-TRAFFIC_DECODE_STEP = 408.7e6
+TRAFFIC_DECODE_STEP = 410.1e6
 # the same passes over the 10 s solve's fused QKV GEMM on bfloat16 planes in fragment order
 # (k_gemm_x3f, [1000, 1024] x [3072, 1024]^T): 53.4 MB read + 12.3 MB written
 TRAFFIC_QKV_GEMM_X3 = 65.7e6
