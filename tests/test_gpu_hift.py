@@ -77,6 +77,33 @@ def test_full_width_one_second(gpu, chunk, graph):
     assert e < 1e-4
 
 
+def test_whole_stack_branches_change_nothing(gpu, monkeypatch):
+    """The whole-input stack captured with its branches on forked streams (each stage's source
+    branch beside the upsampling conv, the resblocks side by side) gives the same samples as
+    the stack captured on one stream and as the direct launches: the same kernels on the same
+    buffers, only their order differs.  Replayed three times, with host reads in between."""
+    from cv3amd import synth
+    import cv3amd.hift as hift
+    from cv3amd.hift import DeviceHiFT
+    from cv3amd.weights import WeightStore
+    T = 50
+    t = synth.hift_tensors(base=512)
+    meta = synth.hift_meta()
+    rng = np.random.default_rng(5)
+    mel = (rng.standard_normal((80, T), dtype=np.float32) * 2.0 - 5.0).astype(np.float32)
+    source = np.tanh(rng.standard_normal(480 * T, dtype=np.float32) * 0.1).astype(np.float32)
+    print(f"[hift] base 512, {T} mel frames, whole stack with and without branches", flush=True)
+    direct = DeviceHiFT(WeightStore(t, meta)).decode(mel, source, graph=False).numpy()
+    monkeypatch.setattr(hift, "BRANCHES", False)
+    one = DeviceHiFT(WeightStore(t, meta)).decode(mel, source, graph=True).numpy()
+    monkeypatch.setattr(hift, "BRANCHES", True)
+    d = DeviceHiFT(WeightStore(t, meta))
+    for _ in range(3):
+        got = d.decode(mel, source, graph=True).numpy()
+        assert np.array_equal(got, one)
+    assert np.array_equal(one, direct)
+
+
 def test_toy_inference_on_the_device(gpu, reference_io):
     """mel -> waveform with nothing on the host: the frozen upstream waveform within 2e-3."""
     import oracle.quant
