@@ -61,12 +61,16 @@ FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 matrix
 SPLIT_BF16_PEAK = 2.5e15 / 6
 # q8 weights on the same cores: three products per code (cv3_linear_q8_x3)
 SPLIT_Q8_PEAK = 2.5e15 / 3
+# per-channel q8 weights on the int8 matrix cores (5.0 POP/s dense): four digit-plane products
+# per code (cv3_linear_q8_digits)
+DIGITS_Q8_PEAK = 5.0e15 / 4
 
 
 def matrix_floor_ms(by_unit) -> float:
     """The solve's matrix-core floor: each part of its flops at the peak of the unit it runs on."""
-    six, three, f32 = by_unit
-    return (six / SPLIT_BF16_PEAK + three / SPLIT_Q8_PEAK + f32 / FP32_MFMA_PEAK) * 1e3
+    six, three, f32 = by_unit[:3]
+    four = by_unit[3] if len(by_unit) > 3 else 0.0
+    return (six / SPLIT_BF16_PEAK + three / SPLIT_Q8_PEAK + four / DIGITS_Q8_PEAK + f32 / FP32_MFMA_PEAK) * 1e3
 PREFILL = 512             # KV cache positions pre-filled before each decode
 DECODE_TOKENS = 256       # tokens per decode: KV 512 -> 768
 AUDIO_SECONDS = 10.0       # 500 mel frames at 50 Hz
@@ -546,6 +550,26 @@ def bench_kernels(args):
             log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (SPLIT_Q8_PEAK / 1e12):.1%} of the "
                 f"split q8 peak)")
             out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
+            if block != kk:
+                continue
+            # the same per-channel weight on the int8 matrix cores as the solve runs it (digit planes)
+            qf32 = DeviceArray((-(-n // 32) * 32 * (kp + 4),), np.int8)
+            _lib.call("pack_q8_frag32", qd.ptr, n, kp, kp, qf32.ptr, None)
+            rexp = DeviceArray((BT3,), np.int32)
+            fn = lambda: _lib.call("linear_q8_digits", a_d.ptr, BT3, kk, F, qf32.ptr, sd.ptr, sdt_c, n, None, y.ptr,
+                                   n, None, rexp.ptr, 0, None)
+            run = replayer(args.graph, lambda: [fn() for _ in range(reps)])
+            run()
+            synchronize()
+            tm.start()
+            for _ in range(5):
+                run()
+            us = tm.stop() / (5 * reps) * 1e3
+            rate = 2.0 * BT3 * n * kk / (us * 1e-6) / 1e12
+            name = f"q8 {label} GEMM [{BT3}, {kk}] x [{n}, {kk}]^T (per-channel, int8 digit planes)"
+            log(f"kernels: {name}: {us:.1f} us, {rate:.1f} TFLOP/s ({rate / (DIGITS_Q8_PEAK / 1e12):.1%} of the "
+                f"digit-plane q8 peak)")
+            out[name] = {"us": round(us, 2), "tflops": round(rate, 2)}
     # the 30 s solve's attention: 1500 x 1500 per head, the CFG pair x 16 heads, on bfloat16 planes
     qkv3 = to_device(rng.standard_normal((BT3, 3 * D), dtype=np.float32))
     att3 = DeviceArray((BT3, D), np.float32)
@@ -888,11 +912,15 @@ def main():
     if flow_q8 is not None:
         scales = {"per_channel": "per-output-channel int8 + float32 scales",
                   "balanced": "block-64 int8 + float16 scales (the converter's balanced profile)"}
+        how = {"per_channel": "each activation row rounded 30 bits below its largest element and split into four "
+                              "int8 digit planes, each times the codes an exact int32 sum on the int8 matrix cores, "
+                              "combined in float64 and scaled per output channel",
+               "balanced": "the activation's three bfloat16 planes times the codes (exact in bfloat16), the block "
+                           "scale on each block sum, fp32 accumulate"}
         for prof, fq in flow_q8.items():
             line["flow_q8_30s" if prof == "per_channel" else "flow_q8_30s_block64"] = {
                 "workload": f"DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
-                            f"({scales[prof]}): the activation's three bfloat16 planes times the codes (exact in "
-                            f"bfloat16), the block scale on each block sum, fp32 accumulate",
+                            f"({scales[prof]}): {how[prof]}",
                 "ms_per_solve": round(fq["ms"], 3), "rtf": round(fq["ms"] / 1e3 / 30.0, 6),
                 "tflops": round(fq["flops"] / (fq["ms"] / 1e3) / 1e12, 2),
                 "roofline_ms": round(matrix_floor_ms(fq["by_unit"]), 3),

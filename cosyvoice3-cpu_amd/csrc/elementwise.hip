@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
                                                          const float* __restrict__ w, const float* __restrict__ b,
                                                          const float* __restrict__ shift,
                                                          const float* __restrict__ scale, int64_t mod_stride,
-                                                         int64_t rows_per_group) {
+                                                         int64_t rows_per_group, int* __restrict__ rexp) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -251,6 +251,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
   }
   const float den = sqrtf(wave_sum(q) / (float)cols + eps);
   float4* yr = reinterpret_cast<float4*>(y + row * cols);
+  float mx = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t j = lane + 64 * i;
@@ -267,8 +268,18 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
         if (scale) o[e] = o[e] * (1.0f + cc[e]);
         if (shift) o[e] = o[e] + ss[e];
       }
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
       yr[j] = make_float4(o[0], o[1], o[2], o[3]);
     }
+  }
+  // optionally the binary exponent of the row's largest |y| (frexp, at least -96): the scale
+  // the digit-plane q8 GEMM rounds this row to, so that GEMM needs no pass of its own
+  if (rexp) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    int ex = 0;
+    if (mx > 0.f) (void)frexpf(mx, &ex);
+    if (lane == 0) rexp[row] = max(ex, -96);
   }
 }
 
@@ -466,19 +477,20 @@ int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t
   return CV3_OK;
 }
 
-int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
-                   const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
-                   cv3_stream_t s) {
-  CV3_ALIVE();
-  if (rows <= 0 || cols <= 0) return CV3_OK;
+namespace {
+int layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
+               const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group, int* rexp,
+               cv3_stream_t s) {
   auto a16 = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
   const bool vec = cols % 4 == 0 && cols <= 4096 && a16(x) && a16(y) && a16(w) && a16(b) && a16(shift) &&
                    a16(scale) && mod_stride % 4 == 0;
+  CV3_REQUIRE(!rexp || (vec && cols <= 1024), CV3_EUNSUPPORTED,
+              "row exponents need 16-byte aligned rows of at most 1024 columns (cols = %lld)", (long long)cols);
   if (vec && cols <= 1024) {
     const dim3 grid((unsigned)ceil_div(rows, 4));
 #define CV3_LNW(NV)                                                                                    \
   hipLaunchKernelGGL(k_layer_norm_wave<NV>, grid, dim3(256), 0, stream_of(s), x, y, rows, cols, eps, w, b, \
-                     shift, scale, mod_stride, rows_per_group);
+                     shift, scale, mod_stride, rows_per_group, rexp);
     if (cols <= 256) {
       CV3_LNW(1)
     } else if (cols <= 512) {
@@ -496,6 +508,24 @@ int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float e
                        scale, mod_stride, rows_per_group);
   CV3_LAUNCHED();
   return CV3_OK;
+}
+}  // namespace
+
+int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
+                   const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
+                   cv3_stream_t s) {
+  CV3_ALIVE();
+  if (rows <= 0 || cols <= 0) return CV3_OK;
+  return layer_norm(x, y, rows, cols, eps, w, b, shift, scale, mod_stride, rows_per_group, nullptr, s);
+}
+
+int cv3_layer_norm_rexp(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w,
+                        const float* b, const float* shift, const float* scale, int64_t mod_stride,
+                        int64_t rows_per_group, int32_t* row_exp, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(row_exp, CV3_EINVAL, "layer_norm_rexp needs a row-exponent output");
+  if (rows <= 0 || cols <= 0) return CV3_OK;
+  return layer_norm(x, y, rows, cols, eps, w, b, shift, scale, mod_stride, rows_per_group, row_exp, s);
 }
 
 int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* cos_out, float* sin_out,

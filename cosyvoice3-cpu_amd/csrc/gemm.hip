@@ -1100,6 +1100,181 @@ __global__ __launch_bounds__(256) void k_split_x3(const float* w, int64_t n, int
   }
 }
 
+
+// q8 linears with the activation as four int8 digit planes (per-channel scales).  Row r of A
+// is rounded once to X = rint(a 2^(30 - E_r)), E_r the exponent of the row's largest |a| (every
+// |a| < 2^E_r, so |X| < 2^30), whose bytes are its base-256 digits: X = b0 + 256 b1 + 65536 b2
+// + 2^24 b3 with b0..b2 unsigned (0..255) and b3 = X >> 24 signed (-64..63).  The matrix cores
+// take signed bytes, so planes 0-2 carry b - 128 (the byte with its top bit flipped) and the
+// epilogue adds back 128 times the column's code sum.  Each plane times the int8 codes is an
+// exact int32 sum on v_mfma_i32_32x32x32_i8 (|sum| < 2^31 for K <= 2048), the four are
+// combined exactly in float64, times 2^(E_r - 30) and the column's scale: the dot product of
+// the codes with a rounded 30 bits below the row's largest element.  Four int8 products where
+// the bfloat16 planes need three bfloat16 ones at half the rate; the digits are byte permutes
+// of X, the codes go to the matrix cores as they are, and A takes 4 bytes of LDS per element
+// instead of 6.
+
+// E_r for each row: one wave per row (frexp of the row's largest |a|; at least -96, so
+// 2^(27 - E) stays finite and tiny rows only lose low bits).
+__global__ __launch_bounds__(256) void k_row_exp(const float* __restrict__ a, int64_t m, int64_t k, int64_t lda,
+                                                 int* __restrict__ e) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m) return;
+  const float* r = a + row * lda;
+  float mx = 0.f;
+  for (int64_t j = 4 * lane; j < k; j += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(r + j);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  int ex = 0;
+  if (mx > 0.f) (void)frexpf(mx, &ex);
+  if (lane == 0) e[row] = max(ex, -96);
+}
+
+// frag[i], i = (nb T + t) 64 + l, T = k / 32: the 16 codes q[32 nb + l % 32][32 t + 16 (l / 32) .. + 15]
+// (rows past n zero), the B operand of v_mfma_i32_32x32x32_i8 for 32-row block nb, step t;
+// then (k_q8_row_sums) each row's code sum as int32.
+__global__ __launch_bounds__(256) void k_pack_q8_frag32(const int8_t* q, int64_t n, int64_t k, int64_t ldq, uint4* frag,
+                                                        int64_t total) {
+  const int64_t T = k / 32;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t t = (i >> 6) % T, nb = (i >> 6) / T;
+    const int64_t row = nb * 32 + (l & 31), k0 = 32 * t + 16 * (l >> 5);
+    frag[i] = row < n ? *reinterpret_cast<const uint4*>(q + row * ldq + k0) : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// sums[row] = sum of the row's k codes (rows past n zero): one wave per row.
+__global__ __launch_bounds__(256) void k_q8_row_sums(const int8_t* q, int64_t n, int64_t npad, int64_t k, int64_t ldq,
+                                                     int* sums) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= npad) return;
+  int acc = 0;
+  if (row < n)
+    for (int64_t j = lane; j < k; j += 64) acc += q[row * ldq + j];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) sums[row] = acc;
+}
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x4v __attribute__((ext_vector_type(4)));
+
+// 64 x 64 tiles, four waves of 32 x 32, 64-k stages.  A goes global -> registers -> its four
+// digit planes -> LDS (16-byte chunk c of row r at slot 4 r + (c ^ (r / 4) % 4), so the 16
+// rows a wave reads at one chunk land on 16 different banks); the codes go global -> registers
+// in fragment order (k_pack_q8_frag32), a stage ahead.
+__global__ __launch_bounds__(256) void k_gemm_q8d(GemmParams p, const uint4* qfrag, const int* qsums, const int* rexp,
+                                                  int tiles_m, int tiles_n, int gm) {
+  __shared__ uint4 sA[2][4][BM * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int64_t m0, n0;
+  tile_xcd(blockIdx.x, gridDim.x, tiles_m, tiles_n, gm, m0, n0);
+  const int lr = tid >> 2, lc = tid & 3;  // staging: row lr, k 16 lc .. + 15 of the stage
+  const int64_t arow = min(m0 + lr, p.m - 1);
+  const float* pa = p.a + arow * p.lda + lc * 16;
+  const float up = ldexpf(1.0f, 30 - rexp[arow]);
+  const int wslot = lr * 4 + (lc ^ ((lr >> 2) & 3));
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, r32 = lane & 31, h = lane >> 5;
+  const int ar = wm + r32;
+  const int64_t S = p.k / 64, T32 = p.k / 32;
+  const int64_t nblk = min((n0 + wn) >> 5, (p.n - 1) >> 5);
+  const uint4* fb = qfrag + nblk * T32 * 64 + lane;
+  i32x16 acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = i32x16{0};
+  struct XA {
+    float4 v[4];
+  };
+  struct BQ {
+    uint4 v[2];  // the stage's two 32-k steps
+  };
+  auto load = [&](XA& x, int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.v[i] = *reinterpret_cast<const float4*>(pa + k0 + 4 * i);
+  };
+  auto loadb = [&](BQ& b, int64_t st) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) b.v[ks] = fb[(2 * st + ks) * 64];
+  };
+  auto store = [&](int buf, const XA& x) {
+    uint32_t pl[4][4];  // plane, 4 bytes of the 16 k
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+      const uint32_t X0 = (uint32_t)__float2int_rn(x.v[w4].x * up), X1 = (uint32_t)__float2int_rn(x.v[w4].y * up);
+      const uint32_t X2 = (uint32_t)__float2int_rn(x.v[w4].z * up), X3 = (uint32_t)__float2int_rn(x.v[w4].w * up);
+      // bytes (X0.b0, X1.b0, X0.b1, X1.b1) and (X0.b2, X1.b2, X0.b3, X1.b3), the same for X2, X3
+      const uint32_t lo01 = __builtin_amdgcn_perm(X1, X0, 0x05010400u), hi01 = __builtin_amdgcn_perm(X1, X0, 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(X3, X2, 0x05010400u), hi23 = __builtin_amdgcn_perm(X3, X2, 0x07030602u);
+      pl[0][w4] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+      pl[1][w4] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+      pl[2][w4] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+      pl[3][w4] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sA[buf][q][wslot] = make_uint4(pl[q][0], pl[q][1], pl[q][2], pl[q][3]);
+  };
+  auto mma = [&](int buf, const BQ& b) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 2 + h;
+      const int sa = ar * 4 + (c ^ ((ar >> 2) & 3));
+      const i32x4v bq = __builtin_bit_cast(i32x4v, b.v[ks]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4v, sA[buf][q][sa]), bq, acc[q], 0, 0, 0);
+    }
+  };
+  XA x, y;
+  BQ b0, b1;
+  load(x, 0);
+  if (S > 1) load(y, 64);
+  loadb(b0, 0);
+  if (S > 1) loadb(b1, 1);
+  store(0, x);
+  __syncthreads();
+  int64_t s = 0;
+  for (; s + 2 < S; s += 2) {
+    load(x, (s + 2) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0, b0);
+    loadb(b0, s + 2);
+    store(1, y);
+    __syncthreads();
+    load(y, (s + 3) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, b1);
+    loadb(b1, s + 3);
+    store(0, x);
+    __syncthreads();
+  }
+  mma(0, b0);
+  if (s + 1 < S) {
+    store(1, y);
+    __syncthreads();
+    mma(1, b1);
+  }
+  // T = sum_q 256^q acc_q + 128 (1 + 256 + 65536) (the column's code sum) exactly in float64,
+  // times 2^(E - 30) and the column's scale
+  const int64_t col = min(n0 + wn + r32, p.n - 1);
+  const double sc = p.sf16 ? (double)__half2float(reinterpret_cast<const __half*>(p.scales)[col])
+                           : (double)reinterpret_cast<const float*>(p.scales)[col];
+  const double corr = 128.0 * 65793.0 * (double)qsums[col];
+  f32x16 out;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = min(m0 + wm + (i >> 2) * 8 + h * 4 + (i & 3), p.m - 1);
+    const double t = (double)acc[0][i] + 256.0 * (double)acc[1][i] + 65536.0 * (double)acc[2][i] +
+                     16777216.0 * (double)acc[3][i] + corr;
+    out[i] = (float)(t * ldexp(1.0, rexp[row] - 30) * sc);
+  }
+  store_tile(p, out, m0 + wm, h, n0 + wn + r32);
+}
 }  // namespace
 
 namespace cv3 {
@@ -1255,6 +1430,60 @@ int gemm_x3qf(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* q
   const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, (double)n * k);
   hipLaunchKernelGGL(k_gemm_x3qf, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
                      reinterpret_cast<const uint2*>(qfrag), (int)tiles_m, (int)tiles_n, gm);
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+
+int pack_q8_frag32(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, hipStream_t st) {
+  CV3_REQUIRE(k % 64 == 0 && ((uintptr_t)q % 16 == 0) && ldq % 16 == 0 && ldq >= k && ((uintptr_t)frag % 16 == 0),
+              CV3_EINVAL, "digit-plane codes need K %% 64 == 0 and 16-byte aligned rows");
+  const int64_t npad = ceil_div(n, 32) * 32, total = npad * k / 16;  // 16-byte fragments
+  if (total == 0) return CV3_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipLaunchKernelGGL(k_pack_q8_frag32, dim3((unsigned)blocks), dim3(256), 0, st, q, n, k, ldq,
+                     reinterpret_cast<uint4*>(frag), total);
+  hipLaunchKernelGGL(k_q8_row_sums, dim3((unsigned)ceil_div(npad, 4)), dim3(256), 0, st, q, n, npad, k, ldq,
+                     reinterpret_cast<int*>(frag + npad * k));
+  CV3_LAUNCHED();
+  return CV3_OK;
+}
+
+// C = epi(A . dequant(q)^T) with A as four int8 digit planes per row and per-channel scales [n];
+// rexp: m ints of workspace (the rows' exponents, written here first).
+int gemm_q8d(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* qfrag32, const void* scales, bool sf16,
+             int64_t n, const float* bias, float* c, int64_t ldc, const cv3_epilogue* epi, int* rexp, bool rexp_given, hipStream_t st) {
+  CV3_REQUIRE(k % 64 == 0 && k <= 2048, CV3_EUNSUPPORTED,
+              "digit-plane q8 GEMM needs K %% 64 == 0 and K <= 2048 (K = %lld)", (long long)k);
+  CV3_REQUIRE(((uintptr_t)a % 16 == 0) && lda % 4 == 0 && ((uintptr_t)qfrag32 % 16 == 0) && rexp, CV3_EINVAL,
+              "digit-plane q8 GEMM operands must be aligned rows, with a row-exponent workspace");
+  GemmParams p{};
+  p.a = a;
+  p.lda = lda;
+  p.scales = scales;
+  p.sf16 = sf16;
+  p.nb = 1;
+  p.block = k;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.bias = bias;
+  p.c = c;
+  p.ldc = ldc;
+  p.epi = epi ? *epi : cv3_epilogue{};
+  CV3_REQUIRE(!p.epi.rope_cos || (p.epi.rope_rows > 0 && p.epi.rope_period > 0 && p.epi.rope_width > 0 &&
+                                  p.epi.rope_rows * p.epi.rope_width < (1ll << 31) && m + 64 < (1ll << 31) &&
+                                  n < (1ll << 31)),
+              CV3_EINVAL, "rotary epilogue: table or GEMM beyond 32-bit indexing");
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  CV3_REQUIRE(tiles_m * tiles_n < (1ll << 31), CV3_EINVAL, "GEMM too large");
+  if (!rexp_given)
+    hipLaunchKernelGGL(k_row_exp, dim3((unsigned)ceil_div(m, 4)), dim3(256), 0, st, a, m, k, lda, rexp);
+  const int gm = tile_group(tiles_m, tiles_n, 4.0 * (double)m * k, (double)n * k);
+  hipLaunchKernelGGL(k_gemm_q8d, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, p,
+                     reinterpret_cast<const uint4*>(qfrag32),
+                     reinterpret_cast<const int*>(qfrag32 + ceil_div(n, 32) * 32 * k), rexp, (int)tiles_m,
+                     (int)tiles_n, gm);
   CV3_LAUNCHED();
   return CV3_OK;
 }

@@ -20,6 +20,9 @@ int split_x3_frag(const float* w, int64_t n, int64_t k, int64_t ldw, uint16_t* f
 int gemm_x3f(const float* a, int64_t m, int64_t k, int64_t lda, const uint16_t* frag, int64_t n, const float* bias,
              float* c, int64_t ldc, const cv3_epilogue* epi, hipStream_t st);
 int pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, hipStream_t st);
+int pack_q8_frag32(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, hipStream_t st);
+int gemm_q8d(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* qfrag32, const void* scales, bool sf16,
+             int64_t n, const float* bias, float* c, int64_t ldc, const cv3_epilogue* epi, int* rexp, bool rexp_given, hipStream_t st);
 int gemm_x3qf(const float* a, int64_t m, int64_t k, int64_t lda, const int8_t* qfrag, const void* scales, bool sf16,
               int64_t nb, int64_t block, int64_t n, const float* bias, float* c, int64_t ldc,
               const cv3_epilogue* epi, hipStream_t st);
@@ -130,6 +133,24 @@ int cv3_linear_q8_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, con
   if (!m || !n) return CV3_OK;
   return gemm_x3qf(x, m, k, ldx, qfrag, scales, scale_dtype == CV3_F16, kp / block, block, n, bias, y, ldy, epi,
                    stream_of(s));
+}
+
+int cv3_pack_q8_frag32(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(n >= 0 && k > 0 && ldq >= k, CV3_EINVAL, "bad code pack shape n=%lld k=%lld", (long long)n,
+              (long long)k);
+  return pack_q8_frag32(q, n, k, ldq, frag, stream_of(s));
+}
+
+int cv3_linear_q8_digits(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qfrag32, const void* scales,
+                         int scale_dtype, int64_t n, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
+                         int32_t* row_exp, int row_exp_given, cv3_stream_t s) {
+  CV3_ALIVE();
+  CV3_REQUIRE(m >= 0 && k > 0 && ldx >= k && ldy >= n, CV3_EINVAL, "bad quantised linear shape m=%lld k=%lld",
+              (long long)m, (long long)k);
+  if (!m || !n) return CV3_OK;
+  return gemm_q8d(x, m, k, ldx, qfrag32, scales, scale_dtype == CV3_F16, n, bias, y, ldy, epi, row_exp,
+                  row_exp_given != 0, stream_of(s));
 }
 
 // quant.qmatmul on q8 weights (quant.py:165-190) with the activation as bfloat16 planes and

@@ -55,6 +55,15 @@ def _host(a) -> np.ndarray:
     return a.numpy() if isinstance(a, DeviceArray) else np.asarray(a)
 
 
+# True puts the per-channel q8 QKV and ff1 linears of the DiT on the int8 matrix cores as digit
+# planes (cv3_linear_q8_digits; 5x smaller error against float64), their row exponents written by
+# the layer norm that feeds them (cv3_layer_norm_rexp).  Off: at the 30 s shapes (3000 rows) the
+# digit-plane QKV ran 78.6-85.1 us against 85.6-86.3 us on the bfloat16 planes
+# (cv3_linear_q8_x3_frag) depending on the machine, and the whole 30 s solve 1.0-1.1 ms slower
+# (92.9 against 91.9 ms); out and ff2 (1024 outputs) were no faster at all.
+DIGITS = False
+
+
 class DeviceLinear:
     """One resident linear weight: float32 ``[N, K]`` or q8 codes + scales.
 
@@ -65,12 +74,17 @@ class DeviceLinear:
     registers (``cv3_linear_x3_frag``): the same float32 linear, with errors against float64
     no larger than the float32 matrix cores' own.  A q8 weight (blocks of a multiple of 64) then runs
     as the activation's three planes times its codes, exact in bfloat16, with the block
-    scale on each block's sum (``cv3_linear_q8_x3``).
+    scale on each block's sum (``cv3_linear_q8_x3``); with one scale per row (per-channel,
+    K <= 2048) it runs on the int8 matrix cores instead, the activation's rows as four int8 digit
+    planes (``cv3_linear_q8_digits``, exact products of the codes with each row rounded 30 bits
+    below its largest element), given ``rexp``, an int32 workspace of at least m entries.
     """
 
-    def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]], planes: bool = False):
+    def __init__(self, weights: List[object], biases: List[Optional[np.ndarray]], planes: bool = False,
+                 digits: bool = False):
         ws = list(weights)
         self.planes = None
+        self.rexp: Optional[DeviceArray] = None
         if all(_is_q(w) for w in ws):
             kinds = {w.kind for w in ws}
             blocks = {int(w.block) for w in ws}
@@ -92,12 +106,21 @@ class DeviceLinear:
             # the activation's bfloat16 planes times the codes, held in the matrix cores' fragment
             # order (cv3_pack_q8_frag, cv3_linear_q8_x3_frag)
             self.q8_planes = bool(planes) and self.k % 64 == 0 and self.block % 64 == 0
-            if self.q8_planes:
+            # per-channel codes on the int8 matrix cores (cv3_pack_q8_frag32, cv3_linear_q8_digits)
+            self.q8_digits = (self.q8_planes and digits and DIGITS and self.kp == self.block
+                              and self.k <= 2048)
+            if self.q8_digits:
+                npad = -(-self.n // 32) * 32
+                qf = DeviceArray((npad * (self.k + 4),), np.int8)
+                _lib.call("pack_q8_frag32", self.q.ptr, self.n, self.k, self.kp, qf.ptr, None)
+                self.q = qf
+                self.q8_planes = False
+            elif self.q8_planes:
                 qf = DeviceArray((-(-self.n // 32) * 32 * self.k,), np.int8)
                 _lib.call("pack_q8_frag", self.q.ptr, self.n, self.k, self.kp, qf.ptr, None)
                 self.q = qf
         elif not any(_is_q(w) for w in ws):
-            self.q8 = False
+            self.q8 = self.q8_digits = False
             w = np.concatenate([np.asarray(_host(w), dtype=np.float32).reshape(np.shape(w)[0], -1) for w in ws],
                                axis=0)
             self.n, self.k = w.shape
@@ -125,11 +148,18 @@ class DeviceLinear:
             return self.q.nbytes + self.scales.nbytes
         return self.planes.nbytes if self.planes is not None else self.w.nbytes
 
-    def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None):
-        """y[m, n] = epi(x[m, :k] . W^T + bias) on the calling thread's stream."""
+    def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None, rexp_given: bool = False):
+        """y[m, n] = epi(x[m, :k] . W^T + bias) on the calling thread's stream.  ``rexp_given``: the
+        digit-plane path's row exponents of this x are already in ``rexp`` (cv3_layer_norm_rexp)."""
         b = self.bias.ptr if self.bias is not None else None
         e = ctypes.byref(epi) if epi is not None else None
-        if self.q8:
+        if self.q8_digits:
+            if self.rexp is None or self.rexp.size < m:
+                raise ValueError("the digit-plane linear needs an int32 workspace of m entries (rexp)")
+            _lib.call("linear_q8_digits", x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
+                      _lib.F16 if self.sf16 else _lib.F32, self.n, b, y, ldy, e, self.rexp.ptr,
+                      int(rexp_given), None)
+        elif self.q8:
             fn = "linear_q8_x3_frag" if self.q8_planes else "linear_q"
             kind = () if self.q8_planes else (_lib.KIND_Q8,)
             _lib.call(fn, *kind, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
@@ -233,9 +263,10 @@ class DeviceDiT:
         for i in range(self.depth):
             b = f"transformer_blocks.{i}."
             self.qkv.append(DeviceLinear([g(b + f"attn.to_{p}.weight") for p in "qkv"],
-                                         [g(b + f"attn.to_{p}.bias") for p in "qkv"], planes))
+                                         [g(b + f"attn.to_{p}.bias") for p in "qkv"], planes, digits=True))
             self.out.append(DeviceLinear([g(b + "attn.to_out.0.weight")], [g(b + "attn.to_out.0.bias")], planes))
-            self.ff1.append(DeviceLinear([g(b + "ff.ff.0.0.weight")], [g(b + "ff.ff.0.0.bias")], planes))
+            self.ff1.append(DeviceLinear([g(b + "ff.ff.0.0.weight")], [g(b + "ff.ff.0.0.bias")], planes,
+                                         digits=True))
             self.ff2.append(DeviceLinear([g(b + "ff.ff.2.weight")], [g(b + "ff.ff.2.bias")], planes))
         self.ff_dim = self.ff1[0].n if self.depth else 2 * D
         self.proj_out = DeviceLinear([g("proj_out.weight")], [g("proj_out.bias")], planes)
@@ -269,6 +300,11 @@ class DeviceDiT:
             self.x = DeviceArray((mel, T))
             c, s = dit_rope_tables(T, self.dim_head)
             self.cos, self.sin = to_device(c), to_device(s)
+            # the row exponents of the digit-plane linears' input (the modulated norm), one at a time
+            self.rexp = DeviceArray((B * T,), np.int32)
+            for lin in (*self.qkv, *self.ff1):
+                if lin.q8_digits:
+                    lin.rexp = self.rexp
         self.ts, self.dts = euler_schedule(self.steps)
         S = self.steps
         self.sin_feat = to_device(sinus_features(self.ts))
@@ -286,6 +322,16 @@ class DeviceDiT:
         self.time2(self.temb_h.ptr, S, D, self.temb.ptr, D)
         _lib.call("act", ACT["silu"], 0.0, self.temb.ptr, self.stemb.ptr, S * D, None)
         self.mod(self.stemb.ptr, S, D, self.mods.ptr, self.ld_mod)
+
+    def _norm(self, shift: int, scale: int, rexp: bool):
+        """n = LN(h) (1 + scale) + shift over all B T rows (dit.py:168-169), with the rows'
+        exponents into ``self.rexp`` when a digit-plane linear reads n next."""
+        BT, D = 2 * self._T, self.dim
+        if rexp:
+            _lib.call("layer_norm_rexp", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, shift, scale, 0, 0,
+                      self.rexp.ptr, None)
+        else:
+            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, shift, scale, 0, 0, None)
 
     def _step(self, s: int, dt: float, update: bool = True):
         T, D, B, mel, H, dh = self._T, self.dim, 2, self.mel, self.heads, self.dim_head
@@ -313,16 +359,16 @@ class DeviceDiT:
         for i in range(self.depth):
             base = mrow + i * 6 * D * f4
             sh_a, sc_a, g_a, sh_m, sc_m, g_m = (base + j * D * f4 for j in range(6))
-            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_a, sc_a, 0, 0, None)
+            self._norm(sh_a, sc_a, self.qkv[i].q8_digits)
             # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120), in the GEMM epilogue
-            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D, rope_epi)
+            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D, rope_epi, rexp_given=True)
             _lib.call("attention_x3" if self.planes else "attention", self.qkvb.ptr, self.qkvb.ptr + D * f4,
                       self.qkvb.ptr + 2 * D * f4, self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0,
                       None)
             self.out[i](self.att.ptr, BT, D, self.h.ptr, D,
                         _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_a, gate_stride=0, rows_per_gate=1))
-            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, sh_m, sc_m, 0, 0, None)
-            self.ff1[i](self.n.ptr, BT, D, self.ffb.ptr, self.ff_dim, _lib.epilogue("gelu_tanh"))
+            self._norm(sh_m, sc_m, self.ff1[i].q8_digits)
+            self.ff1[i](self.n.ptr, BT, D, self.ffb.ptr, self.ff_dim, _lib.epilogue("gelu_tanh"), rexp_given=True)
             self.ff2[i](self.ffb.ptr, BT, self.ff_dim, self.h.ptr, D,
                         _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_m, gate_stride=0, rows_per_gate=1))
         base = mrow + self.depth * 6 * D * f4      # norm_out: (scale, shift) (dit.py:175-178)
@@ -367,7 +413,8 @@ class DeviceDiT:
     def flops_by_unit(self):
         """Flops of one solve by how they run: (float32 weights on bfloat16 planes, six
         products each; q8 weights on bfloat16 planes, three products each; the rest on the
-        float32 matrix cores)."""
+        float32 matrix cores; per-channel q8 weights on the int8 matrix cores, four digit-plane
+        products each)."""
         T, D, B = self._T, self.dim, 2
         M = B * T
         lins = [*self.qkv, *self.out, *self.ff1, *self.ff2, self.proj_in, self.proj_out]
@@ -377,7 +424,8 @@ class DeviceDiT:
         if self.conv_planes:                      # the conv_pos convs (cv3_conv1d_cl_x3f)
             six += self.steps * 2 * 2.0 * M * D * (D // self.conv_groups) * self.conv_k
         three = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.q8 and l.q8_planes)
-        return six, three, self.flops_per_solve() - six - three
+        four = self.steps * sum(2.0 * M * l.n * l.k for l in lins if l.q8_digits)
+        return six, three, self.flops_per_solve() - six - three - four, four
 
     def flops_per_solve(self) -> float:
         """Algorithmic flops of one solve (every contraction, 2 flops per MAC)."""

@@ -167,6 +167,21 @@ int cv3_pack_q8_frag(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t*
 int cv3_linear_q8_x3_frag(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qfrag, const void* scales,
                           int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y,
                           int64_t ldy, const cv3_epilogue* epi, cv3_stream_t s);
+/* quant.qmatmul on q8 weights with per-channel scales (quant.py:165-190) on the int8 matrix cores:
+ * each activation row rounded once to X = rint(x 2^(30 - E)) (E the exponent of the row's largest
+ * |x|) and split into its four bytes as int8 digit planes, each plane times the codes an exact
+ * int32 sum, the four combined in float64, times 2^(E - 30) and the output column's scale: the dot
+ * product of the codes with x rounded 30 bits below the row's largest element.  The codes packed
+ * once by cv3_pack_q8_frag32: frag[nb][t][l] = the 16 codes q[32 nb + l % 32][32 t + 16 (l / 32) .. + 15],
+ * rows past n zero, then each row's code sum as int32 (npad = ceil(n / 32) * 32: npad * k + 4 npad
+ * bytes); scales [n].  row_exp: m int32, the rows' exponents, computed here into it (row_exp_given
+ * = 0) or already there (row_exp_given = 1: cv3_layer_norm_rexp wrote them for this x).  K % 64 == 0,
+ * K <= 2048, 16-byte aligned rows. */
+int cv3_pack_q8_frag32(const int8_t* q, int64_t n, int64_t k, int64_t ldq, int8_t* frag, cv3_stream_t s);
+int cv3_linear_q8_digits(const float* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qfrag32, const void* scales,
+                         int scale_dtype, int64_t n, const float* bias, float* y, int64_t ldy, const cv3_epilogue* epi,
+                         int32_t* row_exp, int row_exp_given,
+                         cv3_stream_t s);
 /* Quantised weights (q8: q [n, kp] int8; q4: q [n, kp/2]); scales [n, kp/block] (f16 or f32). */
 int cv3_linear_q(int kind, const float* x, int64_t m, int64_t k, int64_t ldx, const void* q, const void* scales,
                  int scale_dtype, int64_t kp, int64_t block, int64_t n, const float* bias, float* y, int64_t ldy,
@@ -191,6 +206,14 @@ int cv3_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t
 int cv3_layer_norm(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w, const float* b,
                    const float* shift, const float* scale, int64_t mod_stride, int64_t rows_per_group,
                    cv3_stream_t s);
+/* cv3_layer_norm that also writes each row's binary exponent row_exp[r] = max(e, -96), e the
+ * frexp exponent of the row's largest |y| (0 for an all-zero row): the row scale
+ * cv3_linear_q8_digits rounds to, handed to it with row_exp_given = 1.  Rows of at most 1024
+ * columns, 16-byte aligned (else CV3_EUNSUPPORTED).  No counterpart in the reference: it fuses
+ * the pass the digit-plane GEMM needs into the norm that feeds the GEMM (dit.py:168-169,178). */
+int cv3_layer_norm_rexp(const float* x, float* y, int64_t rows, int64_t cols, float eps, const float* w,
+                        const float* b, const float* shift, const float* scale, int64_t mod_stride,
+                        int64_t rows_per_group, int32_t* row_exp, cv3_stream_t s);
 /* rotary tables: kind 0 = DiT rope_freqs + fp32 cos/sin (dit.py:21-29,51-52); kind 1 = Qwen2 RopeCache (qwen2.py:46-56).
  * cos/sin [n, dim] for positions pos0 .. pos0+n-1. */
 int cv3_rope_table(int kind, double theta, int dim, int64_t n, int64_t pos0, float* cos_out, float* sin_out,

@@ -443,3 +443,187 @@ def test_linear_q8_x3_frag_is_linear_q8_x3(lib, m, k, n, block, sdt):
     want_qf = qp.reshape(nb, 32, k // 16, 2, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
     np.testing.assert_array_equal(qf, want_qf)
     np.testing.assert_array_equal(got, linear_q8_x3(lib, q, s, kp, block, x, n, b))
+
+
+# ---- per-channel q8 linears on the int8 matrix cores (four int8 digit planes of the activation) ----
+
+def linear_q8_digits(lib, q, s, x, n, bias=None, epi=None, rexp_in=None):
+    """cv3_linear_q8_digits; returns the output, the packed codes and the row exponents (``rexp_in``:
+    exponents handed in with row_exp_given = 1 instead of computed)."""
+    _lib, to_device, empty = lib
+    m, k = x.shape
+    dx = to_device(np.ascontiguousarray(x, np.float32))
+    dq = to_device(np.ascontiguousarray(q))
+    npad = -(-n // 32) * 32
+    qf = empty((npad * (k + 4),), np.int8)
+    _lib.call("pack_q8_frag32", dq.ptr, n, k, q.shape[1], qf.ptr, None)
+    ds = to_device(np.ascontiguousarray(s))
+    db = to_device(np.asarray(bias, np.float32)) if bias is not None else None
+    y = empty((m, n))
+    rexp = empty((max(m, 1),), np.int32) if rexp_in is None else to_device(np.asarray(rexp_in, np.int32))
+    _lib.call("linear_q8_digits", dx.ptr, m, k, k, qf.ptr, ds.ptr, _lib.F16 if s.dtype == np.float16 else _lib.F32,
+              n, db.ptr if db is not None else None, y.ptr, n, ctypes.byref(epi) if epi is not None else None,
+              rexp.ptr, int(rexp_in is not None), None)
+    return y.numpy(), qf.numpy(), rexp.numpy()[:m]
+
+
+def digits_numpy(x, q, s):
+    """The digit-plane product restated: each row rounded to X = rint(x 2^(30 - E)) (E: frexp of the
+    row's largest |x|, at least -96), the int8 codes times X exactly, times 2^(E - 30) and the scale."""
+    mx = np.abs(x).max(axis=1)
+    e = np.where(mx > 0, np.frexp(mx)[1], 0).astype(np.int64)
+    e = np.maximum(e, -96)
+    X = np.rint(x.astype(np.float64) * np.exp2(30 - e)[:, None]).astype(np.int64)
+    t = X @ q.astype(np.int64).T                       # exact integers
+    return t.astype(np.float64) * np.exp2(e - 30)[:, None] * s.astype(np.float64).reshape(1, -1), e
+
+
+DIGIT_CASES = [(3000, 1024, 3072, np.float32), (3000, 2048, 1024, np.float32), (1000, 320, 1024, np.float32),
+               (77, 128, 80, np.float32), (65, 64, 130, np.float16), (1, 2048, 32, np.float32)]
+
+
+@pytest.mark.parametrize("m,k,n,sdt", DIGIT_CASES)
+def test_linear_q8_digits_matches_oracle(lib, m, k, n, sdt):
+    """Per-channel scales at the 30 s DiT shapes, proj_in's K = 320, ragged m and n: the codes in
+    fragment order followed by each row's code sum; the row exponents; the output against the oracle
+    within 1e-5 and against float64 no worse than the bfloat16-plane kernel on the same inputs; every
+    output within 1e-6 of a float64 restatement of the digit-plane arithmetic (its only rounding is
+    the final float32 one)."""
+    rng = np.random.default_rng(m + 3 * k + n)
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, kp = refq.quantize_q8(w, k, sdt)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    x[0, :] = 0.0                                    # a zero row
+    if m > 2:
+        x[1] *= np.float32(1e-30)                    # a tiny row (exponent clamped at -96)
+        x[2, 0] = np.float32(3e4)                    # a wide row: one large element
+    b = (rng.normal(size=n) * 0.02).astype(np.float32)
+    print(f"[q8d] m={m} k={k} n={n} {np.dtype(sdt).name}", flush=True)
+    got, qf, rexp = linear_q8_digits(lib, q, s, x, n, b)
+    npad = -(-n // 32) * 32
+    qp = np.zeros((npad, k), np.int8)
+    qp[:n] = q[:, :k]
+    want_qf = qp.reshape(npad // 32, 32, k // 32, 2, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+    np.testing.assert_array_equal(qf[:npad * k], want_qf)
+    np.testing.assert_array_equal(qf[npad * k:].view(np.int32), qp.astype(np.int32).sum(axis=1))
+    want_dig, e = digits_numpy(x, q[:, :k], s[:, 0])
+    np.testing.assert_array_equal(rexp, e)
+    want_dig = want_dig + b.astype(np.float64)
+    assert np.abs(got - want_dig).max() <= 1e-6 * np.abs(want_dig).max() + 1e-30
+    want = refq.qmatmul(x, refq.QTensor("q8", q, s, (n, k), k), b)
+    assert rel_err(got, want) < TOL
+    wd = refq.QTensor("q8", q, s, (n, k), k).dequant().astype(np.float64)
+    exact = x.astype(np.float64) @ wd.T + b
+    e_dig = np.abs(got - exact).max()
+    e_x3 = np.abs(linear_q8_x3(lib, q, s, kp, k, x, n, b) - exact).max()
+    print(f"[q8d]   max err vs float64: digit planes {e_dig:.3e}, bfloat16 planes {e_x3:.3e}", flush=True)
+    assert e_dig <= e_x3 * 1.25 + 1e-30
+
+
+def test_linear_q8_digits_epilogues(lib):
+    """The DiT's epilogues on the digit-plane kernel: GELU, the gated in-place residual and the
+    rotary of the QKV projection, against the bfloat16-plane kernel with the same epilogue."""
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(11)
+    m, k, n = 1000, 1024, 1024
+    w = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+    q, s, kp = refq.quantize_q8(w, k, np.float32)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    res = rng.normal(size=(m, n)).astype(np.float32)
+    gate = rng.normal(size=(2, n)).astype(np.float32)
+    dres, dgate = to_device(res), to_device(gate)
+    e = _lib.epilogue("gelu_tanh", residual=dres.ptr, ld_res=n, gate=dgate.ptr, gate_stride=n, rows_per_gate=500)
+    got, _, _ = linear_q8_digits(lib, q, s, x, n, None, e)
+    want = linear_q8_x3(lib, q, s, kp, k, x, n, None, e)
+    assert rel_err(got, want) < TOL
+    cs = rng.normal(size=(500, 64)).astype(np.float32)
+    sn = rng.normal(size=(500, 64)).astype(np.float32)
+    dcs, dsn = to_device(cs), to_device(sn)
+    er = _lib.epilogue("none")
+    er.rope_cos, er.rope_sin = dcs.ptr, dsn.ptr
+    er.rope_rows, er.rope_width, er.rope_period, er.rope_limit = 500, 64, 64, 128
+    got, _, _ = linear_q8_digits(lib, q, s, x, n, None, er)
+    want = linear_q8_x3(lib, q, s, kp, k, x, n, None, er)
+    assert rel_err(got, want) < TOL
+
+
+def test_linear_q8_digits_rejects_long_or_ragged_k(lib):
+    """K above 2048 could overflow a plane's int32 sum: the product is refused; codes whose K is not
+    a multiple of 64 are refused at packing."""
+    q, s, _ = refq.quantize_q8(np.ones((32, 4096), np.float32), 4096, np.float32)
+    with pytest.raises(NotImplementedError):
+        linear_q8_digits(lib, q, s, np.ones((4, 4096), np.float32), 32)
+    q, s, _ = refq.quantize_q8(np.ones((32, 96), np.float32), 96, np.float32)
+    with pytest.raises(ValueError):
+        linear_q8_digits(lib, q, s, np.ones((4, 96), np.float32), 32)
+
+
+@pytest.mark.parametrize("modulate", [True, False])
+def test_layer_norm_rexp_feeds_digits(lib, modulate):
+    """cv3_layer_norm_rexp at the DiT's 30 s shape: the same output as cv3_layer_norm, bit for bit;
+    each row's exponent that of the row's largest |y| (an all-zero row 0); and the digit-plane linear
+    given those exponents equal, bit for bit, to the one that computes them itself."""
+    _lib, to_device, empty = lib
+    rng = np.random.default_rng(5 + modulate)
+    m, d, n = 3000, 1024, 1024
+    h = rng.normal(size=(m, d)).astype(np.float32)
+    h[7] = 2.5                                       # a constant row: LN gives 0 (then the shift)
+    h[8] *= np.float32(1e-3)
+    sh = (rng.normal(size=d) * 0.1).astype(np.float32)
+    sc = (rng.normal(size=d) * 0.1).astype(np.float32)
+    dh, dsh, dsc = to_device(h), to_device(sh), to_device(sc)
+    shp, scp = (dsh.ptr, dsc.ptr) if modulate else (None, None)
+    y0, y1 = empty((m, d)), empty((m, d))
+    rexp = empty((m,), np.int32)
+    print(f"[lnrexp] m={m} d={d} modulate={modulate}", flush=True)
+    _lib.call("layer_norm", dh.ptr, y0.ptr, m, d, 1e-6, None, None, shp, scp, 0, 0, None)
+    _lib.call("layer_norm_rexp", dh.ptr, y1.ptr, m, d, 1e-6, None, None, shp, scp, 0, 0, rexp.ptr, None)
+    y = y1.numpy()
+    np.testing.assert_array_equal(y, y0.numpy())
+    mx = np.abs(y).max(axis=1)
+    want = np.maximum(np.where(mx > 0, np.frexp(mx)[1], 0), -96).astype(np.int32)
+    if not modulate:
+        assert want[7] == 0
+    got_e = rexp.numpy()
+    np.testing.assert_array_equal(got_e, want)
+    w = (rng.normal(size=(n, d)) * 0.02).astype(np.float32)
+    q, s, _ = refq.quantize_q8(w, d, np.float32)
+    a, _, e_self = linear_q8_digits(lib, q, s, y, n)
+    b, _, _ = linear_q8_digits(lib, q, s, y, n, rexp_in=got_e)
+    np.testing.assert_array_equal(e_self, got_e)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_layer_norm_rexp_refuses_wide_rows(lib):
+    """Row exponents come from the one-wave-per-row norm: rows wider than 1024 are refused."""
+    _lib, to_device, empty = lib
+    x = to_device(np.ones((4, 2048), np.float32))
+    y, e = empty((4, 2048)), empty((4,), np.int32)
+    with pytest.raises(NotImplementedError):
+        _lib.call("layer_norm_rexp", x.ptr, y.ptr, 4, 2048, 1e-6, None, None, None, None, 0, 0, e.ptr, None)
+
+
+def test_dit_digits_switch(lib, monkeypatch):
+    """The DiT with its per-channel q8 QKV and ff1 linears on the digit planes (row exponents from
+    the layer norm) against the same DiT on the bfloat16 planes: two blocks, 256 frames, two Euler
+    steps, outputs within 1e-5."""
+    import cv3amd.dit as dit
+    import cv3amd.quant as quant
+    from cv3amd import synth
+    from cv3amd.weights import WeightStore
+    rng = np.random.default_rng(21)
+    T = 256
+    t2, meta = synth.dit_tensors(depth=2), synth.dit_meta(depth=2)
+    qt = synth.quantize_store(t2, "per_channel", quant.quantize_q8)
+    mu, cond, x0 = (rng.standard_normal((1, 80, T), dtype=np.float32) for _ in range(3))
+    spks = rng.standard_normal((1, 80), dtype=np.float32)
+    outs = []
+    for digits in (False, True):
+        monkeypatch.setattr(dit, "DIGITS", digits)
+        d = dit.DeviceDiT(WeightStore(qt, meta, quant.QTensor), steps=2)
+        assert d.qkv[0].q8_digits == digits and d.ff1[1].q8_digits == digits
+        assert not d.out[0].q8_digits and not d.ff2[0].q8_digits
+        d.prepare(mu, spks, cond)
+        print(f"[dit-digits] digits={digits} T={T}", flush=True)
+        outs.append(d.solve(x0).numpy().copy())
+    assert rel_err(outs[1], outs[0]) < 1e-5
