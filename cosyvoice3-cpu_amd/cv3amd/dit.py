@@ -41,7 +41,7 @@ from typing import Dict, List, Optional
 import numpy as np
 
 from . import _lib
-from .device import DeviceArray, Graph, to_device
+from .device import DeviceArray, Event, Graph, Stream, to_device, wait_event
 from .quant import QTensor
 
 ACT = _lib.ACT
@@ -62,6 +62,13 @@ def _host(a) -> np.ndarray:
 # (cv3_linear_q8_x3_frag) depending on the machine, and the whole 30 s solve 1.0-1.1 ms slower
 # (92.9 against 91.9 ms); out and ff2 (1024 outputs) were no faster at all.
 DIGITS = False
+# From HALVES_MIN_T frames on, the two batch rows of the CFG pair (conditional, unconditional)
+# go through the transformer blocks on two streams, so that one row's norms, attention and
+# launch gaps overlap the other's GEMMs (bit-identical results).  30 s q8 solve: 90.4 -> 86.0 ms;
+# at 10 s (500 frames) one row's GEMMs fill half the machine and the solve was 0.3 ms slower,
+# so below the threshold both rows share each launch.  DeviceDiT.halves overrides it.
+HALVES = True
+HALVES_MIN_T = 1024
 
 
 class DeviceLinear:
@@ -148,26 +155,28 @@ class DeviceLinear:
             return self.q.nbytes + self.scales.nbytes
         return self.planes.nbytes if self.planes is not None else self.w.nbytes
 
-    def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None, rexp_given: bool = False):
+    def __call__(self, x: int, m: int, ldx: int, y: int, ldy: int, epi=None, rexp_given: bool = False,
+                 st=None, rexp_row0: int = 0):
         """y[m, n] = epi(x[m, :k] . W^T + bias) on the calling thread's stream.  ``rexp_given``: the
-        digit-plane path's row exponents of this x are already in ``rexp`` (cv3_layer_norm_rexp)."""
+        digit-plane path's row exponents of this x are already in ``rexp`` from row ``rexp_row0`` on
+        (cv3_layer_norm_rexp); ``st``: a stream handle (None: the calling thread's)."""
         b = self.bias.ptr if self.bias is not None else None
         e = ctypes.byref(epi) if epi is not None else None
         if self.q8_digits:
-            if self.rexp is None or self.rexp.size < m:
+            if self.rexp is None or self.rexp.size < rexp_row0 + m:
                 raise ValueError("the digit-plane linear needs an int32 workspace of m entries (rexp)")
             _lib.call("linear_q8_digits", x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
-                      _lib.F16 if self.sf16 else _lib.F32, self.n, b, y, ldy, e, self.rexp.ptr,
-                      int(rexp_given), None)
+                      _lib.F16 if self.sf16 else _lib.F32, self.n, b, y, ldy, e, self.rexp.ptr + 4 * rexp_row0,
+                      int(rexp_given), st)
         elif self.q8:
             fn = "linear_q8_x3_frag" if self.q8_planes else "linear_q"
             kind = () if self.q8_planes else (_lib.KIND_Q8,)
             _lib.call(fn, *kind, x, m, self.k, ldx, self.q.ptr, self.scales.ptr,
-                      _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, None)
+                      _lib.F16 if self.sf16 else _lib.F32, self.kp, self.block, self.n, b, y, ldy, e, st)
         elif self.planes is not None:
-            _lib.call("linear_x3_frag", x, m, self.k, ldx, self.planes.ptr, self.n, b, y, ldy, e, None)
+            _lib.call("linear_x3_frag", x, m, self.k, ldx, self.planes.ptr, self.n, b, y, ldy, e, st)
         else:
-            _lib.call("linear_f32", x, m, self.k, ldx, self.w.ptr, self.k, self.n, b, y, ldy, e, None)
+            _lib.call("linear_f32", x, m, self.k, ldx, self.w.ptr, self.k, self.n, b, y, ldy, e, st)
 
 
 def sinus_features(t: np.ndarray, dim: int = 256, scale: float = 1000.0) -> np.ndarray:
@@ -272,6 +281,9 @@ class DeviceDiT:
         self.proj_out = DeviceLinear([g("proj_out.weight")], [g("proj_out.bias")], planes)
         self._T = None
         self._graph = None
+        self.halves = False                  # set by prepare() from HALVES and T
+        self._side: Optional[Stream] = None
+        self._ev = None
 
     # -- workspace ------------------------------------------------------------
     def prepare(self, mu: np.ndarray, spks: np.ndarray, cond: np.ndarray):
@@ -287,6 +299,7 @@ class DeviceDiT:
         inp[0, :, 2 * mel:3 * mel] = np.asarray(mu[0], np.float32).T
         inp[0, :, 3 * mel:] = np.asarray(spks[0], np.float32)[None, :]
         self.inp = to_device(inp)
+        self.halves = HALVES and T >= HALVES_MIN_T
         if self._T != T:
             self._T = T
             self.h = DeviceArray((B * T, D))
@@ -323,15 +336,42 @@ class DeviceDiT:
         _lib.call("act", ACT["silu"], 0.0, self.temb.ptr, self.stemb.ptr, S * D, None)
         self.mod(self.stemb.ptr, S, D, self.mods.ptr, self.ld_mod)
 
-    def _norm(self, shift: int, scale: int, rexp: bool):
-        """n = LN(h) (1 + scale) + shift over all B T rows (dit.py:168-169), with the rows'
+    def _norm(self, shift: int, scale: int, rexp: bool, r0: int, rows: int, st):
+        """n = LN(h) (1 + scale) + shift over rows r0 .. r0 + rows (dit.py:168-169), with the rows'
         exponents into ``self.rexp`` when a digit-plane linear reads n next."""
-        BT, D = 2 * self._T, self.dim
+        D = self.dim
+        h, n = self.h.ptr + 4 * r0 * D, self.n.ptr + 4 * r0 * D
         if rexp:
-            _lib.call("layer_norm_rexp", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, shift, scale, 0, 0,
-                      self.rexp.ptr, None)
+            _lib.call("layer_norm_rexp", h, n, rows, D, 1e-6, None, None, shift, scale, 0, 0,
+                      self.rexp.ptr + 4 * r0, st)
         else:
-            _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, shift, scale, 0, 0, None)
+            _lib.call("layer_norm", h, n, rows, D, 1e-6, None, None, shift, scale, 0, 0, st)
+
+    def _block(self, i: int, mrow: int, r0: int, nb: int, st):
+        """Transformer block i (dit.py:114-141,160-171) over batch rows r0 / T .. + nb of the CFG
+        pair, on stream handle ``st``."""
+        T, D, H, dh, f4 = self._T, self.dim, self.heads, self.dim_head, 4
+        S3 = ctypes.c_int64 * 3
+        rows = nb * T
+        h, n, att = (a.ptr + f4 * r0 * D for a in (self.h, self.n, self.att))
+        qkvb, ffb = self.qkvb.ptr + f4 * r0 * 3 * D, self.ffb.ptr + f4 * r0 * self.ff_dim
+        qs = S3(T * 3 * D, dh, 3 * D)
+        os_ = S3(T * D, dh, D)
+        scale = float(np.float32(1.0 / math.sqrt(dh)))
+        base = mrow + i * 6 * D * f4
+        sh_a, sc_a, g_a, sh_m, sc_m, g_m = (base + j * D * f4 for j in range(6))
+        self._norm(sh_a, sc_a, self.qkv[i].q8_digits, r0, rows, st)
+        # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120), in the GEMM epilogue
+        rope_epi = _lib.epilogue(rope=(self.cos.ptr, self.sin.ptr, T, D, dh, 2 * D))
+        self.qkv[i](n, rows, D, qkvb, 3 * D, rope_epi, rexp_given=True, st=st, rexp_row0=r0)
+        _lib.call("attention_x3" if self.planes else "attention", qkvb, qkvb + D * f4, qkvb + 2 * D * f4, att,
+                  nb, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0, st)
+        self.out[i](att, rows, D, h, D,
+                    _lib.epilogue(residual=h, ld_res=D, gate=g_a, gate_stride=0, rows_per_gate=1), st=st)
+        self._norm(sh_m, sc_m, self.ff1[i].q8_digits, r0, rows, st)
+        self.ff1[i](n, rows, D, ffb, self.ff_dim, _lib.epilogue("gelu_tanh"), rexp_given=True, st=st, rexp_row0=r0)
+        self.ff2[i](ffb, rows, self.ff_dim, h, D,
+                    _lib.epilogue(residual=h, ld_res=D, gate=g_m, gate_stride=0, rows_per_gate=1), st=st)
 
     def _step(self, s: int, dt: float, update: bool = True):
         T, D, B, mel, H, dh = self._T, self.dim, 2, self.mel, self.heads, self.dim_head
@@ -352,25 +392,21 @@ class DeviceDiT:
                   self.conv_b[1].ptr, self.h.ptr, D,
                   ctypes.byref(_lib.epilogue("mish", residual=self.h.ptr, ld_res=D)), None)
         mrow = self.mods.ptr + s * self.ld_mod * f4
-        qs = S3(T * 3 * D, dh, 3 * D)
-        rope_epi = _lib.epilogue(rope=(self.cos.ptr, self.sin.ptr, T, D, dh, 2 * D))
-        os_ = S3(T * D, dh, D)
-        scale = float(np.float32(1.0 / math.sqrt(dh)))
-        for i in range(self.depth):
-            base = mrow + i * 6 * D * f4
-            sh_a, sc_a, g_a, sh_m, sc_m, g_m = (base + j * D * f4 for j in range(6))
-            self._norm(sh_a, sc_a, self.qkv[i].q8_digits)
-            # partial rotary on q and k, channels 0..dh-1 (dit.py:119-120), in the GEMM epilogue
-            self.qkv[i](self.n.ptr, BT, D, self.qkvb.ptr, 3 * D, rope_epi, rexp_given=True)
-            _lib.call("attention_x3" if self.planes else "attention", self.qkvb.ptr, self.qkvb.ptr + D * f4,
-                      self.qkvb.ptr + 2 * D * f4, self.att.ptr, B, H, H, T, T, dh, qs, qs, qs, os_, scale, 0, 0, 0,
-                      None)
-            self.out[i](self.att.ptr, BT, D, self.h.ptr, D,
-                        _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_a, gate_stride=0, rows_per_gate=1))
-            self._norm(sh_m, sc_m, self.ff1[i].q8_digits)
-            self.ff1[i](self.n.ptr, BT, D, self.ffb.ptr, self.ff_dim, _lib.epilogue("gelu_tanh"), rexp_given=True)
-            self.ff2[i](self.ffb.ptr, BT, self.ff_dim, self.h.ptr, D,
-                        _lib.epilogue(residual=self.h.ptr, ld_res=D, gate=g_m, gate_stride=0, rows_per_gate=1))
+        if self.halves:
+            # the CFG pair's two batch rows are independent through every block: the second on
+            # a side stream, forked and joined around the blocks (graph edges under capture)
+            if self._side is None:
+                self._side, self._ev = Stream(), (Event(), Event())
+            self._ev[0].record(None)
+            self._side.wait(self._ev[0])
+            for i in range(self.depth):
+                self._block(i, mrow, 0, 1, None)
+                self._block(i, mrow, T, 1, self._side.handle)
+            self._ev[1].record(self._side)
+            wait_event(self._ev[1])
+        else:
+            for i in range(self.depth):
+                self._block(i, mrow, 0, B, None)
         base = mrow + self.depth * 6 * D * f4      # norm_out: (scale, shift) (dit.py:175-178)
         _lib.call("layer_norm", self.h.ptr, self.n.ptr, BT, D, 1e-6, None, None, base + D * f4, base, 0, 0, None)
         self.proj_out(self.n.ptr, BT, D, self.outb.ptr, mel)

@@ -108,3 +108,26 @@ def test_q8_dit_long_utterance(gpu):
     e = rel_err(got, want[0])
     print(f"[flow] rel err {e:.2e}", flush=True)
     assert e < 1e-4
+
+
+@pytest.mark.parametrize("profile", ["f32", "per_channel"])
+def test_cfg_halves_on_two_streams_change_nothing(gpu, profile):
+    """From 1024 frames the CFG pair's two batch rows run through the blocks on two streams
+    (forked and joined around them): the solve, eager and replayed from its graph three times,
+    is bit-identical to the one with both rows in every launch."""
+    import cv3amd.dit as dit
+    _, dev = _stores(2, profile)
+    T = 1100
+    mu, cond, spks, x0 = _inputs(T, seed=7)
+    d = dit.DeviceDiT(dev, steps=2)
+    d.prepare(mu, spks, cond)
+    assert d.halves == dit.HALVES and T >= dit.HALVES_MIN_T
+    print(f"[flow] halves {profile} depth=2 T={T}", flush=True)
+    d.halves = False
+    want = d.solve(x0).numpy().copy()
+    d.halves, d._graph = True, None
+    np.testing.assert_array_equal(d.solve(x0).numpy(), want)
+    for _ in range(3):
+        np.testing.assert_array_equal(d.solve(x0, graph=True).numpy(), want)
+    d.prepare(mu[:, :, :500], spks, cond[:, :, :500])
+    assert not d.halves
