@@ -414,7 +414,8 @@ def bench_flow_q8(args, tensors, meta, profile: str):
     flops = d.flops_per_solve()
     log(f"flow q8 ({profile}) 30 s: {ms:.2f} ms/solve, RTF {ms / 1e3 / 30.0:.2e}, "
         f"{flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
-    return {"ms": ms, "flops": flops, "by_unit": d.flops_by_unit(), "T": T}
+    return {"ms": ms, "flops": flops, "by_unit": d.flops_by_unit(), "T": T, "halves": d.halves,
+            "digits": d.qkv[0].q8_digits if d.depth else False}
 
 
 def bench_kernels(args):
@@ -912,15 +913,21 @@ def main():
     if flow_q8 is not None:
         scales = {"per_channel": "per-output-channel int8 + float32 scales",
                   "balanced": "block-64 int8 + float16 scales (the converter's balanced profile)"}
-        how = {"per_channel": "each activation row rounded 30 bits below its largest element and split into four "
-                              "int8 digit planes, each times the codes an exact int32 sum on the int8 matrix cores, "
-                              "combined in float64 and scaled per output channel",
-               "balanced": "the activation's three bfloat16 planes times the codes (exact in bfloat16), the block "
-                           "scale on each block sum, fp32 accumulate"}
+        planes = ("the activation's three bfloat16 planes times the codes (exact in bfloat16), the {} scale on "
+                  "each {} sum, fp32 accumulate")
+        how = {"per_channel": planes.format("output channel's", "row"),
+               "balanced": planes.format("block", "block")}
+        if flow_q8.get("per_channel", {}).get("digits"):
+            how["per_channel"] = ("QKV and ff1 with each activation row rounded 30 bits below its largest element "
+                                  "and split into four int8 digit planes, each times the codes an exact int32 sum "
+                                  "on the int8 matrix cores, combined in float64 and scaled per output channel; "
+                                  "out and ff2 " + how["per_channel"])
+        halves = ("; the CFG pair's two rows through the blocks on two streams"
+                  if any(fq.get("halves") for fq in flow_q8.values()) else "")
         for prof, fq in flow_q8.items():
             line["flow_q8_30s" if prof == "per_channel" else "flow_q8_30s_block64"] = {
                 "workload": f"DiT flow decoder, 30 s audio (1500 frames), 22 blocks, 10 Euler steps, CFG, q8 linears "
-                            f"({scales[prof]}): {how[prof]}",
+                            f"({scales[prof]}): {how[prof]}{halves}",
                 "ms_per_solve": round(fq["ms"], 3), "rtf": round(fq["ms"] / 1e3 / 30.0, 6),
                 "tflops": round(fq["flops"] / (fq["ms"] / 1e3) / 1e12, 2),
                 "roofline_ms": round(matrix_floor_ms(fq["by_unit"]), 3),
