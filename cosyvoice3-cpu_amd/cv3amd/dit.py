@@ -56,12 +56,13 @@ def _host(a) -> np.ndarray:
 
 
 # True puts the per-channel q8 QKV and ff1 linears of the DiT on the int8 matrix cores as digit
-# planes (cv3_linear_q8_digits; 5x smaller error against float64), their row exponents written by
-# the layer norm that feeds them (cv3_layer_norm_rexp).  Off: at the 30 s shapes (3000 rows) the
-# digit-plane QKV ran 78.6-85.1 us against 85.6-86.3 us on the bfloat16 planes
-# (cv3_linear_q8_x3_frag) depending on the machine, and the whole 30 s solve 1.0-1.1 ms slower
-# (92.9 against 91.9 ms); out and ff2 (1024 outputs) were no faster at all.
-DIGITS = False
+# planes (cv3_linear_q8_digits; every product exact, 5x smaller error against float64 than the
+# bfloat16 planes of cv3_linear_q8_x3_frag), their row exponents written by the layer norm that
+# feeds them (cv3_layer_norm_rexp).  At the 30 s shapes (3000 rows) the digit-plane QKV ran
+# 78.6-85.1 us against 85.6-86.3 us on the planes depending on the machine; with the CFG rows on
+# two streams the 30 s solve ran level (86.3-87.0 against 86.9 ms).  out and ff2 (1024 outputs)
+# were no faster on the digit planes and stay on the bfloat16 planes.
+DIGITS = True
 # From HALVES_MIN_T frames on, the two batch rows of the CFG pair (conditional, unconditional)
 # go through the transformer blocks on two streams, so that one row's norms, attention and
 # launch gaps overlap the other's GEMMs (bit-identical results).  30 s q8 solve: 90.4 -> 86.0 ms;
