@@ -1,6 +1,7 @@
 // Device helpers shared by the decode kernels (decode.hip: the five-kernel step
 // and the one-launch step over the stacked weights; decode_stream.hip: the
-// one-launch step over per-workgroup weight streams).
+// one-launch step over per-workgroup weight streams), and the wave sums of the
+// one-wave-per-row layer norm (elementwise.hip).
 #pragma once
 
 #include "common.hpp"

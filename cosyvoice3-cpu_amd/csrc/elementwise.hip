@@ -10,6 +10,7 @@
 // caller would otherwise make several passes.
 #include "common.hpp"
 #include "epilogue.hpp"
+#include "decode_common.hpp"   // wave_sum_swap: DPP and permlane wave sums
 
 using namespace cv3;
 
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-  const float mu = wave_sum(s) / (float)cols;
+  const float mu = wave_sum_swap(s) / (float)cols;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_wave(const float* __restrict
       q = fmaf(d3, d3, q);
     }
   }
-  const float den = sqrtf(wave_sum(q) / (float)cols + eps);
+  const float den = sqrtf(wave_sum_swap(q) / (float)cols + eps);
   float4* yr = reinterpret_cast<float4*>(y + row * cols);
   float mx = 0.f;
 #pragma unroll
